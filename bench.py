@@ -1,0 +1,308 @@
+# SPDX-License-Identifier: Apache-2.0
+"""Benchmark of the gfx950 quantized-matmul hot path on one MI355X.
+
+Default workload (--config 1): one decode token through a DeepSeek-V4-Flash
+MoE layer's routed experts -- 256 FP4 experts resident in HBM (gate/up
+2048x4096, down 4096x2048, e2m1 packed two per byte, E8M0 scale per 1x32),
+top-6 uniform routing with softmax weights, SwiGLU (limit 10), k-order
+weighted combine. One step = one token. Every step routes to a fresh set of
+six experts, so the weights stream from HBM rather than from the 256 MB
+Infinity Cache. Metric: algorithmic HBM GB/s (6 x 13,369,344 B of expert
+weights and scales + 8 KiB bf16 x + 16 KiB fp32 out per token).
+
+--config 0: one 4096x4096 e4m3 matvec with fp32 128x128 scales, x bf16;
+weights rotated over 40 copies (672 MB) so each step reads from HBM.
+
+Prints ONE JSON line. Synthetic data (seeded), random-init weights.
+"""
+from __future__ import annotations
+
+import argparse
+import ctypes as C
+import importlib.util
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+HBM_PEAK_GBS = 8000.0
+
+EXPERT_BYTES = 13_369_344          # w1,w3: 2048x4096 FP4 + scales; w2: 4096x2048
+HIDDEN, INTER, N_EXPERTS, TOPK = 4096, 2048, 256, 6
+
+
+def load_pkg():
+    spec = importlib.util.spec_from_file_location(
+        "dsv4_amd", os.path.join(ROOT, "deepseek-v4-in-c_amd", "__init__.py"))
+    mod = importlib.util.module_from_spec(spec)
+    sys.modules["dsv4_amd"] = mod
+    spec.loader.exec_module(mod)
+    return mod
+
+
+def log(msg):
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+# ------------------------------------------------------------ workloads ----
+
+class ExpertArena:
+    """256 FP4 experts in one device arena, each laid out like the reference's
+    cache slot (src/60_cache/dsv4_cache_geom.c:14-31): scales s1, s2, s3 then
+    weights w1, w2, w3."""
+
+    def __init__(self, torch, pkg, lib, n_experts, seed):
+        self.n = n_experts
+        dev = "cuda:0"
+        self.buf = torch.empty(n_experts * EXPERT_BYTES, dtype=torch.uint8, device=dev)
+        wb = [INTER * HIDDEN // 2, HIDDEN * INTER // 2, INTER * HIDDEN // 2]
+        sb = [INTER * HIDDEN // 32, HIDDEN * INTER // 32, INTER * HIDDEN // 32]
+        shapes = [(INTER, HIDDEN), (HIDDEN, INTER), (INTER, HIDDEN)]   # w1, w2, w3
+        off_s = [0, sb[0], sb[0] + sb[1]]
+        off_w = [sum(sb), sum(sb) + wb[0], sum(sb) + wb[0] + wb[1]]
+        tmp = torch.empty(INTER * HIDDEN, dtype=torch.float32, device=dev)
+        base = self.buf.data_ptr()
+        descs = []
+        for e in range(n_experts):
+            eb = base + e * EXPERT_BYTES
+            q = []
+            for i, (r, c) in enumerate(shapes):
+                lib.synth_normal_dev(tmp.data_ptr(), r * c, seed * 1000003 + e * 3 + i, 0.02)
+                lib.quant_fp4_mx_dev(eb + off_w[i], eb + off_s[i], tmp.data_ptr(), r, c)
+                q.append(pkg.qmat(pkg.DSV4_WFP4, eb + off_w[i], eb + off_s[i], r, c, 1, 32))
+            descs.append(pkg.ExpertW(q[0], q[2], q[1]))   # (w1, w3, w2)
+        torch.cuda.synchronize()
+        raw = b"".join(bytes(d) for d in descs)
+        self.descs = descs
+        self.table = torch.frombuffer(bytearray(raw), dtype=torch.uint8).to(dev)
+
+    def host_copy(self, torch, e):
+        return self.buf[e * EXPERT_BYTES:(e + 1) * EXPERT_BYTES].cpu().numpy()
+
+
+def routing(n_steps, seed):
+    rng = np.random.default_rng(seed)
+    idx = np.stack([rng.choice(N_EXPERTS, TOPK, replace=False) for _ in range(n_steps)])
+    lg = rng.standard_normal((n_steps, TOPK))
+    w = np.exp(lg) / np.exp(lg).sum(1, keepdims=True)
+    return idx.astype(np.int32), w.astype(np.float32)
+
+
+def time_events(torch, stream, fn, n):
+    """Average duration of fn() over n calls, each bracketed by its own HIP
+    events on `stream` (the stream the kernels are launched on)."""
+    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+           for _ in range(n)]
+    for i, (a, b) in enumerate(evs):
+        a.record(stream)
+        fn(i)
+        b.record(stream)
+    torch.cuda.synchronize()
+    return float(np.mean([a.elapsed_time(b) for a, b in evs])) * 1e-3
+
+
+# --------------------------------------------------------- CPU baseline ----
+
+def omp_threads(n):
+    try:
+        gomp = C.CDLL("libgomp.so.1")
+        gomp.omp_set_num_threads(int(n))
+    except OSError:
+        pass
+
+
+def cpu_baseline_cfg1(torch, arena, x_host, seconds, threads):
+    """The reference's CPU path on the host: dsv4_expert_forward x 6 + the
+    k-order combine, over 16 experts copied from the device arena (214 MB,
+    beyond the host LLC). Runs tokens until `seconds` elapse (min 3)."""
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import pyoracle as P
+    kind = "reference"
+    try:
+        impl = P.Reference()
+    except FileNotFoundError:
+        impl, kind = P.Oracle(), "port"
+    orc = P.Oracle()
+    omp_threads(threads)
+    n_host = 16
+    experts = []
+    keep = []
+    wb = [INTER * HIDDEN // 2, HIDDEN * INTER // 2, INTER * HIDDEN // 2]
+    sb = [INTER * HIDDEN // 32, HIDDEN * INTER // 32, INTER * HIDDEN // 32]
+    off_s = [0, sb[0], sb[0] + sb[1]]
+    off_w = [sum(sb), sum(sb) + wb[0], sum(sb) + wb[0] + wb[1]]
+    shapes = [(INTER, HIDDEN), (HIDDEN, INTER), (INTER, HIDDEN)]
+    for e in range(n_host):
+        raw = arena.host_copy(torch, e)
+        keep.append(raw)
+        mats = [P.HostMat(P.DSV4_WFP4, raw[off_w[i]:off_w[i] + wb[i]],
+                          raw[off_s[i]:off_s[i] + sb[i]], r, c, 1, 32)
+                for i, (r, c) in enumerate(shapes)]
+        experts.append(P.HostExpert(mats[0], mats[2], mats[1]))
+    rng = np.random.default_rng(7)
+    t0 = time.perf_counter()
+    tokens = 0
+    while True:
+        ids = rng.choice(n_host, TOPK, replace=False)
+        lg = rng.standard_normal(TOPK)
+        w = (np.exp(lg) / np.exp(lg).sum()).astype(np.float32)
+        acc = np.stack([impl.expert_forward(experts[i], x_host, 10.0) for i in ids])
+        orc.moe_combine(acc, w)
+        tokens += 1
+        el = time.perf_counter() - t0
+        if tokens >= 3 and el >= seconds:
+            break
+    gbs = tokens * (TOPK * EXPERT_BYTES + 8192 + 16384) / el / 1e9
+    return {"value": round(gbs, 3), "unit": "GB/s", "cores": threads, "kind": kind,
+            "sample": f"{tokens} tokens x top-6 over 16 host-resident FP4 experts "
+                      f"(214 MB), {el:.1f} s, OpenMP {threads} threads"}
+
+
+# ------------------------------------------------------------------ main ----
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--config", type=int, default=1, choices=[0, 1])
+    ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--cpu-threads", type=int, default=0)
+    ap.add_argument("--no-cpu", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only (this build has no multi-GPU path); "
+              f"got --gpus {args.gpus}", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+    pkg = load_pkg()
+    lib = pkg.load()
+    lib.check(lib.init(0), "dsv4_hip_init")
+    stream = torch.cuda.current_stream()
+    sp = stream.cuda_stream
+    K, W = args.steps, args.warmup
+
+    if args.config == 1:
+        log("generating 256 FP4 experts on the device")
+        arena = ExpertArena(torch, pkg, lib, N_EXPERTS, seed=0xD5EED001)
+        idx_h, w_h = routing(K + W + K, seed=0xD5EED001)
+        idx = torch.from_numpy(idx_h).to("cuda:0")
+        wts = torch.from_numpy(w_h).to("cuda:0")
+        xs = torch.empty((K + W + K) * HIDDEN, dtype=torch.float32, device="cuda:0")
+        lib.synth_normal_dev(xs.data_ptr(), xs.numel(), 0xD5EED001 ^ 0x55, 1.0, True)
+        out = torch.empty(HIDDEN, dtype=torch.float32, device="cuda:0")
+        torch.cuda.synchronize()
+
+        def step(i):
+            lib.moe_decode_dev(out.data_ptr(), xs.data_ptr() + 4 * HIDDEN * i,
+                               arena.table.data_ptr(), N_EXPERTS,
+                               idx.data_ptr() + 4 * TOPK * i, wts.data_ptr() + 4 * TOPK * i,
+                               TOPK, None, HIDDEN, INTER, 10.0, sp)
+
+        for i in range(W):
+            step(i)
+        torch.cuda.synchronize()
+        assert lib.status() == 0
+        log(f"timing {K} steps")
+        t0 = time.perf_counter()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        for i in range(K):
+            step(W + i)
+        e1.record(stream)
+        torch.cuda.synchronize()
+        wall = time.perf_counter() - t0
+        t_step = e0.elapsed_time(e1) * 1e-3 / K
+        # per-launch durations (each call bracketed by its own events)
+        t_launch = time_events(torch, stream, lambda i: step(W + K + i), K)
+        assert lib.status() == 0
+        bytes_step = TOPK * EXPERT_BYTES + 8192 + 16384
+        value = bytes_step / t_step / 1e9
+        achieved = bytes_step / t_launch / 1e9
+        cpu = None
+        if not args.no_cpu:
+            threads = args.cpu_threads or min(16, os.cpu_count() or 1)
+            x_host = xs[:HIDDEN].cpu().numpy()
+            log(f"CPU baseline ({threads} threads, {args.cpu_seconds:.0f} s)")
+            cpu = cpu_baseline_cfg1(torch, arena, x_host, args.cpu_seconds, threads)
+        res = {
+            "metric": "quant matvec HBM GB/s (% peak); prefill FP4/FP8 GEMM TFLOP/s (% MFMA peak)",
+            "value": round(value, 2), "unit": "GB/s", "n_gpus": 1, "steps": K, "warmup": W,
+            "ms_per_step": round(t_step * 1e3, 5), "higher_is_better": True, "scaling": "weak",
+            "vs_baseline": None, "dtype": "fp4 e2m1 weights, fp32 accumulate",
+            "data": "synthetic (seeded N(0,0.02) experts, bf16 N(0,1) token), random-init",
+            "config": {"workload": "single-token FP4 MoE expert FFN decode: 256 resident experts, "
+                                   "top-6, gate/up 2048x4096 + down 4096x2048, SwiGLU, combine",
+                       "tokens_per_step": 1, "hidden": HIDDEN, "moe_inter": INTER,
+                       "n_experts": N_EXPERTS, "topk": TOPK, "parallelism": "single GPU"},
+            "tokens_per_s": round(1.0 / t_step, 1),
+            "hbm_frac": round(value / HBM_PEAK_GBS, 4),
+            "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS,
+                         "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
+                         "traffic": None,
+                         "kernel": "moe_decode_dev call (k_gateup + k_down_combine)",
+                         "bytes_per_launch": bytes_step,
+                         "launch_us": round(t_launch * 1e6, 3)},
+            "cpu_baseline": cpu,
+            "wall_s": round(wall, 4),
+        }
+    else:
+        ncopy = 40
+        log(f"generating {ncopy} copies of a 4096x4096 FP8 matrix")
+        Wd = torch.empty(ncopy * 4096 * 4096, dtype=torch.uint8, device="cuda:0")
+        Sd = torch.empty(ncopy * 32 * 32, dtype=torch.float32, device="cuda:0")
+        tmp = torch.empty(4096 * 4096, dtype=torch.float32, device="cuda:0")
+        for c in range(ncopy):
+            lib.synth_normal_dev(tmp.data_ptr(), tmp.numel(), 0xD5EED000 + c, 0.02)
+            lib.quant_fp8_blk128_dev(Wd.data_ptr() + c * 4096 * 4096,
+                                     Sd.data_ptr() + 4 * c * 1024, tmp.data_ptr(), 4096, 4096)
+        xs = torch.empty(4096, dtype=torch.float32, device="cuda:0")
+        lib.synth_normal_dev(xs.data_ptr(), 4096, 0xD5EED000 ^ 0x55, 1.0, True)
+        y = torch.empty(4096, dtype=torch.float32, device="cuda:0")
+        descs = [pkg.qmat(pkg.DSV4_WFP8_F32S, Wd.data_ptr() + c * 4096 * 4096,
+                          Sd.data_ptr() + 4 * c * 1024, 4096, 4096, 128, 128) for c in range(ncopy)]
+        torch.cuda.synchronize()
+
+        def step(i):
+            lib.mmq_n_dev(y.data_ptr(), xs.data_ptr(), descs[i % ncopy], 1, sp)
+
+        for i in range(W):
+            step(i)
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        t0 = time.perf_counter()
+        e0.record(stream)
+        for i in range(K):
+            step(i)
+        e1.record(stream)
+        torch.cuda.synchronize()
+        wall = time.perf_counter() - t0
+        t_step = e0.elapsed_time(e1) * 1e-3 / K
+        t_launch = time_events(torch, stream, step, K)
+        bytes_step = 16_805_888
+        value = bytes_step / t_step / 1e9
+        res = {
+            "metric": "quant matvec HBM GB/s (% peak); prefill FP4/FP8 GEMM TFLOP/s (% MFMA peak)",
+            "value": round(value, 2), "unit": "GB/s", "n_gpus": 1, "steps": K, "warmup": W,
+            "ms_per_step": round(t_step * 1e3, 5), "higher_is_better": True, "scaling": "weak",
+            "vs_baseline": None, "dtype": "fp8 e4m3 weights, fp32 accumulate",
+            "data": "synthetic (seeded), random-init",
+            "config": {"workload": "FP8 matvec 4096x4096, fp32 128x128 scales, bf16 x",
+                       "copies_rotated": ncopy, "parallelism": "single GPU"},
+            "roofline": {"bound": "hbm", "achieved": round(bytes_step / t_launch / 1e9, 2),
+                         "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                         "frac": round(bytes_step / t_launch / 1e9 / HBM_PEAK_GBS, 4),
+                         "traffic": None, "kernel": "k_gemv<FP8_F32S,4,2>",
+                         "bytes_per_launch": bytes_step, "launch_us": round(t_launch * 1e6, 3)},
+            "cpu_baseline": None,
+            "wall_s": round(wall, 4),
+        }
+    print(json.dumps(res), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,222 @@
+# SPDX-License-Identifier: Apache-2.0
+"""Python binding of the gfx950 quantized-matmul library (lib/libdsv4_hip.so).
+
+The product is the C ABI declared in include/dsv4_hip.h and
+include/dsv4_hip_aux.h; this module binds it with ctypes for tests and the
+benchmark. Host-pointer calls take numpy arrays; _dev calls take device
+addresses (e.g. torch tensors' data_ptr()) and a HIP stream handle.
+
+Importing fails loudly when the library has not been built: there is no
+fallback implementation behind this module.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_DIR = os.path.join(HERE, "lib")
+HIP_SO = os.path.join(LIB_DIR, "libdsv4_hip.so")
+AMD_SO = os.path.join(LIB_DIR, "libdsv4_amd.so")
+
+# src/00_base/dsv4.h:86 plus this library's DSV4_WFP8_F32S
+DSV4_WF32, DSV4_WBF16, DSV4_WFP8, DSV4_WFP4, DSV4_WFP8_F32S = 0, 1, 2, 3, 4
+
+# every symbol include/*.h declares
+EXPORTS = (
+    "dsv4_hip_init", "dsv4_hip_shutdown", "dsv4_hip_last_error",
+    "dsv4_hip_register", "dsv4_hip_unregister", "dsv4_hip_device_ptr",
+    "dsv4_hip_mmq_n", "dsv4_hip_mmq", "dsv4_hip_mmq_n_dev",
+    "dsv4_hip_expert_forward", "dsv4_hip_moe_decode", "dsv4_hip_moe_decode_dev",
+    "dsv4_hip_status",
+    "dsv4_hip_dequant_dev", "dsv4_hip_quant_fp8_blk128_dev",
+    "dsv4_hip_quant_fp4_mx_dev", "dsv4_hip_quant_act_fp8_1x128_dev",
+    "dsv4_hip_quant_act_mxfp8_dev", "dsv4_hip_synth_normal_dev",
+)
+# the reference-named C mirror (host/dsv4_compute_hip.c)
+MIRROR_EXPORTS = ("dsv4_mmq_n", "dsv4_mmq", "dsv4_expert_forward")
+
+
+class QMat(C.Structure):
+    """DSV4QMat (src/00_base/dsv4_weights.h:34-40)."""
+    _fields_ = [("w", C.c_void_p), ("s", C.c_void_p), ("wdt", C.c_int),
+                ("rows", C.c_int), ("cols", C.c_int),
+                ("blk_r", C.c_int), ("blk_c", C.c_int)]
+
+
+class ExpertW(C.Structure):
+    """DSV4ExpertW (src/00_base/dsv4_weights.h:103-106)."""
+    _fields_ = [("w1", QMat), ("w3", QMat), ("w2", QMat)]
+
+
+_P, _I, _F = C.c_void_p, C.c_int, C.c_float
+
+
+def weight_bytes(wdt, rows, cols):
+    return rows * (cols // 2) if wdt == DSV4_WFP4 else rows * cols
+
+
+def scale_entries(rows, cols, blk_r, blk_c):
+    return ((rows + blk_r - 1) // blk_r) * ((cols + blk_c - 1) // blk_c)
+
+
+def scale_bytes(wdt, rows, cols, blk_r, blk_c):
+    n = scale_entries(rows, cols, blk_r, blk_c)
+    return 4 * n if wdt == DSV4_WFP8_F32S else n
+
+
+class Dsv4Error(RuntimeError):
+    pass
+
+
+class Lib:
+    """ctypes view of libdsv4_hip.so."""
+
+    def __init__(self, path: str = HIP_SO):
+        if not os.path.exists(path):
+            raise Dsv4Error(f"{path} is not built: run __graft_entry__.build()")
+        self.path = path
+        L = self.lib = C.CDLL(path)
+        L.dsv4_hip_init.restype = _I; L.dsv4_hip_init.argtypes = [_I]
+        L.dsv4_hip_shutdown.restype = None; L.dsv4_hip_shutdown.argtypes = []
+        L.dsv4_hip_last_error.restype = C.c_char_p; L.dsv4_hip_last_error.argtypes = []
+        L.dsv4_hip_register.restype = _I; L.dsv4_hip_register.argtypes = [_P, C.c_size_t]
+        L.dsv4_hip_unregister.restype = _I; L.dsv4_hip_unregister.argtypes = [_P]
+        L.dsv4_hip_device_ptr.restype = _P; L.dsv4_hip_device_ptr.argtypes = [_P]
+        L.dsv4_hip_mmq_n.restype = _I
+        L.dsv4_hip_mmq_n.argtypes = [_P, _P, C.POINTER(QMat), _I]
+        L.dsv4_hip_mmq.restype = _I; L.dsv4_hip_mmq.argtypes = [_P, _P, C.POINTER(QMat)]
+        L.dsv4_hip_mmq_n_dev.restype = _I
+        L.dsv4_hip_mmq_n_dev.argtypes = [_P, _P, C.POINTER(QMat), _I, _P]
+        L.dsv4_hip_expert_forward.restype = _I
+        L.dsv4_hip_expert_forward.argtypes = [_P, _P, C.POINTER(ExpertW), _I, _F]
+        L.dsv4_hip_moe_decode.restype = _I
+        L.dsv4_hip_moe_decode.argtypes = [_P, _P, C.POINTER(C.POINTER(ExpertW)), _P, _I,
+                                          C.POINTER(ExpertW), _F]
+        L.dsv4_hip_moe_decode_dev.restype = _I
+        L.dsv4_hip_moe_decode_dev.argtypes = [_P, _P, _P, _I, _P, _P, _I,
+                                              C.POINTER(ExpertW), _I, _I, _F, _P]
+        L.dsv4_hip_status.restype = _I; L.dsv4_hip_status.argtypes = [C.POINTER(C.c_uint)]
+        L.dsv4_hip_dequant_dev.restype = _I
+        L.dsv4_hip_dequant_dev.argtypes = [_P, C.POINTER(QMat), _P]
+        for n in ("dsv4_hip_quant_fp8_blk128_dev", "dsv4_hip_quant_fp4_mx_dev",
+                  "dsv4_hip_quant_act_fp8_1x128_dev", "dsv4_hip_quant_act_mxfp8_dev"):
+            getattr(L, n).restype = _I
+            getattr(L, n).argtypes = [_P, _P, _P, _I, _I, _P]
+        L.dsv4_hip_synth_normal_dev.restype = _I
+        L.dsv4_hip_synth_normal_dev.argtypes = [_P, C.c_size_t, C.c_uint64, _F, _I, _P]
+
+    # ------------------------------------------------------------ basics
+    def error(self) -> str:
+        return (self.lib.dsv4_hip_last_error() or b"").decode()
+
+    def check(self, rc: int, what: str):
+        if rc != 0:
+            raise Dsv4Error(f"{what}: {self.error()}")
+
+    def init(self, device: int = 0) -> int:
+        return self.lib.dsv4_hip_init(device)
+
+    def shutdown(self):
+        self.lib.dsv4_hip_shutdown()
+
+    def register(self, arr: np.ndarray) -> int:
+        assert arr.flags["C_CONTIGUOUS"]
+        return self.lib.dsv4_hip_register(arr.ctypes.data, arr.nbytes)
+
+    def unregister(self, arr: np.ndarray) -> int:
+        return self.lib.dsv4_hip_unregister(arr.ctypes.data)
+
+    def status(self) -> int:
+        v = C.c_uint(0)
+        self.check(self.lib.dsv4_hip_status(C.byref(v)), "status")
+        return v.value
+
+    # ------------------------------------------------ host-pointer entry points
+    def mmq_n(self, desc: QMat, x: np.ndarray, nt: int = 1) -> np.ndarray:
+        x = np.ascontiguousarray(x, np.float32)
+        assert x.size >= nt * desc.cols
+        y = np.zeros(nt * desc.rows, np.float32)
+        self.check(self.lib.dsv4_hip_mmq_n(y.ctypes.data, x.ctypes.data, C.byref(desc), nt),
+                   "dsv4_hip_mmq_n")
+        return y
+
+    def mmq_n_rc(self, desc: QMat, x: np.ndarray, nt: int = 1) -> int:
+        x = np.ascontiguousarray(x, np.float32)
+        y = np.zeros(max(nt, 1) * desc.rows, np.float32)
+        return self.lib.dsv4_hip_mmq_n(y.ctypes.data, x.ctypes.data, C.byref(desc), nt)
+
+    def expert_forward(self, e: ExpertW, x: np.ndarray, limit: float) -> np.ndarray:
+        x = np.ascontiguousarray(x, np.float32)
+        out = np.zeros(e.w1.cols, np.float32)
+        self.check(self.lib.dsv4_hip_expert_forward(out.ctypes.data, x.ctypes.data,
+                                                    C.byref(e), e.w1.rows, float(limit)),
+                   "dsv4_hip_expert_forward")
+        return out
+
+    def moe_decode(self, experts, w, x, shared=None, limit=10.0) -> np.ndarray:
+        topk = len(experts)
+        arr = (C.POINTER(ExpertW) * topk)(*[C.pointer(e) for e in experts])
+        w = np.ascontiguousarray(w, np.float32)
+        x = np.ascontiguousarray(x, np.float32)
+        out = np.zeros(experts[0].w1.cols, np.float32)
+        sp = C.pointer(shared) if shared is not None else None
+        self.check(self.lib.dsv4_hip_moe_decode(out.ctypes.data, x.ctypes.data, arr,
+                                                w.ctypes.data, topk, sp, float(limit)),
+                   "dsv4_hip_moe_decode")
+        return out
+
+    # ---------------------------------------------------------- _dev entry points
+    def mmq_n_dev(self, y_ptr, x_ptr, desc: QMat, nt, stream=None):
+        self.check(self.lib.dsv4_hip_mmq_n_dev(y_ptr, x_ptr, C.byref(desc), nt, stream),
+                   "dsv4_hip_mmq_n_dev")
+
+    def moe_decode_dev(self, out_ptr, x_ptr, table_ptr, n_experts, idx_ptr, w_ptr, topk,
+                       shared: ExpertW | None, hidden, inter, limit, stream=None):
+        sp = C.pointer(shared) if shared is not None else None
+        self.check(self.lib.dsv4_hip_moe_decode_dev(out_ptr, x_ptr, table_ptr, n_experts,
+                                                    idx_ptr, w_ptr, topk, sp, hidden, inter,
+                                                    float(limit), stream),
+                   "dsv4_hip_moe_decode_dev")
+
+    def dequant_dev(self, out_ptr, desc: QMat, stream=None):
+        self.check(self.lib.dsv4_hip_dequant_dev(out_ptr, C.byref(desc), stream),
+                   "dsv4_hip_dequant_dev")
+
+    def quant_fp8_blk128_dev(self, W, S, w, rows, cols, stream=None):
+        self.check(self.lib.dsv4_hip_quant_fp8_blk128_dev(W, S, w, rows, cols, stream),
+                   "quant_fp8_blk128_dev")
+
+    def quant_fp4_mx_dev(self, W, S, w, rows, cols, stream=None):
+        self.check(self.lib.dsv4_hip_quant_fp4_mx_dev(W, S, w, rows, cols, stream),
+                   "quant_fp4_mx_dev")
+
+    def quant_act_fp8_1x128_dev(self, Q, S, a, n, k, stream=None):
+        self.check(self.lib.dsv4_hip_quant_act_fp8_1x128_dev(Q, S, a, n, k, stream),
+                   "quant_act_fp8_1x128_dev")
+
+    def quant_act_mxfp8_dev(self, Q, S, a, n, k, stream=None):
+        self.check(self.lib.dsv4_hip_quant_act_mxfp8_dev(Q, S, a, n, k, stream),
+                   "quant_act_mxfp8_dev")
+
+    def synth_normal_dev(self, out_ptr, n, seed, sigma, round_bf16=False, stream=None):
+        self.check(self.lib.dsv4_hip_synth_normal_dev(out_ptr, n, seed, float(sigma),
+                                                      int(bool(round_bf16)), stream),
+                   "synth_normal_dev")
+
+
+def qmat(wdt, w_ptr, s_ptr, rows, cols, blk_r, blk_c) -> QMat:
+    return QMat(w_ptr, s_ptr, wdt, rows, cols, blk_r, blk_c)
+
+
+_LIB: Lib | None = None
+
+
+def load() -> Lib:
+    """The process-wide binding (raises Dsv4Error when not built)."""
+    global _LIB
+    if _LIB is None:
+        _LIB = Lib()
+    return _LIB

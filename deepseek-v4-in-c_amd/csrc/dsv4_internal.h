@@ -1,0 +1,128 @@
+/* SPDX-License-Identifier: Apache-2.0 */
+/* dsv4_internal.h - kernel launch interfaces shared between the .hip files of
+ * the library. Not installed; the public boundary is include/dsv4_hip.h. */
+#ifndef DSV4_INTERNAL_H
+#define DSV4_INTERNAL_H
+
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+#include "../../include/dsv4_hip.h"
+#include "dsv4_dev.h"
+
+namespace dsv4 {
+
+/* Kernel-side weight formats. */
+enum {
+    FMT_FP8_E8M0 = 0, /* DSV4_WFP8, blk_c == 128      */
+    FMT_FP8_F32S = 1, /* DSV4_WFP8_F32S, blk_c == 128 */
+    FMT_FP4_E8M0 = 2, /* DSV4_WFP4, blk_c == 32       */
+};
+
+/* Status bits a kernel may raise in the device status word. */
+enum {
+    ST_BAD_EXPERT_ID = 1u << 0,   /* routing index outside [0, n_experts)   */
+    ST_BAD_DESCRIPTOR = 1u << 1,  /* expert descriptor of the wrong format  */
+};
+
+/* Map a descriptor to the kernel format, or -1 when the GPU path does not
+ * support its geometry. */
+static inline int qmat_fmt(const DSV4QMat *m)
+{
+    if (!m || m->rows <= 0 || m->cols <= 0 || m->blk_r <= 0) return -1;
+    if (m->wdt == DSV4_WFP8 && m->blk_c == 128 && (m->cols % 128) == 0)
+        return FMT_FP8_E8M0;
+    if (m->wdt == DSV4_WFP8_F32S && m->blk_c == 128 && (m->cols % 128) == 0)
+        return FMT_FP8_F32S;
+    if (m->wdt == DSV4_WFP4 && m->blk_c == 32 && (m->cols % 32) == 0)
+        return FMT_FP4_E8M0;
+    return -1;
+}
+
+static inline int qmat_row_bytes(const DSV4QMat *m)
+{
+    return m->wdt == DSV4_WFP4 ? m->cols / 2 : m->cols;
+}
+
+/* scale-grid columns (entries per scale row) */
+static inline int qmat_sc_cols(const DSV4QMat *m)
+{
+    return (m->cols + m->blk_c - 1) / m->blk_c;
+}
+
+static inline size_t qmat_w_bytes(const DSV4QMat *m)
+{
+    return (size_t)m->rows * (size_t)qmat_row_bytes(m);
+}
+
+static inline size_t qmat_s_bytes(const DSV4QMat *m)
+{
+    const size_t n = (size_t)((m->rows + m->blk_r - 1) / m->blk_r) *
+                     (size_t)qmat_sc_cols(m);
+    return m->wdt == DSV4_WFP8_F32S ? n * 4u : n;
+}
+
+/* ------------------------------------------------------------- GEMV --- */
+struct GemvArgs {
+    const uint8_t *W;   /* device, 16-byte aligned */
+    const void *S;      /* device scales            */
+    const float *x;     /* device, 16-byte aligned  */
+    float *y;
+    int rows, row_bytes, sc_cols, blk_r;
+    int nt;
+    int x_ld, y_ld;     /* floats between tokens    */
+};
+hipError_t gemv_launch(int fmt, const GemvArgs &a, hipStream_t st);
+
+/* ---------------------------------------------------- decode MoE ------ */
+/* Gate/up + SwiGLU for `nslots` experts: slot s uses table[idx[s]] (or
+ * `direct` when use_direct), writing mid[s * mid_ld + j], j < inter. */
+struct GateUpArgs {
+    const DSV4ExpertW *table; /* device table (ignored when use_direct) */
+    const int *idx;           /* device, nslots entries                 */
+    int n_experts;
+    DSV4ExpertW direct;       /* device pointers                        */
+    int use_direct;
+    int nslots;
+    const float *x;           /* [hidden]                               */
+    float *mid;               /* [nslots][mid_ld]                       */
+    int mid_ld;
+    int inter, hidden;
+    float limit;
+    unsigned *status;
+};
+hipError_t gateup_launch(int fmt, const GateUpArgs &a, hipStream_t st);
+
+/* out[i] = sum_k (k order) w[k] * (table[idx[k]].w2 . mid[k])[i] + shared[i] */
+struct DownCombineArgs {
+    const DSV4ExpertW *table;
+    const int *idx;
+    const float *w;           /* device, topk routing weights           */
+    int n_experts;
+    int topk;
+    const float *mid;         /* [topk][mid_ld]                         */
+    int mid_ld;
+    const float *shared;      /* device [hidden] or NULL                */
+    float *out;               /* [hidden]                               */
+    int inter, hidden;
+    unsigned *status;
+};
+hipError_t down_combine_launch(int fmt, const DownCombineArgs &a, hipStream_t st);
+
+/* ---------------------------------------------- dequant / quantizers --- */
+hipError_t dequant_launch(int fmt, const DSV4QMat &m, float *out, hipStream_t st);
+hipError_t quant_fp4_mx_launch(uint8_t *W, uint8_t *S, const float *w, int rows,
+                               int cols, hipStream_t st);
+hipError_t quant_fp8_blk128_launch(uint8_t *W, float *S, const float *w,
+                                   int rows, int cols, hipStream_t st);
+hipError_t quant_act_fp8_1x128_launch(uint8_t *Q, float *S, const float *a,
+                                      int n, int k, hipStream_t st);
+hipError_t quant_act_mxfp8_launch(uint8_t *Q, uint8_t *S, const float *a,
+                                  int n, int k, hipStream_t st);
+hipError_t synth_normal_launch(float *out, size_t n, uint64_t seed, float sigma,
+                               int round_bf16, hipStream_t st);
+
+} // namespace dsv4
+
+#endif /* DSV4_INTERNAL_H */

@@ -1,0 +1,334 @@
+/* SPDX-License-Identifier: Apache-2.0 */
+/* dsv4_quant.hip - dequantization check kernel, the weight / activation
+ * quantizers, and the seeded synthetic-tensor generator.
+ *
+ * dequant     out[r][c] = decode(W[r][c]) * scale(block of r, c), one fp32
+ *             multiply, with the SAME decoders the matmul kernels use
+ *             (dsv4_dev.h). For E8M0 scales the product is exact; this is the
+ *             reference's dequantized value dsv4_e4m3_to_f32(b) *
+ *             dsv4_e8m0_to_f32(s) / dsv4_fp4_at * e8m0
+ *             (src/10_compute/dsv4_quant.h:72-172).
+ * quantizers  The reference ships pre-quantized weights and never quantizes
+ *             activations, so these are this library's own definitions; the
+ *             CPU oracle states the same rules and the tests compare the two
+ *             byte for byte:
+ *               e4m3(v)   round to nearest even, saturate at +-448
+ *               e2m1(v)   round to nearest even, saturate at +-6
+ *               FP8 weights, fp32 scale per 128x128 = blockmax/448
+ *               FP4 weights, E8M0 per 1x32, 2^e the least power of two with
+ *                 6 * 2^e >= blockmax (exact, no rounded logarithm)
+ *               activations e4m3, fp32 scale per 1x128 = groupmax/448
+ *               activations e4m3, E8M0 per 1x32 with 448 * 2^e >= groupmax
+ *             Division is IEEE correctly rounded (hipcc's default).
+ * synth       counter-based: u64 hash of (seed, index) -> two uniforms ->
+ *             Box-Muller in double -> fp32 (optionally rounded to bf16).
+ */
+#include "dsv4_internal.h"
+
+namespace dsv4 {
+
+/* ------------------------------------------------------------ dequant --- */
+
+template <int FMT>
+__global__ __launch_bounds__(256) void k_dequant(DSV4QMat m, float *out)
+{
+    /* one thread per 16-byte chunk */
+    const int row_bytes = FMT == FMT_FP4_E8M0 ? m.cols / 2 : m.cols;
+    const int chunks = row_bytes / 16;
+    const long id = (long)blockIdx.x * blockDim.x + threadIdx.x;
+    if (id >= (long)m.rows * chunks) return;
+    const int r = (int)(id / chunks), ch = (int)(id % chunks);
+    const u32x4 w = *(const u32x4 *)((const uint8_t *)m.w + (size_t)r * row_bytes + 16 * ch);
+    constexpr int BLK_C = FMT == FMT_FP4_E8M0 ? 32 : 128;
+    const int sc_cols = (m.cols + BLK_C - 1) / BLK_C;
+    const int c0 = FMT == FMT_FP4_E8M0 ? 32 * ch : 16 * ch;
+    const size_t si = (size_t)(r / m.blk_r) * sc_cols + c0 / BLK_C;
+    float s;
+    if constexpr (FMT == FMT_FP8_F32S) s = ((const float *)m.s)[si];
+    else s = dev_e8m0(((const uint8_t *)m.s)[si]);
+    float *o = out + (size_t)r * m.cols + c0;
+    if constexpr (FMT == FMT_FP4_E8M0) {
+        float f[32];
+        dev_dec32_e2m1(w, f);
+#pragma unroll
+        for (int i = 0; i < 32; i++) o[i] = __fmul_rn(f[i], s);
+    } else {
+        float f[16];
+        dev_dec16_e4m3(w, f);
+#pragma unroll
+        for (int i = 0; i < 16; i++) o[i] = __fmul_rn(f[i], s);
+    }
+}
+
+hipError_t dequant_launch(int fmt, const DSV4QMat &m, float *out, hipStream_t st)
+{
+    const int row_bytes = qmat_row_bytes(&m);
+    const long n = (long)m.rows * (row_bytes / 16);
+    const unsigned blocks = (unsigned)((n + 255) / 256);
+    switch (fmt) {
+    case FMT_FP8_E8M0: hipLaunchKernelGGL(k_dequant<FMT_FP8_E8M0>, dim3(blocks), dim3(256), 0, st, m, out); break;
+    case FMT_FP8_F32S: hipLaunchKernelGGL(k_dequant<FMT_FP8_F32S>, dim3(blocks), dim3(256), 0, st, m, out); break;
+    case FMT_FP4_E8M0: hipLaunchKernelGGL(k_dequant<FMT_FP4_E8M0>, dim3(blocks), dim3(256), 0, st, m, out); break;
+    default: return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
+}
+
+/* ------------------------------------------------------- element rounding */
+
+__device__ __forceinline__ uint32_t q_e4m3(float v)
+{
+    const uint32_t sign = (__float_as_uint(v) >> 24) & 0x80u;
+    if (__builtin_isnan(v)) return sign | 0x7Fu;
+    const float a = fabsf(v);
+    int code;
+    if (a < 0x1p-6f) {
+        code = (int)rintf(a * 512.0f);
+    } else {
+        int e2;
+        (void)frexpf(a, &e2);
+        const int E = e2 - 1;
+        if (E > 8) return sign | 0x7Eu;
+        const float frac = ldexpf(a, -E) - 1.0f;
+        code = ((E + 7) << 3) + (int)rintf(frac * 8.0f);
+    }
+    if (code > 0x7E) code = 0x7E;
+    return sign | (uint32_t)code;
+}
+
+__device__ __forceinline__ uint32_t q_e2m1(float v)
+{
+    const uint32_t sign = (__float_as_uint(v) >> 28) & 0x08u;
+    if (__builtin_isnan(v)) return sign | 0x7u;
+    const float a = fabsf(v);
+    int code;
+    if (a < 1.0f) {
+        code = (int)rintf(a * 2.0f);
+    } else {
+        int e2;
+        (void)frexpf(a, &e2);
+        const int E = e2 - 1;
+        if (E > 2) return sign | 0x7u;
+        const float frac = ldexpf(a, -E) - 1.0f;
+        code = ((E + 1) << 1) + (int)rintf(frac * 2.0f);
+    }
+    if (code > 7) code = 7;
+    return sign | (uint32_t)code;
+}
+
+/* least e with (frac_lim * 2^exp_lim) * 2^e >= amax, amax > 0 */
+__device__ __forceinline__ int pow2_ceil_ratio(float amax, float frac_lim, int exp_lim)
+{
+    int e2;
+    const float f = frexpf(amax, &e2);
+    return (f <= frac_lim) ? e2 - exp_lim : e2 - exp_lim + 1;
+}
+
+__device__ __forceinline__ uint32_t e8m0_clamp(int e)
+{
+    int b = 127 + e;
+    b = b < 0 ? 0 : (b > 254 ? 254 : b);
+    return (uint32_t)b;
+}
+
+/* ---------------------------------------------------- FP4 weight quant --- */
+
+/* one thread per 1x32 block */
+__global__ __launch_bounds__(256) void k_quant_fp4_mx(uint8_t *W, uint8_t *S,
+                                                     const float *w, int rows, int cols)
+{
+    const int nb = cols / 32;
+    const long id = (long)blockIdx.x * blockDim.x + threadIdx.x;
+    if (id >= (long)rows * nb) return;
+    const float *src = w + (size_t)id * 32;
+    float v[32];
+    float amax = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 32; i += 4) {
+        const f32x4 q = *(const f32x4 *)(src + i);
+        v[i] = q.x; v[i + 1] = q.y; v[i + 2] = q.z; v[i + 3] = q.w;
+    }
+#pragma unroll
+    for (int i = 0; i < 32; i++) amax = fabsf(v[i]) > amax ? fabsf(v[i]) : amax;
+    const uint32_t sb = amax > 0.0f ? e8m0_clamp(pow2_ceil_ratio(amax, 0.75f, 3)) : 127u;
+    const int e = (int)sb - 127;
+    S[id] = (uint8_t)sb;
+    u32x4 out;
+#pragma unroll
+    for (int d = 0; d < 4; d++) {
+        uint32_t word = 0;
+#pragma unroll
+        for (int b = 0; b < 4; b++) {
+            const uint32_t lo = q_e2m1(ldexpf(v[8 * d + 2 * b], -e));
+            const uint32_t hi = q_e2m1(ldexpf(v[8 * d + 2 * b + 1], -e));
+            word |= (lo | (hi << 4)) << (8 * b);
+        }
+        out[d] = word;
+    }
+    *(u32x4 *)(W + (size_t)id * 16) = out;
+}
+
+hipError_t quant_fp4_mx_launch(uint8_t *W, uint8_t *S, const float *w, int rows,
+                               int cols, hipStream_t st)
+{
+    const long n = (long)rows * (cols / 32);
+    hipLaunchKernelGGL(k_quant_fp4_mx, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st,
+                       W, S, w, rows, cols);
+    return hipGetLastError();
+}
+
+/* ------------------------------------------ FP8 weight quant, fp32 128x128 */
+
+/* one workgroup (256 threads) per 128x128 block */
+__global__ __launch_bounds__(256) void k_quant_fp8_blk128(uint8_t *W, float *S,
+                                                         const float *w, int rows, int cols)
+{
+    __shared__ float red[256];
+    const int ncb = (cols + 127) / 128;
+    const int rb = blockIdx.x / ncb, cb = blockIdx.x % ncb;
+    const int r0 = rb * 128, c0 = cb * 128;
+    float amax = 0.0f;
+    for (int i = threadIdx.x; i < 128 * 128; i += 256) {
+        const int r = r0 + i / 128, c = c0 + i % 128;
+        if (r < rows && c < cols) {
+            const float a = fabsf(w[(size_t)r * cols + c]);
+            amax = a > amax ? a : amax;
+        }
+    }
+    red[threadIdx.x] = amax;
+    __syncthreads();
+    for (int s = 128; s > 0; s >>= 1) {
+        if ((int)threadIdx.x < s) {
+            const float o = red[threadIdx.x + s];
+            red[threadIdx.x] = o > red[threadIdx.x] ? o : red[threadIdx.x];
+        }
+        __syncthreads();
+    }
+    amax = red[0];
+    const float sc = amax > 0.0f ? amax / 448.0f : 1.0f;
+    if (threadIdx.x == 0) S[(size_t)rb * ncb + cb] = sc;
+    for (int i = threadIdx.x; i < 128 * 128; i += 256) {
+        const int r = r0 + i / 128, c = c0 + i % 128;
+        if (r < rows && c < cols)
+            W[(size_t)r * cols + c] = (uint8_t)q_e4m3(w[(size_t)r * cols + c] / sc);
+    }
+}
+
+hipError_t quant_fp8_blk128_launch(uint8_t *W, float *S, const float *w,
+                                   int rows, int cols, hipStream_t st)
+{
+    const int nblk = ((rows + 127) / 128) * ((cols + 127) / 128);
+    hipLaunchKernelGGL(k_quant_fp8_blk128, dim3(nblk), dim3(256), 0, st, W, S, w, rows, cols);
+    return hipGetLastError();
+}
+
+/* --------------------------------------------- activation quantizers ---- */
+
+/* one wave per 1x128 group: 2 elements per lane */
+__global__ __launch_bounds__(256) void k_quant_act_fp8_1x128(uint8_t *Q, float *S,
+                                                            const float *a, int n, int k)
+{
+    const int lane = threadIdx.x & 63;
+    const long g = (long)blockIdx.x * 4 + (threadIdx.x >> 6);
+    const int ng = k / 128;
+    if (g >= (long)n * ng) return;
+    const float *src = a + (size_t)g * 128;
+    const float v0 = src[2 * lane], v1 = src[2 * lane + 1];
+    float m = fmaxf(fabsf(v0), fabsf(v1));
+    for (int off = 32; off > 0; off >>= 1) m = fmaxf(m, __shfl_xor(m, off));
+    const float sc = m > 0.0f ? m / 448.0f : 1.0f;
+    if (lane == 0) S[g] = sc;
+    const uint32_t q = q_e4m3(v0 / sc) | (q_e4m3(v1 / sc) << 8);
+    *(uint16_t *)(Q + (size_t)g * 128 + 2 * lane) = (uint16_t)q;
+}
+
+hipError_t quant_act_fp8_1x128_launch(uint8_t *Q, float *S, const float *a,
+                                      int n, int k, hipStream_t st)
+{
+    const long groups = (long)n * (k / 128);
+    hipLaunchKernelGGL(k_quant_act_fp8_1x128, dim3((unsigned)((groups + 3) / 4)), dim3(256), 0, st,
+                       Q, S, a, n, k);
+    return hipGetLastError();
+}
+
+/* one thread per 1x32 group */
+__global__ __launch_bounds__(256) void k_quant_act_mxfp8(uint8_t *Q, uint8_t *S,
+                                                        const float *a, int n, int k)
+{
+    const long g = (long)blockIdx.x * blockDim.x + threadIdx.x;
+    if (g >= (long)n * (k / 32)) return;
+    const float *src = a + (size_t)g * 32;
+    float v[32], amax = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 32; i += 4) {
+        const f32x4 q = *(const f32x4 *)(src + i);
+        v[i] = q.x; v[i + 1] = q.y; v[i + 2] = q.z; v[i + 3] = q.w;
+    }
+#pragma unroll
+    for (int i = 0; i < 32; i++) amax = fabsf(v[i]) > amax ? fabsf(v[i]) : amax;
+    const uint32_t sb = amax > 0.0f ? e8m0_clamp(pow2_ceil_ratio(amax, 0.875f, 9)) : 127u;
+    const int e = (int)sb - 127;
+    S[g] = (uint8_t)sb;
+    u32x4 o0, o1;
+#pragma unroll
+    for (int d = 0; d < 8; d++) {
+        uint32_t word = 0;
+#pragma unroll
+        for (int b = 0; b < 4; b++) word |= q_e4m3(ldexpf(v[4 * d + b], -e)) << (8 * b);
+        if (d < 4) o0[d] = word; else o1[d - 4] = word;
+    }
+    *(u32x4 *)(Q + (size_t)g * 32) = o0;
+    *(u32x4 *)(Q + (size_t)g * 32 + 16) = o1;
+}
+
+hipError_t quant_act_mxfp8_launch(uint8_t *Q, uint8_t *S, const float *a,
+                                  int n, int k, hipStream_t st)
+{
+    const long groups = (long)n * (k / 32);
+    hipLaunchKernelGGL(k_quant_act_mxfp8, dim3((unsigned)((groups + 255) / 256)), dim3(256), 0, st,
+                       Q, S, a, n, k);
+    return hipGetLastError();
+}
+
+/* -------------------------------------------------------------- synth --- */
+
+__device__ __forceinline__ uint64_t mix64(uint64_t z)
+{
+    z += 0x9E3779B97F4A7C15ull;
+    z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+    z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+    return z ^ (z >> 31);
+}
+
+/* uniform in (0, 1): 53 random bits + half an ulp */
+__device__ __forceinline__ double unif(uint64_t key, uint64_t ctr)
+{
+    return ((double)(mix64(key ^ mix64(ctr)) >> 11) + 0.5) * 0x1p-53;
+}
+
+__global__ __launch_bounds__(256) void k_synth_normal(float *out, size_t n, uint64_t seed,
+                                                     float sigma, int round_bf16)
+{
+    const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n) return;
+    const uint64_t key = mix64(seed);
+    const double u1 = unif(key, 2 * (uint64_t)i), u2 = unif(key, 2 * (uint64_t)i + 1);
+    const double z = sqrt(-2.0 * log(u1)) * cos(6.283185307179586 * u2);
+    float v = (float)(z * (double)sigma);
+    if (round_bf16) {
+        const uint32_t u = __float_as_uint(v);
+        v = __uint_as_float(((u + 0x7FFFu + ((u >> 16) & 1u)) >> 16) << 16);
+    }
+    out[i] = v;
+}
+
+hipError_t synth_normal_launch(float *out, size_t n, uint64_t seed, float sigma,
+                               int round_bf16, hipStream_t st)
+{
+    const size_t blocks = (n + 255) / 256;
+    hipLaunchKernelGGL(k_synth_normal, dim3((unsigned)blocks), dim3(256), 0, st,
+                       out, n, seed, sigma, round_bf16);
+    return hipGetLastError();
+}
+
+} // namespace dsv4

@@ -1,0 +1,572 @@
+/* SPDX-License-Identifier: Apache-2.0 */
+/* dsv4_runtime.hip - the C ABI (include/dsv4_hip.h, include/dsv4_hip_aux.h):
+ * device selection, the upload-once weight registry, staging for the
+ * host-pointer entry points, and argument checking before any launch.
+ *
+ * Conventions follow the reference's GPU backend
+ * (src/80_prefill/dsv4_prefill_vk.h:31-49, dsv4_prefill_vk_gemm.c:63-132):
+ * init returns -1 when no device is usable; a call returns 0 when the GPU
+ * produced the whole result and -1 otherwise, leaving the caller's CPU path in
+ * charge; a HIP runtime failure latches `dead` so every later call returns -1
+ * at once. The library is not re-entrant across host threads (one mutex
+ * serialises the host-pointer calls, as the Vulkan backend's single command
+ * buffer and fence do) and nothing here computes on the CPU.
+ */
+#include <map>
+#include <mutex>
+#include <string>
+
+#include <stdarg.h>
+#include <stdio.h>
+#include <string.h>
+
+#include "dsv4_internal.h"
+#include "../../include/dsv4_hip_aux.h"
+
+using namespace dsv4;
+
+namespace {
+
+struct Region {
+    size_t bytes;
+    void *dev;
+};
+
+/* A device buffer that only grows. */
+struct DevBuf {
+    void *p = nullptr;
+    size_t cap = 0;
+    hipError_t need(size_t bytes)
+    {
+        if (bytes <= cap) return hipSuccess;
+        if (p) { (void)hipFree(p); p = nullptr; cap = 0; }
+        const size_t want = bytes < 4096 ? 4096 : bytes;
+        hipError_t e = hipMalloc(&p, want);
+        if (e == hipSuccess) cap = want;
+        return e;
+    }
+    void release()
+    {
+        if (p) (void)hipFree(p);
+        p = nullptr;
+        cap = 0;
+    }
+};
+
+struct State {
+    std::mutex mu;
+    int ready = 0;
+    int dead = 0;
+    int device = -1;
+    hipStream_t stream = nullptr;
+    unsigned *status = nullptr;          /* device status word            */
+    std::map<uintptr_t, Region> regions; /* host start -> resident copy   */
+    DevBuf x, y, mid, table, small, ys;
+};
+
+State g;
+thread_local std::string g_err;
+
+int fail(const char *fmt, ...)
+{
+    char buf[512];
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(buf, sizeof buf, fmt, ap);
+    va_end(ap);
+    g_err = buf;
+    return -1;
+}
+
+int hip_fail(hipError_t e, const char *what)
+{
+    g.dead = 1;
+    return fail("%s: %s (backend latched dead)", what, hipGetErrorString(e));
+}
+
+#define HIPCHK(expr, what)                                                     \
+    do {                                                                       \
+        hipError_t e_ = (expr);                                                \
+        if (e_ != hipSuccess) return hip_fail(e_, what);                       \
+    } while (0)
+
+int usable(void)
+{
+    if (!g.ready) return fail("dsv4_hip_init has not succeeded");
+    if (g.dead) return fail("backend is dead after an earlier HIP failure");
+    return 0;
+}
+
+/* Device copy of [p, p + bytes) when it lies inside one registered range. */
+const void *translate(const void *p, size_t bytes)
+{
+    if (!p) return nullptr;
+    const uintptr_t a = (uintptr_t)p;
+    auto it = g.regions.upper_bound(a);
+    if (it == g.regions.begin()) return nullptr;
+    --it;
+    const uintptr_t s = it->first;
+    if (a < s || a + bytes > s + it->second.bytes) return nullptr;
+    return (const uint8_t *)it->second.dev + (a - s);
+}
+
+bool aligned16(const void *p) { return ((uintptr_t)p & 15u) == 0; }
+
+/* Check a descriptor the GPU path can run and compute its byte sizes. */
+int check_qmat(const DSV4QMat *m, const char *what, int *fmt)
+{
+    if (!m) return fail("%s: NULL matrix", what);
+    *fmt = qmat_fmt(m);
+    if (*fmt < 0)
+        return fail("%s: unsupported geometry wdt=%d %dx%d blk %dx%d", what,
+                    m->wdt, m->rows, m->cols, m->blk_r, m->blk_c);
+    if (qmat_row_bytes(m) > 4096)
+        return fail("%s: rows wider than 4096 bytes are not supported", what);
+    return 0;
+}
+
+/* Host descriptor -> descriptor with resident device pointers. */
+int resident(const DSV4QMat *m, DSV4QMat *out, const char *what)
+{
+    int fmt;
+    if (check_qmat(m, what, &fmt)) return -1;
+    *out = *m;
+    out->w = translate(m->w, qmat_w_bytes(m));
+    out->s = translate(m->s, qmat_s_bytes(m));
+    if (!out->w || !out->s)
+        return fail("%s: weights or scales are not inside a registered range", what);
+    if (!aligned16(out->w)) return fail("%s: weights are not 16-byte aligned", what);
+    return 0;
+}
+
+int expert_geometry(const DSV4ExpertW *e, int *fmt, int *inter, int *hidden,
+                    const char *what)
+{
+    int f1, f3, f2;
+    if (check_qmat(&e->w1, what, &f1) || check_qmat(&e->w3, what, &f3) ||
+        check_qmat(&e->w2, what, &f2))
+        return -1;
+    if (f1 != f3 || f1 != f2) return fail("%s: w1/w3/w2 formats differ", what);
+    if (e->w1.rows != e->w3.rows || e->w1.cols != e->w3.cols ||
+        e->w2.rows != e->w1.cols || e->w2.cols != e->w1.rows)
+        return fail("%s: w1/w3/w2 shapes do not chain", what);
+    *fmt = f1;
+    *inter = e->w1.rows;
+    *hidden = e->w1.cols;
+    return 0;
+}
+
+int resident_expert(const DSV4ExpertW *e, DSV4ExpertW *out, const char *what)
+{
+    if (resident(&e->w1, &out->w1, what) || resident(&e->w3, &out->w3, what) ||
+        resident(&e->w2, &out->w2, what))
+        return -1;
+    return 0;
+}
+
+GemvArgs gemv_args(const DSV4QMat &m, const float *x, float *y, int nt)
+{
+    GemvArgs a;
+    a.W = (const uint8_t *)m.w;
+    a.S = m.s;
+    a.x = x;
+    a.y = y;
+    a.rows = m.rows;
+    a.row_bytes = qmat_row_bytes(&m);
+    a.sc_cols = qmat_sc_cols(&m);
+    a.blk_r = m.blk_r;
+    a.nt = nt;
+    a.x_ld = m.cols;
+    a.y_ld = m.rows;
+    return a;
+}
+
+/* Enqueue one expert (gate/up + SwiGLU -> mid, then w2 -> out) from a
+ * descriptor holding device pointers. */
+int enqueue_expert(const DSV4ExpertW &e, int fmt, int inter, int hidden,
+                   const float *x, float *mid, float *out, float limit,
+                   hipStream_t st)
+{
+    GateUpArgs ga;
+    memset(&ga, 0, sizeof ga);
+    ga.direct = e;
+    ga.use_direct = 1;
+    ga.nslots = 1;
+    ga.x = x;
+    ga.mid = mid;
+    ga.mid_ld = inter;
+    ga.inter = inter;
+    ga.hidden = hidden;
+    ga.limit = limit;
+    ga.status = g.status;
+    HIPCHK(gateup_launch(fmt, ga, st), "gate/up launch");
+    HIPCHK(gemv_launch(fmt, gemv_args(e.w2, mid, out, 1), st), "down launch");
+    return 0;
+}
+
+/* Enqueue the decode MoE from device tables. */
+int enqueue_moe(const DSV4ExpertW *table, int n_experts, const int *idx,
+                const float *w, int topk, const DSV4ExpertW *shared_dev,
+                int shared_fmt, int shared_inter, int hidden, int inter,
+                const float *x, float *out, float limit, hipStream_t st)
+{
+    const size_t mid_ld = (size_t)((inter + 3) & ~3);
+    const size_t smid_ld = (size_t)((shared_inter + 3) & ~3);
+    HIPCHK(g.mid.need(((size_t)topk * mid_ld + (shared_dev ? smid_ld : 0)) * 4), "mid alloc");
+    float *mid = (float *)g.mid.p;
+    float *ys = nullptr;
+    if (shared_dev) {
+        HIPCHK(g.ys.need((size_t)hidden * 4), "shared output alloc");
+        ys = (float *)g.ys.p;
+        float *smid = mid + (size_t)topk * mid_ld;
+        if (enqueue_expert(*shared_dev, shared_fmt, shared_inter, hidden, x, smid,
+                           ys, limit, st))
+            return -1;
+    }
+    GateUpArgs ga;
+    memset(&ga, 0, sizeof ga);
+    ga.table = table;
+    ga.idx = idx;
+    ga.n_experts = n_experts;
+    ga.nslots = topk;
+    ga.x = x;
+    ga.mid = mid;
+    ga.mid_ld = (int)mid_ld;
+    ga.inter = inter;
+    ga.hidden = hidden;
+    ga.limit = limit;
+    ga.status = g.status;
+    HIPCHK(gateup_launch(FMT_FP4_E8M0, ga, st), "routed gate/up launch");
+    DownCombineArgs da;
+    memset(&da, 0, sizeof da);
+    da.table = table;
+    da.idx = idx;
+    da.w = w;
+    da.n_experts = n_experts;
+    da.topk = topk;
+    da.mid = mid;
+    da.mid_ld = (int)mid_ld;
+    da.shared = ys;
+    da.out = out;
+    da.inter = inter;
+    da.hidden = hidden;
+    da.status = g.status;
+    HIPCHK(down_combine_launch(FMT_FP4_E8M0, da, st), "down/combine launch");
+    return 0;
+}
+
+} // namespace
+
+extern "C" {
+
+int dsv4_hip_init(int device)
+{
+    std::lock_guard<std::mutex> lk(g.mu);
+    if (g.ready && g.device == device && !g.dead) return 0;
+    if (g.ready) return fail("already initialised on device %d", g.device);
+    int n = 0;
+    if (hipGetDeviceCount(&n) != hipSuccess || n <= 0)
+        return fail("no HIP device");
+    if (device < 0 || device >= n) return fail("device %d out of range (%d)", device, n);
+    hipDeviceProp_t prop;
+    if (hipGetDeviceProperties(&prop, device) != hipSuccess)
+        return fail("hipGetDeviceProperties failed");
+    if (strncmp(prop.gcnArchName, "gfx950", 6) != 0)
+        return fail("device %d is %s, this library is built for gfx950", device,
+                    prop.gcnArchName);
+    if (hipSetDevice(device) != hipSuccess) return fail("hipSetDevice failed");
+    if (hipStreamCreateWithFlags(&g.stream, hipStreamNonBlocking) != hipSuccess)
+        return fail("stream creation failed");
+    if (hipMalloc((void **)&g.status, 256) != hipSuccess) return fail("status alloc failed");
+    if (hipMemset(g.status, 0, 256) != hipSuccess) return fail("status clear failed");
+    g.device = device;
+    g.ready = 1;
+    g.dead = 0;
+    return 0;
+}
+
+void dsv4_hip_shutdown(void)
+{
+    std::lock_guard<std::mutex> lk(g.mu);
+    if (!g.ready) return;
+    (void)hipDeviceSynchronize();
+    for (auto &kv : g.regions) (void)hipFree(kv.second.dev);
+    g.regions.clear();
+    g.x.release(); g.y.release(); g.mid.release();
+    g.table.release(); g.small.release(); g.ys.release();
+    if (g.status) (void)hipFree(g.status);
+    g.status = nullptr;
+    if (g.stream) (void)hipStreamDestroy(g.stream);
+    g.stream = nullptr;
+    g.ready = 0;
+    g.dead = 0;
+    g.device = -1;
+}
+
+const char *dsv4_hip_last_error(void) { return g_err.c_str(); }
+
+int dsv4_hip_register(const void *host, size_t bytes)
+{
+    std::lock_guard<std::mutex> lk(g.mu);
+    if (usable()) return -1;
+    if (!host || !bytes) return fail("register: empty range");
+    const uintptr_t a = (uintptr_t)host;
+    auto it = g.regions.lower_bound(a);
+    if (it != g.regions.end() && it->first < a + bytes)
+        return fail("register: range overlaps a registered one");
+    if (it != g.regions.begin()) {
+        auto pv = std::prev(it);
+        if (pv->first + pv->second.bytes > a)
+            return fail("register: range overlaps a registered one");
+    }
+    void *dev = nullptr;
+    hipError_t e = hipMalloc(&dev, bytes);
+    if (e != hipSuccess) return fail("register: hipMalloc(%zu) failed", bytes);
+    e = hipMemcpy(dev, host, bytes, hipMemcpyHostToDevice);
+    if (e != hipSuccess) {
+        (void)hipFree(dev);
+        return hip_fail(e, "register: upload");
+    }
+    g.regions[a] = Region{bytes, dev};
+    return 0;
+}
+
+int dsv4_hip_unregister(const void *host)
+{
+    std::lock_guard<std::mutex> lk(g.mu);
+    if (!g.ready) return fail("not initialised");
+    auto it = g.regions.find((uintptr_t)host);
+    if (it == g.regions.end()) return fail("unregister: unknown range");
+    (void)hipStreamSynchronize(g.stream);
+    (void)hipFree(it->second.dev);
+    g.regions.erase(it);
+    return 0;
+}
+
+void *dsv4_hip_device_ptr(const void *p)
+{
+    std::lock_guard<std::mutex> lk(g.mu);
+    return (void *)translate(p, 1);
+}
+
+int dsv4_hip_mmq_n(float *y, const float *x, const DSV4QMat *m, int nt)
+{
+    std::lock_guard<std::mutex> lk(g.mu);
+    if (usable()) return -1;
+    if (nt <= 0) return 0;
+    if (!x || !y) return fail("mmq_n: NULL x or y");
+    DSV4QMat d;
+    if (resident(m, &d, "mmq_n")) return -1;
+    const int fmt = qmat_fmt(m);
+    const size_t xb = (size_t)nt * m->cols * 4, yb = (size_t)nt * m->rows * 4;
+    HIPCHK(g.x.need(xb), "x staging");
+    HIPCHK(g.y.need(yb), "y staging");
+    HIPCHK(hipMemcpyAsync(g.x.p, x, xb, hipMemcpyHostToDevice, g.stream), "x upload");
+    HIPCHK(gemv_launch(fmt, gemv_args(d, (const float *)g.x.p, (float *)g.y.p, nt), g.stream),
+           "gemv launch");
+    HIPCHK(hipMemcpyAsync(y, g.y.p, yb, hipMemcpyDeviceToHost, g.stream), "y download");
+    HIPCHK(hipStreamSynchronize(g.stream), "mmq_n sync");
+    return 0;
+}
+
+int dsv4_hip_mmq(float *y, const float *x, const DSV4QMat *m)
+{
+    return dsv4_hip_mmq_n(y, x, m, 1);
+}
+
+int dsv4_hip_mmq_n_dev(float *y, const float *x, const DSV4QMat *m, int nt,
+                       void *stream)
+{
+    std::lock_guard<std::mutex> lk(g.mu);
+    if (usable()) return -1;
+    if (nt <= 0) return 0;
+    int fmt;
+    if (check_qmat(m, "mmq_n_dev", &fmt)) return -1;
+    if (!x || !y || !m->w || !m->s) return fail("mmq_n_dev: NULL pointer");
+    if (!aligned16(x) || !aligned16(m->w)) return fail("mmq_n_dev: x and W must be 16-byte aligned");
+    HIPCHK(gemv_launch(fmt, gemv_args(*m, x, y, nt), (hipStream_t)stream), "gemv launch");
+    return 0;
+}
+
+int dsv4_hip_expert_forward(float *out, const float *x, const DSV4ExpertW *e,
+                            int inter, float limit)
+{
+    std::lock_guard<std::mutex> lk(g.mu);
+    if (usable()) return -1;
+    if (!out || !x || !e) return fail("expert_forward: NULL pointer");
+    int fmt, ei, eh;
+    if (expert_geometry(e, &fmt, &ei, &eh, "expert_forward")) return -1;
+    if (ei != inter) return fail("expert_forward: inter %d != w1 rows %d", inter, ei);
+    DSV4ExpertW d;
+    if (resident_expert(e, &d, "expert_forward")) return -1;
+    HIPCHK(g.x.need((size_t)eh * 4), "x staging");
+    HIPCHK(g.y.need((size_t)eh * 4), "y staging");
+    HIPCHK(g.mid.need((size_t)inter * 4), "mid alloc");
+    HIPCHK(hipMemcpyAsync(g.x.p, x, (size_t)eh * 4, hipMemcpyHostToDevice, g.stream), "x upload");
+    if (enqueue_expert(d, fmt, inter, eh, (const float *)g.x.p, (float *)g.mid.p,
+                       (float *)g.y.p, limit, g.stream))
+        return -1;
+    HIPCHK(hipMemcpyAsync(out, g.y.p, (size_t)eh * 4, hipMemcpyDeviceToHost, g.stream), "out download");
+    HIPCHK(hipStreamSynchronize(g.stream), "expert sync");
+    return 0;
+}
+
+int dsv4_hip_moe_decode(float *out, const float *x, const DSV4ExpertW *const *ex,
+                        const float *w, int topk, const DSV4ExpertW *shared,
+                        float limit)
+{
+    std::lock_guard<std::mutex> lk(g.mu);
+    if (usable()) return -1;
+    if (!out || !x || !ex || !w) return fail("moe_decode: NULL pointer");
+    if (topk < 1 || topk > 16) return fail("moe_decode: topk %d outside 1..16", topk);
+    DSV4ExpertW tab[16];
+    int inter = 0, hidden = 0;
+    for (int k = 0; k < topk; k++) {
+        int fmt, ei, eh;
+        if (!ex[k]) return fail("moe_decode: expert %d is NULL", k);
+        if (expert_geometry(ex[k], &fmt, &ei, &eh, "moe_decode routed")) return -1;
+        if (fmt != FMT_FP4_E8M0) return fail("moe_decode: routed experts must be FP4");
+        if (k == 0) { inter = ei; hidden = eh; }
+        else if (ei != inter || eh != hidden) return fail("moe_decode: routed shapes differ");
+        if (resident_expert(ex[k], &tab[k], "moe_decode routed")) return -1;
+    }
+    DSV4ExpertW sdev;
+    int sfmt = -1, sinter = 0;
+    if (shared) {
+        int sh;
+        if (expert_geometry(shared, &sfmt, &sinter, &sh, "moe_decode shared")) return -1;
+        if (sh != hidden) return fail("moe_decode: shared hidden %d != %d", sh, hidden);
+        if (resident_expert(shared, &sdev, "moe_decode shared")) return -1;
+    }
+    /* table, identity routing and weights in one small upload */
+    const size_t tb = (size_t)topk * sizeof(DSV4ExpertW);
+    const size_t ib = 16 * sizeof(int), wb = 16 * sizeof(float);
+    HIPCHK(g.table.need(tb + ib + wb), "table alloc");
+    unsigned char host[16 * sizeof(DSV4ExpertW) + 16 * 8];
+    memcpy(host, tab, tb);
+    int *hidx = (int *)(host + tb);
+    float *hw = (float *)(host + tb + ib);
+    for (int k = 0; k < topk; k++) { hidx[k] = k; hw[k] = w[k]; }
+    HIPCHK(g.x.need((size_t)hidden * 4), "x staging");
+    HIPCHK(g.y.need((size_t)hidden * 4), "y staging");
+    HIPCHK(hipMemcpyAsync(g.table.p, host, tb + ib + wb, hipMemcpyHostToDevice, g.stream), "table upload");
+    HIPCHK(hipMemcpyAsync(g.x.p, x, (size_t)hidden * 4, hipMemcpyHostToDevice, g.stream), "x upload");
+    const unsigned char *tp = (const unsigned char *)g.table.p;
+    if (enqueue_moe((const DSV4ExpertW *)tp, topk, (const int *)(tp + tb),
+                    (const float *)(tp + tb + ib), topk, shared ? &sdev : nullptr,
+                    sfmt, sinter, hidden, inter, (const float *)g.x.p,
+                    (float *)g.y.p, limit, g.stream))
+        return -1;
+    HIPCHK(hipMemcpyAsync(out, g.y.p, (size_t)hidden * 4, hipMemcpyDeviceToHost, g.stream), "out download");
+    HIPCHK(hipStreamSynchronize(g.stream), "moe sync");
+    return 0;
+}
+
+int dsv4_hip_moe_decode_dev(float *out, const float *x, const DSV4ExpertW *experts,
+                            int n_experts, const int *idx, const float *w, int topk,
+                            const DSV4ExpertW *shared, int hidden, int inter,
+                            float limit, void *stream)
+{
+    std::lock_guard<std::mutex> lk(g.mu);
+    if (usable()) return -1;
+    if (!out || !x || !experts || !idx || !w) return fail("moe_decode_dev: NULL pointer");
+    if (topk < 1 || topk > 16) return fail("moe_decode_dev: topk %d outside 1..16", topk);
+    if (n_experts < 1) return fail("moe_decode_dev: no experts");
+    if (hidden % 32 || inter % 32 || hidden / 2 > 4096 || inter / 2 > 2048 || hidden <= 0 || inter <= 0)
+        return fail("moe_decode_dev: unsupported hidden %d / inter %d", hidden, inter);
+    if (!aligned16(x)) return fail("moe_decode_dev: x must be 16-byte aligned");
+    int sfmt = -1, sinter = 0;
+    if (shared) {
+        int sh;
+        if (expert_geometry(shared, &sfmt, &sinter, &sh, "moe_decode_dev shared")) return -1;
+        if (sh != hidden) return fail("moe_decode_dev: shared hidden %d != %d", sh, hidden);
+        if (!aligned16(shared->w1.w) || !aligned16(shared->w3.w) || !aligned16(shared->w2.w))
+            return fail("moe_decode_dev: shared weights must be 16-byte aligned");
+    }
+    return enqueue_moe(experts, n_experts, idx, w, topk, shared, sfmt, sinter,
+                       hidden, inter, x, out, limit, (hipStream_t)stream);
+}
+
+int dsv4_hip_status(unsigned *bits)
+{
+    std::lock_guard<std::mutex> lk(g.mu);
+    if (!g.ready) return fail("not initialised");
+    HIPCHK(hipDeviceSynchronize(), "status sync");
+    unsigned v = 0;
+    HIPCHK(hipMemcpy(&v, g.status, sizeof v, hipMemcpyDeviceToHost), "status read");
+    HIPCHK(hipMemset(g.status, 0, sizeof v), "status clear");
+    if (bits) *bits = v;
+    return 0;
+}
+
+/* ------------------------------------------------------------- aux ---- */
+
+int dsv4_hip_dequant_dev(float *out, const DSV4QMat *m, void *stream)
+{
+    std::lock_guard<std::mutex> lk(g.mu);
+    if (usable()) return -1;
+    int fmt;
+    if (check_qmat(m, "dequant_dev", &fmt)) return -1;
+    if (!out || !m->w || !m->s) return fail("dequant_dev: NULL pointer");
+    if (!aligned16(m->w)) return fail("dequant_dev: W must be 16-byte aligned");
+    HIPCHK(dequant_launch(fmt, *m, out, (hipStream_t)stream), "dequant launch");
+    return 0;
+}
+
+int dsv4_hip_quant_fp8_blk128_dev(uint8_t *W, float *S, const float *w, int rows,
+                                  int cols, void *stream)
+{
+    std::lock_guard<std::mutex> lk(g.mu);
+    if (usable()) return -1;
+    if (!W || !S || !w || rows <= 0 || cols <= 0) return fail("quant_fp8_blk128_dev: bad argument");
+    HIPCHK(quant_fp8_blk128_launch(W, S, w, rows, cols, (hipStream_t)stream), "quant launch");
+    return 0;
+}
+
+int dsv4_hip_quant_fp4_mx_dev(uint8_t *W, uint8_t *S, const float *w, int rows,
+                              int cols, void *stream)
+{
+    std::lock_guard<std::mutex> lk(g.mu);
+    if (usable()) return -1;
+    if (!W || !S || !w || rows <= 0 || cols <= 0 || cols % 32)
+        return fail("quant_fp4_mx_dev: bad argument");
+    if (!aligned16(W) || !aligned16(w)) return fail("quant_fp4_mx_dev: W and w must be 16-byte aligned");
+    HIPCHK(quant_fp4_mx_launch(W, S, w, rows, cols, (hipStream_t)stream), "quant launch");
+    return 0;
+}
+
+int dsv4_hip_quant_act_fp8_1x128_dev(uint8_t *Q, float *S, const float *a, int n,
+                                     int k, void *stream)
+{
+    std::lock_guard<std::mutex> lk(g.mu);
+    if (usable()) return -1;
+    if (!Q || !S || !a || n <= 0 || k <= 0 || k % 128)
+        return fail("quant_act_fp8_1x128_dev: bad argument");
+    if (((uintptr_t)Q & 1u) != 0) return fail("quant_act_fp8_1x128_dev: Q must be 2-byte aligned");
+    HIPCHK(quant_act_fp8_1x128_launch(Q, S, a, n, k, (hipStream_t)stream), "quant launch");
+    return 0;
+}
+
+int dsv4_hip_quant_act_mxfp8_dev(uint8_t *Q, uint8_t *S, const float *a, int n,
+                                 int k, void *stream)
+{
+    std::lock_guard<std::mutex> lk(g.mu);
+    if (usable()) return -1;
+    if (!Q || !S || !a || n <= 0 || k <= 0 || k % 32)
+        return fail("quant_act_mxfp8_dev: bad argument");
+    if (!aligned16(Q) || !aligned16(a)) return fail("quant_act_mxfp8_dev: Q and a must be 16-byte aligned");
+    HIPCHK(quant_act_mxfp8_launch(Q, S, a, n, k, (hipStream_t)stream), "quant launch");
+    return 0;
+}
+
+int dsv4_hip_synth_normal_dev(float *out, size_t n, uint64_t seed, float sigma,
+                              int round_bf16, void *stream)
+{
+    std::lock_guard<std::mutex> lk(g.mu);
+    if (usable()) return -1;
+    if (!out || !n) return fail("synth_normal_dev: bad argument");
+    HIPCHK(synth_normal_launch(out, n, seed, sigma, round_bf16, (hipStream_t)stream), "synth launch");
+    return 0;
+}
+
+} // extern "C"

@@ -1,0 +1,146 @@
+/* SPDX-License-Identifier: Apache-2.0 */
+/* dsv4_hip.h - C ABI of the MI355X (gfx950) quantized-matmul hot path.
+ *
+ * Plain C: pointers, sizes and the reference's own matrix descriptor. No HIP,
+ * torch or C++ types cross this boundary; a HIP stream is passed as void *.
+ *
+ * Two families of entry points:
+ *   host-pointer   x / y / out are caller-owned host fp32 arrays, exactly as
+ *                  the reference's src/10_compute entry points take them.
+ *                  Weight pointers (DSV4QMat.w / .s) are host addresses inside
+ *                  ranges uploaded once with dsv4_hip_register(); the library
+ *                  maps them to their resident HBM copies. These return 0 when
+ *                  the GPU produced the whole result and -1 when it did not
+ *                  (no device, unregistered weights, unsupported geometry) --
+ *                  the convention of the reference's GPU backend
+ *                  (src/80_prefill/dsv4_prefill_vk.h:31-41): on -1 the caller
+ *                  keeps its own CPU path. Nothing in this library computes on
+ *                  the CPU.
+ *   _dev           every pointer (activations, outputs, weights, scales,
+ *                  routing) is a device address and work is enqueued on
+ *                  `stream` (NULL = the default stream) without synchronising.
+ *
+ * Numerics: weights are decoded exactly (e4m3 / e2m1 / e8m0 as the reference
+ * defines them); products accumulate in fp32. The reduction order differs from
+ * the reference's AVX2 tree, so results agree within relative L2 1e-3 (typically
+ * ~1e-7), not bit for bit -- the same contract the reference states for its own
+ * Vulkan path (src/10_compute/dsv4_matmul.h:10-17).
+ */
+#ifndef DSV4_HIP_H
+#define DSV4_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---------------------------------------------------------------- types ---
+ * Byte-for-byte the reference's descriptor (src/00_base/dsv4_weights.h:34-40,
+ * 103-106) and format tags (src/00_base/dsv4.h:86). When the reference's
+ * headers are already included (DSV4_WEIGHTS_H defined) their definitions are
+ * used and only the tag this library adds is declared here. */
+#ifndef DSV4_WEIGHTS_H
+enum { DSV4_WF32 = 0, DSV4_WBF16 = 1, DSV4_WFP8 = 2, DSV4_WFP4 = 3 };
+
+typedef struct {
+    const void *w;          /* packed weight bytes                              */
+    const void *s;          /* block scales                                     */
+    int         wdt;        /* DSV4_W*                                          */
+    int         rows, cols; /* logical element dims                             */
+    int         blk_r, blk_c;
+} DSV4QMat;
+
+typedef struct {
+    DSV4QMat w1, w3;        /* FP4 [moe_inter, hidden]                          */
+    DSV4QMat w2;            /* FP4 [hidden, moe_inter]                          */
+} DSV4ExpertW;
+#endif
+
+/* New tag, no counterpart in the reference: e4m3 weights whose block scales
+ * are fp32 (one float per blk_r x blk_c block, row-major grid
+ * [ceil(rows/blk_r)][ceil(cols/blk_c)]) instead of E8M0 bytes. The value of an
+ * element is e4m3(w) * scale, one fp32 multiply. */
+#define DSV4_WFP8_F32S 4
+
+/* ---------------------------------------------------------- lifecycle ---- */
+
+/* Select and initialise `device`. 0 ok, -1 when no usable gfx950 GPU exists
+ * (the caller keeps its CPU path), mirroring dsv4_prefill_vk_init
+ * (src/80_prefill/dsv4_prefill_vk.h:31-35). Idempotent. */
+int  dsv4_hip_init(int device);
+
+/* Release every resident copy and staging buffer. */
+void dsv4_hip_shutdown(void);
+
+/* Human-readable reason for the last -1 on this thread ("" if none). */
+const char *dsv4_hip_last_error(void);
+
+/* Upload [host, host + bytes) to HBM once and remember the mapping. Any
+ * DSV4QMat whose w / s lie inside a registered range then runs from the
+ * resident copy. Replaces the host-pointer import table of the reference's
+ * Vulkan backend (src/80_prefill/dsv4_prefill_vk_region.c:99-148) and the
+ * NVMe slot streaming of src/60_cache: the loader (src/50_loader) calls it once
+ * per arena. 0 ok, -1 on allocation failure or overlap. */
+int  dsv4_hip_register(const void *host, size_t bytes);
+
+/* Drop one registered range (by its start address). 0 ok, -1 unknown. */
+int  dsv4_hip_unregister(const void *host);
+
+/* Device address of the resident copy of host byte `p`, or NULL. */
+void *dsv4_hip_device_ptr(const void *p);
+
+/* ------------------------------------------------- packed matmul (a7-a9) --
+ * y[t*rows + o] = sum_c x[t*cols + c] * W[o, c] for t in 0..nt-1.
+ * Replaces the body of dsv4_mmq_n (src/10_compute/dsv4_matmul.h:40,
+ * dsv4_matmul.c:117-127): DSV4_WFP8 (E8M0 128x128 or any blk_r x 128),
+ * DSV4_WFP8_F32S and DSV4_WFP4 (E8M0 1x32). Other tags return -1. */
+int  dsv4_hip_mmq_n(float *y, const float *x, const DSV4QMat *m, int nt);
+
+/* One token: dsv4_mmq (src/10_compute/dsv4_matmul.h:43). */
+int  dsv4_hip_mmq(float *y, const float *x, const DSV4QMat *m);
+
+int  dsv4_hip_mmq_n_dev(float *y, const float *x, const DSV4QMat *m, int nt,
+                        void *stream);
+
+/* -------------------------------------------- expert FFN (a10, a11) -------
+ * out = w2 . swiglu(w1 . x, w3 . x) for one token, SwiGLU with the
+ * reference's asymmetric clamp (src/10_compute/dsv4_ops.c:61-79; limit <= 0
+ * disables it). Replaces dsv4_expert_forward (src/10_compute/dsv4_kernels.h:30-32)
+ * minus its caller-owned gate/up/mid rows, which stay on the device. */
+int  dsv4_hip_expert_forward(float *out, const float *x, const DSV4ExpertW *e,
+                             int inter, float limit);
+
+/* ----------------------------------------- decode MoE (a11 + a12) --------
+ * out = sum_{k in 0..topk-1, in k order} w[k] * expert(ex[k], x)  +  shared(x)
+ * for one token; the shared expert (may be NULL) is added unweighted after the
+ * routed sum. Replaces the compute of dsv4_layer_moe
+ * (src/70_decode/dsv4_layer.c:57-116) once routing is known; all experts run
+ * in one pass over their resident weights. topk <= 16. */
+int  dsv4_hip_moe_decode(float *out, const float *x,
+                         const DSV4ExpertW *const *ex, const float *w, int topk,
+                         const DSV4ExpertW *shared, float limit);
+
+/* Device form. `experts` is a DEVICE array of descriptors (with device w / s
+ * pointers) indexed by expert id; idx / w are device arrays of topk entries.
+ * `shared` is a HOST descriptor holding device pointers (or NULL). Every
+ * routed expert must be DSV4_WFP4 [inter x hidden] / [hidden x inter] with
+ * 1x32 blocks. */
+int  dsv4_hip_moe_decode_dev(float *out, const float *x,
+                             const DSV4ExpertW *experts, int n_experts,
+                             const int *idx, const float *w, int topk,
+                             const DSV4ExpertW *shared, int hidden, int inter,
+                             float limit, void *stream);
+
+/* Read and clear the device status word that the _dev kernels raise when a
+ * routing id is out of range (bit 0) or an expert descriptor in the device
+ * table does not match the expected format and geometry (bit 1); the affected
+ * outputs are NaN. Synchronises the library's streams. 0 ok, -1 no device. */
+int  dsv4_hip_status(unsigned *bits);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* DSV4_HIP_H */

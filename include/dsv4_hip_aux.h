@@ -1,0 +1,53 @@
+/* SPDX-License-Identifier: Apache-2.0 */
+/* dsv4_hip_aux.h - device-pointer helpers around the hot path: the
+ * dequantization check, the quantizers that produce the packed formats, and
+ * the seeded synthetic-tensor generator. None has a counterpart in the
+ * reference, which ships pre-quantized weights and never quantizes
+ * activations; they exist so the formats can be produced and checked on the
+ * device. All pointers are device addresses; work is enqueued on `stream`.
+ * Each returns 0 when enqueued, -1 on an invalid argument or no device. */
+#ifndef DSV4_HIP_AUX_H
+#define DSV4_HIP_AUX_H
+
+#include "dsv4_hip.h"
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* out[r * cols + c] = decode(W[r, c]) * its block scale (one fp32 multiply),
+ * through the same decoders the matmul kernels use. m->w / m->s are device
+ * pointers; geometry as accepted by dsv4_hip_mmq_n. */
+int dsv4_hip_dequant_dev(float *out, const DSV4QMat *m, void *stream);
+
+/* rows x cols fp32 -> e4m3 bytes W[rows*cols] + fp32 scale per 128x128 block
+ * S[ceil(rows/128)][ceil(cols/128)], scale = blockmax/448 (1 if all zero). */
+int dsv4_hip_quant_fp8_blk128_dev(uint8_t *W, float *S, const float *w,
+                                  int rows, int cols, void *stream);
+
+/* rows x cols fp32 (cols % 32 == 0) -> packed e2m1 W[rows*cols/2] (low nibble
+ * = even element) + E8M0 per 1x32 S[rows*cols/32]: 2^e least with
+ * 6 * 2^e >= blockmax, byte 127 + e clamped to [0, 254] (127 if all zero). */
+int dsv4_hip_quant_fp4_mx_dev(uint8_t *W, uint8_t *S, const float *w,
+                              int rows, int cols, void *stream);
+
+/* n x k activations (k % 128 == 0) -> e4m3 Q[n*k] + fp32 scale per 1x128
+ * S[n][k/128] = groupmax/448 (1 if all zero). */
+int dsv4_hip_quant_act_fp8_1x128_dev(uint8_t *Q, float *S, const float *a,
+                                     int n, int k, void *stream);
+
+/* n x k activations (k % 32 == 0) -> e4m3 Q[n*k] + E8M0 per 1x32 S[n][k/32]:
+ * 2^e least with 448 * 2^e >= groupmax (127 if all zero). */
+int dsv4_hip_quant_act_mxfp8_dev(uint8_t *Q, uint8_t *S, const float *a,
+                                 int n, int k, void *stream);
+
+/* out[i] = sigma * N(0,1) sample i of stream `seed` (counter-based splitmix64
+ * hash -> Box-Muller in double -> fp32), rounded to bf16 when round_bf16. */
+int dsv4_hip_synth_normal_dev(float *out, size_t n, uint64_t seed, float sigma,
+                              int round_bf16, void *stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* DSV4_HIP_AUX_H */

@@ -1,0 +1,384 @@
+# SPDX-License-Identifier: Apache-2.0
+"""GPU parity for the decode path: dequantized weights bit-exact against the
+oracle's decoders; GEMV, expert FFN and decode MoE within relative L2 1e-3 of
+the oracle (the reference's CPU arithmetic restated) on the same inputs,
+including the reference's own golden outputs and its exact-value gates."""
+import ctypes as C
+import math
+
+import numpy as np
+import pytest
+import torch
+
+import pyoracle as P
+from conftest import REL_L2_TOL, bits, golden, max_abs, rel_l2
+
+pytestmark = pytest.mark.gpu
+
+DEV = "cuda:0"
+
+
+def dev_u8(a):
+    return torch.from_numpy(np.ascontiguousarray(a).view(np.uint8).reshape(-1)).to(DEV)
+
+
+def dev_f32(a):
+    return torch.from_numpy(np.ascontiguousarray(a, np.float32).reshape(-1)).to(DEV)
+
+
+class Resident:
+    """Host matrix registered with the library (upload once)."""
+
+    def __init__(self, lib, pkg, wdt, W, S, rows, cols, blk_r, blk_c):
+        self.W = np.ascontiguousarray(W, np.uint8)
+        self.S = np.ascontiguousarray(S, np.float32 if wdt == pkg.DSV4_WFP8_F32S else np.uint8)
+        for a in (self.W, self.S):
+            lib.check(lib.register(a), "register")
+        self.lib = lib
+        self.desc = pkg.qmat(wdt, self.W.ctypes.data, self.S.ctypes.data, rows, cols, blk_r, blk_c)
+        self.hm = P.HostMat(wdt, self.W, self.S, rows, cols, blk_r, blk_c)
+
+    def drop(self):
+        self.lib.unregister(self.W)
+        self.lib.unregister(self.S)
+
+
+def check_close(got, want, tol=REL_L2_TOL):
+    e = rel_l2(got, want)
+    assert np.all(np.isfinite(got)), "non-finite output"
+    assert e <= tol, f"rel L2 {e:.3e} > {tol} (max abs {max_abs(got, want):.3e})"
+    return e
+
+
+# ------------------------------------------------------------- dequant ----
+
+def test_dequant_fp8_every_code_every_scale(lib, pkg, oracle):
+    rows, cols = 256, 256
+    W = np.tile(np.arange(256, dtype=np.uint8), rows).reshape(rows, cols)
+    W = np.stack([np.roll(W[r], r) for r in range(rows)]).reshape(-1)
+    S = np.stack([np.arange(256), (np.arange(256) + 100) % 256], 1).astype(np.uint8).reshape(-1)
+    out = torch.empty(rows * cols, dtype=torch.float32, device=DEV)
+    dW, dS = dev_u8(W), dev_u8(S)
+    d = pkg.qmat(pkg.DSV4_WFP8, dW.data_ptr(), dS.data_ptr(), rows, cols, 1, 128)
+    lib.dequant_dev(out.data_ptr(), d)
+    got = out.cpu().numpy()
+    dec = np.array([oracle.e4m3(b) for b in range(256)], np.float32)
+    sc = np.array([oracle.e8m0(b) for b in range(256)], np.float32)
+    want = dec[W] * sc[S.reshape(rows, 2)[:, np.arange(cols) // 128].reshape(-1)]
+    nan = np.isnan(want)
+    assert np.array_equal(np.isnan(got), nan)
+    assert np.array_equal(bits(got)[~nan], bits(want)[~nan])
+
+
+def test_dequant_fp4_every_byte_every_scale(lib, pkg, oracle):
+    rows, cols = 256, 512
+    W = np.stack([np.roll(np.arange(256, dtype=np.uint8), r) for r in range(rows)]).reshape(-1)
+    S = np.stack([(np.arange(256) + 7 * b) % 256 for b in range(16)], 1).astype(np.uint8).reshape(-1)
+    out = torch.empty(rows * cols, dtype=torch.float32, device=DEV)
+    dW, dS = dev_u8(W), dev_u8(S)
+    d = pkg.qmat(pkg.DSV4_WFP4, dW.data_ptr(), dS.data_ptr(), rows, cols, 1, 32)
+    lib.dequant_dev(out.data_ptr(), d)
+    got = out.cpu().numpy()
+    e2 = np.array([oracle.e2m1(n) for n in range(16)], np.float32)
+    codes = np.stack([W & 15, W >> 4], 1).reshape(-1)
+    sc = np.array([oracle.e8m0(b) for b in range(256)], np.float32)
+    sidx = (np.arange(rows * cols) // cols) * 16 + (np.arange(rows * cols) % cols) // 32
+    want = e2[codes] * sc[S[sidx]]
+    nan = np.isnan(want)
+    assert np.array_equal(np.isnan(got), nan)
+    assert np.array_equal(bits(got)[~nan], bits(want)[~nan])
+
+
+def test_dequant_fp8_f32_scales(lib, pkg, oracle):
+    rng = np.random.default_rng(1)
+    rows, cols = 384, 512
+    W = rng.integers(0, 256, rows * cols).astype(np.uint8)
+    S = (rng.standard_normal(3 * 4) * 1e-3).astype(np.float32)
+    out = torch.empty(rows * cols, dtype=torch.float32, device=DEV)
+    dW, dS = dev_u8(W), dev_f32(S)
+    d = pkg.qmat(pkg.DSV4_WFP8_F32S, dW.data_ptr(), dS.data_ptr(), rows, cols, 128, 128)
+    lib.dequant_dev(out.data_ptr(), d)
+    got = out.cpu().numpy()
+    dec = np.array([oracle.e4m3(b) for b in range(256)], np.float32)
+    r, c = np.divmod(np.arange(rows * cols), cols)
+    want = dec[W] * S[(r // 128) * 4 + c // 128]
+    nan = np.isnan(want)
+    assert np.array_equal(np.isnan(got), nan)
+    assert np.array_equal(bits(got)[~nan], bits(want)[~nan])
+
+
+# ------------------------------------------------- reference known answers
+
+def test_reference_exact_gates_through_mirror(lib, pkg):
+    """tests/unit/test_matmul.c GATE 1, 1b, 2, 3, 4, 5, 5b through the
+    reference-named entry point dsv4_mmq (lib/libdsv4_amd.so): these inputs
+    are exactly representable, so the GPU must return the exact answers."""
+    mirror = C.CDLL(pkg.AMD_SO)
+    mirror.dsv4_mmq.restype = None
+    mirror.dsv4_mmq.argtypes = [C.c_void_p, C.c_void_p, C.POINTER(pkg.QMat)]
+
+    def run(wdt, W, S, rows, cols, br, bc, x):
+        m = Resident(lib, pkg, wdt, W, S, rows, cols, br, bc)
+        x = np.ascontiguousarray(x, np.float32)
+        y = np.zeros(rows, np.float32)
+        mirror.dsv4_mmq(y.ctypes.data, x.ctypes.data, C.byref(m.desc))
+        m.drop()
+        return y
+
+    ones = lambda n: np.ones(n, np.float32)
+    y = run(2, np.r_[np.full(128, 0x38), np.full(128, 0x40)], [128, 0], 2, 128, 128, 128, ones(128))
+    assert list(y) == [256.0, 512.0]
+    y = run(2, np.full(256 * 128, 0x38), [127, 129], 256, 128, 128, 128, ones(128))
+    assert y[0] == y[127] == 128.0 and y[128] == y[255] == 512.0
+    y = run(2, np.full(256, 0x38), [127, 128], 1, 256, 128, 128, ones(256))
+    assert y[0] == 384.0
+    y = run(3, np.full(64, 0x22), [127, 128, 127, 127], 2, 64, 1, 32, ones(64))
+    assert list(y) == [96.0, 64.0]
+    y = run(3, np.r_[np.full(16, 0x22), np.full(16, 0x44)], [127, 127], 2, 32, 1, 32, ones(32))
+    assert list(y) == [32.0, 64.0]
+    y = run(3, np.full(16, 0xA2), [128], 1, 32, 1, 32, np.arange(1, 33))
+    assert y[0] == -32.0
+    S = [127 + ((b + o) % 5) for o in range(3) for b in range(5)]
+    y = run(3, np.full(3 * 80, 0x22), S, 3, 160, 1, 32, ones(160))
+    for o in range(3):
+        assert y[o] == sum(32.0 * 2.0 ** ((b + o) % 5) for b in range(5))
+
+
+@pytest.mark.parametrize("name", ["fp8_fast", "fp8_tail", "fp8_wide", "fp4_wide", "fp4_tail"])
+def test_golden_reference_outputs(lib, pkg, name):
+    """The reference's own fp8_n / fp4_n outputs (tests/golden) reproduced by
+    the GPU within the tolerance."""
+    g = golden(name)
+    rows, cols, br, bc, nt = (int(v) for v in g["dims"])
+    wdt = pkg.DSV4_WFP8 if name.startswith("fp8") else pkg.DSV4_WFP4
+    m = Resident(lib, pkg, wdt, g["W"], g["S"], rows, cols, br, bc)
+    y = lib.mmq_n(m.desc, g["x"], nt)
+    m.drop()
+    check_close(y, g["y"])
+
+
+@pytest.mark.parametrize("name", ["fp8_generic", "fp4_generic"])
+def test_unsupported_geometry_declines(lib, pkg, name):
+    """A block width other than 128 (FP8) / 32 (FP4) is the reference's generic
+    path; the GPU declines with -1 and a reason, so the caller keeps its CPU path
+    (src/80_prefill/dsv4_prefill_vk.h:37-41)."""
+    g = golden(name)
+    rows, cols, br, bc, nt = (int(v) for v in g["dims"])
+    wdt = pkg.DSV4_WFP8 if name.startswith("fp8") else pkg.DSV4_WFP4
+    m = Resident(lib, pkg, wdt, g["W"], g["S"], rows, cols, br, bc)
+    assert lib.mmq_n_rc(m.desc, g["x"], nt) == -1
+    assert "unsupported" in lib.error()
+    m.drop()
+
+
+def test_unregistered_weights_decline(lib, pkg):
+    W = np.zeros(128 * 128, np.uint8); S = np.zeros(1, np.uint8)
+    d = pkg.qmat(pkg.DSV4_WFP8, W.ctypes.data, S.ctypes.data, 128, 128, 128, 128)
+    assert lib.mmq_n_rc(d, np.zeros(128, np.float32)) == -1
+    assert "registered" in lib.error()
+
+
+# --------------------------------------------------------- GEMV parity ----
+
+def _rand_fp8(rng, n):
+    b = rng.integers(0, 256, n).astype(np.uint8)
+    b[(b & 0x7F) == 0x7F] &= 0xFE
+    return b
+
+
+@pytest.mark.parametrize("rows,cols,nt,blk_r", [
+    (4096, 4096, 1, 128), (1024, 4096, 2, 128), (37, 384, 3, 128), (130, 256, 1, 128),
+    (2048, 2048, 1, 128), (100, 1024, 1, 1), (9, 3072, 1, 128)])
+def test_fp8_e8m0_gemv(lib, pkg, oracle, rows, cols, nt, blk_r):
+    rng = np.random.default_rng(rows * 7 + cols)
+    W = _rand_fp8(rng, rows * cols)
+    S = rng.integers(118, 134, ((rows + blk_r - 1) // blk_r) * (cols // 128)).astype(np.uint8)
+    x = rng.standard_normal(nt * cols).astype(np.float32)
+    m = Resident(lib, pkg, pkg.DSV4_WFP8, W, S, rows, cols, blk_r, 128)
+    y = lib.mmq_n(m.desc, x, nt)
+    m.drop()
+    check_close(y, oracle.fp8_n(W, S, x, rows, cols, blk_r, 128, nt))
+
+
+@pytest.mark.parametrize("rows,cols,nt", [
+    (2048, 4096, 1), (4096, 2048, 1), (9, 160, 3), (64, 4096, 2), (33, 32, 1), (5, 8192, 1)])
+def test_fp4_gemv(lib, pkg, oracle, rows, cols, nt):
+    rng = np.random.default_rng(rows * 3 + cols)
+    W = rng.integers(0, 256, rows * cols // 2).astype(np.uint8)
+    S = rng.integers(118, 134, rows * cols // 32).astype(np.uint8)
+    x = rng.standard_normal(nt * cols).astype(np.float32)
+    m = Resident(lib, pkg, pkg.DSV4_WFP4, W, S, rows, cols, 1, 32)
+    y = lib.mmq_n(m.desc, x, nt)
+    m.drop()
+    check_close(y, oracle.fp4_n(W, S, x, rows, cols, 1, 32, nt))
+
+
+def test_fp8_f32s_gemv_config_shape(lib, pkg, oracle):
+    """4096 x 4096 e4m3 with fp32 128x128 scales = blockmax/448, x bf16 N(0,1)."""
+    rng = np.random.default_rng(0)
+    w = (rng.standard_normal((4096, 4096)) * 0.02).astype(np.float32)
+    W, S = oracle.quant_fp8_blk128(w)
+    x = torch.randn(4096, generator=torch.Generator().manual_seed(0)).bfloat16().float().numpy()
+    m = Resident(lib, pkg, pkg.DSV4_WFP8_F32S, W, S, 4096, 4096, 128, 128)
+    y = lib.mmq_n(m.desc, x, 1)
+    m.drop()
+    e = check_close(y, oracle.fp8f_n(W, S, x, 4096, 4096, 128, 128, 1))
+    assert e < 1e-5  # fp32 accumulation of exact products: far below the gate
+
+
+def test_gemv_deterministic(lib, pkg):
+    rng = np.random.default_rng(9)
+    W = rng.integers(0, 256, 1024 * 2048).astype(np.uint8)
+    S = rng.integers(118, 134, 1024 * 4096 // 32).astype(np.uint8)
+    x = rng.standard_normal(4096).astype(np.float32)
+    m = Resident(lib, pkg, pkg.DSV4_WFP4, W, S, 1024, 4096, 1, 32)
+    a = lib.mmq_n(m.desc, x)
+    b = lib.mmq_n(m.desc, x)
+    m.drop()
+    assert np.array_equal(bits(a), bits(b))
+
+
+# ------------------------------------------------------- expert + MoE ----
+
+def make_fp4_expert(lib, pkg, oracle, rng, inter=2048, hidden=4096):
+    mats = []
+    for (r, c) in ((inter, hidden), (inter, hidden), (hidden, inter)):
+        w = (rng.standard_normal((r, c)) * 0.02).astype(np.float32)
+        W, S = oracle.quant_fp4_mx(w)
+        mats.append(Resident(lib, pkg, pkg.DSV4_WFP4, W, S, r, c, 1, 32))
+    e = pkg.ExpertW(mats[0].desc, mats[1].desc, mats[2].desc)
+    he = P.HostExpert(mats[0].hm, mats[1].hm, mats[2].hm)
+    return e, he, mats
+
+
+def make_fp8_shared(lib, pkg, oracle, rng, inter=2048, hidden=4096):
+    mats = []
+    for (r, c) in ((inter, hidden), (inter, hidden), (hidden, inter)):
+        w = (rng.standard_normal((r, c)) * 0.02).astype(np.float32)
+        W, S = oracle.quant_fp8_blk128(w)
+        mats.append(Resident(lib, pkg, pkg.DSV4_WFP8_F32S, W, S, r, c, 128, 128))
+    e = pkg.ExpertW(mats[0].desc, mats[1].desc, mats[2].desc)
+    he = P.HostExpert(mats[0].hm, mats[1].hm, mats[2].hm)
+    return e, he, mats
+
+
+def bf16_x(seed, n):
+    return torch.randn(n, generator=torch.Generator().manual_seed(seed)).bfloat16().float().numpy()
+
+
+def test_expert_forward_fp4(lib, pkg, oracle):
+    rng = np.random.default_rng(21)
+    e, he, mats = make_fp4_expert(lib, pkg, oracle, rng)
+    x = bf16_x(1, 4096)
+    y = lib.expert_forward(e, x, 10.0)
+    check_close(y, oracle.expert_forward(he, x, 10.0))
+    for m in mats:
+        m.drop()
+
+
+def test_moe_decode_top6(lib, pkg, oracle):
+    """Config 1 semantics: six FP4 experts, softmax weights, k-order combine."""
+    rng = np.random.default_rng(22)
+    experts = [make_fp4_expert(lib, pkg, oracle, rng) for _ in range(6)]
+    x = bf16_x(2, 4096)
+    logits = rng.standard_normal(6)
+    w = (np.exp(logits) / np.exp(logits).sum()).astype(np.float32)
+    y = lib.moe_decode([e for e, _, _ in experts], w, x, None, 10.0)
+    acc = np.stack([oracle.expert_forward(he, x, 10.0) for _, he, _ in experts])
+    check_close(y, oracle.moe_combine(acc, w))
+    for _, _, mats in experts:
+        for m in mats:
+            m.drop()
+
+
+def test_moe_decode_with_fp8_shared(lib, pkg, oracle):
+    rng = np.random.default_rng(23)
+    experts = [make_fp4_expert(lib, pkg, oracle, rng) for _ in range(3)]
+    sh, hsh, smats = make_fp8_shared(lib, pkg, oracle, rng)
+    x = bf16_x(3, 4096)
+    w = np.array([0.5, 0.3, 0.2], np.float32)
+    y = lib.moe_decode([e for e, _, _ in experts], w, x, sh, 10.0)
+    acc = np.stack([oracle.expert_forward(he, x, 10.0) for _, he, _ in experts])
+    check_close(y, oracle.moe_combine(acc, w, oracle.expert_forward(hsh, x, 10.0)))
+    for _, _, mats in experts:
+        for m in mats:
+            m.drop()
+    for m in smats:
+        m.drop()
+
+
+def test_moe_decode_dev_bad_id_flags_status(lib, pkg, oracle):
+    """A routing id outside the table raises status bit 0 and poisons the
+    output with NaN instead of reading out of bounds."""
+    rng = np.random.default_rng(24)
+    inter, hidden = 64, 256
+    mats = []
+    for (r, c) in ((inter, hidden), (inter, hidden), (hidden, inter)):
+        W, S = oracle.quant_fp4_mx((rng.standard_normal((r, c)) * 0.02).astype(np.float32))
+        mats.append((dev_u8(W), dev_u8(S), r, c))
+    descs = [pkg.qmat(pkg.DSV4_WFP4, w.data_ptr(), s.data_ptr(), r, c, 1, 32) for w, s, r, c in mats]
+    table = pkg.ExpertW(descs[0], descs[1], descs[2])
+    tbl = torch.from_numpy(np.frombuffer(bytes(table), np.uint8).copy()).to(DEV)
+    x = dev_f32(rng.standard_normal(hidden))
+    w = dev_f32(np.array([0.5, 0.5], np.float32))
+    out = torch.zeros(hidden, dtype=torch.float32, device=DEV)
+    lib.status()
+    good = torch.tensor([0, 0], dtype=torch.int32, device=DEV)
+    lib.moe_decode_dev(out.data_ptr(), x.data_ptr(), tbl.data_ptr(), 1, good.data_ptr(),
+                       w.data_ptr(), 2, None, hidden, inter, 10.0)
+    assert lib.status() == 0 and torch.isfinite(out).all()
+    bad = torch.tensor([0, 5], dtype=torch.int32, device=DEV)
+    lib.moe_decode_dev(out.data_ptr(), x.data_ptr(), tbl.data_ptr(), 1, bad.data_ptr(),
+                       w.data_ptr(), 2, None, hidden, inter, 10.0)
+    assert lib.status() & 1
+    assert torch.isnan(out).all()
+
+
+# ---------------------------------------------------------- quantizers ----
+
+def test_gpu_quantizers_bitexact(lib, pkg, oracle):
+    rng = np.random.default_rng(31)
+    w = (rng.standard_normal((256, 512)) * 0.02).astype(np.float32)
+    w[0, :32] = 0.0
+    dw = dev_f32(w)
+    W = torch.empty(256 * 256, dtype=torch.uint8, device=DEV)
+    S = torch.empty(256 * 16, dtype=torch.uint8, device=DEV)
+    lib.quant_fp4_mx_dev(W.data_ptr(), S.data_ptr(), dw.data_ptr(), 256, 512)
+    Wo, So = oracle.quant_fp4_mx(w)
+    assert np.array_equal(W.cpu().numpy(), Wo) and np.array_equal(S.cpu().numpy(), So)
+
+    W8 = torch.empty(256 * 512, dtype=torch.uint8, device=DEV)
+    S8 = torch.empty(2 * 4, dtype=torch.float32, device=DEV)
+    lib.quant_fp8_blk128_dev(W8.data_ptr(), S8.data_ptr(), dw.data_ptr(), 256, 512)
+    Wo, So = oracle.quant_fp8_blk128(w)
+    assert np.array_equal(W8.cpu().numpy(), Wo) and np.array_equal(bits(S8.cpu().numpy()), bits(So))
+
+    a = bf16_x(5, 6 * 512).reshape(6, 512)
+    a[1, :128] = 0.0
+    da = dev_f32(a)
+    Q = torch.empty(6 * 512, dtype=torch.uint8, device=DEV)
+    Sa = torch.empty(6 * 4, dtype=torch.float32, device=DEV)
+    lib.quant_act_fp8_1x128_dev(Q.data_ptr(), Sa.data_ptr(), da.data_ptr(), 6, 512)
+    Qo, So = oracle.quant_act_fp8_1x128(a)
+    assert np.array_equal(Q.cpu().numpy(), Qo) and np.array_equal(bits(Sa.cpu().numpy()), bits(So))
+
+    Qm = torch.empty(6 * 512, dtype=torch.uint8, device=DEV)
+    Sm = torch.empty(6 * 16, dtype=torch.uint8, device=DEV)
+    lib.quant_act_mxfp8_dev(Qm.data_ptr(), Sm.data_ptr(), da.data_ptr(), 6, 512)
+    Qo, So = oracle.quant_act_mxfp8(a)
+    assert np.array_equal(Qm.cpu().numpy(), Qo) and np.array_equal(Sm.cpu().numpy(), So)
+
+
+def test_synth_normal_deterministic(lib):
+    n = 1 << 20
+    a = torch.empty(n, dtype=torch.float32, device=DEV)
+    b = torch.empty(n, dtype=torch.float32, device=DEV)
+    lib.synth_normal_dev(a.data_ptr(), n, 1234, 0.02)
+    lib.synth_normal_dev(b.data_ptr(), n, 1234, 0.02)
+    torch.cuda.synchronize()
+    assert torch.equal(a, b)
+    assert abs(a.mean().item()) < 1e-4 and abs(a.std().item() - 0.02) < 1e-4
+    lib.synth_normal_dev(b.data_ptr(), n, 1234, 1.0, round_bf16=True)
+    torch.cuda.synchronize()
+    bb = b.cpu()
+    assert torch.equal(bb, bb.bfloat16().float())
