@@ -119,12 +119,133 @@ __device__ __forceinline__ float dot16(const u32x4 w, const float *xs)
     else return dot16_e4m3(w, xs);
 }
 
-/* Global loads that bypass nothing but are marked non-temporal for streamed
- * weights: each weight byte is read exactly once per call. */
+/* Pointers read from device memory (descriptor tables) are generic to the
+ * compiler, and generic (flat) loads are waited for all at once. Every weight
+ * and scale access goes through a global-address-space pointer so loads
+ * complete in issue order and are waited for one by one. */
+#define DSV4_GLOBAL __attribute__((address_space(1)))
+template <class T>
+__device__ __forceinline__ const DSV4_GLOBAL T *gptr(const T *p)
+{
+    return (const DSV4_GLOBAL T *)p;
+}
+
+/* Wave-uniform reads (routing ids, descriptor tables) go through the
+ * constant address space so they become scalar loads into SGPRs; the data
+ * must not be written while the kernel runs. */
+#define DSV4_CONST __attribute__((address_space(4)))
+template <class T>
+__device__ __forceinline__ T ld_uniform(const T *base, int i)
+{
+    static_assert(sizeof(T) % 4 == 0, "uniform reads move whole dwords");
+    const DSV4_CONST uint32_t *p = (const DSV4_CONST uint32_t *)(base + i);
+    T r;
+    uint32_t *q = (uint32_t *)&r;
+#pragma unroll
+    for (unsigned k = 0; k < sizeof(T) / 4; k++) q[k] = p[k];
+    return r;
+}
+
+/* The index of the calling wave in the grid, provably wave-uniform. */
+__device__ __forceinline__ int wave_id()
+{
+    return __builtin_amdgcn_readfirstlane((int)(blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6)));
+}
+
+/* Weight chunk loads, marked non-temporal: each weight byte is read exactly
+ * once per call. */
 __device__ __forceinline__ u32x4 ld_stream16(const void *p)
 {
-    return __builtin_nontemporal_load((const u32x4 *)p);
+    return __builtin_nontemporal_load(gptr((const u32x4 *)p));
 }
+
+/* One scale: an E8M0 byte or an fp32. */
+__device__ __forceinline__ uint32_t ld_u8(const void *base, size_t i)
+{
+    return gptr((const uint8_t *)base)[i];
+}
+__device__ __forceinline__ float ld_f32(const void *base, size_t i)
+{
+    return gptr((const float *)base)[i];
+}
+
+/* Keep the compiler from moving instructions across this point: the decode
+ * kernels use it to pin the issue order of their load groups. */
+#define DSV4_ORDER() __builtin_amdgcn_sched_barrier(0)
+
+/* A uniform `true` the compiler cannot see through. Arithmetic placed under
+ * `if (dsv4_opaque_true())` lands in its own basic block, so instruction
+ * selection cannot hoist it (e.g. a scale-byte decode) in between loads that
+ * must all be issued before the wave waits for the first of them. */
+__device__ __forceinline__ bool dsv4_opaque_true()
+{
+    int v;
+    asm volatile("s_mov_b32 %0, 1" : "=s"(v));
+    return v != 0;
+}
+
+/* Chunk geometry of the decode kernels: lane `lane` reads the 16 weight bytes
+ * at row byte offset 16 * lane + 1024 * j (j < KCH). A row is FULL when
+ * row_bytes == KCH * 1024, i.e. every lane's every chunk is inside the row;
+ * otherwise chunks past row_bytes are "out". Loads are never skipped, so no
+ * load sits behind a branch: an out chunk loads the row's first chunk
+ * instead, its activations read as zero and its scale as zero, so it adds an
+ * exact zero (or the NaN that the row's first chunk already contributes). */
+__device__ __forceinline__ int chunk_byte(int lane, int j) { return 16 * lane + 1024 * j; }
+
+/* The lane's slice of an fp32 activation row: chunk j covers CPL columns
+ * starting at (FP4 ? 2 : 1) * chunk_byte(lane, j); an out chunk reads the
+ * row's first CPL columns (its scale is zero). x must be 16-byte aligned and
+ * hold at least 32 (FP4) or 16 (FP8) columns. No arithmetic touches the
+ * loaded values here, so issuing these loads never waits for them. */
+template <bool FP4, int KCH, bool FULL>
+__device__ __forceinline__ void load_x_slice(float (&xs)[KCH][FP4 ? 32 : 16],
+                                             const float *x, int lane,
+                                             int row_bytes)
+{
+    constexpr int CPL = FP4 ? 32 : 16;
+#pragma unroll
+    for (int j = 0; j < KCH; j++) {
+        const int b = chunk_byte(lane, j);
+        const bool in = FULL || b < row_bytes;
+        const float *p = x + (in ? (FP4 ? 2 * b : b) : 0);
+#pragma unroll
+        for (int i = 0; i < CPL; i += 4) {
+            const f32x4 v = *(const f32x4 *)(p + i);
+            xs[j][i] = v.x; xs[j][i + 1] = v.y; xs[j][i + 2] = v.z; xs[j][i + 3] = v.w;
+        }
+    }
+}
+
+/* Raw scale words: the E8M0 byte or the fp32 bits of one block scale. They
+ * are loaded with the other early loads and decoded only at first use, so
+ * the weight loads behind them are issued without waiting. */
+template <bool F32S>
+__device__ __forceinline__ uint32_t ld_scale_raw(const void *S, size_t idx)
+{
+    if constexpr (F32S) return gptr((const uint32_t *)S)[idx];
+    else return gptr((const uint8_t *)S)[idx];
+}
+template <bool F32S>
+__device__ __forceinline__ float scale_from_raw(uint32_t raw)
+{
+    if constexpr (F32S) return __uint_as_float(raw);
+    else return dev_e8m0(raw);
+}
+
+/* The lane's KCH weight chunks of one row (row start `wr`). */
+template <int KCH, bool FULL>
+__device__ __forceinline__ void load_w_row(u32x4 (&w)[KCH], const uint8_t *wr,
+                                           int lane, int row_bytes)
+{
+#pragma unroll
+    for (int j = 0; j < KCH; j++) {
+        const int b = chunk_byte(lane, j);
+        const bool in = FULL || b < row_bytes;
+        w[j] = ld_stream16(wr + (in ? b : 0));
+    }
+}
+
 
 __device__ __forceinline__ f32x4 ld_f4(const float *p)
 {

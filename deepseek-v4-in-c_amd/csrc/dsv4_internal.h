@@ -94,21 +94,23 @@ struct GateUpArgs {
 };
 hipError_t gateup_launch(int fmt, const GateUpArgs &a, hipStream_t st);
 
-/* out[i] = sum_k (k order) w[k] * (table[idx[k]].w2 . mid[k])[i] + shared[i] */
-struct DownCombineArgs {
+/* out[i] = sum_k (k order) w[k] * (table[idx[k]].w2 . mid[k])[i] + shared[i]
+ * for FP4 routed experts, topk <= 16. */
+struct DownArgs {
     const DSV4ExpertW *table;
     const int *idx;
     const float *w;           /* device, topk routing weights           */
     int n_experts;
     int topk;
-    const float *mid;         /* [topk][mid_ld]                         */
+    const float *mid;         /* [topk][mid_ld], mid_ld % 4 == 0         */
     int mid_ld;
     const float *shared;      /* device [hidden] or NULL                */
     float *out;               /* [hidden]                               */
     int inter, hidden;
     unsigned *status;
 };
-hipError_t down_combine_launch(int fmt, const DownCombineArgs &a, hipStream_t st);
+int down_groups(int hidden);
+hipError_t down_launch(const DownArgs &a, hipStream_t st);
 
 /* ---------------------------------------------- dequant / quantizers --- */
 hipError_t dequant_launch(int fmt, const DSV4QMat &m, float *out, hipStream_t st);

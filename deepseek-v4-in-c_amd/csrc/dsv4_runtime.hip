@@ -237,7 +237,7 @@ int enqueue_moe(const DSV4ExpertW *table, int n_experts, const int *idx,
     ga.limit = limit;
     ga.status = g.status;
     HIPCHK(gateup_launch(FMT_FP4_E8M0, ga, st), "routed gate/up launch");
-    DownCombineArgs da;
+    DownArgs da;
     memset(&da, 0, sizeof da);
     da.table = table;
     da.idx = idx;
@@ -251,7 +251,7 @@ int enqueue_moe(const DSV4ExpertW *table, int n_experts, const int *idx,
     da.inter = inter;
     da.hidden = hidden;
     da.status = g.status;
-    HIPCHK(down_combine_launch(FMT_FP4_E8M0, da, st), "down/combine launch");
+    HIPCHK(down_launch(da, st), "down/combine launch");
     return 0;
 }
 
@@ -279,6 +279,7 @@ int dsv4_hip_init(int device)
         return fail("stream creation failed");
     if (hipMalloc((void **)&g.status, 256) != hipSuccess) return fail("status alloc failed");
     if (hipMemset(g.status, 0, 256) != hipSuccess) return fail("status clear failed");
+
     g.device = device;
     g.ready = 1;
     g.dead = 0;
@@ -428,6 +429,7 @@ int dsv4_hip_moe_decode(float *out, const float *x, const DSV4ExpertW *const *ex
         if (fmt != FMT_FP4_E8M0) return fail("moe_decode: routed experts must be FP4");
         if (k == 0) { inter = ei; hidden = eh; }
         else if (ei != inter || eh != hidden) return fail("moe_decode: routed shapes differ");
+        if (inter / 2 > 2048) return fail("moe_decode: routed inter %d above 4096", inter);
         if (resident_expert(ex[k], &tab[k], "moe_decode routed")) return -1;
     }
     DSV4ExpertW sdev;
