@@ -13,6 +13,10 @@ weights and scales + 8 KiB bf16 x + 16 KiB fp32 out per token).
 --config 0: one 4096x4096 e4m3 matvec with fp32 128x128 scales, x bf16;
 weights rotated over 40 copies (672 MB) so each step reads from HBM.
 
+--config 3: prefill GEMM, 2048 tokens x 4096 (bf16 A, quantized on the fly to
+e4m3 with an fp32 scale per 1x128) times a 4096x4096 e4m3 weight with fp32
+128x128 scales, bf16 output, on FP8 MFMA. Metric: TFLOP/s (2 M N K per step).
+
 Prints ONE JSON line. Synthetic data (seeded), random-init weights.
 """
 from __future__ import annotations
@@ -29,6 +33,7 @@ import numpy as np
 
 ROOT = os.path.dirname(os.path.abspath(__file__))
 HBM_PEAK_GBS = 8000.0
+FP8_PEAK_TFLOPS = 5000.0          # MI355X dense FP8 MFMA
 
 EXPERT_BYTES = 13_369_344          # w1,w3: 2048x4096 FP4 + scales; w2: 4096x2048
 HIDDEN, INTER, N_EXPERTS, TOPK = 4096, 2048, 256, 6
@@ -161,6 +166,105 @@ def cpu_baseline_cfg1(torch, arena, x_host, seconds, threads):
                       f"(214 MB), {el:.1f} s, OpenMP {threads} threads"}
 
 
+def cpu_baseline_cfg3(Wq, Sw_e8m0, x_sample, seconds, threads):
+    """The reference's CPU fp8_n (nt > 1 body, src/10_compute/dsv4_matmul_fp8.c:
+    102-155) on the same 4096x4096 e4m3 weight, over blocks of 128 tokens
+    (dsv4_mmq_n's tile), repeated until `seconds` elapse. The reference only
+    stores E8M0 block scales, so it runs with the power of two at or above each
+    fp32 scale; the arithmetic per token is the same."""
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import pyoracle as P
+    kind = "reference"
+    try:
+        impl = P.Reference()
+    except FileNotFoundError:
+        impl, kind = P.Oracle(), "port"
+    omp_threads(threads)
+    nt = x_sample.shape[0]
+    t0 = time.perf_counter()
+    blocks = 0
+    while True:
+        impl.fp8_n(Wq, Sw_e8m0, x_sample.reshape(-1), 4096, 4096, 128, 128, nt)
+        blocks += 1
+        el = time.perf_counter() - t0
+        if el >= seconds and blocks >= 2:
+            break
+    tflops = blocks * 2.0 * nt * 4096 * 4096 / el / 1e12
+    return {"value": round(tflops, 5), "unit": "TFLOP/s", "cores": threads, "kind": kind,
+            "sample": f"{blocks} x {nt} tokens through fp8_n 4096x4096 (E8M0 scales), {el:.1f} s, "
+                      f"OpenMP {threads} threads"}
+
+
+def bench_cfg3(args, torch, pkg, lib, stream, sp, K, W):
+    M, N, KD = 2048, 4096, 4096
+    flops = 2.0 * M * N * KD
+    dev = "cuda:0"
+    log("generating the 4096x4096 FP8 weight and 2048x4096 bf16 activations")
+    tmp = torch.empty(N * KD, dtype=torch.float32, device=dev)
+    Wd = torch.empty(N * KD, dtype=torch.uint8, device=dev)
+    Sd = torch.empty((N // 128) * (KD // 128), dtype=torch.float32, device=dev)
+    lib.synth_normal_dev(tmp.data_ptr(), tmp.numel(), 0xD5EED003, 0.02)
+    lib.quant_fp8_blk128_dev(Wd.data_ptr(), Sd.data_ptr(), tmp.data_ptr(), N, KD)
+    af = torch.empty(M * KD, dtype=torch.float32, device=dev)
+    lib.synth_normal_dev(af.data_ptr(), af.numel(), 0xD5EED003 ^ 0x55, 1.0, True)
+    A = af.bfloat16()
+    C = torch.empty((M, N), dtype=torch.bfloat16, device=dev)
+    Aq = torch.empty(M * KD, dtype=torch.uint8, device=dev)
+    Sa = torch.empty(M * KD // 128, dtype=torch.float32, device=dev)
+    lib.quant_act_fp8_1x128_dev(Aq.data_ptr(), Sa.data_ptr(), af.data_ptr(), M, KD)
+    desc = pkg.qmat(pkg.DSV4_WFP8_F32S, Wd.data_ptr(), Sd.data_ptr(), N, KD, 128, 128)
+    torch.cuda.synchronize()
+
+    def step(i):
+        lib.gemm_fp8_dev(C.data_ptr(), 1, A.data_ptr(), 1, M, desc, sp)
+
+    def gemm_only(i):
+        lib.gemm_fp8q_dev(C.data_ptr(), 1, Aq.data_ptr(), Sa.data_ptr(), M, desc, sp)
+
+    for i in range(W):
+        step(i)
+    torch.cuda.synchronize()
+    log(f"timing {K} steps")
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    e0.record(stream)
+    for i in range(K):
+        step(i)
+    e1.record(stream)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    t_step = e0.elapsed_time(e1) * 1e-3 / K
+    t_gemm = time_events(torch, stream, gemm_only, K)
+    value = flops / t_step / 1e12
+    achieved = flops / t_gemm / 1e12
+    cpu = None
+    if not args.no_cpu:
+        threads = args.cpu_threads or min(16, os.cpu_count() or 1)
+        Wh = Wd.cpu().numpy()
+        Se = torch.clamp(torch.ceil(torch.log2(Sd)) + 127, 0, 254).to(torch.uint8).cpu().numpy()
+        xs = A.view(M, KD)[:128].float().cpu().numpy()
+        log(f"CPU baseline ({threads} threads, {args.cpu_seconds:.0f} s)")
+        cpu = cpu_baseline_cfg3(Wh, Se, xs, args.cpu_seconds, threads)
+    return {
+        "metric": "quant matvec HBM GB/s (% peak); prefill FP4/FP8 GEMM TFLOP/s (% MFMA peak)",
+        "value": round(value, 2), "unit": "TFLOP/s", "n_gpus": 1, "steps": K, "warmup": W,
+        "ms_per_step": round(t_step * 1e3, 5), "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "fp8 e4m3 x e4m3 (fp32 block scales), fp32 accumulate, bf16 out",
+        "data": "synthetic (seeded bf16 N(0,1) activations, N(0,0.02) weight), random-init",
+        "config": {"workload": "prefill FP8 GEMM 2048x4096x4096: bf16 A quantized on the fly "
+                               "(e4m3, fp32 1x128 scales), e4m3 W (fp32 128x128 scales), bf16 out",
+                   "tokens": M, "n": N, "k": KD, "parallelism": "single GPU"},
+        "tokens_per_s": round(M / t_step, 1),
+        "roofline": {"bound": "mfma", "achieved": round(achieved, 2), "peak": FP8_PEAK_TFLOPS,
+                     "unit": "TFLOP/s", "frac": round(achieved / FP8_PEAK_TFLOPS, 4),
+                     "traffic": None, "kernel": "k_gemm_fp8<true,true>",
+                     "flops_per_launch": flops, "launch_us": round(t_gemm * 1e6, 3)},
+        "step_includes": "activation quantization kernel + GEMM kernel",
+        "cpu_baseline": cpu,
+        "wall_s": round(wall, 4),
+    }
+
+
 # ------------------------------------------------------------------ main ----
 
 def main():
@@ -168,7 +272,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
-    ap.add_argument("--config", type=int, default=1, choices=[0, 1])
+    ap.add_argument("--config", type=int, default=1, choices=[0, 1, 3])
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--cpu-threads", type=int, default=0)
     ap.add_argument("--no-cpu", action="store_true")
@@ -250,6 +354,8 @@ def main():
             "cpu_baseline": cpu,
             "wall_s": round(wall, 4),
         }
+    elif args.config == 3:
+        res = bench_cfg3(args, torch, pkg, lib, stream, sp, K, W)
     else:
         ncopy = 40
         log(f"generating {ncopy} copies of a 4096x4096 FP8 matrix")

@@ -30,7 +30,7 @@ EXPORTS = (
     "dsv4_hip_register", "dsv4_hip_unregister", "dsv4_hip_device_ptr",
     "dsv4_hip_mmq_n", "dsv4_hip_mmq", "dsv4_hip_mmq_n_dev",
     "dsv4_hip_expert_forward", "dsv4_hip_moe_decode", "dsv4_hip_moe_decode_dev",
-    "dsv4_hip_status",
+    "dsv4_hip_status", "dsv4_hip_gemm_fp8_dev", "dsv4_hip_gemm_fp8q_dev",
     "dsv4_hip_dequant_dev", "dsv4_hip_quant_fp8_blk128_dev",
     "dsv4_hip_quant_fp4_mx_dev", "dsv4_hip_quant_act_fp8_1x128_dev",
     "dsv4_hip_quant_act_mxfp8_dev", "dsv4_hip_synth_normal_dev",
@@ -99,6 +99,10 @@ class Lib:
         L.dsv4_hip_moe_decode_dev.argtypes = [_P, _P, _P, _I, _P, _P, _I,
                                               C.POINTER(ExpertW), _I, _I, _F, _P]
         L.dsv4_hip_status.restype = _I; L.dsv4_hip_status.argtypes = [C.POINTER(C.c_uint)]
+        L.dsv4_hip_gemm_fp8_dev.restype = _I
+        L.dsv4_hip_gemm_fp8_dev.argtypes = [_P, _I, _P, _I, _I, C.POINTER(QMat), _P]
+        L.dsv4_hip_gemm_fp8q_dev.restype = _I
+        L.dsv4_hip_gemm_fp8q_dev.argtypes = [_P, _I, _P, _P, _I, C.POINTER(QMat), _P]
         L.dsv4_hip_dequant_dev.restype = _I
         L.dsv4_hip_dequant_dev.argtypes = [_P, C.POINTER(QMat), _P]
         for n in ("dsv4_hip_quant_fp8_blk128_dev", "dsv4_hip_quant_fp4_mx_dev",
@@ -180,6 +184,16 @@ class Lib:
                                                     idx_ptr, w_ptr, topk, sp, hidden, inter,
                                                     float(limit), stream),
                    "dsv4_hip_moe_decode_dev")
+
+    def gemm_fp8_dev(self, c_ptr, out_bf16, a_ptr, a_bf16, m, desc: QMat, stream=None):
+        self.check(self.lib.dsv4_hip_gemm_fp8_dev(c_ptr, int(bool(out_bf16)), a_ptr,
+                                                  int(bool(a_bf16)), m, C.byref(desc), stream),
+                   "dsv4_hip_gemm_fp8_dev")
+
+    def gemm_fp8q_dev(self, c_ptr, out_bf16, aq_ptr, sa_ptr, m, desc: QMat, stream=None):
+        self.check(self.lib.dsv4_hip_gemm_fp8q_dev(c_ptr, int(bool(out_bf16)), aq_ptr, sa_ptr,
+                                                   m, C.byref(desc), stream),
+                   "dsv4_hip_gemm_fp8q_dev")
 
     def dequant_dev(self, out_ptr, desc: QMat, stream=None):
         self.check(self.lib.dsv4_hip_dequant_dev(out_ptr, C.byref(desc), stream),

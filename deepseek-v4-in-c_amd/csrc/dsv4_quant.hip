@@ -224,16 +224,25 @@ hipError_t quant_fp8_blk128_launch(uint8_t *W, float *S, const float *w,
 
 /* --------------------------------------------- activation quantizers ---- */
 
-/* one wave per 1x128 group: 2 elements per lane */
+/* one wave per 1x128 group: 2 elements per lane; input fp32 or bf16 bits */
+template <bool BF16_IN>
 __global__ __launch_bounds__(256) void k_quant_act_fp8_1x128(uint8_t *Q, float *S,
-                                                            const float *a, int n, int k)
+                                                            const void *a, int n, int k)
 {
     const int lane = threadIdx.x & 63;
     const long g = (long)blockIdx.x * 4 + (threadIdx.x >> 6);
     const int ng = k / 128;
     if (g >= (long)n * ng) return;
-    const float *src = a + (size_t)g * 128;
-    const float v0 = src[2 * lane], v1 = src[2 * lane + 1];
+    float v0, v1;
+    if constexpr (BF16_IN) {
+        const uint32_t w = ((const uint32_t *)a)[(size_t)g * 64 + lane];
+        v0 = __uint_as_float(w << 16);
+        v1 = __uint_as_float(w & 0xFFFF0000u);
+    } else {
+        const float *src = (const float *)a + (size_t)g * 128;
+        v0 = src[2 * lane];
+        v1 = src[2 * lane + 1];
+    }
     float m = fmaxf(fabsf(v0), fabsf(v1));
     for (int off = 32; off > 0; off >>= 1) m = fmaxf(m, __shfl_xor(m, off));
     const float sc = m > 0.0f ? m / 448.0f : 1.0f;
@@ -242,12 +251,13 @@ __global__ __launch_bounds__(256) void k_quant_act_fp8_1x128(uint8_t *Q, float *
     *(uint16_t *)(Q + (size_t)g * 128 + 2 * lane) = (uint16_t)q;
 }
 
-hipError_t quant_act_fp8_1x128_launch(uint8_t *Q, float *S, const float *a,
-                                      int n, int k, hipStream_t st)
+hipError_t quant_act_fp8_1x128_launch(uint8_t *Q, float *S, const void *a,
+                                      int n, int k, bool bf16_in, hipStream_t st)
 {
     const long groups = (long)n * (k / 128);
-    hipLaunchKernelGGL(k_quant_act_fp8_1x128, dim3((unsigned)((groups + 3) / 4)), dim3(256), 0, st,
-                       Q, S, a, n, k);
+    const dim3 grid((unsigned)((groups + 3) / 4)), block(256);
+    if (bf16_in) hipLaunchKernelGGL(k_quant_act_fp8_1x128<true>, grid, block, 0, st, Q, S, a, n, k);
+    else hipLaunchKernelGGL(k_quant_act_fp8_1x128<false>, grid, block, 0, st, Q, S, a, n, k);
     return hipGetLastError();
 }
 

@@ -61,7 +61,7 @@ struct State {
     hipStream_t stream = nullptr;
     unsigned *status = nullptr;          /* device status word            */
     std::map<uintptr_t, Region> regions; /* host start -> resident copy   */
-    DevBuf x, y, mid, table, small, ys;
+    DevBuf x, y, mid, table, small, ys, gemm_ws;
 };
 
 State g;
@@ -294,7 +294,7 @@ void dsv4_hip_shutdown(void)
     for (auto &kv : g.regions) (void)hipFree(kv.second.dev);
     g.regions.clear();
     g.x.release(); g.y.release(); g.mid.release();
-    g.table.release(); g.small.release(); g.ys.release();
+    g.table.release(); g.small.release(); g.ys.release(); g.gemm_ws.release();
     if (g.status) (void)hipFree(g.status);
     g.status = nullptr;
     if (g.stream) (void)hipStreamDestroy(g.stream);
@@ -489,6 +489,59 @@ int dsv4_hip_moe_decode_dev(float *out, const float *x, const DSV4ExpertW *exper
                        hidden, inter, x, out, limit, (hipStream_t)stream);
 }
 
+/* Shared checks of the FP8 GEMM entry points; returns the weight format. */
+int gemm_checks(const void *C, const void *A, int M, const DSV4QMat *W, const char *what, int *fmt)
+{
+    if (!C || !A || !W || !W->w || !W->s) return fail("%s: NULL pointer", what);
+    *fmt = qmat_fmt(W);
+    if ((*fmt != FMT_FP8_E8M0 && *fmt != FMT_FP8_F32S) || W->blk_r != 128 || W->blk_c != 128)
+        return fail("%s: W must be e4m3 with 128x128 block scales", what);
+    if (M <= 0 || W->cols % 128 || W->rows % 128)
+        return fail("%s: need M > 0 and rows, cols multiples of 128 (got M %d, %d x %d)", what,
+                    M, W->rows, W->cols);
+    if (!aligned16(A) || !aligned16(W->w) || ((uintptr_t)C & 15u))
+        return fail("%s: A, C and W must be 16-byte aligned", what);
+    return 0;
+}
+
+int enqueue_gemm(void *C, int out_bf16, const uint8_t *Aq, const float *Sa, int M,
+                 const DSV4QMat *W, int fmt, hipStream_t st)
+{
+    GemmArgs ga;
+    ga.Aq = Aq; ga.Sa = Sa; ga.W = (const uint8_t *)W->w; ga.Sw = W->s; ga.C = C;
+    ga.M = M; ga.N = W->rows; ga.K = W->cols; ga.ldc = W->rows;
+    HIPCHK(gemm_fp8_launch(ga, fmt == FMT_FP8_F32S, out_bf16 != 0, st), "gemm launch");
+    return 0;
+}
+
+int dsv4_hip_gemm_fp8_dev(void *C, int out_bf16, const void *A, int a_bf16, int M,
+                          const DSV4QMat *W, void *stream)
+{
+    std::lock_guard<std::mutex> lk(g.mu);
+    if (usable()) return -1;
+    int fmt;
+    if (gemm_checks(C, A, M, W, "gemm_fp8_dev", &fmt)) return -1;
+    const int K = W->cols;
+    const size_t qbytes = ((size_t)M * K + 255) & ~(size_t)255;
+    HIPCHK(g.gemm_ws.need(qbytes + (size_t)M * (K / 128) * 4), "gemm workspace");
+    uint8_t *Aq = (uint8_t *)g.gemm_ws.p;
+    float *Sa = (float *)(Aq + qbytes);
+    hipStream_t st = (hipStream_t)stream;
+    HIPCHK(quant_act_fp8_1x128_launch(Aq, Sa, A, M, K, a_bf16 != 0, st), "activation quant launch");
+    return enqueue_gemm(C, out_bf16, Aq, Sa, M, W, fmt, st);
+}
+
+int dsv4_hip_gemm_fp8q_dev(void *C, int out_bf16, const uint8_t *Aq, const float *Sa,
+                           int M, const DSV4QMat *W, void *stream)
+{
+    std::lock_guard<std::mutex> lk(g.mu);
+    if (usable()) return -1;
+    int fmt;
+    if (gemm_checks(C, Aq, M, W, "gemm_fp8q_dev", &fmt)) return -1;
+    if (!Sa) return fail("gemm_fp8q_dev: NULL scales");
+    return enqueue_gemm(C, out_bf16, Aq, Sa, M, W, fmt, (hipStream_t)stream);
+}
+
 int dsv4_hip_status(unsigned *bits)
 {
     std::lock_guard<std::mutex> lk(g.mu);
@@ -545,7 +598,7 @@ int dsv4_hip_quant_act_fp8_1x128_dev(uint8_t *Q, float *S, const float *a, int n
     if (!Q || !S || !a || n <= 0 || k <= 0 || k % 128)
         return fail("quant_act_fp8_1x128_dev: bad argument");
     if (((uintptr_t)Q & 1u) != 0) return fail("quant_act_fp8_1x128_dev: Q must be 2-byte aligned");
-    HIPCHK(quant_act_fp8_1x128_launch(Q, S, a, n, k, (hipStream_t)stream), "quant launch");
+    HIPCHK(quant_act_fp8_1x128_launch(Q, S, a, n, k, false, (hipStream_t)stream), "quant launch");
     return 0;
 }
 

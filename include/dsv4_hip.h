@@ -133,6 +133,26 @@ int  dsv4_hip_moe_decode_dev(float *out, const float *x,
                              const DSV4ExpertW *shared, int hidden, int inter,
                              float limit, void *stream);
 
+/* ------------------------------------------------ prefill GEMM (a16, a17) --
+ * C[m][n] = sum_k A[m][k] * W[n][k] for m < M on CDNA4 FP8 MFMA, replacing the
+ * GPU leg of the prefill projection seam, dsv4_prefill_vk_gemm
+ * (src/80_prefill/dsv4_prefill_vk.h:37-41; seam src/80_prefill/dsv4_prefill_proj.c:17-27).
+ * W: DSV4_WFP8 (E8M0) or DSV4_WFP8_F32S with 128 x 128 blocks, rows and cols
+ * multiples of 128, device pointers. A [M][W->cols] fp32 (a_bf16 = 0) or bf16
+ * (a_bf16 = 1), device, quantized on the fly to e4m3 with one fp32 scale per
+ * 1 x 128 group (groupmax / 448) into a library-owned workspace. C [M][W->rows]
+ * fp32 (out_bf16 = 0) or bf16 (out_bf16 = 1, round to nearest even). All
+ * pointers 16-byte aligned. Enqueued on `stream`. 0 enqueued, -1 otherwise. */
+int  dsv4_hip_gemm_fp8_dev(void *C, int out_bf16, const void *A, int a_bf16,
+                           int M, const DSV4QMat *W, void *stream);
+
+/* The same GEMM on activations the caller already quantized:
+ * Aq [M][W->cols] e4m3, Sa [M][W->cols / 128] fp32 (as produced by
+ * dsv4_hip_quant_act_fp8_1x128_dev). No workspace. */
+int  dsv4_hip_gemm_fp8q_dev(void *C, int out_bf16, const uint8_t *Aq,
+                            const float *Sa, int M, const DSV4QMat *W,
+                            void *stream);
+
 /* Read and clear the device status word that the _dev kernels raise when a
  * routing id is out of range (bit 0) or an expert descriptor in the device
  * table does not match the expected format and geometry (bit 1); the affected

@@ -1,0 +1,151 @@
+# SPDX-License-Identifier: Apache-2.0
+"""GPU parity for the prefill GEMM (dsv4_hip_gemm_fp8_dev / _fp8q_dev).
+
+The oracle is the reference's fp8_n restated (oracle/dsv4_oracle.c, nt > 1
+body of src/10_compute/dsv4_matmul_fp8.c:102-155) run on the activations the
+GPU multiplies: quantized with the same 1x128 e4m3 rule and dequantized with
+one fp32 multiply (q * s). Tolerance: relative L2 1e-3 on fp32 output; bf16
+output is compared with bf16(oracle) at the same bound."""
+import numpy as np
+import pytest
+import torch
+
+from conftest import REL_L2_TOL, bits, max_abs, rel_l2
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda:0"
+
+
+def dev(a, dtype=None):
+    t = torch.from_numpy(np.ascontiguousarray(a))
+    return t.to(DEV)
+
+
+def e4m3_table(oracle):
+    return np.array([oracle.e4m3(b) for b in range(256)], np.float32)
+
+
+def dequant_act(oracle, Q, S, m, k):
+    vals = e4m3_table(oracle)[Q].reshape(m, k)
+    return (vals * np.repeat(S.reshape(m, k // 128), 128, axis=1)).astype(np.float32)
+
+
+def make_weight(oracle, rng, n, k, f32s=True):
+    w = (rng.standard_normal((n, k)) * 0.02).astype(np.float32)
+    W, S = oracle.quant_fp8_blk128(w)
+    if not f32s:
+        # E8M0 scales: the power of two at or above each fp32 block scale
+        S = np.clip(np.ceil(np.log2(S)) + 127, 0, 254).astype(np.uint8)
+    return W, S
+
+
+def bf16_round(a):
+    return torch.from_numpy(np.ascontiguousarray(a, np.float32)).bfloat16().float().numpy()
+
+
+def run_gemm(lib, pkg, A, W, S, n, k, f32s, out_bf16, a_bf16):
+    m = A.shape[0]
+    dW, dS = dev(W), dev(S)
+    wdt = pkg.DSV4_WFP8_F32S if f32s else pkg.DSV4_WFP8
+    desc = pkg.qmat(wdt, dW.data_ptr(), dS.data_ptr(), n, k, 128, 128)
+    if a_bf16:
+        dA = torch.from_numpy(A).to(DEV).bfloat16()
+    else:
+        dA = dev(A.astype(np.float32))
+    C = torch.empty((m, n), dtype=torch.bfloat16 if out_bf16 else torch.float32, device=DEV)
+    lib.gemm_fp8_dev(C.data_ptr(), out_bf16, dA.data_ptr(), a_bf16, m, desc)
+    torch.cuda.synchronize()
+    return C.float().cpu().numpy()
+
+
+def oracle_gemm(oracle, A, W, S, n, k, f32s):
+    m = A.shape[0]
+    Q, Sa = oracle.quant_act_fp8_1x128(A)
+    x = dequant_act(oracle, Q, Sa, m, k).reshape(-1)
+    if f32s:
+        return oracle.fp8f_n(W, S, x, n, k, 128, 128, m).reshape(m, n)
+    return oracle.fp8_n(W, S, x, n, k, 128, 128, m).reshape(m, n)
+
+
+@pytest.mark.parametrize("m,n,k,f32s", [
+    (256, 512, 1024, True), (200, 384, 512, True), (8, 256, 256, True),
+    (130, 640, 768, False), (1, 128, 128, True)])
+def test_gemm_fp32_out(lib, pkg, oracle, m, n, k, f32s):
+    rng = np.random.default_rng(m * 31 + n + k)
+    A = bf16_round(rng.standard_normal((m, k)).astype(np.float32))
+    W, S = make_weight(oracle, rng, n, k, f32s)
+    got = run_gemm(lib, pkg, A, W, S, n, k, f32s, out_bf16=0, a_bf16=0)
+    want = oracle_gemm(oracle, A, W, S, n, k, f32s)
+    e = rel_l2(got, want)
+    assert np.all(np.isfinite(got))
+    assert e <= REL_L2_TOL, f"rel L2 {e:.3e} (max abs {max_abs(got, want):.3e})"
+
+
+def test_gemm_bf16_in_equals_fp32_in(lib, pkg, oracle):
+    rng = np.random.default_rng(5)
+    m, n, k = 160, 256, 512
+    A = bf16_round(rng.standard_normal((m, k)).astype(np.float32))
+    W, S = make_weight(oracle, rng, n, k)
+    a = run_gemm(lib, pkg, A, W, S, n, k, True, out_bf16=0, a_bf16=0)
+    b = run_gemm(lib, pkg, A, W, S, n, k, True, out_bf16=0, a_bf16=1)
+    assert np.array_equal(bits(a), bits(b))
+
+
+def test_gemm_bf16_out(lib, pkg, oracle):
+    rng = np.random.default_rng(6)
+    m, n, k = 128, 512, 1024
+    A = bf16_round(rng.standard_normal((m, k)).astype(np.float32))
+    W, S = make_weight(oracle, rng, n, k)
+    got = run_gemm(lib, pkg, A, W, S, n, k, True, out_bf16=1, a_bf16=1)
+    want = bf16_round(oracle_gemm(oracle, A, W, S, n, k, True))
+    assert rel_l2(got, want) <= REL_L2_TOL
+
+
+def test_gemm_config_shape_row_sample(lib, pkg, oracle):
+    """2048 tokens x 4096 x 4096 (bf16 A, fp32 128x128 weight scales, bf16
+    output) on the GPU; 24 seeded rows checked against the oracle (rows are
+    independent: each token is quantized and multiplied on its own)."""
+    rng = np.random.default_rng(3)
+    m, n, k = 2048, 4096, 4096
+    A = bf16_round(rng.standard_normal((m, k)).astype(np.float32))
+    W, S = make_weight(oracle, rng, n, k)
+    got = run_gemm(lib, pkg, A, W, S, n, k, True, out_bf16=1, a_bf16=1)
+    rows = np.sort(rng.choice(m, 24, replace=False))
+    want = bf16_round(oracle_gemm(oracle, np.ascontiguousarray(A[rows]), W, S, n, k, True))
+    assert np.all(np.isfinite(got))
+    assert rel_l2(got[rows], want) <= REL_L2_TOL
+
+
+def test_gemm_prequantized_matches_fused(lib, pkg, oracle):
+    rng = np.random.default_rng(8)
+    m, n, k = 96, 256, 384
+    A = bf16_round(rng.standard_normal((m, k)).astype(np.float32))
+    W, S = make_weight(oracle, rng, n, k)
+    fused = run_gemm(lib, pkg, A, W, S, n, k, True, out_bf16=0, a_bf16=0)
+    Q, Sa = oracle.quant_act_fp8_1x128(A)
+    dW, dS, dQ, dSa = dev(W), dev(S), dev(Q), dev(Sa)
+    desc = pkg.qmat(pkg.DSV4_WFP8_F32S, dW.data_ptr(), dS.data_ptr(), n, k, 128, 128)
+    C = torch.empty((m, n), dtype=torch.float32, device=DEV)
+    lib.gemm_fp8q_dev(C.data_ptr(), 0, dQ.data_ptr(), dSa.data_ptr(), m, desc)
+    torch.cuda.synchronize()
+    assert np.array_equal(bits(C.cpu().numpy()), bits(fused))
+
+
+def test_gemm_deterministic(lib, pkg, oracle):
+    rng = np.random.default_rng(9)
+    m, n, k = 256, 512, 512
+    A = bf16_round(rng.standard_normal((m, k)).astype(np.float32))
+    W, S = make_weight(oracle, rng, n, k)
+    a = run_gemm(lib, pkg, A, W, S, n, k, True, 0, 0)
+    b = run_gemm(lib, pkg, A, W, S, n, k, True, 0, 0)
+    assert np.array_equal(bits(a), bits(b))
+
+
+def test_gemm_rejects_bad_geometry(lib, pkg):
+    W = torch.zeros(100 * 128, dtype=torch.uint8, device=DEV)
+    S = torch.zeros(4, dtype=torch.float32, device=DEV)
+    A = torch.zeros(128, dtype=torch.float32, device=DEV)
+    C = torch.zeros(100, dtype=torch.float32, device=DEV)
+    desc = pkg.qmat(pkg.DSV4_WFP8_F32S, W.data_ptr(), S.data_ptr(), 100, 128, 128, 128)
+    rc = lib.lib.dsv4_hip_gemm_fp8_dev(C.data_ptr(), 0, A.data_ptr(), 0, 1, desc, None)
+    assert rc == -1 and "multiples of 128" in lib.error()
