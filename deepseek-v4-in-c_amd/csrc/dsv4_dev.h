@@ -152,6 +152,12 @@ __device__ __forceinline__ int wave_id()
     return __builtin_amdgcn_readfirstlane((int)(blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6)));
 }
 
+/* The index of the calling wave within its workgroup, provably wave-uniform. */
+__device__ __forceinline__ int wave_in_group()
+{
+    return __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+}
+
 /* Weight chunk loads, marked non-temporal: each weight byte is read exactly
  * once per call. */
 __device__ __forceinline__ u32x4 ld_stream16(const void *p)

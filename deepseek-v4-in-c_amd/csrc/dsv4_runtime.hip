@@ -597,7 +597,8 @@ int dsv4_hip_quant_act_fp8_1x128_dev(uint8_t *Q, float *S, const float *a, int n
     if (usable()) return -1;
     if (!Q || !S || !a || n <= 0 || k <= 0 || k % 128)
         return fail("quant_act_fp8_1x128_dev: bad argument");
-    if (((uintptr_t)Q & 1u) != 0) return fail("quant_act_fp8_1x128_dev: Q must be 2-byte aligned");
+    if (((uintptr_t)Q & 7u) != 0 || ((uintptr_t)a & 15u) != 0 || ((uintptr_t)S & 3u) != 0)
+        return fail("quant_act_fp8_1x128_dev: need Q 8-, a 16- and S 4-byte aligned");
     HIPCHK(quant_act_fp8_1x128_launch(Q, S, a, n, k, false, (hipStream_t)stream), "quant launch");
     return 0;
 }

@@ -149,3 +149,34 @@ def test_gemm_rejects_bad_geometry(lib, pkg):
     desc = pkg.qmat(pkg.DSV4_WFP8_F32S, W.data_ptr(), S.data_ptr(), 100, 128, 128, 128)
     rc = lib.lib.dsv4_hip_gemm_fp8_dev(C.data_ptr(), 0, A.data_ptr(), 0, 1, desc, None)
     assert rc == -1 and "multiples of 128" in lib.error()
+
+
+def test_act_quant_1x128_edge_cases(lib, pkg, oracle):
+    """Bit-exact against the oracle on values the fast path must get right:
+    magnitudes from e4m3's subnormal range to its maximum, exact
+    round-to-nearest-even ties (amax 448 makes the scale exactly 1), signed
+    zeros, an all-zero group and a NaN (ignored by the group max, encoded as
+    sign | 0x7F)."""
+    rng = np.random.default_rng(17)
+    n, k = 12, 512
+    a = (rng.standard_normal((n, k)) * np.exp(rng.uniform(-30, 30, (n, k)))).astype(np.float32)
+    a[0, :] = 0.0
+    a[0, 5] = -0.0
+    a[1, :128] = 0.0
+    ties = np.array([1.0625, 1.1875, 0.015625 * 1.5, 0.001953125 * 2.5, 240.0 + 8.0, 416.0 + 16.0,
+                     -1.0625, -0.0029296875], np.float32)
+    a[2, :8] = ties
+    a[2, 8] = 448.0
+    a[3, 200] = np.float32("nan")
+    a[4, :] = (rng.standard_normal(k) * 1e-3).astype(np.float32)
+    a[5, :] = np.float32(3.0e38) * np.sign(rng.standard_normal(k)).astype(np.float32)
+    da = dev(a)
+    Q = torch.empty(n * k, dtype=torch.uint8, device=DEV)
+    S = torch.empty(n * (k // 128), dtype=torch.float32, device=DEV)
+    lib.quant_act_fp8_1x128_dev(Q.data_ptr(), S.data_ptr(), da.data_ptr(), n, k)
+    torch.cuda.synchronize()
+    Qo, So = oracle.quant_act_fp8_1x128(a)
+    got_q, got_s = Q.cpu().numpy(), S.cpu().numpy()
+    assert np.array_equal(bits(got_s), bits(So))
+    bad = np.nonzero(got_q != Qo)[0]
+    assert bad.size == 0, f"{bad.size} codes differ, first at {bad[:4]}: {got_q[bad[:4]]} vs {Qo[bad[:4]]}"
