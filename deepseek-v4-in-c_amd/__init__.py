@@ -30,6 +30,7 @@ EXPORTS = (
     "dsv4_hip_register", "dsv4_hip_unregister", "dsv4_hip_device_ptr",
     "dsv4_hip_mmq_n", "dsv4_hip_mmq", "dsv4_hip_mmq_n_dev",
     "dsv4_hip_expert_forward", "dsv4_hip_moe_decode", "dsv4_hip_moe_decode_dev",
+    "dsv4_hip_moe_grouped", "dsv4_hip_moe_grouped_dev",
     "dsv4_hip_status", "dsv4_hip_gemm_fp8_dev", "dsv4_hip_gemm_fp8q_dev",
     "dsv4_hip_dequant_dev", "dsv4_hip_quant_fp8_blk128_dev",
     "dsv4_hip_quant_fp4_mx_dev", "dsv4_hip_quant_act_fp8_1x128_dev",
@@ -98,6 +99,12 @@ class Lib:
         L.dsv4_hip_moe_decode_dev.restype = _I
         L.dsv4_hip_moe_decode_dev.argtypes = [_P, _P, _P, _I, _P, _P, _I,
                                               C.POINTER(ExpertW), _I, _I, _F, _P]
+        L.dsv4_hip_moe_grouped.restype = _I
+        L.dsv4_hip_moe_grouped.argtypes = [_P, _P, _I, _P, _P, _I, C.POINTER(ExpertW), _I,
+                                           C.POINTER(ExpertW), _F]
+        L.dsv4_hip_moe_grouped_dev.restype = _I
+        L.dsv4_hip_moe_grouped_dev.argtypes = [_P, _P, _I, _P, _I, _P, _P, _I,
+                                               C.POINTER(ExpertW), _I, _I, _F, _P]
         L.dsv4_hip_status.restype = _I; L.dsv4_hip_status.argtypes = [C.POINTER(C.c_uint)]
         L.dsv4_hip_gemm_fp8_dev.restype = _I
         L.dsv4_hip_gemm_fp8_dev.argtypes = [_P, _I, _P, _I, _I, C.POINTER(QMat), _P]
@@ -172,6 +179,22 @@ class Lib:
                    "dsv4_hip_moe_decode")
         return out
 
+    def moe_grouped(self, experts, idx, w, x, shared=None, limit=10.0) -> np.ndarray:
+        """experts: list of ExpertW (host pointers inside registered ranges);
+        idx, w: [n][topk]; x: [n][hidden] fp32. Returns out [n][hidden]."""
+        idx = np.ascontiguousarray(idx, np.int32)
+        w = np.ascontiguousarray(w, np.float32)
+        x = np.ascontiguousarray(x, np.float32)
+        n, topk = idx.shape
+        arr = (ExpertW * len(experts))(*experts)
+        out = np.zeros((n, experts[0].w1.cols), np.float32)
+        sp = C.pointer(shared) if shared is not None else None
+        self.check(self.lib.dsv4_hip_moe_grouped(out.ctypes.data, x.ctypes.data, n,
+                                                 idx.ctypes.data, w.ctypes.data, topk, arr,
+                                                 len(experts), sp, float(limit)),
+                   "dsv4_hip_moe_grouped")
+        return out
+
     # ---------------------------------------------------------- _dev entry points
     def mmq_n_dev(self, y_ptr, x_ptr, desc: QMat, nt, stream=None):
         self.check(self.lib.dsv4_hip_mmq_n_dev(y_ptr, x_ptr, C.byref(desc), nt, stream),
@@ -184,6 +207,14 @@ class Lib:
                                                     idx_ptr, w_ptr, topk, sp, hidden, inter,
                                                     float(limit), stream),
                    "dsv4_hip_moe_decode_dev")
+
+    def moe_grouped_dev(self, out_ptr, x_ptr, n, table_ptr, n_experts, idx_ptr, w_ptr, topk,
+                        shared: ExpertW | None, hidden, inter, limit, stream=None):
+        sp = C.pointer(shared) if shared is not None else None
+        self.check(self.lib.dsv4_hip_moe_grouped_dev(out_ptr, x_ptr, n, table_ptr, n_experts,
+                                                     idx_ptr, w_ptr, topk, sp, hidden, inter,
+                                                     float(limit), stream),
+                   "dsv4_hip_moe_grouped_dev")
 
     def gemm_fp8_dev(self, c_ptr, out_bf16, a_ptr, a_bf16, m, desc: QMat, stream=None):
         self.check(self.lib.dsv4_hip_gemm_fp8_dev(c_ptr, int(bool(out_bf16)), a_ptr,

@@ -24,6 +24,9 @@ enum {
 enum {
     ST_BAD_EXPERT_ID = 1u << 0,   /* routing index outside [0, n_experts)   */
     ST_BAD_DESCRIPTOR = 1u << 1,  /* expert descriptor of the wrong format  */
+    ST_SCALE_RANGE = 1u << 2,     /* FP4 E8M0 scale byte outside 104..140:
+                                     the grouped path's fp16 decode is not
+                                     exact for that block                   */
 };
 
 /* Map a descriptor to the kernel format, or -1 when the GPU path does not
@@ -139,6 +142,53 @@ hipError_t quant_act_mxfp8_launch(uint8_t *Q, uint8_t *S, const float *a,
                                   int n, int k, hipStream_t st);
 hipError_t synth_normal_launch(float *out, size_t n, uint64_t seed, float sigma,
                                int round_bf16, hipStream_t st);
+
+/* ------------------------------------------------------ grouped MoE --- */
+
+/* counting sort of the npairs = n * topk routing ids by expert */
+struct RouteArgs {
+    const int *idx;           /* device [npairs]                          */
+    int npairs, topk, n_experts;
+    int tile_rows;            /* rows per tile of the grouped GEMM        */
+    int *grp_off;             /* [n_experts + 1] first row of each bucket */
+    int *tile_pre;            /* [n_experts + 1] prefix of tiles          */
+    int *pos;                 /* [npairs] row of each pair (-1: bad id)   */
+    int *row_tok;             /* [npairs] token of each row               */
+    unsigned *status;
+};
+hipError_t moe_route_launch(const RouteArgs &a, hipStream_t st);
+
+/* o[i] = fp16(x[i]), n % 8 == 0 */
+hipError_t to_f16_launch(uint16_t *o, const float *x, size_t n, hipStream_t st);
+
+/* out[row][f] for row-groups of one expert each: gate/up with SwiGLU (fp16
+ * out, uses w1 and w3) or down (fp32 out). table == NULL: one group, the
+ * rows 0..nrows-1, matrices m1 (and m3). */
+struct GroupedArgs {
+    const DSV4ExpertW *table;
+    int n_experts;
+    const int *grp_off, *tile_pre;
+    const int *row_tok;       /* B row of each output row, NULL = itself  */
+    DSV4QMat m1, m3;
+    int nrows;
+    const uint16_t *B;        /* fp16 [.][K]                              */
+    int K, N;
+    void *out;                /* [rows][N]                                */
+    float limit;
+    unsigned *status;
+};
+int grouped_rows_per_tile(int tt);
+hipError_t grouped_launch(int fmt, bool swiglu, int tt, const GroupedArgs &a, long max_tiles,
+                          hipStream_t st);
+
+/* out[t] = sum_k w[t][k] * Y[pos[t][k]] (k order) + YS[t] */
+struct CombineArgs {
+    float *out;
+    const float *Y, *YS, *w;
+    const int *pos;
+    int n, topk, hidden;
+};
+hipError_t moe_combine_launch(const CombineArgs &a, hipStream_t st);
 
 } // namespace dsv4
 

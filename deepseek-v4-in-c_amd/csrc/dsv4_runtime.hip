@@ -15,6 +15,7 @@
 #include <map>
 #include <mutex>
 #include <string>
+#include <vector>
 
 #include <stdarg.h>
 #include <stdio.h>
@@ -61,7 +62,7 @@ struct State {
     hipStream_t stream = nullptr;
     unsigned *status = nullptr;          /* device status word            */
     std::map<uintptr_t, Region> regions; /* host start -> resident copy   */
-    DevBuf x, y, mid, table, small, ys, gemm_ws;
+    DevBuf x, y, mid, table, small, ys, gemm_ws, moe_ws;
 };
 
 State g;
@@ -295,6 +296,7 @@ void dsv4_hip_shutdown(void)
     g.regions.clear();
     g.x.release(); g.y.release(); g.mid.release();
     g.table.release(); g.small.release(); g.ys.release(); g.gemm_ws.release();
+    g.moe_ws.release();
     if (g.status) (void)hipFree(g.status);
     g.status = nullptr;
     if (g.stream) (void)hipStreamDestroy(g.stream);
@@ -540,6 +542,170 @@ int dsv4_hip_gemm_fp8q_dev(void *C, int out_bf16, const uint8_t *Aq, const float
     if (gemm_checks(C, Aq, M, W, "gemm_fp8q_dev", &fmt)) return -1;
     if (!Sa) return fail("gemm_fp8q_dev: NULL scales");
     return enqueue_gemm(C, out_bf16, Aq, Sa, M, W, fmt, (hipStream_t)stream);
+}
+
+/* ------------------------------------------------------ grouped MoE --- */
+
+/* 16-row tiles when buckets are small (batched decode: few tokens per expert,
+ * weight streaming dominates and occupancy matters), 64-row tiles otherwise
+ * (prefill: weights are reused across a tile's rows). */
+int grouped_tt(long pairs) { return pairs <= 4096 ? 1 : 4; }
+
+int enqueue_moe_grouped(float *out, const float *x, int n, const DSV4ExpertW *table,
+                        int n_experts, const int *idx, const float *w, int topk,
+                        const DSV4ExpertW *shared, int sfmt, int sinter, int hidden,
+                        int inter, float limit, hipStream_t st)
+{
+    const long P = (long)n * topk;
+    const int tt = grouped_tt(P);
+    const int trows = grouped_rows_per_tile(tt);
+    size_t off = 0;
+    auto take = [&](size_t b) { const size_t o = off; off += (b + 255) & ~(size_t)255; return o; };
+    const size_t o_grp = take((size_t)(n_experts + 1) * 4), o_tp = take((size_t)(n_experts + 1) * 4);
+    const size_t o_pos = take((size_t)P * 4), o_row = take((size_t)P * 4);
+    const size_t o_x16 = take((size_t)n * hidden * 2), o_mid = take((size_t)P * inter * 2);
+    const size_t o_y = take((size_t)P * hidden * 4);
+    size_t o_smid = 0, o_ys = 0;
+    if (shared) {
+        o_smid = take((size_t)n * sinter * 2);
+        o_ys = take((size_t)n * hidden * 4);
+    }
+    HIPCHK(g.moe_ws.need(off), "grouped MoE workspace");
+    uint8_t *ws = (uint8_t *)g.moe_ws.p;
+    int *grp = (int *)(ws + o_grp), *tp = (int *)(ws + o_tp);
+    int *pos = (int *)(ws + o_pos), *row = (int *)(ws + o_row);
+    uint16_t *x16 = (uint16_t *)(ws + o_x16), *mid = (uint16_t *)(ws + o_mid);
+    float *y = (float *)(ws + o_y);
+
+    RouteArgs ra;
+    ra.idx = idx; ra.npairs = (int)P; ra.topk = topk; ra.n_experts = n_experts;
+    ra.tile_rows = trows; ra.grp_off = grp; ra.tile_pre = tp; ra.pos = pos; ra.row_tok = row;
+    ra.status = g.status;
+    HIPCHK(moe_route_launch(ra, st), "route launch");
+    HIPCHK(to_f16_launch(x16, x, (size_t)n * hidden, st), "x fp16 launch");
+
+    /* every bucket adds at most one partial tile */
+    const long max_tiles = (P + trows - 1) / trows + n_experts;
+    GroupedArgs ga;
+    memset(&ga, 0, sizeof ga);
+    ga.table = table; ga.n_experts = n_experts; ga.grp_off = grp; ga.tile_pre = tp;
+    ga.row_tok = row; ga.B = x16; ga.K = hidden; ga.N = inter; ga.out = mid;
+    ga.limit = limit; ga.status = g.status;
+    HIPCHK(grouped_launch(FMT_FP4_E8M0, true, tt, ga, max_tiles, st), "routed gate/up launch");
+    ga.row_tok = nullptr; ga.B = mid; ga.K = inter; ga.N = hidden; ga.out = y;
+    HIPCHK(grouped_launch(FMT_FP4_E8M0, false, tt, ga, max_tiles, st), "routed down launch");
+
+    float *ys = nullptr;
+    if (shared) {
+        uint16_t *smid = (uint16_t *)(ws + o_smid);
+        ys = (float *)(ws + o_ys);
+        const int stt = n <= 16 ? 1 : 4;
+        const long stiles = (n + grouped_rows_per_tile(stt) - 1) / grouped_rows_per_tile(stt);
+        GroupedArgs sa;
+        memset(&sa, 0, sizeof sa);
+        sa.m1 = shared->w1; sa.m3 = shared->w3; sa.nrows = n; sa.B = x16;
+        sa.K = hidden; sa.N = sinter; sa.out = smid; sa.limit = limit; sa.status = g.status;
+        HIPCHK(grouped_launch(sfmt, true, stt, sa, stiles, st), "shared gate/up launch");
+        sa.m1 = shared->w2; sa.B = smid; sa.K = sinter; sa.N = hidden; sa.out = ys;
+        HIPCHK(grouped_launch(sfmt, false, stt, sa, stiles, st), "shared down launch");
+    }
+    CombineArgs ca;
+    ca.out = out; ca.Y = y; ca.YS = ys; ca.w = w; ca.pos = pos;
+    ca.n = n; ca.topk = topk; ca.hidden = hidden;
+    HIPCHK(moe_combine_launch(ca, st), "combine launch");
+    return 0;
+}
+
+/* Checks shared by both grouped entry points; returns the shared format. */
+int grouped_checks(int n, int topk, int n_experts, int hidden, int inter,
+                   const DSV4ExpertW *shared, int *sfmt, int *sinter, const char *what)
+{
+    if (n < 1) return fail("%s: n %d < 1", what, n);
+    if (topk < 1 || topk > 16) return fail("%s: topk %d outside 1..16", what, topk);
+    if (n_experts < 1 || n_experts > 1024) return fail("%s: n_experts %d outside 1..1024", what, n_experts);
+    if (hidden <= 0 || inter <= 0 || hidden % 128 || inter % 128)
+        return fail("%s: hidden %d and inter %d must be multiples of 128", what, hidden, inter);
+    if ((long)n * topk > (1L << 26)) return fail("%s: %d x %d pairs is too many", what, n, topk);
+    *sfmt = -1;
+    *sinter = 0;
+    if (shared) {
+        int sh;
+        if (expert_geometry(shared, sfmt, sinter, &sh, what)) return -1;
+        if (sh != hidden) return fail("%s: shared hidden %d != %d", what, sh, hidden);
+        if (*sinter % 128) return fail("%s: shared inter %d is not a multiple of 128", what, *sinter);
+        if (*sfmt == FMT_FP8_E8M0 || *sfmt == FMT_FP8_F32S) {
+            if (shared->w1.blk_r != 128 || shared->w3.blk_r != 128 || shared->w2.blk_r != 128)
+                return fail("%s: shared FP8 needs 128x128 scale blocks", what);
+        } else if (shared->w1.blk_r != 1 || shared->w3.blk_r != 1 || shared->w2.blk_r != 1) {
+            return fail("%s: shared FP4 needs 1x32 scale blocks", what);
+        }
+        const DSV4QMat *ms[3] = {&shared->w1, &shared->w3, &shared->w2};
+        for (int i = 0; i < 3; i++)
+            if (!aligned16(ms[i]->w) || ((uintptr_t)ms[i]->s & 3u))
+                return fail("%s: shared weights must be 16-byte and scales 4-byte aligned", what);
+    }
+    return 0;
+}
+
+int dsv4_hip_moe_grouped_dev(float *out, const float *x, int n, const DSV4ExpertW *experts,
+                             int n_experts, const int *idx, const float *w, int topk,
+                             const DSV4ExpertW *shared, int hidden, int inter, float limit,
+                             void *stream)
+{
+    std::lock_guard<std::mutex> lk(g.mu);
+    if (usable()) return -1;
+    if (!out || !x || !experts || !idx || !w) return fail("moe_grouped_dev: NULL pointer");
+    int sfmt, sinter;
+    if (grouped_checks(n, topk, n_experts, hidden, inter, shared, &sfmt, &sinter, "moe_grouped_dev"))
+        return -1;
+    if (!aligned16(x) || !aligned16(out)) return fail("moe_grouped_dev: x and out must be 16-byte aligned");
+    return enqueue_moe_grouped(out, x, n, experts, n_experts, idx, w, topk, shared, sfmt, sinter,
+                               hidden, inter, limit, (hipStream_t)stream);
+}
+
+int dsv4_hip_moe_grouped(float *out, const float *x, int n, const int *topk_idx,
+                         const float *topk_w, int topk, const DSV4ExpertW *experts,
+                         int n_experts, const DSV4ExpertW *shared, float limit)
+{
+    std::lock_guard<std::mutex> lk(g.mu);
+    if (usable()) return -1;
+    if (!out || !x || !topk_idx || !topk_w || !experts) return fail("moe_grouped: NULL pointer");
+    if (n_experts < 1 || n_experts > 1024) return fail("moe_grouped: n_experts %d outside 1..1024", n_experts);
+    std::vector<DSV4ExpertW> tab((size_t)n_experts);
+    int inter = 0, hidden = 0;
+    for (int e = 0; e < n_experts; e++) {
+        int fmt, ei, eh;
+        if (expert_geometry(&experts[e], &fmt, &ei, &eh, "moe_grouped routed")) return -1;
+        if (fmt != FMT_FP4_E8M0 || experts[e].w1.blk_r != 1)
+            return fail("moe_grouped: routed expert %d is not FP4 with 1x32 scales", e);
+        if (e == 0) { inter = ei; hidden = eh; }
+        else if (ei != inter || eh != hidden) return fail("moe_grouped: routed shapes differ (expert %d)", e);
+        if (resident_expert(&experts[e], &tab[(size_t)e], "moe_grouped routed")) return -1;
+    }
+    DSV4ExpertW sdev;
+    int sfmt, sinter;
+    if (shared && resident_expert(shared, &sdev, "moe_grouped shared")) return -1;
+    if (grouped_checks(n, topk, n_experts, hidden, inter, shared ? &sdev : nullptr, &sfmt, &sinter,
+                       "moe_grouped"))
+        return -1;
+    const size_t P = (size_t)n * topk;
+    const size_t tb = ((size_t)n_experts * sizeof(DSV4ExpertW) + 255) & ~(size_t)255;
+    const size_t ib = (P * 4 + 255) & ~(size_t)255;
+    HIPCHK(g.table.need(tb + 2 * ib), "table alloc");
+    HIPCHK(g.x.need((size_t)n * hidden * 4), "x staging");
+    HIPCHK(g.y.need((size_t)n * hidden * 4), "out staging");
+    uint8_t *tp = (uint8_t *)g.table.p;
+    HIPCHK(hipMemcpyAsync(tp, tab.data(), (size_t)n_experts * sizeof(DSV4ExpertW), hipMemcpyHostToDevice, g.stream), "table upload");
+    HIPCHK(hipMemcpyAsync(tp + tb, topk_idx, P * 4, hipMemcpyHostToDevice, g.stream), "routing upload");
+    HIPCHK(hipMemcpyAsync(tp + tb + ib, topk_w, P * 4, hipMemcpyHostToDevice, g.stream), "weights upload");
+    HIPCHK(hipMemcpyAsync(g.x.p, x, (size_t)n * hidden * 4, hipMemcpyHostToDevice, g.stream), "x upload");
+    if (enqueue_moe_grouped((float *)g.y.p, (const float *)g.x.p, n, (const DSV4ExpertW *)tp,
+                            n_experts, (const int *)(tp + tb), (const float *)(tp + tb + ib), topk,
+                            shared ? &sdev : nullptr, sfmt, sinter, hidden, inter, limit, g.stream))
+        return -1;
+    HIPCHK(hipMemcpyAsync(out, g.y.p, (size_t)n * hidden * 4, hipMemcpyDeviceToHost, g.stream), "out download");
+    HIPCHK(hipStreamSynchronize(g.stream), "grouped sync");
+    return 0;
 }
 
 int dsv4_hip_status(unsigned *bits)

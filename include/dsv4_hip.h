@@ -133,6 +133,40 @@ int  dsv4_hip_moe_decode_dev(float *out, const float *x,
                              const DSV4ExpertW *shared, int hidden, int inter,
                              float limit, void *stream);
 
+/* ------------------------------------- grouped MoE (a13-a15, a18) ---------
+ * For n tokens (batched decode or a prefill block):
+ *   out[t] = sum_{k in 0..topk-1, in k order} w[t][k] * expert_{idx[t][k]}(x[t])
+ *            + shared(x[t])            (shared may be NULL; added unweighted)
+ * with expert(x) = w2 . swiglu(w1 . x, w3 . x) as in dsv4_expert_forward.
+ * Replaces the reference's prefill union path: the permutation of (token, k)
+ * pairs by expert (src/80_prefill/dsv4_prefill_union.c:30-66), the per-expert
+ * bucket GEMMs (src/80_prefill/dsv4_prefill_experts.c:23-77 and its Vulkan
+ * leg src/80_prefill/dsv4_prefill_vk_expert.c:45-172) and the combine
+ * (src/80_prefill/dsv4_prefill_union_run.c:109-121); the CPU/GPU bucket
+ * scheduler is replaced by one device pass over every bucket.
+ * Routed experts: DSV4_WFP4 with 1x32 E8M0 scales, w1/w3 [inter x hidden],
+ * w2 [hidden x inter]. Shared: FP4 (1x32) or FP8 (128x128, E8M0 or fp32
+ * scales). hidden, inter multiples of 128; n_experts <= 1024; topk <= 16.
+ * Numerics: fp16 MFMA with fp32 accumulation; weights decoded exactly (FP4
+ * scale bytes 104..140, i.e. |w| in [2^-24, 2^14), else status bit 2); x and
+ * the SwiGLU output are rounded to fp16 on the way into the MFMA, a relative
+ * error of at most 2^-11 per element. Tolerance: relative L2 1e-3 against the
+ * reference's fp32 path (typically ~1e-4). */
+int  dsv4_hip_moe_grouped(float *out, const float *x, int n, const int *topk_idx,
+                          const float *topk_w, int topk, const DSV4ExpertW *experts,
+                          int n_experts, const DSV4ExpertW *shared, float limit);
+
+/* Device form: x [n][hidden], out [n][hidden] (16-byte aligned), idx and w
+ * [n][topk], `experts` a DEVICE table of n_experts descriptors with device
+ * pointers; `shared` a HOST descriptor holding device pointers (or NULL).
+ * Out-of-range ids raise status bit 0 and make that token's output NaN; a
+ * table entry of the wrong format raises bit 1. */
+int  dsv4_hip_moe_grouped_dev(float *out, const float *x, int n,
+                              const DSV4ExpertW *experts, int n_experts,
+                              const int *idx, const float *w, int topk,
+                              const DSV4ExpertW *shared, int hidden, int inter,
+                              float limit, void *stream);
+
 /* ------------------------------------------------ prefill GEMM (a16, a17) --
  * C[m][n] = sum_k A[m][k] * W[n][k] for m < M on CDNA4 FP8 MFMA, replacing the
  * GPU leg of the prefill projection seam, dsv4_prefill_vk_gemm
@@ -156,7 +190,9 @@ int  dsv4_hip_gemm_fp8q_dev(void *C, int out_bf16, const uint8_t *Aq,
 /* Read and clear the device status word that the _dev kernels raise when a
  * routing id is out of range (bit 0) or an expert descriptor in the device
  * table does not match the expected format and geometry (bit 1); the affected
- * outputs are NaN. Synchronises the library's streams. 0 ok, -1 no device. */
+ * outputs are NaN. Bit 2: the grouped MoE met an FP4 scale byte outside
+ * 104..140, whose blocks it cannot decode exactly. Synchronises the library's
+ * streams. 0 ok, -1 no device. */
 int  dsv4_hip_status(unsigned *bits);
 
 #ifdef __cplusplus

@@ -1,0 +1,239 @@
+# SPDX-License-Identifier: Apache-2.0
+"""GPU parity for the grouped MoE (dsv4_hip_moe_grouped / _dev): batched
+decode and the prefill MoE layer.
+
+The oracle is the reference's per-token path restated: expert_forward
+(src/10_compute/dsv4_ops.c:85-93 over fp4_n / fp8_n) for each routed pair and
+the shared expert, then the k-order combine
+(src/80_prefill/dsv4_prefill_union_run.c:109-121). The reference's bucket
+path is bitwise equal to it (tests/unit/test_matmul.c:690-792), so per-token
+oracle outputs are the reference's prefill outputs. Tolerance: relative L2
+1e-3 (the GPU rounds x and the SwiGLU output to fp16 on the way into the
+MFMA)."""
+import numpy as np
+import pytest
+import torch
+
+import pyoracle as P
+from conftest import REL_L2_TOL, bits, max_abs, rel_l2
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda:0"
+
+
+class DevMat:
+    """A quantized matrix generated and quantized on the GPU, with host copies
+    for the oracle."""
+
+    def __init__(self, lib, pkg, fmt, rows, cols, gen, sigma=0.02):
+        w = torch.randn(rows, cols, generator=gen, device=DEV) * sigma
+        if fmt == "fp4":
+            W = torch.empty(rows * cols // 2, dtype=torch.uint8, device=DEV)
+            S = torch.empty(rows * cols // 32, dtype=torch.uint8, device=DEV)
+            lib.quant_fp4_mx_dev(W.data_ptr(), S.data_ptr(), w.data_ptr(), rows, cols)
+            wdt, br, bc = pkg.DSV4_WFP4, 1, 32
+        else:
+            W = torch.empty(rows * cols, dtype=torch.uint8, device=DEV)
+            S = torch.empty(((rows + 127) // 128) * ((cols + 127) // 128), dtype=torch.float32, device=DEV)
+            lib.quant_fp8_blk128_dev(W.data_ptr(), S.data_ptr(), w.data_ptr(), rows, cols)
+            wdt, br, bc = pkg.DSV4_WFP8_F32S, 128, 128
+            if fmt == "fp8e8m0":   # power-of-two scales at or above the fp32 ones
+                S = torch.clamp(torch.ceil(torch.log2(S)) + 127, 0, 254).to(torch.uint8)
+                wdt = pkg.DSV4_WFP8
+        torch.cuda.synchronize()
+        self.W, self.S = W, S
+        self.desc = pkg.qmat(wdt, W.data_ptr(), S.data_ptr(), rows, cols, br, bc)
+        self.hm = P.HostMat(wdt, W.cpu().numpy(), S.cpu().numpy(), rows, cols, br, bc)
+
+
+class DevExpert:
+    def __init__(self, lib, pkg, fmt, inter, hidden, gen):
+        self.m = [DevMat(lib, pkg, fmt, inter, hidden, gen), DevMat(lib, pkg, fmt, inter, hidden, gen),
+                  DevMat(lib, pkg, fmt, hidden, inter, gen)]
+        self.desc = pkg.ExpertW(self.m[0].desc, self.m[1].desc, self.m[2].desc)
+        self.he = P.HostExpert(self.m[0].hm, self.m[1].hm, self.m[2].hm)
+
+
+def table_of(experts):
+    raw = b"".join(bytes(e.desc) for e in experts)
+    return torch.from_numpy(np.frombuffer(raw, np.uint8).copy()).to(DEV)
+
+
+def routing(rng, n, topk, ne, zipf=None):
+    idx = np.empty((n, topk), np.int32)
+    p = None
+    if zipf:
+        p = 1.0 / np.arange(1, ne + 1) ** zipf
+        p /= p.sum()
+    for t in range(n):
+        idx[t] = rng.choice(ne, topk, replace=False, p=p)
+    logits = rng.standard_normal((n, topk))
+    w = (np.exp(logits) / np.exp(logits).sum(1, keepdims=True)).astype(np.float32)
+    return idx, w
+
+
+def oracle_tokens(oracle, experts, shared, x, idx, w, tokens, limit=10.0):
+    out = []
+    for t in tokens:
+        acc = np.stack([oracle.expert_forward(experts[e].he, x[t], limit) for e in idx[t]])
+        sh = oracle.expert_forward(shared.he, x[t], limit) if shared is not None else None
+        out.append(oracle.moe_combine(acc, w[t], sh))
+    return np.stack(out)
+
+
+def run_dev(lib, experts, shared, x, idx, w, hidden, inter, limit=10.0):
+    n, topk = idx.shape
+    tbl = table_of(experts)
+    dx = torch.from_numpy(np.ascontiguousarray(x, np.float32)).to(DEV)
+    di = torch.from_numpy(idx).to(DEV)
+    dw = torch.from_numpy(w).to(DEV)
+    out = torch.empty((n, hidden), dtype=torch.float32, device=DEV)
+    lib.moe_grouped_dev(out.data_ptr(), dx.data_ptr(), n, tbl.data_ptr(), len(experts), di.data_ptr(),
+                        dw.data_ptr(), topk, shared.desc if shared is not None else None, hidden, inter,
+                        limit)
+    torch.cuda.synchronize()
+    return out.cpu().numpy()
+
+
+def bf16_rows(gen, n, hidden):
+    return torch.randn(n, hidden, generator=gen).bfloat16().float().numpy()
+
+
+@pytest.mark.parametrize("n,topk,ne,shared_fmt", [
+    (20, 4, 12, "fp8f32"),      # 16-row tiles, FP8 shared with fp32 block scales
+    (7, 6, 16, "fp8e8m0"),      # FP8 shared with E8M0 scales, ragged buckets
+    (1100, 4, 8, "fp4"),        # 64-row tiles (more than 4096 pairs), FP4 shared
+    (33, 3, 5, None),           # no shared expert
+])
+def test_grouped_small_shapes(lib, pkg, oracle, n, topk, ne, shared_fmt):
+    gen = torch.Generator().manual_seed(n * 7 + ne)
+    dgen = torch.Generator(device=DEV).manual_seed(n * 7 + ne)
+    rng = np.random.default_rng(n + topk)
+    hidden, inter = (256, 128) if n > 500 else (512, 256)
+    experts = [DevExpert(lib, pkg, "fp4", inter, hidden, dgen) for _ in range(ne)]
+    shared = DevExpert(lib, pkg, shared_fmt, inter, hidden, dgen) if shared_fmt else None
+    x = bf16_rows(gen, n, hidden)
+    idx, w = routing(rng, n, topk, ne)
+    got = run_dev(lib, experts, shared, x, idx, w, hidden, inter)
+    tokens = range(n) if n <= 64 else rng.choice(n, 48, replace=False)
+    want = oracle_tokens(oracle, experts, shared, x, idx, w, tokens)
+    got = got[list(tokens)]
+    assert lib.status() == 0
+    assert np.all(np.isfinite(got))
+    e = rel_l2(got, want)
+    assert e <= REL_L2_TOL, f"rel L2 {e:.3e} (max abs {max_abs(got, want):.3e})"
+
+
+def test_grouped_host_entry_point(lib, pkg, oracle):
+    """dsv4_hip_moe_grouped with host descriptors inside registered ranges."""
+    gen = torch.Generator().manual_seed(5)
+    rng = np.random.default_rng(5)
+    hidden, inter, ne, n, topk = 256, 128, 6, 10, 3
+    host = []
+    for _ in range(ne + 1):
+        mats = []
+        fmt = "fp4" if len(host) < ne else "fp8"
+        for (r, c) in ((inter, hidden), (inter, hidden), (hidden, inter)):
+            wf = (torch.randn(r, c, generator=gen) * 0.02).numpy()
+            if fmt == "fp4":
+                W, S = oracle.quant_fp4_mx(wf)
+                args = (pkg.DSV4_WFP4, W, S, r, c, 1, 32)
+            else:
+                W, S = oracle.quant_fp8_blk128(wf)
+                args = (pkg.DSV4_WFP8_F32S, W, S, r, c, 128, 128)
+            W = np.ascontiguousarray(args[1]); S = np.ascontiguousarray(args[2])
+            lib.check(lib.register(W), "register"); lib.check(lib.register(S), "register")
+            mats.append((W, S, pkg.qmat(args[0], W.ctypes.data, S.ctypes.data, r, c, args[5], args[6]),
+                         P.HostMat(args[0], W, S, r, c, args[5], args[6])))
+        host.append(mats)
+    descs = [pkg.ExpertW(m[0][2], m[1][2], m[2][2]) for m in host]
+    hes = [P.HostExpert(m[0][3], m[1][3], m[2][3]) for m in host]
+    x = bf16_rows(gen, n, hidden)
+    idx, w = routing(rng, n, topk, ne)
+    got = lib.moe_grouped(descs[:ne], idx, w, x, descs[ne], 10.0)
+    want = []
+    for t in range(n):
+        acc = np.stack([oracle.expert_forward(hes[e], x[t], 10.0) for e in idx[t]])
+        want.append(oracle.moe_combine(acc, w[t], oracle.expert_forward(hes[ne], x[t], 10.0)))
+    e = rel_l2(got, np.stack(want))
+    for mats in host:
+        for W, S, _, _ in mats:
+            lib.unregister(W); lib.unregister(S)
+    assert e <= REL_L2_TOL, f"rel L2 {e:.3e}"
+
+
+def test_grouped_deterministic_and_order_free(lib, pkg, oracle):
+    """Two calls agree bit for bit, and a token's output does not depend on
+    where its rows land in the expert buckets (token order permuted)."""
+    gen = torch.Generator().manual_seed(9)
+    dgen = torch.Generator(device=DEV).manual_seed(9)
+    rng = np.random.default_rng(9)
+    hidden, inter, ne, n, topk = 256, 128, 6, 40, 3
+    experts = [DevExpert(lib, pkg, "fp4", inter, hidden, dgen) for _ in range(ne)]
+    x = bf16_rows(gen, n, hidden)
+    idx, w = routing(rng, n, topk, ne)
+    a = run_dev(lib, experts, None, x, idx, w, hidden, inter)
+    b = run_dev(lib, experts, None, x, idx, w, hidden, inter)
+    assert np.array_equal(bits(a), bits(b))
+    perm = rng.permutation(n)
+    c = run_dev(lib, experts, None, x[perm], idx[perm], w[perm], hidden, inter)
+    assert np.array_equal(bits(c), bits(a[perm]))
+
+
+def test_grouped_bad_id_flags_status(lib, pkg, oracle):
+    gen = torch.Generator().manual_seed(11)
+    dgen = torch.Generator(device=DEV).manual_seed(11)
+    rng = np.random.default_rng(11)
+    hidden, inter, ne, n, topk = 256, 128, 4, 6, 2
+    experts = [DevExpert(lib, pkg, "fp4", inter, hidden, dgen) for _ in range(ne)]
+    x = bf16_rows(gen, n, hidden)
+    idx, w = routing(rng, n, topk, ne)
+    lib.status()
+    idx[2, 1] = 99
+    got = run_dev(lib, experts, None, x, idx, w, hidden, inter)
+    assert lib.status() & 1
+    assert np.isnan(got[2]).all()
+    ok = [t for t in range(n) if t != 2]
+    assert np.all(np.isfinite(got[ok]))
+    want = oracle_tokens(oracle, experts, None, x, idx, w, ok)
+    assert rel_l2(got[ok], want) <= REL_L2_TOL
+
+
+def test_grouped_scale_range_flag(lib, pkg, oracle):
+    """An FP4 scale byte outside 104..140 cannot be decoded exactly into fp16:
+    the call raises status bit 2."""
+    gen = torch.Generator().manual_seed(13)
+    dgen = torch.Generator(device=DEV).manual_seed(13)
+    rng = np.random.default_rng(13)
+    hidden, inter, ne, n, topk = 256, 128, 2, 4, 1
+    experts = [DevExpert(lib, pkg, "fp4", inter, hidden, dgen) for _ in range(ne)]
+    x = bf16_rows(gen, n, hidden)
+    idx, w = routing(rng, n, topk, ne)
+    lib.status()
+    run_dev(lib, experts, None, x, idx, w, hidden, inter)
+    assert lib.status() == 0
+    experts[0].m[0].S[5] = 150
+    experts[1].m[0].S[5] = 150
+    torch.cuda.synchronize()
+    run_dev(lib, experts, None, x, idx, w, hidden, inter)
+    assert lib.status() & 4
+
+
+def test_grouped_config2_shape_sampled(lib, pkg, oracle):
+    """64 tokens, top-6 of 32 real-size FP4 experts (2048 x 4096) under Zipf
+    routing, FP8 shared expert with fp32 scales; 4 tokens checked against the
+    oracle."""
+    gen = torch.Generator().manual_seed(2)
+    dgen = torch.Generator(device=DEV).manual_seed(2)
+    rng = np.random.default_rng(2)
+    hidden, inter, ne, n, topk = 4096, 2048, 32, 64, 6
+    experts = [DevExpert(lib, pkg, "fp4", inter, hidden, dgen) for _ in range(ne)]
+    shared = DevExpert(lib, pkg, "fp8f32", inter, hidden, dgen)
+    x = bf16_rows(gen, n, hidden)
+    idx, w = routing(rng, n, topk, ne, zipf=1.1)
+    got = run_dev(lib, experts, shared, x, idx, w, hidden, inter)
+    assert lib.status() == 0
+    tokens = [0, 17, 40, 63]
+    want = oracle_tokens(oracle, experts, shared, x, idx, w, tokens)
+    e = rel_l2(got[tokens], want)
+    assert e <= REL_L2_TOL, f"rel L2 {e:.3e} (max abs {max_abs(got[tokens], want):.3e})"
