@@ -13,9 +13,19 @@ weights and scales + 8 KiB bf16 x + 16 KiB fp32 out per token).
 --config 0: one 4096x4096 e4m3 matvec with fp32 128x128 scales, x bf16;
 weights rotated over 40 copies (672 MB) so each step reads from HBM.
 
+--config 2: batched decode MoE, 64 tokens per step, top-6 of the 256 FP4
+experts under Zipf(1.1) popularity (fresh routing every step), plus an FP8
+shared expert (fp32 128x128 scales), through the grouped MoE. Metric:
+algorithmic HBM GB/s (distinct routed experts x 13,369,344 B + shared
+25,171,968 B + bf16 x + fp32 out per step).
+
 --config 3: prefill GEMM, 2048 tokens x 4096 (bf16 A, quantized on the fly to
 e4m3 with an fp32 scale per 1x128) times a 4096x4096 e4m3 weight with fp32
 128x128 scales, bf16 output, on FP8 MFMA. Metric: TFLOP/s (2 M N K per step).
+
+--config 4: the prefill MoE layer, 4096 tokens, top-6 Zipf(1.1) routing over
+the 256 FP4 experts plus the FP8 shared expert, permute -> grouped MFMA GEMMs
+with SwiGLU -> combine. Metric: TFLOP/s of the routed + shared FLOPs.
 
 Prints ONE JSON line. Synthetic data (seeded), random-init weights.
 """
@@ -34,6 +44,8 @@ import numpy as np
 ROOT = os.path.dirname(os.path.abspath(__file__))
 HBM_PEAK_GBS = 8000.0
 FP8_PEAK_TFLOPS = 5000.0          # MI355X dense FP8 MFMA
+FP16_PEAK_TFLOPS = 2500.0         # MI355X dense fp16 / bf16 MFMA
+SHARED_BYTES = 3 * (2048 * 4096 + 16 * 32 * 4)   # FP8 gate/up/down + fp32 128x128 scales
 
 EXPERT_BYTES = 13_369_344          # w1,w3: 2048x4096 FP4 + scales; w2: 4096x2048
 HIDDEN, INTER, N_EXPERTS, TOPK = 4096, 2048, 256, 6
@@ -94,6 +106,35 @@ def routing(n_steps, seed):
     lg = rng.standard_normal((n_steps, TOPK))
     w = np.exp(lg) / np.exp(lg).sum(1, keepdims=True)
     return idx.astype(np.int32), w.astype(np.float32)
+
+
+def zipf_routing(n_tokens, seed, s=1.1):
+    """top-6 of 256 experts per token, expert e drawn with weight (e+1)^-s
+    without replacement within a token; softmax weights of N(0,1) logits."""
+    rng = np.random.default_rng(seed)
+    p = 1.0 / np.arange(1, N_EXPERTS + 1) ** s
+    p /= p.sum()
+    idx = np.stack([rng.choice(N_EXPERTS, TOPK, replace=False, p=p) for _ in range(n_tokens)])
+    lg = rng.standard_normal((n_tokens, TOPK))
+    w = np.exp(lg) / np.exp(lg).sum(1, keepdims=True)
+    return idx.astype(np.int32), w.astype(np.float32)
+
+
+def make_shared_fp8(torch, pkg, lib, seed):
+    """The shared expert: e4m3 gate/up [2048 x 4096] and down [4096 x 2048],
+    fp32 scale per 128 x 128 block."""
+    dev = "cuda:0"
+    tmp = torch.empty(INTER * HIDDEN, dtype=torch.float32, device=dev)
+    keep, q = [], []
+    for i, (r, c) in enumerate(((INTER, HIDDEN), (INTER, HIDDEN), (HIDDEN, INTER))):
+        W = torch.empty(r * c, dtype=torch.uint8, device=dev)
+        S = torch.empty((r // 128) * (c // 128), dtype=torch.float32, device=dev)
+        lib.synth_normal_dev(tmp.data_ptr(), r * c, seed + i, 0.02)
+        lib.quant_fp8_blk128_dev(W.data_ptr(), S.data_ptr(), tmp.data_ptr(), r, c)
+        keep += [W, S]
+        q.append(pkg.qmat(pkg.DSV4_WFP8_F32S, W.data_ptr(), S.data_ptr(), r, c, 128, 128))
+    torch.cuda.synchronize()
+    return pkg.ExpertW(q[0], q[1], q[2]), keep
 
 
 def time_events(torch, stream, fn, n):
@@ -164,6 +205,176 @@ def cpu_baseline_cfg1(torch, arena, x_host, seconds, threads):
     return {"value": round(gbs, 3), "unit": "GB/s", "cores": threads, "kind": kind,
             "sample": f"{tokens} tokens x top-6 over 16 host-resident FP4 experts "
                       f"(214 MB), {el:.1f} s, OpenMP {threads} threads"}
+
+
+def cpu_baseline_buckets(torch, arena, idx, x_host, seconds, threads, unit):
+    """The reference's prefill bucket path on the host
+    (src/80_prefill/dsv4_prefill_experts.c:60-69): per expert, its routed
+    tokens through fp4_n with nt = bucket size for w1 and w3, SwiGLU, fp4_n
+    for w2. Runs the buckets of the 8 most-loaded experts of the given routing
+    (copied from the device arena) until `seconds` elapse. Reports expert
+    bytes streamed per second (GB/s) or routed FLOP/s (TFLOP/s)."""
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import pyoracle as P
+    kind = "reference"
+    try:
+        impl = P.Reference()
+    except FileNotFoundError:
+        impl, kind = P.Oracle(), "port"
+    omp_threads(threads)
+    counts = np.bincount(idx.reshape(-1), minlength=N_EXPERTS)
+    sel = np.argsort(-counts, kind="stable")[:8]
+    wb = [INTER * HIDDEN // 2, HIDDEN * INTER // 2, INTER * HIDDEN // 2]
+    sb = [INTER * HIDDEN // 32, HIDDEN * INTER // 32, INTER * HIDDEN // 32]
+    off_s = [0, sb[0], sb[0] + sb[1]]
+    off_w = [sum(sb), sum(sb) + wb[0], sum(sb) + wb[0] + wb[1]]
+    buckets = []
+    for e in sel:
+        raw = arena.host_copy(torch, int(e))
+        toks = np.nonzero((idx == e).any(1))[0]
+        X = np.ascontiguousarray(x_host[toks], np.float32)
+        mats = [(raw[off_w[i]:off_w[i] + wb[i]], raw[off_s[i]:off_s[i] + sb[i]]) for i in range(3)]
+        buckets.append((raw, mats, X, len(toks)))
+    def mmq_n(mat, X, rows, cols, nt):
+        """dsv4_mmq_n's tiling: the fp4_n body takes at most 128 tokens
+        (DSV4_MAX_BATCH, src/10_compute/dsv4_matmul.c:63-73)"""
+        out = np.empty(nt * rows, np.float32)
+        for o in range(0, nt, 128):
+            t = min(128, nt - o)
+            out[o * rows:(o + t) * rows] = impl.fp4_n(mat[0], mat[1], X[o * cols:(o + t) * cols],
+                                                      rows, cols, 1, 32, t)
+        return out
+
+    t0 = time.perf_counter()
+    passes = nbytes = flops = 0
+    while True:
+        for raw, mats, X, nt in buckets:
+            g = mmq_n(mats[0], X.reshape(-1), INTER, HIDDEN, nt)
+            u = mmq_n(mats[2], X.reshape(-1), INTER, HIDDEN, nt)
+            m = impl.swiglu(g, u, 10.0)
+            mmq_n(mats[1], m, HIDDEN, INTER, nt)
+            nbytes += EXPERT_BYTES
+            flops += 2.0 * nt * 3 * INTER * HIDDEN
+        passes += 1
+        el = time.perf_counter() - t0
+        if el >= seconds and passes >= 1:
+            break
+    loads = ",".join(str(b[3]) for b in buckets)
+    value = nbytes / el / 1e9 if unit == "GB/s" else flops / el / 1e12
+    return {"value": round(value, 5), "unit": unit, "cores": threads, "kind": kind,
+            "sample": f"{passes} passes over the buckets of the 8 most-loaded experts "
+                      f"(tokens {loads}) through fp4_n/SwiGLU/fp4_n, {el:.1f} s, "
+                      f"OpenMP {threads} threads"}
+
+
+def bench_grouped(args, torch, pkg, lib, stream, sp, K, W, cfg):
+    """Configs 2 (64 tokens per step) and 4 (4096 tokens per step)."""
+    n = 64 if cfg == 2 else 4096
+    dev = "cuda:0"
+    seed = 0xD5EED000 + cfg
+    log("generating 256 FP4 experts and the FP8 shared expert on the device")
+    arena = ExpertArena(torch, pkg, lib, N_EXPERTS, seed=seed)
+    shared, keep = make_shared_fp8(torch, pkg, lib, seed * 7)
+    # fresh routing and tokens for every step (config 2: K + W steps; config
+    # 4: four rotating token blocks, a block being 4096 x 4096 fp32)
+    nsets = K + W if cfg == 2 else 4
+    idx_h, w_h = zipf_routing(n * nsets, seed)
+    idx = torch.from_numpy(idx_h).to(dev)
+    wts = torch.from_numpy(w_h).to(dev)
+    xs = torch.empty(n * nsets * HIDDEN, dtype=torch.float32, device=dev)
+    lib.synth_normal_dev(xs.data_ptr(), xs.numel(), seed ^ 0x55, 1.0, True)
+    out = torch.empty(n * HIDDEN, dtype=torch.float32, device=dev)
+    torch.cuda.synchronize()
+
+    def step(i):
+        j = i % nsets
+        lib.moe_grouped_dev(out.data_ptr(), xs.data_ptr() + 4 * HIDDEN * n * j, n,
+                            arena.table.data_ptr(), N_EXPERTS, idx.data_ptr() + 4 * TOPK * n * j,
+                            wts.data_ptr() + 4 * TOPK * n * j, TOPK, shared, HIDDEN, INTER, 10.0, sp)
+
+    def step_bytes(j):
+        d = len(np.unique(idx_h[n * j:n * (j + 1)]))
+        return d * EXPERT_BYTES + SHARED_BYTES + n * HIDDEN * 2 + n * HIDDEN * 4
+
+    flops_step = 2.0 * n * TOPK * 3 * INTER * HIDDEN + 2.0 * n * 3 * INTER * HIDDEN
+    for i in range(W):
+        step(i)
+    torch.cuda.synchronize()
+    assert lib.status() == 0
+    log(f"timing {K} steps")
+    t0 = time.perf_counter()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(stream)
+    for i in range(K):
+        step(W + i)
+    e1.record(stream)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    t_step = e0.elapsed_time(e1) * 1e-3 / K
+    t_launch = time_events(torch, stream, lambda i: step(W + i), K)
+    assert lib.status() == 0
+    bytes_avg = float(np.mean([step_bytes((W + i) % nsets) for i in range(K)]))
+    d_avg = (bytes_avg - SHARED_BYTES - n * HIDDEN * 6) / EXPERT_BYTES
+    cpu = None
+    if not args.no_cpu:
+        threads = args.cpu_threads or min(16, os.cpu_count() or 1)
+        x_host = xs[:n * HIDDEN].view(n, HIDDEN).cpu().numpy()
+        log(f"CPU baseline ({threads} threads, {args.cpu_seconds:.0f} s)")
+        cpu = cpu_baseline_buckets(torch, arena, idx_h[:n], x_host, args.cpu_seconds, threads,
+                                   "GB/s" if cfg == 2 else "TFLOP/s")
+    res = {
+        "metric": "quant matvec HBM GB/s (% peak); prefill FP4/FP8 GEMM TFLOP/s (% MFMA peak)",
+        "n_gpus": 1, "steps": K, "warmup": W, "ms_per_step": round(t_step * 1e3, 5),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "fp16 MFMA on exactly decoded FP4 (routed) / FP8 (shared) weights, fp32 accumulate",
+        "data": "synthetic (seeded N(0,0.02) experts, bf16 N(0,1) tokens, Zipf(1.1) top-6 routing), "
+                "random-init",
+        "tokens_per_s": round(n / t_step, 1),
+        "cpu_baseline": cpu,
+        "wall_s": round(wall, 4),
+    }
+    if cfg == 2:
+        value = bytes_avg / t_step / 1e9
+        achieved = bytes_avg / t_launch / 1e9
+        res.update({
+            "value": round(value, 2), "unit": "GB/s",
+            "config": {"workload": "batched decode MoE: 64 tokens x top-6 of 256 FP4 experts "
+                                   "(Zipf 1.1) + FP8 shared expert, grouped GEMM, SwiGLU, combine",
+                       "tokens_per_step": n, "distinct_experts_avg": round(d_avg, 1),
+                       "parallelism": "single GPU"},
+            "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS,
+                         "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                         "kernel": "moe_grouped_dev call (route, fp16 convert, grouped gate/up, "
+                                   "grouped down, shared gate/up + down, combine)",
+                         "bytes_per_launch": round(bytes_avg), "launch_us": round(t_launch * 1e6, 3)},
+        })
+    else:
+        value = flops_step / t_step / 1e12
+        achieved = flops_step / t_launch / 1e12
+        # composite bound: each distinct expert at max(bytes / HBM, flops / fp16 peak)
+        j = (W) % nsets
+        cnt = np.bincount(idx_h[n * j:n * (j + 1)].reshape(-1), minlength=N_EXPERTS)
+        t_roof = sum(max(EXPERT_BYTES / (HBM_PEAK_GBS * 1e9),
+                         2.0 * c * 3 * INTER * HIDDEN / (FP16_PEAK_TFLOPS * 1e12)) for c in cnt if c)
+        t_roof += max(SHARED_BYTES / (HBM_PEAK_GBS * 1e9),
+                      2.0 * n * 3 * INTER * HIDDEN / (FP16_PEAK_TFLOPS * 1e12))
+        res.update({
+            "value": round(value, 2), "unit": "TFLOP/s",
+            "config": {"workload": "prefill MoE layer: 4096 tokens x top-6 of 256 FP4 experts "
+                                   "(Zipf 1.1) + FP8 shared expert, permute, grouped GEMM with "
+                                   "SwiGLU, combine",
+                       "tokens_per_step": n, "distinct_experts_avg": round(d_avg, 1),
+                       "parallelism": "single GPU"},
+            "roofline": {"bound": "mfma", "achieved": round(achieved, 2), "peak": FP16_PEAK_TFLOPS,
+                         "unit": "TFLOP/s", "frac": round(achieved / FP16_PEAK_TFLOPS, 4),
+                         "traffic": None,
+                         "kernel": "moe_grouped_dev call (route, fp16 convert, grouped gate/up, "
+                                   "grouped down, shared gate/up + down, combine)",
+                         "flops_per_launch": flops_step, "launch_us": round(t_launch * 1e6, 3),
+                         "composite_t_roof_us": round(t_roof * 1e6, 1),
+                         "composite_frac": round(t_roof / t_launch, 4)},
+        })
+    return res
 
 
 def cpu_baseline_cfg3(Wq, Sw_e8m0, x_sample, seconds, threads):
@@ -272,7 +483,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
-    ap.add_argument("--config", type=int, default=1, choices=[0, 1, 3])
+    ap.add_argument("--config", type=int, default=1, choices=[0, 1, 2, 3, 4])
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--cpu-threads", type=int, default=0)
     ap.add_argument("--no-cpu", action="store_true")
@@ -354,6 +565,10 @@ def main():
             "cpu_baseline": cpu,
             "wall_s": round(wall, 4),
         }
+    elif args.config in (2, 4):
+        if args.config == 4 and K > 50:
+            K, W = 50, min(W, 5)      # about 1 ms per step; keeps the timed region short
+        res = bench_grouped(args, torch, pkg, lib, stream, sp, K, W, args.config)
     elif args.config == 3:
         res = bench_cfg3(args, torch, pkg, lib, stream, sp, K, W)
     else:
