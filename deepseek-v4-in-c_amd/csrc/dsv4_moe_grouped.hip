@@ -30,9 +30,10 @@
  *   v_mfma_f32_16x16x32_f16, fp32 accumulation. Weights are decoded into the
  *   MFMA operand with v_cvt_scalef32_pk_f16_{fp4,fp8}: e2m1 * 2^e is exact in
  *   fp16 for E8M0 scale bytes 104..140 (checked on every block: outside it
- *   the status word gets ST_SCALE_RANGE), e4m3 values are exact. fp32 128x128
- *   block scales (DSV4_WFP8_F32S) are applied per 128-K chunk to a partial
- *   sum, as the reference's fp8_n applies them per block. The activations and
+ *   the status word gets ST_SCALE_RANGE); e4m3 values enter unscaled (exact)
+ *   and the 128x128 block scale, E8M0 or fp32, multiplies each 128-K chunk's
+ *   partial sum in fp32, as the reference's fp8_n applies it per block. The
+ *   activations and
  *   the SwiGLU output enter the MFMA rounded to fp16 (relative error at most
  *   2^-11 each); everything else is fp32.
  *
@@ -325,12 +326,10 @@ __global__ __launch_bounds__(256) void k_grouped(GroupedArgs a)
                 const uint32_t b = (sc4[rb] >> (8 * gq)) & 0xFFu;
                 scale_bad |= (b - 104u) > 36u;
                 cvt_scale = dev_e8m0(b);
-            } else if constexpr (WF == FMT_FP8_E8M0) {
-                cvt_scale = (SWIGLU && rb >= 4) ? s_hi : s_lo;
             } else {
-                cvt_scale = 1.0f;
+                cvt_scale = 1.0f;          /* raw e4m3, exact in fp16 */
             }
-            if constexpr (WF == FMT_FP8_F32S) {
+            if constexpr (!FP4) {
                 f4v part[TT];
 #pragma unroll
                 for (int tt = 0; tt < TT; tt++) part[tt] = f4v{0.0f, 0.0f, 0.0f, 0.0f};

@@ -62,7 +62,7 @@ struct State {
     hipStream_t stream = nullptr;
     unsigned *status = nullptr;          /* device status word            */
     std::map<uintptr_t, Region> regions; /* host start -> resident copy   */
-    DevBuf x, y, mid, table, small, ys, gemm_ws, moe_ws;
+    DevBuf x, y, mid, table, small, ys, gemm_ws, moe_ws, x16;
 };
 
 State g;
@@ -296,7 +296,7 @@ void dsv4_hip_shutdown(void)
     g.regions.clear();
     g.x.release(); g.y.release(); g.mid.release();
     g.table.release(); g.small.release(); g.ys.release(); g.gemm_ws.release();
-    g.moe_ws.release();
+    g.moe_ws.release(); g.x16.release();
     if (g.status) (void)hipFree(g.status);
     g.status = nullptr;
     if (g.stream) (void)hipStreamDestroy(g.stream);
@@ -352,6 +352,34 @@ void *dsv4_hip_device_ptr(const void *p)
     return (void *)translate(p, 1);
 }
 
+/* y = W . x for nt tokens. From MMQ_MFMA_MIN_TOKENS tokens on, matrices the
+ * grouped kernel takes (rows, cols multiples of 128; FP8 with 128x128 blocks
+ * or FP4 with 1x32) run as one dense fp16-MFMA GEMM (x rounded to fp16, weights
+ * decoded exactly, fp32 accumulation); fewer tokens or other geometries run
+ * the per-token GEMV. */
+constexpr int MMQ_MFMA_MIN_TOKENS = 32;
+
+int enqueue_mmq(const DSV4QMat &d, int fmt, const float *x, float *y, int nt, hipStream_t st)
+{
+    const bool blocks = fmt == FMT_FP4_E8M0 ? d.blk_r == 1 : d.blk_r == 128;
+    if (nt >= MMQ_MFMA_MIN_TOKENS && blocks && d.rows % 128 == 0 && d.cols % 128 == 0 &&
+        ((uintptr_t)d.s & 3u) == 0) {
+        HIPCHK(g.x16.need((size_t)nt * d.cols * 2), "fp16 staging");
+        uint16_t *x16 = (uint16_t *)g.x16.p;
+        HIPCHK(to_f16_launch(x16, x, (size_t)nt * d.cols, st), "x fp16 launch");
+        GroupedArgs a;
+        memset(&a, 0, sizeof a);
+        a.m1 = d; a.nrows = nt; a.B = x16; a.K = d.cols; a.N = d.rows; a.out = y;
+        a.status = g.status;
+        const int tt = nt <= 16 ? 1 : 4;
+        const long tiles = (nt + grouped_rows_per_tile(tt) - 1) / grouped_rows_per_tile(tt);
+        HIPCHK(grouped_launch(fmt, false, tt, a, tiles, st), "dense MFMA launch");
+        return 0;
+    }
+    HIPCHK(gemv_launch(fmt, gemv_args(d, x, y, nt), st), "gemv launch");
+    return 0;
+}
+
 int dsv4_hip_mmq_n(float *y, const float *x, const DSV4QMat *m, int nt)
 {
     std::lock_guard<std::mutex> lk(g.mu);
@@ -365,8 +393,7 @@ int dsv4_hip_mmq_n(float *y, const float *x, const DSV4QMat *m, int nt)
     HIPCHK(g.x.need(xb), "x staging");
     HIPCHK(g.y.need(yb), "y staging");
     HIPCHK(hipMemcpyAsync(g.x.p, x, xb, hipMemcpyHostToDevice, g.stream), "x upload");
-    HIPCHK(gemv_launch(fmt, gemv_args(d, (const float *)g.x.p, (float *)g.y.p, nt), g.stream),
-           "gemv launch");
+    if (enqueue_mmq(d, fmt, (const float *)g.x.p, (float *)g.y.p, nt, g.stream)) return -1;
     HIPCHK(hipMemcpyAsync(y, g.y.p, yb, hipMemcpyDeviceToHost, g.stream), "y download");
     HIPCHK(hipStreamSynchronize(g.stream), "mmq_n sync");
     return 0;
@@ -387,8 +414,7 @@ int dsv4_hip_mmq_n_dev(float *y, const float *x, const DSV4QMat *m, int nt,
     if (check_qmat(m, "mmq_n_dev", &fmt)) return -1;
     if (!x || !y || !m->w || !m->s) return fail("mmq_n_dev: NULL pointer");
     if (!aligned16(x) || !aligned16(m->w)) return fail("mmq_n_dev: x and W must be 16-byte aligned");
-    HIPCHK(gemv_launch(fmt, gemv_args(*m, x, y, nt), (hipStream_t)stream), "gemv launch");
-    return 0;
+    return enqueue_mmq(*m, fmt, x, y, nt, (hipStream_t)stream);
 }
 
 int dsv4_hip_expert_forward(float *out, const float *x, const DSV4ExpertW *e,

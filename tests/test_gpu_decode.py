@@ -382,3 +382,37 @@ def test_synth_normal_deterministic(lib):
     torch.cuda.synchronize()
     bb = b.cpu()
     assert torch.equal(bb, bb.bfloat16().float())
+
+
+# ------------------------------------------- many tokens: dense MFMA path
+
+@pytest.mark.parametrize("wdt_name,rows,cols,nt", [
+    ("fp8", 512, 1024, 64), ("fp8", 256, 512, 300), ("fp8f32", 384, 1024, 100),
+    ("fp4", 512, 2048, 32), ("fp4", 256, 512, 200), ("fp8", 130, 512, 64)])
+def test_mmq_n_many_tokens(lib, pkg, oracle, wdt_name, rows, cols, nt):
+    """dsv4_mmq_n with nt >= 32 (the prefill seam, src/80_prefill/
+    dsv4_prefill_proj.c:17-27) runs as one fp16-MFMA GEMM when rows and cols
+    are multiples of 128 (x rounded to fp16, weights exact, fp32
+    accumulation); 130 rows takes the per-token GEMV. Both within 1e-3 of the
+    reference's fp8_n / fp4_n nt > 1 bodies."""
+    rng = np.random.default_rng(rows + cols + nt)
+    x = rng.standard_normal(nt * cols).astype(np.float32)
+    if wdt_name == "fp4":
+        W = rng.integers(0, 256, rows * cols // 2).astype(np.uint8)
+        S = rng.integers(118, 134, rows * cols // 32).astype(np.uint8)
+        m = Resident(lib, pkg, pkg.DSV4_WFP4, W, S, rows, cols, 1, 32)
+        want = oracle.fp4_n(W, S, x, rows, cols, 1, 32, nt)
+    elif wdt_name == "fp8":
+        W = _rand_fp8(rng, rows * cols)
+        S = rng.integers(100, 150, ((rows + 127) // 128) * (cols // 128)).astype(np.uint8)
+        m = Resident(lib, pkg, pkg.DSV4_WFP8, W, S, rows, cols, 128, 128)
+        want = oracle.fp8_n(W, S, x, rows, cols, 128, 128, nt)
+    else:
+        w = (rng.standard_normal((rows, cols)) * 0.02).astype(np.float32)
+        W, S = oracle.quant_fp8_blk128(w)
+        m = Resident(lib, pkg, pkg.DSV4_WFP8_F32S, W, S, rows, cols, 128, 128)
+        want = oracle.fp8f_n(W, S, x, rows, cols, 128, 128, nt)
+    y = lib.mmq_n(m.desc, x, nt)
+    m.drop()
+    assert lib.status() == 0
+    check_close(y, want)
