@@ -406,6 +406,32 @@ def cpu_baseline_cfg3(Wq, Sw_e8m0, x_sample, seconds, threads):
                       f"OpenMP {threads} threads"}
 
 
+def cpu_baseline_cfg0(Wq, Sw_e8m0, x, seconds, threads):
+    """The reference's fp8_n with nt = 1 (src/10_compute/dsv4_matmul_fp8.c:
+    57-99) on one 4096x4096 e4m3 weight (16.8 MB, beyond the host LLC),
+    repeated until `seconds` elapse. The reference stores E8M0 block scales, so
+    it runs with the power of two at or above each fp32 scale."""
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import pyoracle as P
+    kind = "reference"
+    try:
+        impl = P.Reference()
+    except FileNotFoundError:
+        impl, kind = P.Oracle(), "port"
+    omp_threads(threads)
+    t0 = time.perf_counter()
+    calls = 0
+    while True:
+        impl.fp8_n(Wq, Sw_e8m0, x, 4096, 4096, 128, 128, 1)
+        calls += 1
+        el = time.perf_counter() - t0
+        if el >= seconds and calls >= 3:
+            break
+    return {"value": round(calls * 16_805_888 / el / 1e9, 3), "unit": "GB/s", "cores": threads,
+            "kind": kind, "sample": f"{calls} matvecs 4096x4096 through fp8_n (E8M0 scales), "
+                                    f"{el:.1f} s, OpenMP {threads} threads"}
+
+
 def bench_cfg3(args, torch, pkg, lib, stream, sp, K, W):
     M, N, KD = 2048, 4096, 4096
     flops = 2.0 * M * N * KD
@@ -606,6 +632,13 @@ def main():
         t_launch = time_events(torch, stream, step, K)
         bytes_step = 16_805_888
         value = bytes_step / t_step / 1e9
+        cpu = None
+        if not args.no_cpu:
+            threads = args.cpu_threads or min(16, os.cpu_count() or 1)
+            Wh = Wd[:4096 * 4096].cpu().numpy()
+            Se = torch.clamp(torch.ceil(torch.log2(Sd[:1024])) + 127, 0, 254).to(torch.uint8).cpu().numpy()
+            log(f"CPU baseline ({threads} threads, {args.cpu_seconds:.0f} s)")
+            cpu = cpu_baseline_cfg0(Wh, Se, xs.cpu().numpy(), args.cpu_seconds, threads)
         res = {
             "metric": "quant matvec HBM GB/s (% peak); prefill FP4/FP8 GEMM TFLOP/s (% MFMA peak)",
             "value": round(value, 2), "unit": "GB/s", "n_gpus": 1, "steps": K, "warmup": W,
@@ -619,7 +652,7 @@ def main():
                          "frac": round(bytes_step / t_launch / 1e9 / HBM_PEAK_GBS, 4),
                          "traffic": None, "kernel": "k_gemv<FP8_F32S,4,2>",
                          "bytes_per_launch": bytes_step, "launch_us": round(t_launch * 1e6, 3)},
-            "cpu_baseline": None,
+            "cpu_baseline": cpu,
             "wall_s": round(wall, 4),
         }
     print(json.dumps(res), flush=True)
