@@ -152,6 +152,7 @@ struct RouteArgs {
     int tile_rows;            /* rows per tile of the grouped GEMM        */
     int *grp_off;             /* [n_experts + 1] first row of each bucket */
     int *tile_pre;            /* [n_experts + 1] prefix of tiles          */
+    int *tile_grp;            /* [tiles] bucket (expert) of each tile     */
     int *pos;                 /* [npairs] row of each pair (-1: bad id)   */
     int *row_tok;             /* [npairs] token of each row               */
     unsigned *status;
@@ -167,7 +168,7 @@ hipError_t to_f16_launch(uint16_t *o, const float *x, size_t n, hipStream_t st);
 struct GroupedArgs {
     const DSV4ExpertW *table;
     int n_experts;
-    const int *grp_off, *tile_pre;
+    const int *grp_off, *tile_pre, *tile_grp;
     const int *row_tok;       /* B row of each output row, NULL = itself  */
     DSV4QMat m1, m3;
     int nrows;

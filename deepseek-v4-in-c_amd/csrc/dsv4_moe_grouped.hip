@@ -144,17 +144,32 @@ __global__ __launch_bounds__(1024) void k_moe_route(RouteArgs a)
         else bad = ST_BAD_EXPERT_ID;
     }
     __syncthreads();
-    if (tid == 0) {
-        int o = 0, tp = 0;
-        for (int e = 0; e < E; e++) {
-            a.grp_off[e] = o;
-            a.tile_pre[e] = tp;
-            cur[e] = o;
-            o += hist[e];
-            tp += (hist[e] + a.tile_rows - 1) / a.tile_rows;
+    /* inclusive scans of the bucket sizes and tile counts (Hillis-Steele,
+     * one expert per thread; E <= 1024) */
+    __shared__ int scan_r[MAX_ROUTE_EXPERTS], scan_t[MAX_ROUTE_EXPERTS];
+    const int cnt = tid < E ? hist[tid] : 0;
+    const int tls = (cnt + a.tile_rows - 1) / a.tile_rows;
+    scan_r[tid] = cnt;
+    scan_t[tid] = tls;
+    __syncthreads();
+    for (int d = 1; d < MAX_ROUTE_EXPERTS; d <<= 1) {
+        const int xr = tid >= d ? scan_r[tid - d] : 0;
+        const int xt = tid >= d ? scan_t[tid - d] : 0;
+        __syncthreads();
+        scan_r[tid] += xr;
+        scan_t[tid] += xt;
+        __syncthreads();
+    }
+    if (tid < E) {
+        const int o = scan_r[tid] - cnt;
+        a.grp_off[tid] = o;
+        a.tile_pre[tid] = scan_t[tid] - tls;
+        cur[tid] = o;
+        for (int t = scan_t[tid] - tls; t < scan_t[tid]; t++) a.tile_grp[t] = tid;
+        if (tid == E - 1) {
+            a.grp_off[E] = scan_r[tid];
+            a.tile_pre[E] = scan_t[tid];
         }
-        a.grp_off[E] = o;
-        a.tile_pre[E] = tp;
     }
     __syncthreads();
     /* rows inside a bucket are claimed by LDS atomics; a row's result does
@@ -206,13 +221,7 @@ __global__ __launch_bounds__(256) void k_grouped(GroupedArgs a)
     if (a.table) {
         const int E = a.n_experts;
         if (tile >= ld_uniform(a.tile_pre, E)) return;
-        int lo = 0, hi = E;    /* largest g with tile_pre[g] <= tile: a non-empty bucket */
-        while (hi - lo > 1) {
-            const int mid = (lo + hi) >> 1;
-            if (ld_uniform(a.tile_pre, mid) <= tile) lo = mid;
-            else hi = mid;
-        }
-        const int grp = lo;
+        const int grp = ld_uniform(a.tile_grp, tile);   /* the bucket owning this tile */
         const int go = ld_uniform(a.grp_off, grp), ge = ld_uniform(a.grp_off, grp + 1);
         r0 = go + (tile - ld_uniform(a.tile_pre, grp)) * TROWS;
         ntok = min(TROWS, ge - r0);
@@ -245,15 +254,17 @@ __global__ __launch_bounds__(256) void k_grouped(GroupedArgs a)
     /* this lane's weight rows: SwiGLU items take w1 rows in blocks 0-3 and
      * the matching w3 rows in blocks 4-7 */
     const int rowb = FP4 ? K / 2 : K;              /* bytes per weight row */
-    const uint8_t *wrow[RB];
-    const uint8_t *srow[RB];                       /* FP4: the row's E8M0 bytes */
+    /* 32-bit per-lane offsets from the wave-uniform matrix bases (a matrix is
+     * below 4 GiB): the weight byte of block rb is base(rb) + wofs[rb], its
+     * FP4 scale row base_s(rb) + sofs[rb] */
+    const uint8_t *wb1 = (const uint8_t *)m1.w, *wb3 = (const uint8_t *)m3.w;
+    const uint8_t *sb1 = (const uint8_t *)m1.s, *sb3 = (const uint8_t *)m3.s;
+    uint32_t wofs[RB], sofs[RB];
 #pragma unroll
     for (int rb = 0; rb < RB; rb++) {
-        const bool up = SWIGLU && rb >= 4;
-        const DSV4QMat &m = up ? m3 : m1;
         const int row = f0 + 16 * (SWIGLU ? (rb & 3) : rb) + rr;
-        wrow[rb] = (const uint8_t *)m.w + (size_t)row * rowb + 16 * gq;
-        srow[rb] = (const uint8_t *)m.s + (size_t)row * (K / 32);
+        wofs[rb] = (uint32_t)row * (uint32_t)rowb + 16u * (uint32_t)gq;
+        sofs[rb] = (uint32_t)row * (uint32_t)(K / 32);
     }
     /* FP8: one scale per (128-row block, 128-K chunk) per matrix */
     const int nb = f0 / 128, kbn = K / 128;
@@ -276,58 +287,53 @@ __global__ __launch_bounds__(256) void k_grouped(GroupedArgs a)
 
     unsigned scale_bad = 0;
     const int nchunk = K / KC;
-    /* raw weights of the next chunk are in flight while this one multiplies */
-    u32x4 wn[RB][2];
-    uint32_t sn[RB];
-#pragma unroll
-    for (int rb = 0; rb < RB; rb++) {
-        wn[rb][0] = ld_stream16(wrow[rb]);
-        wn[rb][1] = FP4 ? wn[rb][0] : ld_stream16(wrow[rb] + 64);
-        sn[rb] = FP4 ? *gptr((const uint32_t *)srow[rb]) : 0u;
-    }
-    for (int c = 0; c < nchunk; c++) {
-        u32x4 wc[RB][2];
-        uint32_t sc4[RB];
+    /* Raw weights of the next PF chunks are in flight while one multiplies:
+     * with 16-row tiles the item is a weight stream and needs several chunks
+     * in flight to cover HBM latency; with 64-row tiles one chunk of compute
+     * covers it. The B operands (tokens, from L2) are fetched one chunk
+     * ahead. */
+    constexpr int PF = (TT == 1 && FP4) ? 3 : 1;
+    constexpr int CB = FP4 ? 64 : 128;             /* weight bytes per row per chunk */
+    struct WChunk {
+        u32x4 w[RB][2];
+        uint32_t s[RB];                            /* FP4: the lane's 4 E8M0 bytes  */
+        float fs[2];                               /* FP8: chunk scale of m1, m3    */
+    };
+    auto load_w = [&](int c, WChunk &o) {
 #pragma unroll
         for (int rb = 0; rb < RB; rb++) {
-            wc[rb][0] = wn[rb][0];
-            wc[rb][1] = wn[rb][1];
-            sc4[rb] = sn[rb];
+            const bool up = SWIGLU && rb >= 4;
+            const uint8_t *p = (up ? wb3 : wb1) + (wofs[rb] + (uint32_t)(c * CB));
+            o.w[rb][0] = ld_stream16(p);
+            if constexpr (!FP4) o.w[rb][1] = ld_stream16(p + 64);
+            if constexpr (FP4)
+                o.s[rb] = *gptr((const uint32_t *)((up ? sb3 : sb1) + (sofs[rb] + 4u * (uint32_t)c)));
         }
-        if (c + 1 < nchunk) {
-#pragma unroll
-            for (int rb = 0; rb < RB; rb++) {
-                const uint8_t *p = wrow[rb] + (size_t)(c + 1) * (FP4 ? 64 : 128);
-                wn[rb][0] = ld_stream16(p);
-                wn[rb][1] = FP4 ? wn[rb][0] : ld_stream16(p + 64);
-                sn[rb] = FP4 ? *gptr((const uint32_t *)(srow[rb] + 4 * (c + 1))) : 0u;
-            }
+        if constexpr (WF == FMT_FP8_E8M0) {
+            o.fs[0] = dev_e8m0(ld_u8(m1.s, (size_t)nb * kbn + c));
+            o.fs[1] = SWIGLU ? dev_e8m0(ld_u8(m3.s, (size_t)nb * kbn + c)) : 0.0f;
+        } else if constexpr (WF == FMT_FP8_F32S) {
+            o.fs[0] = ld_f32(m1.s, (size_t)nb * kbn + c);
+            o.fs[1] = SWIGLU ? ld_f32(m3.s, (size_t)nb * kbn + c) : 0.0f;
+        } else {
+            o.fs[0] = o.fs[1] = 1.0f;
         }
-        /* B operands of this chunk */
-        h8 bop[TT][4];
+    };
+    auto load_b = [&](int c, h8 (&b)[TT][4]) {
 #pragma unroll
         for (int tt = 0; tt < TT; tt++)
 #pragma unroll
             for (int j = 0; j < 4; j++)
-                bop[tt][j] = *gptr((const h8 *)(brow[tt] + c * KC + kmap<WF>(gq, j)));
-        /* FP8 chunk scales (wave-uniform), one per matrix */
-        float s_lo = 1.0f, s_hi = 1.0f;
-        if constexpr (WF == FMT_FP8_E8M0) {
-            s_lo = dev_e8m0(ld_u8(m1.s, (size_t)nb * kbn + c));
-            if (SWIGLU) s_hi = dev_e8m0(ld_u8(m3.s, (size_t)nb * kbn + c));
-        } else if constexpr (WF == FMT_FP8_F32S) {
-            s_lo = ld_f32(m1.s, (size_t)nb * kbn + c);
-            if (SWIGLU) s_hi = ld_f32(m3.s, (size_t)nb * kbn + c);
-        }
+                b[tt][j] = *gptr((const h8 *)(brow[tt] + c * KC + kmap<WF>(gq, j)));
+    };
+    auto compute = [&](const WChunk &wc, const h8 (&bop)[TT][4]) {
 #pragma unroll
         for (int rb = 0; rb < RB; rb++) {
-            float cvt_scale;
+            float cvt_scale = 1.0f;                /* FP8: raw e4m3, exact in fp16 */
             if constexpr (FP4) {
-                const uint32_t b = (sc4[rb] >> (8 * gq)) & 0xFFu;
+                const uint32_t b = (wc.s[rb] >> (8 * gq)) & 0xFFu;
                 scale_bad |= (b - 104u) > 36u;
                 cvt_scale = dev_e8m0(b);
-            } else {
-                cvt_scale = 1.0f;          /* raw e4m3, exact in fp16 */
             }
             if constexpr (!FP4) {
                 f4v part[TT];
@@ -335,25 +341,63 @@ __global__ __launch_bounds__(256) void k_grouped(GroupedArgs a)
                 for (int tt = 0; tt < TT; tt++) part[tt] = f4v{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
                 for (int j = 0; j < 4; j++) {
-                    const h8 av = a_operand<WF>(wc[rb], cvt_scale, j);
+                    const h8 av = a_operand<WF>(wc.w[rb], cvt_scale, j);
 #pragma unroll
                     for (int tt = 0; tt < TT; tt++)
                         if (tt < ntt) part[tt] = mfma16(av, bop[tt][j], part[tt]);
                 }
-                const float s = (SWIGLU && rb >= 4) ? s_hi : s_lo;
+                const float sc = (SWIGLU && rb >= 4) ? wc.fs[1] : wc.fs[0];
 #pragma unroll
                 for (int tt = 0; tt < TT; tt++)
 #pragma unroll
-                    for (int e = 0; e < 4; e++) acc[rb][tt][e] = fmaf(part[tt][e], s, acc[rb][tt][e]);
+                    for (int e = 0; e < 4; e++) acc[rb][tt][e] = fmaf(part[tt][e], sc, acc[rb][tt][e]);
             } else {
 #pragma unroll
                 for (int j = 0; j < 4; j++) {
-                    const h8 av = a_operand<WF>(wc[rb], cvt_scale, j);
+                    const h8 av = a_operand<WF>(wc.w[rb], cvt_scale, j);
 #pragma unroll
                     for (int tt = 0; tt < TT; tt++)
                         if (tt < ntt) acc[rb][tt] = mfma16(av, bop[tt][j], acc[rb][tt]);
                 }
             }
+        }
+    };
+
+    /* Loads are issued unconditionally (past the end they repeat the last
+     * chunk, an L2 hit): a load behind a branch makes the wait-count pass
+     * drain every outstanding load at the join, prefetches included. */
+    const int last = nchunk - 1;
+    WChunk ring[PF];
+#pragma unroll
+    for (int i = 0; i < PF; i++) load_w(min(i, last), ring[i]);
+    h8 bnext[TT][4];
+    load_b(0, bnext);
+    int c = 0;
+    for (; c + PF <= nchunk; c += PF) {
+#pragma unroll
+        for (int i = 0; i < PF; i++) {
+            const WChunk wc = ring[i];
+            load_w(min(c + i + PF, last), ring[i]);
+            h8 bop[TT][4];
+#pragma unroll
+            for (int tt = 0; tt < TT; tt++)
+#pragma unroll
+                for (int j = 0; j < 4; j++) bop[tt][j] = bnext[tt][j];
+            load_b(min(c + i + 1, last), bnext);
+            compute(wc, bop);
+        }
+    }
+    /* at most PF - 1 chunks remain; they are already in the ring */
+#pragma unroll
+    for (int i = 0; i + 1 < PF; i++) {
+        if (c + i < nchunk) {
+            h8 bop[TT][4];
+#pragma unroll
+            for (int tt = 0; tt < TT; tt++)
+#pragma unroll
+                for (int j = 0; j < 4; j++) bop[tt][j] = bnext[tt][j];
+            load_b(min(c + i + 1, last), bnext);
+            compute(ring[i], bop);
         }
     }
     if (scale_bad) atomicOr(a.status, ST_SCALE_RANGE);
@@ -380,6 +424,302 @@ __global__ __launch_bounds__(256) void k_grouped(GroupedArgs a)
 #pragma unroll
             for (int rb = 0; rb < RB; rb++)
                 *(f4v *)((float *)a.out + orow + f0 + 16 * rb + 4 * gq) = acc[rb][tt];
+        }
+    }
+}
+
+/* ------------------------------------------- LDS-staged grouped GEMM --- */
+
+/* The same work as k_grouped, for K a multiple of 256, with a workgroup per
+ * item and every operand staged through LDS by direct loads. Direct global
+ * loads in the MFMA layout make each instruction touch 16 rows (64 B each)
+ * and keep the texture-address units ~85 % busy; here every 1 KiB load
+ * instruction covers whole 128-byte lines of at most 8 rows.
+ *
+ * Workgroup: 4 waves, 128 weight rows (gate/up: 64 w1 rows + the matching 64
+ * w3 rows; down: 128 w2 rows) x TOK = 16*TT token rows. Waves split the rows
+ * (TT = 1: 4 x 32 rows, a weight stream) or rows and tokens (TT = 4: 2 x 64
+ * rows by 2 x 32 tokens, so that each wave's operand reads from LDS stay
+ * below its ~27 B/clk). A stage is 256 reduction indices: weights (FP4 128 B
+ * or FP8 256 B per row), the FP4 rows' eight E8M0 bytes, and the token rows
+ * (fp16, 512 B each), in NST ring buffers; stage s+NST-1 is loaded while s
+ * multiplies. 16-byte chunks are XOR-swizzled so the operand reads of 16
+ * rows hit distinct banks. */
+namespace {
+
+typedef __attribute__((address_space(3))) void lds_void;
+constexpr int KS = 256;
+
+__device__ __forceinline__ void dma16(const void *src, uint8_t *dst)
+{
+    __builtin_amdgcn_global_load_lds(gptr(src), (lds_void *)dst, 16, 0, 0);
+}
+__device__ __forceinline__ void dma4(const void *src, uint8_t *dst)
+{
+    __builtin_amdgcn_global_load_lds(gptr(src), (lds_void *)dst, 4, 0, 0);
+}
+
+template <int WF, int TT>
+struct G2 {
+    static constexpr bool FP4 = WF == FMT_FP4_E8M0;
+    static constexpr int WB = FP4 ? KS / 2 : KS;         /* weight bytes per row per stage */
+    static constexpr int ROWS = 128;
+    static constexpr int TOK = 16 * TT;
+    static constexpr int WR = TT == 1 ? 4 : 2;           /* waves along rows           */
+    static constexpr int WT = 4 / WR;                    /* waves along tokens         */
+    static constexpr int RBW = 8 / WR;                   /* 16-row blocks per wave     */
+    static constexpr int TTW = TT / WT;                  /* 16-token tiles per wave    */
+    static constexpr int OFF_S = ROWS * WB;
+    static constexpr int OFF_B = OFF_S + (FP4 ? ROWS * 8 : 0);
+    static constexpr int STAGE = OFF_B + TOK * KS * 2;
+    /* FP4 16-row tiles: 3 x 25 KiB, two workgroups per CU overlap each
+     * other's pipeline ramp */
+    static constexpr int NST = (FP4 && TT == 1) ? 2 : (FP4 || TT == 1) ? 3 : 2;
+    static constexpr int LDS = NST * STAGE;
+    static constexpr int NW = ROWS * WB / 1024 / 4;      /* weight loads per wave per stage */
+    static constexpr int NS = FP4 ? 1 : 0;               /* scale loads                */
+    static constexpr int NB = TOK * KS * 2 / 1024 / 4;   /* token-row loads            */
+    static constexpr int VM = NW + NS + NB;
+    static_assert(LDS <= 160 * 1024, "LDS ring exceeds 160 KiB");
+    static_assert((NST - 2) * VM <= 63, "vmcnt range");
+};
+
+/* physical 16-byte slot of logical chunk c in staged row r */
+__device__ __forceinline__ int swz_w4(int r, int c) { return c ^ ((r >> 1) & 7); }   /* 8 slots   */
+__device__ __forceinline__ int swz_w8(int r, int c) { return c ^ (r & 15); }         /* 16 slots  */
+__device__ __forceinline__ int swz_b(int r, int c) { return c ^ (r & 15); }          /* 32 slots  */
+
+/* B chunk (8 halves) of MFMA step sg (0..7) for lane group gq: the token side
+ * of the reduction order the weight side is read in */
+template <int WF>
+__device__ __forceinline__ int bchunk(int gq, int sg)
+{
+    if constexpr (WF == FMT_FP4_E8M0) return 16 * (sg >> 2) + 4 * gq + (sg & 3);
+    else return 8 * (sg >> 1) + 2 * gq + (sg & 1);
+}
+
+} // namespace
+
+template <int WF, bool SWIGLU, int TT>
+__global__ __launch_bounds__(256) void k_grouped2(GroupedArgs a)
+{
+    using C = G2<WF, TT>;
+    constexpr bool FP4 = C::FP4;
+    constexpr int FEAT = SWIGLU ? 64 : 128;
+    extern __shared__ __align__(16) uint8_t lds[];
+    const int lane = threadIdx.x & 63;
+    const int wave = wave_in_group();
+    const int rr = lane & 15, gq = lane >> 4;
+    const int nslab = a.N / FEAT;
+    const int tile = blockIdx.x / nslab, slab = blockIdx.x - tile * nslab;
+
+    int r0, ntok;
+    DSV4QMat m1, m3;
+    if (a.table) {
+        const int E = a.n_experts;
+        if (tile >= ld_uniform(a.tile_pre, E)) return;            /* whole workgroup */
+        const int lo = ld_uniform(a.tile_grp, tile);     /* the bucket owning this tile */
+        const int go = ld_uniform(a.grp_off, lo), ge = ld_uniform(a.grp_off, lo + 1);
+        r0 = go + (tile - ld_uniform(a.tile_pre, lo)) * C::TOK;
+        ntok = min(C::TOK, ge - r0);
+        const DSV4ExpertW e = ld_uniform(a.table, lo);
+        m1 = SWIGLU ? e.w1 : e.w2;
+        m3 = e.w3;
+    } else {
+        r0 = tile * C::TOK;
+        if (r0 >= a.nrows) return;
+        ntok = min(C::TOK, a.nrows - r0);
+        m1 = a.m1;
+        m3 = a.m3;
+    }
+    const int f0 = slab * FEAT;
+    const int K = a.K, N = a.N;
+    if (!qmat_matches<WF>(m1, N, K) || (SWIGLU && !qmat_matches<WF>(m3, N, K))) {
+        if (threadIdx.x == 0) atomicOr(a.status, ST_BAD_DESCRIPTOR);
+        const float nan = __builtin_nanf("");
+        for (int i = threadIdx.x; i < ntok * FEAT; i += 256) {
+            const size_t o = (size_t)(r0 + i / FEAT) * N + f0 + i % FEAT;
+            if constexpr (SWIGLU) ((uint16_t *)a.out)[o] = (uint16_t)f16_bits(nan);
+            else ((float *)a.out)[o] = nan;
+        }
+        return;
+    }
+
+    /* ---- load plan: per-lane source offsets of this wave's loads ---- */
+    const int rowb = FP4 ? K / 2 : K;
+    const int nst = K / KS, last = nst - 1;
+    const uint8_t *wbase[C::NW];
+    int wdst[C::NW];
+#pragma unroll
+    for (int i = 0; i < C::NW; i++) {
+        const int j = wave * C::NW + i;                    /* 1 KiB instruction index */
+        const int rpi = 1024 / C::WB;                      /* rows per instruction    */
+        const int r = j * rpi + lane / (C::WB / 16);
+        const int p = lane % (C::WB / 16);
+        const bool up = SWIGLU && r >= 64;
+        const int row = f0 + (SWIGLU ? (r & 63) : r);
+        const int c = FP4 ? swz_w4(r, p) : swz_w8(r, p);
+        wbase[i] = (const uint8_t *)(up ? m3.w : m1.w) + (size_t)row * rowb + 16 * c;
+        wdst[i] = 1024 * j;
+    }
+    const uint8_t *sbase = nullptr;
+    if constexpr (FP4) {
+        const int r = 32 * wave + lane / 2;
+        const bool up = SWIGLU && r >= 64;
+        const int row = f0 + (SWIGLU ? (r & 63) : r);
+        sbase = (const uint8_t *)(up ? m3.s : m1.s) + (size_t)row * (K / 32) + 4 * (lane & 1);
+    }
+    const uint16_t *bbase[C::NB];
+#pragma unroll
+    for (int i = 0; i < C::NB; i++) {
+        const int j = wave * C::NB + i;
+        const int t = 2 * j + lane / 32, p = lane & 31;
+        const int r = t < ntok ? r0 + t : r0;
+        const int src = a.row_tok ? a.row_tok[r] : r;
+        bbase[i] = a.B + (size_t)src * K + 8 * swz_b(t, p);
+    }
+    auto issue = [&](int stg, uint8_t *buf) {
+#pragma unroll
+        for (int i = 0; i < C::NW; i++) dma16(wbase[i] + (size_t)stg * C::WB, buf + wdst[i]);
+        if constexpr (FP4) dma4(sbase + (size_t)stg * 8, buf + C::OFF_S + 256 * wave);
+#pragma unroll
+        for (int i = 0; i < C::NB; i++)
+            dma16(bbase[i] + (size_t)stg * KS, buf + C::OFF_B + 1024 * (wave * C::NB + i));
+    };
+
+    /* ---- this wave's share ---- */
+    const int wr = wave % C::WR, wt = wave / C::WR;
+    int blk[C::RBW];
+#pragma unroll
+    for (int i = 0; i < C::RBW; i++) {
+        constexpr int H = C::RBW / 2;
+        blk[i] = SWIGLU ? (i < H ? H * wr + i : 4 + H * wr + (i - H)) : C::RBW * wr + i;
+    }
+    int ntw = 0;                                           /* live tiles of this wave */
+#pragma unroll
+    for (int u = 0; u < C::TTW; u++) ntw += 16 * (wt * C::TTW + u) < ntok ? 1 : 0;
+
+    f4v acc[C::RBW][C::TTW];
+#pragma unroll
+    for (int i = 0; i < C::RBW; i++)
+#pragma unroll
+        for (int u = 0; u < C::TTW; u++) acc[i][u] = f4v{0.0f, 0.0f, 0.0f, 0.0f};
+    unsigned scale_bad = 0;
+
+#pragma unroll
+    for (int s0 = 0; s0 < C::NST - 1; s0++) issue(min(s0, last), lds + s0 * C::STAGE);
+
+    for (int st = 0; st < nst; st++) {
+        __builtin_amdgcn_s_waitcnt(0x0F70 | ((C::NST - 2) * C::VM & 15) | ((((C::NST - 2) * C::VM) >> 4) << 14));
+        __builtin_amdgcn_s_barrier();
+        asm volatile("" ::: "memory");
+        {
+            int nb = st + C::NST - 1;
+            nb = nb >= C::NST ? nb - C::NST * (nb / C::NST) : nb;
+            issue(min(st + C::NST - 1, last), lds + nb * C::STAGE);
+        }
+        const uint8_t *buf = lds + (st % C::NST) * C::STAGE;
+
+        /* token operands of this wave's tiles, all 8 steps */
+        h8 bop[C::TTW][8];
+#pragma unroll
+        for (int u = 0; u < C::TTW; u++) {
+            const int t = 16 * (wt * C::TTW + u) + rr;
+            const uint8_t *brow = buf + C::OFF_B + t * (KS * 2);
+#pragma unroll
+            for (int sg = 0; sg < 8; sg++)
+                bop[u][sg] = *(const h8 *)(brow + 16 * swz_b(t, bchunk<WF>(gq, sg)));
+        }
+        /* FP8 chunk scales: 2 blocks of 128 per stage, per matrix */
+        float fs[2][2] = {{1.0f, 1.0f}, {1.0f, 1.0f}};
+        if constexpr (!FP4) {
+            const int nb = f0 / 128, kbn = K / 128;
+#pragma unroll
+            for (int b = 0; b < 2; b++) {
+                const size_t si = (size_t)nb * kbn + 2 * st + b;
+                if constexpr (WF == FMT_FP8_E8M0) {
+                    fs[0][b] = dev_e8m0(ld_u8(m1.s, si));
+                    fs[1][b] = SWIGLU ? dev_e8m0(ld_u8(m3.s, si)) : 1.0f;
+                } else {
+                    fs[0][b] = ld_f32(m1.s, si);
+                    fs[1][b] = SWIGLU ? ld_f32(m3.s, si) : 1.0f;
+                }
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < C::RBW; i++) {
+            const int r = 16 * blk[i] + rr;                /* staged row */
+            if constexpr (FP4) {
+                const uint2 sc8 = *(const uint2 *)(buf + C::OFF_S + r * 8);
+#pragma unroll
+                for (int h = 0; h < 2; h++) {
+                    const int c = 4 * h + gq;
+                    const u32x4 w16 = *(const u32x4 *)(buf + r * C::WB + 16 * swz_w4(r, c));
+                    const uint32_t sb = ((c < 4 ? sc8.x : sc8.y) >> (8 * (c & 3))) & 0xFFu;
+                    scale_bad |= (sb - 104u) > 36u;
+                    const float cs = dev_e8m0(sb);
+                    const u32x4 wv[2] = {w16, w16};
+#pragma unroll
+                    for (int s = 0; s < 4; s++) {
+                        const h8 av = a_operand<WF>(wv, cs, s);
+#pragma unroll
+                        for (int u = 0; u < C::TTW; u++)
+                            if (u < ntw) acc[i][u] = mfma16(av, bop[u][4 * h + s], acc[i][u]);
+                    }
+                }
+            } else {
+                const float *fsm = fs[(SWIGLU && blk[i] >= 4) ? 1 : 0];
+#pragma unroll
+                for (int b = 0; b < 2; b++) {              /* 128-K block of the stage */
+                    f4v part[C::TTW];
+#pragma unroll
+                    for (int u = 0; u < C::TTW; u++) part[u] = f4v{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+                    for (int q2 = 0; q2 < 2; q2++) {
+                        const int q = 2 * b + q2;
+                        const int c = 4 * q + gq;
+                        const u32x4 w16 = *(const u32x4 *)(buf + r * C::WB + 16 * swz_w8(r, c));
+                        const u32x4 wv[2] = {w16, w16};
+#pragma unroll
+                        for (int s = 0; s < 2; s++) {
+                            const h8 av = a_operand<WF>(wv, 1.0f, s);   /* dwords 2s, 2s+1 */
+#pragma unroll
+                            for (int u = 0; u < C::TTW; u++)
+                                if (u < ntw) part[u] = mfma16(av, bop[u][2 * q + s], part[u]);
+                        }
+                    }
+#pragma unroll
+                    for (int u = 0; u < C::TTW; u++)
+#pragma unroll
+                        for (int e = 0; e < 4; e++) acc[i][u][e] = fmaf(part[u][e], fsm[b], acc[i][u][e]);
+                }
+            }
+        }
+    }
+    __builtin_amdgcn_s_waitcnt(0x0F70);     /* trailing repeat loads drain before exit */
+    if (scale_bad) atomicOr(a.status, ST_SCALE_RANGE);
+
+#pragma unroll
+    for (int u = 0; u < C::TTW; u++) {
+        const int t = 16 * (wt * C::TTW + u) + rr;
+        if (t >= ntok) continue;
+        const size_t orow = (size_t)(r0 + t) * N;
+        if constexpr (SWIGLU) {
+            constexpr int H = C::RBW / 2;
+#pragma unroll
+            for (int i = 0; i < H; i++) {
+                float m[4];
+#pragma unroll
+                for (int e = 0; e < 4; e++) m[e] = dev_swiglu(acc[i][u][e], acc[i + H][u][e], a.limit);
+                uint2 pk;
+                pk.x = f16_bits(m[0]) | (f16_bits(m[1]) << 16);
+                pk.y = f16_bits(m[2]) | (f16_bits(m[3]) << 16);
+                *(uint2 *)((uint16_t *)a.out + orow + f0 + 16 * blk[i] + 4 * gq) = pk;
+            }
+        } else {
+#pragma unroll
+            for (int i = 0; i < C::RBW; i++)
+                *(f4v *)((float *)a.out + orow + f0 + 16 * blk[i] + 4 * gq) = acc[i][u];
         }
     }
 }
@@ -438,9 +778,28 @@ hipError_t to_f16_launch(uint16_t *o, const float *x, size_t n, hipStream_t st)
 
 int grouped_rows_per_tile(int tt) { return 16 * tt; }
 
+template <int WF, bool SW, int TT>
+static hipError_t grouped2(const GroupedArgs &a, long items, hipStream_t st)
+{
+    static bool attr_done = false;
+    if (!attr_done) {
+        const hipError_t e = hipFuncSetAttribute((const void *)k_grouped2<WF, SW, TT>,
+                                                 hipFuncAttributeMaxDynamicSharedMemorySize,
+                                                 G2<WF, TT>::LDS);
+        if (e != hipSuccess) return e;
+        attr_done = true;
+    }
+    constexpr int lds_bytes = G2<WF, TT>::LDS;
+    hipLaunchKernelGGL((k_grouped2<WF, SW, TT>), dim3((unsigned)items), dim3(256), lds_bytes, st, a);
+    return hipGetLastError();
+}
+
 template <int WF, bool SW>
 static hipError_t grouped_tt(const GroupedArgs &a, int tt, long items, hipStream_t st)
 {
+    if (a.K % KS == 0) {        /* LDS-staged form: one workgroup per item */
+        return tt == 1 ? grouped2<WF, SW, 1>(a, items, st) : grouped2<WF, SW, 4>(a, items, st);
+    }
     const dim3 grid((unsigned)((items + 3) / 4)), block(256);
     if (tt == 1) hipLaunchKernelGGL((k_grouped<WF, SW, 1>), grid, block, 0, st, a);
     else hipLaunchKernelGGL((k_grouped<WF, SW, 4>), grid, block, 0, st, a);

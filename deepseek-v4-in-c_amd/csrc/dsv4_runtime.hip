@@ -60,6 +60,8 @@ struct State {
     int dead = 0;
     int device = -1;
     hipStream_t stream = nullptr;
+    hipStream_t side = nullptr;          /* concurrent work of one call (shared expert) */
+    hipEvent_t fork = nullptr, join = nullptr;
     unsigned *status = nullptr;          /* device status word            */
     std::map<uintptr_t, Region> regions; /* host start -> resident copy   */
     DevBuf x, y, mid, table, small, ys, gemm_ws, moe_ws, x16;
@@ -276,8 +278,12 @@ int dsv4_hip_init(int device)
         return fail("device %d is %s, this library is built for gfx950", device,
                     prop.gcnArchName);
     if (hipSetDevice(device) != hipSuccess) return fail("hipSetDevice failed");
-    if (hipStreamCreateWithFlags(&g.stream, hipStreamNonBlocking) != hipSuccess)
+    if (hipStreamCreateWithFlags(&g.stream, hipStreamNonBlocking) != hipSuccess ||
+        hipStreamCreateWithFlags(&g.side, hipStreamNonBlocking) != hipSuccess)
         return fail("stream creation failed");
+    if (hipEventCreateWithFlags(&g.fork, hipEventDisableTiming) != hipSuccess ||
+        hipEventCreateWithFlags(&g.join, hipEventDisableTiming) != hipSuccess)
+        return fail("event creation failed");
     if (hipMalloc((void **)&g.status, 256) != hipSuccess) return fail("status alloc failed");
     if (hipMemset(g.status, 0, 256) != hipSuccess) return fail("status clear failed");
 
@@ -300,7 +306,11 @@ void dsv4_hip_shutdown(void)
     if (g.status) (void)hipFree(g.status);
     g.status = nullptr;
     if (g.stream) (void)hipStreamDestroy(g.stream);
-    g.stream = nullptr;
+    if (g.side) (void)hipStreamDestroy(g.side);
+    if (g.fork) (void)hipEventDestroy(g.fork);
+    if (g.join) (void)hipEventDestroy(g.join);
+    g.stream = g.side = nullptr;
+    g.fork = g.join = nullptr;
     g.ready = 0;
     g.dead = 0;
     g.device = -1;
@@ -341,6 +351,7 @@ int dsv4_hip_unregister(const void *host)
     auto it = g.regions.find((uintptr_t)host);
     if (it == g.regions.end()) return fail("unregister: unknown range");
     (void)hipStreamSynchronize(g.stream);
+    (void)hipStreamSynchronize(g.side);
     (void)hipFree(it->second.dev);
     g.regions.erase(it);
     return 0;
@@ -587,7 +598,10 @@ int enqueue_moe_grouped(float *out, const float *x, int n, const DSV4ExpertW *ta
     const int trows = grouped_rows_per_tile(tt);
     size_t off = 0;
     auto take = [&](size_t b) { const size_t o = off; off += (b + 255) & ~(size_t)255; return o; };
+    /* every bucket adds at most one partial tile */
+    const long max_tiles = (P + trows - 1) / trows + n_experts;
     const size_t o_grp = take((size_t)(n_experts + 1) * 4), o_tp = take((size_t)(n_experts + 1) * 4);
+    const size_t o_tg = take((size_t)max_tiles * 4);
     const size_t o_pos = take((size_t)P * 4), o_row = take((size_t)P * 4);
     const size_t o_x16 = take((size_t)n * hidden * 2), o_mid = take((size_t)P * inter * 2);
     const size_t o_y = take((size_t)P * hidden * 4);
@@ -598,23 +612,22 @@ int enqueue_moe_grouped(float *out, const float *x, int n, const DSV4ExpertW *ta
     }
     HIPCHK(g.moe_ws.need(off), "grouped MoE workspace");
     uint8_t *ws = (uint8_t *)g.moe_ws.p;
-    int *grp = (int *)(ws + o_grp), *tp = (int *)(ws + o_tp);
+    int *grp = (int *)(ws + o_grp), *tp = (int *)(ws + o_tp), *tg = (int *)(ws + o_tg);
     int *pos = (int *)(ws + o_pos), *row = (int *)(ws + o_row);
     uint16_t *x16 = (uint16_t *)(ws + o_x16), *mid = (uint16_t *)(ws + o_mid);
     float *y = (float *)(ws + o_y);
 
     RouteArgs ra;
     ra.idx = idx; ra.npairs = (int)P; ra.topk = topk; ra.n_experts = n_experts;
-    ra.tile_rows = trows; ra.grp_off = grp; ra.tile_pre = tp; ra.pos = pos; ra.row_tok = row;
+    ra.tile_rows = trows; ra.grp_off = grp; ra.tile_pre = tp; ra.tile_grp = tg; ra.pos = pos;
+    ra.row_tok = row;
     ra.status = g.status;
     HIPCHK(moe_route_launch(ra, st), "route launch");
     HIPCHK(to_f16_launch(x16, x, (size_t)n * hidden, st), "x fp16 launch");
 
-    /* every bucket adds at most one partial tile */
-    const long max_tiles = (P + trows - 1) / trows + n_experts;
     GroupedArgs ga;
     memset(&ga, 0, sizeof ga);
-    ga.table = table; ga.n_experts = n_experts; ga.grp_off = grp; ga.tile_pre = tp;
+    ga.table = table; ga.n_experts = n_experts; ga.grp_off = grp; ga.tile_pre = tp; ga.tile_grp = tg;
     ga.row_tok = row; ga.B = x16; ga.K = hidden; ga.N = inter; ga.out = mid;
     ga.limit = limit; ga.status = g.status;
     HIPCHK(grouped_launch(FMT_FP4_E8M0, true, tt, ga, max_tiles, st), "routed gate/up launch");
@@ -623,18 +636,24 @@ int enqueue_moe_grouped(float *out, const float *x, int n, const DSV4ExpertW *ta
 
     float *ys = nullptr;
     if (shared) {
+        /* the shared expert needs only x16: it runs on the side stream,
+         * forked after the fp16 convert and joined before the combine */
+        HIPCHK(hipEventRecord(g.fork, st), "fork record");
+        HIPCHK(hipStreamWaitEvent(g.side, g.fork, 0), "fork wait");
         uint16_t *smid = (uint16_t *)(ws + o_smid);
         ys = (float *)(ws + o_ys);
-        const int stt = n <= 16 ? 1 : 4;
+        const int stt = n <= 64 ? 1 : 4;     /* enough workgroups for a small batch */
         const long stiles = (n + grouped_rows_per_tile(stt) - 1) / grouped_rows_per_tile(stt);
         GroupedArgs sa;
         memset(&sa, 0, sizeof sa);
         sa.m1 = shared->w1; sa.m3 = shared->w3; sa.nrows = n; sa.B = x16;
         sa.K = hidden; sa.N = sinter; sa.out = smid; sa.limit = limit; sa.status = g.status;
-        HIPCHK(grouped_launch(sfmt, true, stt, sa, stiles, st), "shared gate/up launch");
+        HIPCHK(grouped_launch(sfmt, true, stt, sa, stiles, g.side), "shared gate/up launch");
         sa.m1 = shared->w2; sa.B = smid; sa.K = sinter; sa.N = hidden; sa.out = ys;
-        HIPCHK(grouped_launch(sfmt, false, stt, sa, stiles, st), "shared down launch");
+        HIPCHK(grouped_launch(sfmt, false, stt, sa, stiles, g.side), "shared down launch");
+        HIPCHK(hipEventRecord(g.join, g.side), "join record");
     }
+    if (shared) HIPCHK(hipStreamWaitEvent(st, g.join, 0), "join wait");
     CombineArgs ca;
     ca.out = out; ca.Y = y; ca.YS = ys; ca.w = w; ca.pos = pos;
     ca.n = n; ca.topk = topk; ca.hidden = hidden;
