@@ -171,8 +171,8 @@ struct GroupedArgs {
     const int *grp_off, *tile_pre, *tile_grp;
     const int *row_tok;       /* B row of each output row, NULL = itself  */
     DSV4QMat m1, m3;
-    int nrows;
-    const uint16_t *B;        /* fp16 [.][K]                              */
+    int nrows;                /* rows of B                                */
+    const uint16_t *B;        /* fp16 [nrows][K]                          */
     int K, N;
     void *out;                /* [rows][N]                                */
     float limit;

@@ -57,6 +57,7 @@ typedef _Float16 h8 __attribute__((ext_vector_type(8)));
 typedef float f4v __attribute__((ext_vector_type(4)));
 
 constexpr int KC = 128;           /* reduction chunk */
+template <int N> struct IC { static constexpr int value = N; };
 constexpr int RB = 8;             /* 16-row weight blocks per item */
 constexpr int MAX_ROUTE_EXPERTS = 1024;
 
@@ -436,11 +437,11 @@ __global__ __launch_bounds__(256) void k_grouped(GroupedArgs a)
  * and keep the texture-address units ~85 % busy; here every 1 KiB load
  * instruction covers whole 128-byte lines of at most 8 rows.
  *
- * Workgroup: 4 waves, 128 weight rows (gate/up: 64 w1 rows + the matching 64
- * w3 rows; down: 128 w2 rows) x TOK = 16*TT token rows. Waves split the rows
- * (TT = 1: 4 x 32 rows, a weight stream) or rows and tokens (TT = 4: 2 x 64
- * rows by 2 x 32 tokens, so that each wave's operand reads from LDS stay
- * below its ~27 B/clk). A stage is 256 reduction indices: weights (FP4 128 B
+ * Workgroup: 128 weight rows (gate/up: 64 w1 rows + the matching 64 w3 rows;
+ * down: 128 w2 rows) x TOK = 16*TT token rows. TT = 1 (a weight stream): 4
+ * waves of 32 rows each. TT = 4: 8 waves, 4 x 32 rows by 2 x 32 tokens, two
+ * waves per SIMD, so that one wave's LDS operand reads (~27 B/clk each) and
+ * conversions overlap the other's MFMAs. A stage is 256 reduction indices: weights (FP4 128 B
  * or FP8 256 B per row), the FP4 rows' eight E8M0 bytes, and the token rows
  * (fp16, 512 B each), in NST ring buffers; stage s+NST-1 is loaded while s
  * multiplies. 16-byte chunks are XOR-swizzled so the operand reads of 16
@@ -465,20 +466,23 @@ struct G2 {
     static constexpr int WB = FP4 ? KS / 2 : KS;         /* weight bytes per row per stage */
     static constexpr int ROWS = 128;
     static constexpr int TOK = 16 * TT;
-    static constexpr int WR = TT == 1 ? 4 : 2;           /* waves along rows           */
-    static constexpr int WT = 4 / WR;                    /* waves along tokens         */
+    static constexpr int NWAVE = TT == 1 ? 4 : 8;        /* 64-row tiles: 2 waves / SIMD */
+    static constexpr int WR = 4;                         /* waves along rows           */
+    static constexpr int WT = NWAVE / WR;                /* waves along tokens         */
     static constexpr int RBW = 8 / WR;                   /* 16-row blocks per wave     */
     static constexpr int TTW = TT / WT;                  /* 16-token tiles per wave    */
     static constexpr int OFF_S = ROWS * WB;
-    static constexpr int OFF_B = OFF_S + (FP4 ? ROWS * 8 : 0);
+    static constexpr int OFF_PAD = OFF_S + (FP4 ? ROWS * 8 : 0);   /* scale loads of waves 4+ */
+    static constexpr int OFF_B = OFF_PAD + (FP4 && NWAVE > 4 ? 256 : 0);
     static constexpr int STAGE = OFF_B + TOK * KS * 2;
     /* FP4 16-row tiles: 3 x 25 KiB, two workgroups per CU overlap each
      * other's pipeline ramp */
     static constexpr int NST = (FP4 && TT == 1) ? 2 : (FP4 || TT == 1) ? 3 : 2;
     static constexpr int LDS = NST * STAGE;
-    static constexpr int NW = ROWS * WB / 1024 / 4;      /* weight loads per wave per stage */
+    static constexpr int NW = ROWS * WB / 1024 / NWAVE;  /* weight loads per wave per stage */
     static constexpr int NS = FP4 ? 1 : 0;               /* scale loads                */
-    static constexpr int NB = TOK * KS * 2 / 1024 / 4;   /* token-row loads            */
+    static constexpr int NB = TOK * KS * 2 / 1024 / NWAVE;   /* token-row loads        */
+    static_assert(NW * NWAVE * 1024 == ROWS * WB && NB * NWAVE * 1024 == TOK * KS * 2, "load split");
     static constexpr int VM = NW + NS + NB;
     static_assert(LDS <= 160 * 1024, "LDS ring exceeds 160 KiB");
     static_assert((NST - 2) * VM <= 63, "vmcnt range");
@@ -501,7 +505,7 @@ __device__ __forceinline__ int bchunk(int gq, int sg)
 } // namespace
 
 template <int WF, bool SWIGLU, int TT>
-__global__ __launch_bounds__(256) void k_grouped2(GroupedArgs a)
+__global__ __launch_bounds__(512) void k_grouped2(GroupedArgs a)
 {
     using C = G2<WF, TT>;
     constexpr bool FP4 = C::FP4;
@@ -537,7 +541,7 @@ __global__ __launch_bounds__(256) void k_grouped2(GroupedArgs a)
     if (!qmat_matches<WF>(m1, N, K) || (SWIGLU && !qmat_matches<WF>(m3, N, K))) {
         if (threadIdx.x == 0) atomicOr(a.status, ST_BAD_DESCRIPTOR);
         const float nan = __builtin_nanf("");
-        for (int i = threadIdx.x; i < ntok * FEAT; i += 256) {
+        for (int i = threadIdx.x; i < ntok * FEAT; i += 64 * C::NWAVE) {
             const size_t o = (size_t)(r0 + i / FEAT) * N + f0 + i % FEAT;
             if constexpr (SWIGLU) ((uint16_t *)a.out)[o] = (uint16_t)f16_bits(nan);
             else ((float *)a.out)[o] = nan;
@@ -564,7 +568,7 @@ __global__ __launch_bounds__(256) void k_grouped2(GroupedArgs a)
     }
     const uint8_t *sbase = nullptr;
     if constexpr (FP4) {
-        const int r = 32 * wave + lane / 2;
+        const int r = 32 * (wave & 3) + lane / 2;          /* waves 4+ repeat rows into the pad */
         const bool up = SWIGLU && r >= 64;
         const int row = f0 + (SWIGLU ? (r & 63) : r);
         sbase = (const uint8_t *)(up ? m3.s : m1.s) + (size_t)row * (K / 32) + 4 * (lane & 1);
@@ -581,7 +585,8 @@ __global__ __launch_bounds__(256) void k_grouped2(GroupedArgs a)
     auto issue = [&](int stg, uint8_t *buf) {
 #pragma unroll
         for (int i = 0; i < C::NW; i++) dma16(wbase[i] + (size_t)stg * C::WB, buf + wdst[i]);
-        if constexpr (FP4) dma4(sbase + (size_t)stg * 8, buf + C::OFF_S + 256 * wave);
+        if constexpr (FP4)
+            dma4(sbase + (size_t)stg * 8, buf + (wave < 4 ? C::OFF_S + 256 * wave : C::OFF_PAD));
 #pragma unroll
         for (int i = 0; i < C::NB; i++)
             dma16(bbase[i] + (size_t)stg * KS, buf + C::OFF_B + 1024 * (wave * C::NB + i));
@@ -609,93 +614,104 @@ __global__ __launch_bounds__(256) void k_grouped2(GroupedArgs a)
 #pragma unroll
     for (int s0 = 0; s0 < C::NST - 1; s0++) issue(min(s0, last), lds + s0 * C::STAGE);
 
-    for (int st = 0; st < nst; st++) {
-        __builtin_amdgcn_s_waitcnt(0x0F70 | ((C::NST - 2) * C::VM & 15) | ((((C::NST - 2) * C::VM) >> 4) << 14));
-        __builtin_amdgcn_s_barrier();
-        asm volatile("" ::: "memory");
-        {
-            int nb = st + C::NST - 1;
-            nb = nb >= C::NST ? nb - C::NST * (nb / C::NST) : nb;
-            issue(min(st + C::NST - 1, last), lds + nb * C::STAGE);
-        }
-        const uint8_t *buf = lds + (st % C::NST) * C::STAGE;
-
-        /* token operands of this wave's tiles, all 8 steps */
-        h8 bop[C::TTW][8];
-#pragma unroll
-        for (int u = 0; u < C::TTW; u++) {
-            const int t = 16 * (wt * C::TTW + u) + rr;
-            const uint8_t *brow = buf + C::OFF_B + t * (KS * 2);
-#pragma unroll
-            for (int sg = 0; sg < 8; sg++)
-                bop[u][sg] = *(const h8 *)(brow + 16 * swz_b(t, bchunk<WF>(gq, sg)));
-        }
-        /* FP8 chunk scales: 2 blocks of 128 per stage, per matrix */
-        float fs[2][2] = {{1.0f, 1.0f}, {1.0f, 1.0f}};
-        if constexpr (!FP4) {
-            const int nb = f0 / 128, kbn = K / 128;
-#pragma unroll
-            for (int b = 0; b < 2; b++) {
-                const size_t si = (size_t)nb * kbn + 2 * st + b;
-                if constexpr (WF == FMT_FP8_E8M0) {
-                    fs[0][b] = dev_e8m0(ld_u8(m1.s, si));
-                    fs[1][b] = SWIGLU ? dev_e8m0(ld_u8(m3.s, si)) : 1.0f;
-                } else {
-                    fs[0][b] = ld_f32(m1.s, si);
-                    fs[1][b] = SWIGLU ? ld_f32(m3.s, si) : 1.0f;
-                }
+    /* The main loop, instantiated per count NT of this wave's live 16-token
+     * tiles so that the MFMA sequence of a stage is straight-line code (a
+     * branch per MFMA splits it into blocks the scheduler cannot overlap). */
+    auto run = [&](auto ntc) {
+        constexpr int NT = decltype(ntc)::value;
+        for (int st = 0; st < nst; st++) {
+            __builtin_amdgcn_s_waitcnt(0x0F70 | ((C::NST - 2) * C::VM & 15) | ((((C::NST - 2) * C::VM) >> 4) << 14));
+            __builtin_amdgcn_s_barrier();
+            asm volatile("" ::: "memory");
+            {
+                int nb = st + C::NST - 1;
+                nb = nb >= C::NST ? nb - C::NST * (nb / C::NST) : nb;
+                issue(min(st + C::NST - 1, last), lds + nb * C::STAGE);
             }
-        }
+            if constexpr (NT > 0) {
+                const uint8_t *buf = lds + (st % C::NST) * C::STAGE;
+
+                /* token operands of this wave's live tiles, all 8 steps */
+                h8 bop[NT][8];
 #pragma unroll
-        for (int i = 0; i < C::RBW; i++) {
-            const int r = 16 * blk[i] + rr;                /* staged row */
-            if constexpr (FP4) {
-                const uint2 sc8 = *(const uint2 *)(buf + C::OFF_S + r * 8);
+                for (int u = 0; u < NT; u++) {
+                    const int t = 16 * (wt * C::TTW + u) + rr;
+                    const uint8_t *brow = buf + C::OFF_B + t * (KS * 2);
 #pragma unroll
-                for (int h = 0; h < 2; h++) {
-                    const int c = 4 * h + gq;
-                    const u32x4 w16 = *(const u32x4 *)(buf + r * C::WB + 16 * swz_w4(r, c));
-                    const uint32_t sb = ((c < 4 ? sc8.x : sc8.y) >> (8 * (c & 3))) & 0xFFu;
-                    scale_bad |= (sb - 104u) > 36u;
-                    const float cs = dev_e8m0(sb);
-                    const u32x4 wv[2] = {w16, w16};
-#pragma unroll
-                    for (int s = 0; s < 4; s++) {
-                        const h8 av = a_operand<WF>(wv, cs, s);
-#pragma unroll
-                        for (int u = 0; u < C::TTW; u++)
-                            if (u < ntw) acc[i][u] = mfma16(av, bop[u][4 * h + s], acc[i][u]);
-                    }
+                    for (int sg = 0; sg < 8; sg++)
+                        bop[u][sg] = *(const h8 *)(brow + 16 * swz_b(t, bchunk<WF>(gq, sg)));
                 }
-            } else {
-                const float *fsm = fs[(SWIGLU && blk[i] >= 4) ? 1 : 0];
+                /* FP8 chunk scales: 2 blocks of 128 per stage, per matrix */
+                float fs[2][2] = {{1.0f, 1.0f}, {1.0f, 1.0f}};
+                if constexpr (!FP4) {
+                    const int nb = f0 / 128, kbn = K / 128;
 #pragma unroll
-                for (int b = 0; b < 2; b++) {              /* 128-K block of the stage */
-                    f4v part[C::TTW];
-#pragma unroll
-                    for (int u = 0; u < C::TTW; u++) part[u] = f4v{0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-                    for (int q2 = 0; q2 < 2; q2++) {
-                        const int q = 2 * b + q2;
-                        const int c = 4 * q + gq;
-                        const u32x4 w16 = *(const u32x4 *)(buf + r * C::WB + 16 * swz_w8(r, c));
-                        const u32x4 wv[2] = {w16, w16};
-#pragma unroll
-                        for (int s = 0; s < 2; s++) {
-                            const h8 av = a_operand<WF>(wv, 1.0f, s);   /* dwords 2s, 2s+1 */
-#pragma unroll
-                            for (int u = 0; u < C::TTW; u++)
-                                if (u < ntw) part[u] = mfma16(av, bop[u][2 * q + s], part[u]);
+                    for (int b = 0; b < 2; b++) {
+                        const size_t si = (size_t)nb * kbn + 2 * st + b;
+                        if constexpr (WF == FMT_FP8_E8M0) {
+                            fs[0][b] = dev_e8m0(ld_u8(m1.s, si));
+                            fs[1][b] = SWIGLU ? dev_e8m0(ld_u8(m3.s, si)) : 1.0f;
+                        } else {
+                            fs[0][b] = ld_f32(m1.s, si);
+                            fs[1][b] = SWIGLU ? ld_f32(m3.s, si) : 1.0f;
                         }
                     }
+                }
 #pragma unroll
-                    for (int u = 0; u < C::TTW; u++)
+                for (int i = 0; i < C::RBW; i++) {
+                    const int r = 16 * blk[i] + rr;            /* staged row */
+                    if constexpr (FP4) {
+                        const uint2 sc8 = *(const uint2 *)(buf + C::OFF_S + r * 8);
 #pragma unroll
-                        for (int e = 0; e < 4; e++) acc[i][u][e] = fmaf(part[u][e], fsm[b], acc[i][u][e]);
+                        for (int h = 0; h < 2; h++) {
+                            const int c = 4 * h + gq;
+                            const u32x4 w16 = *(const u32x4 *)(buf + r * C::WB + 16 * swz_w4(r, c));
+                            const uint32_t sb = ((c < 4 ? sc8.x : sc8.y) >> (8 * (c & 3))) & 0xFFu;
+                            scale_bad |= (sb - 104u) > 36u;
+                            const float cs = dev_e8m0(sb);
+                            const u32x4 wv[2] = {w16, w16};
+#pragma unroll
+                            for (int s = 0; s < 4; s++) {
+                                const h8 av = a_operand<WF>(wv, cs, s);
+#pragma unroll
+                                for (int u = 0; u < NT; u++) acc[i][u] = mfma16(av, bop[u][4 * h + s], acc[i][u]);
+                            }
+                        }
+                    } else {
+                        const float *fsm = fs[(SWIGLU && blk[i] >= 4) ? 1 : 0];
+#pragma unroll
+                        for (int b = 0; b < 2; b++) {          /* 128-K block of the stage */
+                            f4v part[NT];
+#pragma unroll
+                            for (int u = 0; u < NT; u++) part[u] = f4v{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+                            for (int q2 = 0; q2 < 2; q2++) {
+                                const int q = 2 * b + q2;
+                                const int c = 4 * q + gq;
+                                const u32x4 w16 = *(const u32x4 *)(buf + r * C::WB + 16 * swz_w8(r, c));
+                                const u32x4 wv[2] = {w16, w16};
+#pragma unroll
+                                for (int s = 0; s < 2; s++) {
+                                    const h8 av = a_operand<WF>(wv, 1.0f, s);   /* dwords 2s, 2s+1 */
+#pragma unroll
+                                    for (int u = 0; u < NT; u++) part[u] = mfma16(av, bop[u][2 * q + s], part[u]);
+                                }
+                            }
+#pragma unroll
+                            for (int u = 0; u < NT; u++)
+#pragma unroll
+                                for (int e = 0; e < 4; e++) acc[i][u][e] = fmaf(part[u][e], fsm[b], acc[i][u][e]);
+                        }
+                    }
                 }
             }
         }
-    }
+    };
+    if (ntw >= C::TTW) run(IC<C::TTW>{});
+    else if constexpr (C::TTW > 1) {
+        if (ntw == 1) run(IC<1>{});
+        else run(IC<0>{});
+    } else run(IC<0>{});
     __builtin_amdgcn_s_waitcnt(0x0F70);     /* trailing repeat loads drain before exit */
     if (scale_bad) atomicOr(a.status, ST_SCALE_RANGE);
 
@@ -719,6 +735,267 @@ __global__ __launch_bounds__(256) void k_grouped2(GroupedArgs a)
         } else {
 #pragma unroll
             for (int i = 0; i < C::RBW; i++)
+                *(f4v *)((float *)a.out + orow + f0 + 16 * blk[i] + 4 * gq) = acc[i][u];
+        }
+    }
+}
+
+/* ------------------------------------------- 128-token FP4 tiles (prefill) --- */
+
+/* For buckets of many tokens (the prefill MoE layer). Workgroup: 8 waves,
+ * 256 FP4 weight rows (gate/up: 128 w1 rows + the matching 128 w3 rows;
+ * down: 256 w2 rows) x 128 token rows; each wave owns 64 rows x 64 tokens
+ * (4 x 4 MFMA tiles), so one converted weight operand feeds 4 MFMAs and one
+ * token operand 4 more, which keeps both the conversions (VALU) and the LDS
+ * operand reads below the MFMA time.
+ *
+ * A stage is 128 reduction indices: 256 x 64 weight bytes, the rows' four
+ * E8M0 bytes, and 128 x 256 bytes of fp16 token rows; three stages in flight.
+ * Every operand arrives by buffer loads straight into LDS; token rows past
+ * the end of the bucket use an offset beyond the buffer, which the hardware
+ * answers with zeros and no memory traffic. Chunks are XOR-swizzled so that
+ * the 16 rows of an MFMA operand read hit distinct banks:
+ *   weight row r (64 B):  chunk c at slot c ^ ((r >> 2) & 3)
+ *   token row t (256 B):  chunk c at slot c ^ (t & 15)
+ * Reduction order: lane group gq's 16 weight bytes of a row (32 values, one
+ * E8M0 block) feed MFMA steps s = 0..3, 8 values each; the token side reads
+ * the same 8 indices, chunk 4 gq + s of the row. */
+namespace {
+
+struct G3 {
+    static constexpr int KS = 128;
+    static constexpr int ROWS = 256, TOK = 128, NWAVE = 8;
+    static constexpr int WB = KS / 2;                        /* FP4 bytes per row per stage */
+    static constexpr int OFF_S = ROWS * WB;                  /* E8M0: 256 B per wave        */
+    static constexpr int OFF_B = OFF_S + NWAVE * 256;
+    static constexpr int STAGE = OFF_B + TOK * KS * 2;
+    static constexpr int NST = 3;
+    static constexpr int LDS = NST * STAGE;
+    static constexpr int NW = ROWS * WB / 1024 / NWAVE;      /* 16-row weight loads per wave */
+    static constexpr int NB = TOK * KS * 2 / 1024 / NWAVE;   /* 4-row token loads per wave   */
+    static constexpr int VM = NW + 1 + NB;
+    static_assert(LDS <= 160 * 1024, "LDS ring exceeds 160 KiB");
+    static_assert(NW * NWAVE * 1024 == ROWS * WB && NB * NWAVE * 1024 == TOK * KS * 2, "load split");
+};
+
+constexpr uint32_t RSRC_WORD3 = 0x00020000u;      /* raw dword buffer, gfx9 */
+constexpr uint32_t OOB_OFFSET = 0x80000000u;      /* beyond every buffer    */
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t buf_rsrc(const void *p, uint32_t bytes)
+{
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(p), (short)0, (int)bytes, (int)RSRC_WORD3);
+}
+__device__ __forceinline__ void bdma16(__amdgpu_buffer_rsrc_t r, uint32_t voff, int soff, uint8_t *dst)
+{
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_void *)dst, 16, (int)voff, soff, 0, 0);
+}
+__device__ __forceinline__ void bdma4(__amdgpu_buffer_rsrc_t r, uint32_t voff, int soff, uint8_t *dst)
+{
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_void *)dst, 4, (int)voff, soff, 0, 0);
+}
+
+/* 8 e2m1 values (one dword, low nibble first) times 2^e -> fp16 operand */
+__device__ __forceinline__ h8 fp4_h8(uint32_t d, float sc)
+{
+    u32x4 v;
+    v.x = pk_f16_fp4(d, sc, 0);
+    v.y = pk_f16_fp4(d, sc, 1);
+    v.z = pk_f16_fp4(d, sc, 2);
+    v.w = pk_f16_fp4(d, sc, 3);
+    return __builtin_bit_cast(h8, v);
+}
+
+} // namespace
+
+template <bool SWIGLU>
+__global__ __launch_bounds__(512) void k_grouped3(GroupedArgs a)
+{
+    using C = G3;
+    constexpr int FEAT = SWIGLU ? 128 : 256;
+    extern __shared__ __align__(16) uint8_t lds[];
+    const int lane = threadIdx.x & 63;
+    const int wave = wave_in_group();
+    const int rr = lane & 15, gq = lane >> 4;
+    const int nslab = a.N / FEAT;
+    const int tile = blockIdx.x / nslab, slab = blockIdx.x - tile * nslab;
+
+    int r0, ntok;
+    DSV4QMat m1, m3;
+    if (a.table) {
+        const int E = a.n_experts;
+        if (tile >= ld_uniform(a.tile_pre, E)) return;            /* whole workgroup */
+        const int lo = ld_uniform(a.tile_grp, tile);
+        const int go = ld_uniform(a.grp_off, lo), ge = ld_uniform(a.grp_off, lo + 1);
+        r0 = go + (tile - ld_uniform(a.tile_pre, lo)) * C::TOK;
+        ntok = min(C::TOK, ge - r0);
+        const DSV4ExpertW e = ld_uniform(a.table, lo);
+        m1 = SWIGLU ? e.w1 : e.w2;
+        m3 = e.w3;
+    } else {
+        r0 = tile * C::TOK;
+        if (r0 >= a.nrows) return;
+        ntok = min(C::TOK, a.nrows - r0);
+        m1 = a.m1;
+        m3 = a.m3;
+    }
+    const int f0 = slab * FEAT;
+    const int K = a.K, N = a.N;
+    /* buffer loads need 16-byte aligned weights and 4-byte aligned scales */
+    const bool aligned = ((uintptr_t)m1.w & 15) == 0 && ((uintptr_t)m1.s & 3) == 0 &&
+                         (!SWIGLU || (((uintptr_t)m3.w & 15) == 0 && ((uintptr_t)m3.s & 3) == 0));
+    if (!qmat_matches<FMT_FP4_E8M0>(m1, N, K) || (SWIGLU && !qmat_matches<FMT_FP4_E8M0>(m3, N, K)) ||
+        !aligned) {
+        if (threadIdx.x == 0) atomicOr(a.status, ST_BAD_DESCRIPTOR);
+        const float nan = __builtin_nanf("");
+        for (int i = threadIdx.x; i < ntok * FEAT; i += 64 * C::NWAVE) {
+            const size_t o = (size_t)(r0 + i / FEAT) * N + f0 + i % FEAT;
+            if constexpr (SWIGLU) ((uint16_t *)a.out)[o] = (uint16_t)f16_bits(nan);
+            else ((float *)a.out)[o] = nan;
+        }
+        return;
+    }
+
+    /* ---- load plan: per-lane byte offsets into the buffers ---- */
+    const uint32_t rowb = (uint32_t)K / 2, srow = (uint32_t)K / 32;
+    const int nst = K / C::KS, last = nst - 1;
+    const __amdgpu_buffer_rsrc_t rw1 = buf_rsrc(m1.w, (uint32_t)N * rowb);
+    const __amdgpu_buffer_rsrc_t rs1 = buf_rsrc(m1.s, (uint32_t)N * srow);
+    const __amdgpu_buffer_rsrc_t rw3 = SWIGLU ? buf_rsrc(m3.w, (uint32_t)N * rowb) : rw1;
+    const __amdgpu_buffer_rsrc_t rs3 = SWIGLU ? buf_rsrc(m3.s, (uint32_t)N * srow) : rs1;
+    const __amdgpu_buffer_rsrc_t rb = buf_rsrc(a.B, (uint32_t)a.nrows * (uint32_t)K * 2u);
+    uint32_t wofs[C::NW];
+#pragma unroll
+    for (int i = 0; i < C::NW; i++) {
+        const int j = wave * C::NW + i;                 /* rows 16 j .. 16 j + 15 */
+        const int r = 16 * j + lane / 4;
+        const int c = (lane & 3) ^ ((r >> 2) & 3);
+        const int row = f0 + (SWIGLU ? (r & 127) : r);
+        wofs[i] = (uint32_t)row * rowb + 16u * c;
+    }
+    uint32_t sofs;
+    {
+        const int r = 32 * wave + (lane & 31);           /* lanes 32..63 repeat 0..31 */
+        const int row = f0 + (SWIGLU ? (r & 127) : r);
+        sofs = (uint32_t)row * srow;
+    }
+    uint32_t bofs[C::NB];
+#pragma unroll
+    for (int i = 0; i < C::NB; i++) {
+        const int j = wave * C::NB + i;                 /* token rows 4 j .. 4 j + 3 */
+        const int t = 4 * j + lane / 16;
+        const int c = (lane & 15) ^ (t & 15);
+        if (t < ntok) {
+            const int src = a.row_tok ? a.row_tok[r0 + t] : r0 + t;
+            bofs[i] = (uint32_t)src * (uint32_t)K * 2u + 16u * c;
+        } else {
+            bofs[i] = OOB_OFFSET;
+        }
+    }
+    /* wave-uniform: which matrix each weight load and the scale load read */
+    const bool up_s = SWIGLU && wave >= 4;
+    auto issue = [&](int stg, uint8_t *buf) {
+#pragma unroll
+        for (int i = 0; i < C::NW; i++) {
+            const bool up = SWIGLU && (wave * C::NW + i) >= 8;
+            bdma16(up ? rw3 : rw1, wofs[i], stg * C::WB, buf + 1024 * (wave * C::NW + i));
+        }
+        bdma4(up_s ? rs3 : rs1, sofs, stg * (C::KS / 32), buf + C::OFF_S + 256 * wave);
+#pragma unroll
+        for (int i = 0; i < C::NB; i++)
+            bdma16(rb, bofs[i], stg * C::KS * 2, buf + C::OFF_B + 1024 * (wave * C::NB + i));
+    };
+
+    /* ---- this wave's share: 4 row blocks x 4 token tiles ---- */
+    const int wr = wave & 3, wt = wave >> 2;
+    int blk[4];
+#pragma unroll
+    for (int i = 0; i < 4; i++) blk[i] = SWIGLU ? (i < 2 ? 2 * wr + i : 8 + 2 * wr + (i - 2)) : 4 * wr + i;
+    int ntw = 0;
+#pragma unroll
+    for (int u = 0; u < 4; u++) ntw += 64 * wt + 16 * u < ntok ? 1 : 0;
+
+    f4v acc[4][4];
+#pragma unroll
+    for (int i = 0; i < 4; i++)
+#pragma unroll
+        for (int u = 0; u < 4; u++) acc[i][u] = f4v{0.0f, 0.0f, 0.0f, 0.0f};
+    unsigned scale_bad = 0;
+
+#pragma unroll
+    for (int s0 = 0; s0 < C::NST - 1; s0++) issue(min(s0, last), lds + s0 * C::STAGE);
+
+    auto run = [&](auto ntc) {
+        constexpr int NT = decltype(ntc)::value;
+        for (int st = 0; st < nst; st++) {
+            __builtin_amdgcn_s_waitcnt(0x0F70 | ((C::NST - 2) * C::VM & 15) | ((((C::NST - 2) * C::VM) >> 4) << 14));
+            __builtin_amdgcn_s_barrier();
+            asm volatile("" ::: "memory");
+            {
+                int nb = st + C::NST - 1;
+                nb = nb >= C::NST ? nb - C::NST * (nb / C::NST) : nb;
+                issue(min(st + C::NST - 1, last), lds + nb * C::STAGE);
+            }
+            if constexpr (NT > 0) {
+                const uint8_t *buf = lds + (st % C::NST) * C::STAGE;
+                u32x4 wraw[4];
+                float cs[4];
+#pragma unroll
+                for (int i = 0; i < 4; i++) {
+                    const int r = 16 * blk[i] + rr;
+                    wraw[i] = *(const u32x4 *)(buf + r * C::WB + 16 * (gq ^ ((r >> 2) & 3)));
+                    const uint32_t sw = *(const uint32_t *)(buf + C::OFF_S + (r >> 5) * 256 + (r & 31) * 4);
+                    const uint32_t sb = (sw >> (8 * gq)) & 0xFFu;
+                    scale_bad |= (sb - 104u) > 36u;
+                    cs[i] = dev_e8m0(sb);
+                }
+#pragma unroll
+                for (int s = 0; s < 4; s++) {
+                    h8 bop[NT];
+#pragma unroll
+                    for (int u = 0; u < NT; u++) {
+                        const int t = 64 * wt + 16 * u + rr;
+                        bop[u] = *(const h8 *)(buf + C::OFF_B + t * (C::KS * 2) + 16 * ((4 * gq + s) ^ rr));
+                    }
+#pragma unroll
+                    for (int i = 0; i < 4; i++) {
+                        const uint32_t d = s == 0 ? wraw[i].x : s == 1 ? wraw[i].y : s == 2 ? wraw[i].z : wraw[i].w;
+                        const h8 av = fp4_h8(d, cs[i]);
+#pragma unroll
+                        for (int u = 0; u < NT; u++) acc[i][u] = mfma16(av, bop[u], acc[i][u]);
+                    }
+                }
+            }
+        }
+    };
+    switch (ntw) {
+    case 4: run(IC<4>{}); break;
+    case 3: run(IC<3>{}); break;
+    case 2: run(IC<2>{}); break;
+    case 1: run(IC<1>{}); break;
+    default: run(IC<0>{}); break;
+    }
+    __builtin_amdgcn_s_waitcnt(0x0F70);     /* trailing repeat loads drain before exit */
+    if (scale_bad) atomicOr(a.status, ST_SCALE_RANGE);
+
+#pragma unroll
+    for (int u = 0; u < 4; u++) {
+        const int t = 64 * wt + 16 * u + rr;
+        if (t >= ntok) continue;
+        const size_t orow = (size_t)(r0 + t) * N;
+        if constexpr (SWIGLU) {
+#pragma unroll
+            for (int i = 0; i < 2; i++) {
+                float m[4];
+#pragma unroll
+                for (int e = 0; e < 4; e++) m[e] = dev_swiglu(acc[i][u][e], acc[i + 2][u][e], a.limit);
+                uint2 pk;
+                pk.x = f16_bits(m[0]) | (f16_bits(m[1]) << 16);
+                pk.y = f16_bits(m[2]) | (f16_bits(m[3]) << 16);
+                *(uint2 *)((uint16_t *)a.out + orow + f0 + 16 * blk[i] + 4 * gq) = pk;
+            }
+        } else {
+#pragma unroll
+            for (int i = 0; i < 4; i++)
                 *(f4v *)((float *)a.out + orow + f0 + 16 * blk[i] + 4 * gq) = acc[i][u];
         }
     }
@@ -789,8 +1066,8 @@ static hipError_t grouped2(const GroupedArgs &a, long items, hipStream_t st)
         if (e != hipSuccess) return e;
         attr_done = true;
     }
-    constexpr int lds_bytes = G2<WF, TT>::LDS;
-    hipLaunchKernelGGL((k_grouped2<WF, SW, TT>), dim3((unsigned)items), dim3(256), lds_bytes, st, a);
+    constexpr int lds_bytes = G2<WF, TT>::LDS, threads = 64 * G2<WF, TT>::NWAVE;
+    hipLaunchKernelGGL((k_grouped2<WF, SW, TT>), dim3((unsigned)items), dim3(threads), lds_bytes, st, a);
     return hipGetLastError();
 }
 
@@ -806,9 +1083,33 @@ static hipError_t grouped_tt(const GroupedArgs &a, int tt, long items, hipStream
     return hipGetLastError();
 }
 
+template <bool SW>
+static hipError_t grouped3(const GroupedArgs &a, long items, hipStream_t st)
+{
+    static bool attr_done = false;
+    if (!attr_done) {
+        const hipError_t e = hipFuncSetAttribute((const void *)k_grouped3<SW>,
+                                                 hipFuncAttributeMaxDynamicSharedMemorySize, G3::LDS);
+        if (e != hipSuccess) return e;
+        attr_done = true;
+    }
+    constexpr int lds_bytes = G3::LDS, threads = 64 * G3::NWAVE;
+    hipLaunchKernelGGL((k_grouped3<SW>), dim3((unsigned)items), dim3(threads), lds_bytes, st, a);
+    return hipGetLastError();
+}
+
 hipError_t grouped_launch(int fmt, bool swiglu, int tt, const GroupedArgs &a, long max_tiles,
                           hipStream_t st)
 {
+    if (tt == 8) {
+        /* 128-token tiles: FP4 only; byte offsets of every buffer fit 31 bits */
+        const int feat = swiglu ? 128 : 256;
+        if (fmt != FMT_FP4_E8M0 || a.N % feat || a.K % G3::KS || max_tiles <= 0 || a.nrows <= 0 ||
+            (size_t)a.nrows * a.K * 2 >= (1u << 31) || (size_t)a.N * a.K / 2 >= (1u << 31))
+            return hipErrorInvalidValue;
+        const long items = max_tiles * (a.N / feat);
+        return swiglu ? grouped3<true>(a, items, st) : grouped3<false>(a, items, st);
+    }
     const int feat = swiglu ? 64 : 128;
     if (a.N % feat || a.K % KC || (tt != 1 && tt != 4) || max_tiles <= 0) return hipErrorInvalidValue;
     const long items = max_tiles * (a.N / feat);

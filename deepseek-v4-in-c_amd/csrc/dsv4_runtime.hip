@@ -584,9 +584,9 @@ int dsv4_hip_gemm_fp8q_dev(void *C, int out_bf16, const uint8_t *Aq, const float
 /* ------------------------------------------------------ grouped MoE --- */
 
 /* 16-row tiles when buckets are small (batched decode: few tokens per expert,
- * weight streaming dominates and occupancy matters), 64-row tiles otherwise
+ * weight streaming dominates and occupancy matters), 128-row tiles otherwise
  * (prefill: weights are reused across a tile's rows). */
-int grouped_tt(long pairs) { return pairs <= 4096 ? 1 : 4; }
+int grouped_tt(long pairs) { return pairs <= 4096 ? 1 : 8; }
 
 int enqueue_moe_grouped(float *out, const float *x, int n, const DSV4ExpertW *table,
                         int n_experts, const int *idx, const float *w, int topk,
@@ -594,7 +594,11 @@ int enqueue_moe_grouped(float *out, const float *x, int n, const DSV4ExpertW *ta
                         int inter, float limit, hipStream_t st)
 {
     const long P = (long)n * topk;
-    const int tt = grouped_tt(P);
+    int tt = grouped_tt(P);
+    /* the 128-row kernel takes 256 down rows per workgroup and 31-bit offsets */
+    if (tt == 8 && (hidden % 256 || (size_t)P * inter * 2 >= (1u << 31) ||
+                    (size_t)n * hidden * 2 >= (1u << 31) || (size_t)inter * hidden / 2 >= (1u << 31)))
+        tt = 4;
     const int trows = grouped_rows_per_tile(tt);
     size_t off = 0;
     auto take = [&](size_t b) { const size_t o = off; off += (b + 255) & ~(size_t)255; return o; };
@@ -628,10 +632,10 @@ int enqueue_moe_grouped(float *out, const float *x, int n, const DSV4ExpertW *ta
     GroupedArgs ga;
     memset(&ga, 0, sizeof ga);
     ga.table = table; ga.n_experts = n_experts; ga.grp_off = grp; ga.tile_pre = tp; ga.tile_grp = tg;
-    ga.row_tok = row; ga.B = x16; ga.K = hidden; ga.N = inter; ga.out = mid;
+    ga.row_tok = row; ga.nrows = n; ga.B = x16; ga.K = hidden; ga.N = inter; ga.out = mid;
     ga.limit = limit; ga.status = g.status;
     HIPCHK(grouped_launch(FMT_FP4_E8M0, true, tt, ga, max_tiles, st), "routed gate/up launch");
-    ga.row_tok = nullptr; ga.B = mid; ga.K = inter; ga.N = hidden; ga.out = y;
+    ga.row_tok = nullptr; ga.nrows = (int)P; ga.B = mid; ga.K = inter; ga.N = hidden; ga.out = y;
     HIPCHK(grouped_launch(FMT_FP4_E8M0, false, tt, ga, max_tiles, st), "routed down launch");
 
     float *ys = nullptr;

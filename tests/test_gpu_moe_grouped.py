@@ -102,7 +102,7 @@ def bf16_rows(gen, n, hidden):
 @pytest.mark.parametrize("n,topk,ne,shared_fmt", [
     (20, 4, 12, "fp8f32"),      # 16-row tiles, FP8 shared with fp32 block scales
     (7, 6, 16, "fp8e8m0"),      # FP8 shared with E8M0 scales, ragged buckets
-    (1100, 4, 8, "fp4"),        # 64-row tiles (more than 4096 pairs), FP4 shared
+    (1100, 4, 8, "fp4"),        # 128-row tiles (more than 4096 pairs), FP4 shared
     (33, 3, 5, None),           # no shared expert
 ])
 def test_grouped_small_shapes(lib, pkg, oracle, n, topk, ne, shared_fmt):
@@ -118,6 +118,37 @@ def test_grouped_small_shapes(lib, pkg, oracle, n, topk, ne, shared_fmt):
     tokens = range(n) if n <= 64 else rng.choice(n, 48, replace=False)
     want = oracle_tokens(oracle, experts, shared, x, idx, w, tokens)
     got = got[list(tokens)]
+    assert lib.status() == 0
+    assert np.all(np.isfinite(got))
+    e = rel_l2(got, want)
+    assert e <= REL_L2_TOL, f"rel L2 {e:.3e} (max abs {max_abs(got, want):.3e})"
+
+
+@pytest.mark.parametrize("n,topk,ne,zipf,hidden,inter", [
+    (1500, 6, 40, 1.2, 512, 256),   # 128-row tiles: skewed buckets, partial and empty tiles
+    (700, 8, 9, None, 768, 384),    # 3 down slabs, K = 384 (3 stages)
+    (4100, 1, 3, None, 256, 128),   # single stage (K = 128) down, many full tiles
+])
+def test_grouped_prefill_tiles(lib, pkg, oracle, n, topk, ne, zipf, hidden, inter):
+    """More than 4096 pairs: 128-row tiles, gate/up 128 features and down 256
+    features per workgroup; bucket sizes cover every count of live 16-row
+    tiles per wave (0..4)."""
+    gen = torch.Generator().manual_seed(n + ne)
+    dgen = torch.Generator(device=DEV).manual_seed(n + ne)
+    rng = np.random.default_rng(n * 3 + topk)
+    experts = [DevExpert(lib, pkg, "fp4", inter, hidden, dgen) for _ in range(ne)]
+    shared = DevExpert(lib, pkg, "fp8f32", inter, hidden, dgen)
+    x = bf16_rows(gen, n, hidden)
+    idx, w = routing(rng, n, topk, ne, zipf)
+    got = run_dev(lib, experts, shared, x, idx, w, hidden, inter)
+    counts = np.bincount(idx.ravel(), minlength=ne)
+    assert (counts % 128 > 0).sum() >= 2            # partial tiles exist
+    # tokens of the smallest and largest buckets plus a random sample
+    small = np.nonzero((idx == np.argmin(np.where(counts > 0, counts, 1 << 30))).any(1))[0][:8]
+    big = np.nonzero((idx == np.argmax(counts)).any(1))[0][-8:]
+    tokens = np.unique(np.concatenate([small, big, rng.choice(n, 32, replace=False)]))
+    want = oracle_tokens(oracle, experts, shared, x, idx, w, tokens)
+    got = got[tokens]
     assert lib.status() == 0
     assert np.all(np.isfinite(got))
     e = rel_l2(got, want)
