@@ -1,0 +1,1073 @@
+/* SPDX-License-Identifier: Apache-2.0 */
+/* dsv4_decode_mx.hip - decode matvec, expert gate/up (+ SwiGLU) and routed
+ * down (+ k-order combine) on the block-scaled MFMA of gfx950.
+ *
+ * What it replaces: the nt <= 31 bodies of fp8_n / fp4_n
+ * (src/10_compute/dsv4_matmul_fp8.c:55-155, src/10_compute/dsv4_matmul_fp4.c:
+ * 51-139), dsv4_expert_forward (src/10_compute/dsv4_ops.c:85-93) and the
+ * compute of dsv4_layer_moe (src/70_decode/dsv4_layer.c:57-116).
+ *
+ * ARITHMETIC
+ *   y[o] = sum_k W[o][k] x[k] runs on v_mfma_scale_f32_16x16x128_f8f6f4 with
+ *   the packed weights as the A operand exactly as stored (FP4 e2m1 or FP8
+ *   e4m3, 16 rows x 128 k per instruction) and their E8M0 block scales in the
+ *   hardware scale operand, so no instruction decodes a weight. fp32 block
+ *   scales (DSV4_WFP8_F32S) multiply each 128-k partial (one MFMA from zero)
+ *   into the fp32 accumulator.
+ *   The activations are the B operand. An fp32 activation is split exactly
+ *   into NPART e4m3 "parts", each with its own E8M0 scale per 32-element
+ *   block: part p is the round-to-nearest-even e4m3 of the block's residual
+ *   after parts 0..p-1, at the smallest power-of-two scale that keeps the
+ *   block's largest residual at or below 448. Every residual is exact in fp32
+ *   and each part removes at least four significant bits, so after four
+ *   parts what is left is below 2^-19 of the block maximum. The parts of one
+ *   token occupy four of the MFMA's sixteen B columns and the four column
+ *   results are added in a fixed order, so up to four tokens share one MFMA.
+ *   Every part accumulates in a column of its own, so the hardware's
+ *   alignment of products within an MFMA (about 14 bits below the largest
+ *   product of a group) is relative to that part's own magnitude.
+ *
+ * OPERAND LAYOUT (measured on gfx950)
+ *   Of a 128-k step, A lane l holds row l % 16: FP4 k in [32 g, +32) as 16
+ *   bytes (low nibble first), FP8 k in [16 g, +16) in bytes 0-15 and
+ *   [64 + 16 g, +16) in bytes 16-31, g = l / 16. B lane l holds column l % 16
+ *   with the FP8 layout. Scale lane l covers row (A) or column (B) l % 16 and
+ *   the 32-element block l / 16. Accumulator element e of lane l is row
+ *   4 (l / 16) + e, column l % 16. A chunk (128 k) of a row is 64 (FP4) or
+ *   128 (FP8) contiguous bytes, so four lanes of a row read it whole.
+ *
+ * SCHEDULE
+ *   A wave owns one 16-row tile and a contiguous range of chunks of K. It
+ *   issues its activation loads first, then its scale bytes, then every
+ *   weight chunk of its range (loads complete in issue order), splits its
+ *   activations into an LDS table in the B-operand layout while the weights
+ *   are in flight, and then runs one MFMA per chunk. The four waves of a
+ *   workgroup cover the four quarters of K of one tile and add their
+ *   partials through LDS in a fixed order.
+ *
+ * Bound: HBM (each weight byte is read once per call).
+ */
+#include "dsv4_internal.h"
+
+namespace dsv4 {
+
+namespace {
+
+typedef int v8i __attribute__((ext_vector_type(8)));
+typedef float v4f __attribute__((ext_vector_type(4)));
+
+constexpr int NPART = 4;                          /* e4m3 parts per activation */
+constexpr int TAB_DATA = 4 * NPART * 32;          /* operand bytes of one chunk */
+constexpr int TAB_CHUNK = TAB_DATA + 4 * NPART * 4; /* + one scale dword per (block, part) */
+constexpr int TAB_ZERO = 64;                      /* zero operand + unit scale */
+constexpr int E8M0_ONE = 127;
+constexpr int KSLICES = 4;                        /* waves per tile along K */
+
+/* The zero B operand and unit scale for columns that carry no token, in
+ * kernels whose split tables live in global memory. */
+__device__ uint32_t g_zero_operand[16] = {0, 0, 0, 0, 0, 0, 0, 0, E8M0_ONE, 0, 0, 0, 0, 0, 0, 0};
+
+template <int CTRL>
+__device__ __forceinline__ float dpp_f(float v)
+{
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, false));
+}
+
+/* E8M0 byte of the smallest power of two 2^e with amax / 2^e <= 448
+ * (448 = 1.75 * 2^8), for a finite amax >= 0; zero and fp32 subnormals take
+ * byte 0 (2^-127). */
+__device__ __forceinline__ int part_e8m0(float amax)
+{
+    const uint32_t b = __float_as_uint(amax);
+    const int f = (int)(b >> 23);
+    const int E = f - 8 + ((b & 0x7FFFFFu) > 0x600000u ? 1 : 0);
+    return f == 0 ? 0 : min(max(E, 0), 254);
+}
+
+__device__ __forceinline__ uint32_t e4m3_pk4(float a, float b, float c, float d)
+{
+    uint32_t w = (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(a, b, 0, false);
+    return (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(c, d, (int)w, true);
+}
+
+/* Split the eight activations of one lane -- a quarter of a 32-element block
+ * whose four quarters sit in the four lanes of a DPP quad -- into NPART e4m3
+ * parts: v = sum_p e4m3(code[p]) * 2^(E[p] - 127) + (the final residual).
+ * code[p] holds the eight codes in element order, four per dword. */
+__device__ __forceinline__ void split8(float (&v)[8], uint32_t (&code)[NPART][2], int (&E)[NPART])
+{
+#pragma unroll
+    for (int p = 0; p < NPART; p++) {
+        float m = fabsf(v[0]);
+#pragma unroll
+        for (int i = 1; i < 8; i++) m = fmaxf(m, fabsf(v[i]));
+        m = fmaxf(m, dpp_f<DPP_QUAD_1032>(m));
+        m = fmaxf(m, dpp_f<DPP_QUAD_2301>(m));
+        E[p] = part_e8m0(m);
+        const int e = E[p] - E8M0_ONE;
+        float s[8];
+#pragma unroll
+        for (int i = 0; i < 8; i++) s[i] = ldexpf(v[i], -e);
+        code[p][0] = e4m3_pk4(s[0], s[1], s[2], s[3]);
+        code[p][1] = e4m3_pk4(s[4], s[5], s[6], s[7]);
+        if (p + 1 < NPART) {
+#pragma unroll
+            for (int d = 0; d < 2; d++) {
+                const f32x2 lo = __builtin_amdgcn_cvt_pk_f32_fp8((int)code[p][d], false);
+                const f32x2 hi = __builtin_amdgcn_cvt_pk_f32_fp8((int)code[p][d], true);
+                v[4 * d + 0] -= ldexpf(lo.x, e);
+                v[4 * d + 1] -= ldexpf(lo.y, e);
+                v[4 * d + 2] -= ldexpf(hi.x, e);
+                v[4 * d + 3] -= ldexpf(hi.y, e);
+            }
+        }
+    }
+}
+
+/* Split table of one wave's chunks for its tokens (LDS, wave-private).
+ * For token t and chunk j (of the wave's ncw) the TAB_CHUNK bytes at
+ * (t * ncw + j) * TAB_CHUNK hold:
+ *   for lane group h and part p, 32 operand bytes at (h * NPART + p) * 32:
+ *     bytes 0-15 = part p of the chunk's elements 16 h .. 16 h + 15,
+ *     bytes 16-31 = part p of elements 64 + 16 h .. 64 + 16 h + 15;
+ *   for 32-element block b of the chunk and part p, the E8M0 byte as a dword
+ *     at TAB_DATA + (b * NPART + p) * 4.
+ * After the last token's chunks: TAB_ZERO bytes, a zero operand and a unit
+ * scale, read by the columns no token uses.
+ * A "unit" is eight consecutive elements; unit u of the wave is token
+ * u / (16 ncw), chunk (u / 16) % ncw, elements 8 (u % 16) .. +8 of the chunk. */
+template <int UPL>
+struct XUnits {
+    float v[UPL][8];
+};
+
+template <int UPL, int NTHR = 64>
+__device__ __forceinline__ void load_units(XUnits<UPL> &xu, const float *x, size_t x_ld,
+                                           int ntok, int c0, int ncw, int lane)
+{
+    const int units = ntok * ncw * 16;
+#pragma unroll
+    for (int i = 0; i < UPL; i++) {
+        int u = NTHR * i + lane;
+        u = u < units ? u : 0;
+        const int per = ncw > 0 ? ncw * 16 : 16;
+        const int t = u / per, rem = u - t * per;
+        const float *src = x + (size_t)t * x_ld + (size_t)(c0 + (rem >> 4)) * 128 + 8 * (rem & 15);
+        const f32x4 a = *(const f32x4 *)src, b = *(const f32x4 *)(src + 4);
+        xu.v[i][0] = a.x; xu.v[i][1] = a.y; xu.v[i][2] = a.z; xu.v[i][3] = a.w;
+        xu.v[i][4] = b.x; xu.v[i][5] = b.y; xu.v[i][6] = b.z; xu.v[i][7] = b.w;
+    }
+}
+
+template <int UPL, int NTHR = 64>
+__device__ __forceinline__ void store_units(uint8_t *tab, XUnits<UPL> &xu, int ntok, int ncw, int lane)
+{
+    const int units = ntok * ncw * 16;
+#pragma unroll
+    for (int i = 0; i < UPL; i++) {
+        const int u = NTHR * i + lane;
+        if (u < units) {                            /* whole quads: units % 16 == 0 */
+            uint32_t code[NPART][2];
+            int E[NPART];
+            split8(xu.v[i], code, E);
+            const int per = ncw * 16;
+            const int t = u / per, rem = u - t * per;
+            const int j = rem >> 4, q16 = rem & 15, kk = 8 * q16;
+            uint8_t *cb = tab + (size_t)(t * ncw + j) * TAB_CHUNK;
+            const int h = (kk & 63) >> 4, half = kk >> 6;
+#pragma unroll
+            for (int p = 0; p < NPART; p++)
+                *(uint2 *)(cb + (h * NPART + p) * 32 + half * 16 + (kk & 15)) =
+                    make_uint2(code[p][0], code[p][1]);
+            if ((q16 & 3) == 0) {
+#pragma unroll
+                for (int p = 0; p < NPART; p++)
+                    *(int *)(cb + TAB_DATA + ((q16 >> 2) * NPART + p) * 4) = E[p];
+            }
+        }
+    }
+    if (lane < TAB_ZERO / 4)
+        ((uint32_t *)(tab + (size_t)ntok * ncw * TAB_CHUNK))[lane] = lane == 8 ? E8M0_ONE : 0u;
+}
+
+/* B operand source of this lane: column col = 4 t + p is part p of token t. */
+struct BSrc {
+    const uint8_t *d;   /* operand bytes of chunk 0 */
+    const uint8_t *s;   /* scale dword of chunk 0   */
+    int step;           /* bytes per chunk          */
+    const uint8_t *z;   /* zero operand, unit scale at z + 32 */
+};
+
+__device__ __forceinline__ BSrc lds_bsrc(const uint8_t *tab, int ntok, int ncw, int lane)
+{
+    const int col = lane & 15, h = lane >> 4, t = col >> 2, p = col & 3;
+    BSrc b;
+    b.z = tab + (size_t)ntok * ncw * TAB_CHUNK;
+    if (t < ntok) {
+        const uint8_t *cb = tab + (size_t)t * ncw * TAB_CHUNK;
+        b.d = cb + (h * NPART + p) * 32;
+        b.s = cb + TAB_DATA + (h * NPART + p) * 4;
+        b.step = TAB_CHUNK;
+    } else {
+        b.d = b.z;
+        b.s = b.z + 32;
+        b.step = 0;
+    }
+    return b;
+}
+
+/* Chunk j's operand; j >= ncw (a wave with fewer chunks than CPW) reads the
+ * zero operand, so its MFMA adds zero (the A side re-reads a chunk of the same
+ * row, so a NaN weight there is already in the row's sum). */
+__device__ __forceinline__ v8i ld_b(const BSrc &b, int j, int ncw)
+{
+    const uint8_t *p = j < ncw ? b.d + j * b.step : b.z;
+    const u32x4 lo = *(const u32x4 *)p;
+    const u32x4 hi = *(const u32x4 *)(p + 16);
+    v8i r;
+    r[0] = (int)lo.x; r[1] = (int)lo.y; r[2] = (int)lo.z; r[3] = (int)lo.w;
+    r[4] = (int)hi.x; r[5] = (int)hi.y; r[6] = (int)hi.z; r[7] = (int)hi.w;
+    return r;
+}
+
+__device__ __forceinline__ int ld_bs(const BSrc &b, int j, int ncw)
+{
+    return *(const int *)(j < ncw ? b.s + j * b.step : b.z + 32);
+}
+
+/* A operand of one chunk: FP4 16 bytes, FP8 32 bytes. */
+template <bool FP4>
+struct AChunk {
+    u32x4 q[FP4 ? 1 : 2];
+};
+
+template <bool FP4>
+__device__ __forceinline__ void ld_a(AChunk<FP4> &a, const uint8_t *wrow, int c, int g)
+{
+    if constexpr (FP4) {
+        a.q[0] = ld_stream16(wrow + 64 * c + 16 * g);
+    } else {
+        a.q[0] = ld_stream16(wrow + 128 * c + 16 * g);
+        a.q[1] = ld_stream16(wrow + 128 * c + 64 + 16 * g);
+    }
+}
+
+template <bool FP4>
+__device__ __forceinline__ v4f mfma_a(const AChunk<FP4> &a, const v8i &b, const v4f &c, int sa, int sb)
+{
+    v8i av;
+    av[0] = (int)a.q[0].x; av[1] = (int)a.q[0].y; av[2] = (int)a.q[0].z; av[3] = (int)a.q[0].w;
+    if constexpr (FP4) {
+        av[4] = 0; av[5] = 0; av[6] = 0; av[7] = 0;
+        return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(av, b, c, 4, 0, 0, sa, 0, sb);
+    } else {
+        av[4] = (int)a.q[1].x; av[5] = (int)a.q[1].y; av[6] = (int)a.q[1].z; av[7] = (int)a.q[1].w;
+        return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(av, b, c, 0, 0, 0, sa, 0, sb);
+    }
+}
+
+/* The scale side of one matrix for a wave's chunk range: FP4 a byte per lane
+ * and chunk (row l % 16, block 4 c + l / 16); FP8 one value per chunk for the
+ * whole tile (the 16 rows lie in one row block), E8M0 byte or fp32 bits. */
+template <int FMT, int CPW>
+struct AScales {
+    uint32_t v[CPW];
+};
+
+template <int FMT, int CPW>
+__device__ __forceinline__ void ld_ascales(AScales<FMT, CPW> &s, const void *S, int sc_cols,
+                                           int blk_r, int row, int tile_row0, int c0, int ncw, int g,
+                                           int row_max)
+{
+    if constexpr (FMT == FMT_FP4_E8M0) {
+        /* Row r's bytes for the wave's chunks, [4 c0, 4 c0 + 4 CPW), are
+         * contiguous: CPW / 4 lanes load them as 16-byte pieces (one load per
+         * row piece instead of one per chunk), then every lane fetches the
+         * dword of chunk j from the lane holding it and keeps its block's byte.
+         * Needs whole pieces inside the row and 16-byte aligned rows. */
+        constexpr int NL = CPW / 4;
+        const uint8_t *S8 = (const uint8_t *)S;
+        bool wide = CPW >= 4 && ncw == CPW && (sc_cols & 15) == 0 && (c0 & 3) == 0 &&
+                    ((uintptr_t)S8 & 15u) == 0;
+        wide = __builtin_amdgcn_readfirstlane((int)wide) != 0;
+        if constexpr (CPW >= 4) {
+            if (wide) {
+                const int lane = threadIdx.x & 63;
+                const int L = lane % (16 * NL);
+                const int rl = min(tile_row0 + L / NL, row_max);   /* tile row loaded by this lane */
+                const u32x4 piece = *gptr((const u32x4 *)(S8 + (size_t)(rl / blk_r) * sc_cols +
+                                                          4 * c0 + 16 * (L % NL)));
+#pragma unroll
+                for (int j = 0; j < CPW; j++) {
+                    const int src = ((lane & 15) * NL + j / 4) * 4;
+                    const uint32_t d = (uint32_t)__builtin_amdgcn_ds_bpermute(src, (int)piece[j & 3]);
+                    s.v[j] = (d >> (8 * g)) & 0xFFu;
+                }
+                return;
+            }
+        }
+#pragma unroll
+        for (int j = 0; j < CPW; j++) {
+            const int c = c0 + (j < ncw ? j : 0);
+            s.v[j] = ld_u8(S, (size_t)(row / blk_r) * sc_cols + 4 * c + g);
+        }
+    } else {
+#pragma unroll
+        for (int j = 0; j < CPW; j++) {
+            const int c = c0 + (j < ncw ? j : 0);
+            if constexpr (FMT == FMT_FP8_E8M0) s.v[j] = ld_u8(S, (size_t)(tile_row0 / blk_r) * sc_cols + c);
+            else s.v[j] = gptr((const uint32_t *)S)[(size_t)(tile_row0 / blk_r) * sc_cols + c];
+        }
+    }
+}
+
+/* acc += W[tile rows][chunks] . B over the wave's CPW chunk slots; slots
+ * j >= ncw multiply the zero operand. Straight-line: every register index
+ * is a compile-time constant. */
+template <int FMT, int CPW>
+__device__ __forceinline__ v4f mma_rows(const AChunk<FMT == FMT_FP4_E8M0> (&a)[CPW],
+                                        const AScales<FMT, CPW> &s, const BSrc &bs, int ncw)
+{
+    constexpr bool FP4 = FMT == FMT_FP4_E8M0;
+    v4f acc = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int j = 0; j < CPW; j++) {
+        const v8i b = ld_b(bs, j, ncw);
+        const int sb = ld_bs(bs, j, ncw);
+        if constexpr (FMT == FMT_FP8_F32S) {
+            const v4f zero = {0.0f, 0.0f, 0.0f, 0.0f};
+            const v4f p = mfma_a<FP4>(a[j], b, zero, E8M0_ONE, sb);
+            const float sw = __uint_as_float(s.v[j]);
+#pragma unroll
+            for (int e = 0; e < 4; e++) acc[e] = fmaf(p[e], sw, acc[e]);
+        } else {
+            acc = mfma_a<FP4>(a[j], b, acc, (int)s.v[j], sb);
+        }
+    }
+    return acc;
+}
+
+/* Sum the four part columns of every token: afterwards the lane of column
+ * 4 t (of each 16-lane group h) holds token t's rows 4 h .. 4 h + 3. */
+__device__ __forceinline__ void sum_parts(v4f &acc)
+{
+#pragma unroll
+    for (int e = 0; e < 4; e++) {
+        acc[e] = acc[e] + dpp_f<DPP_QUAD_1032>(acc[e]);
+        acc[e] = acc[e] + dpp_f<DPP_QUAD_2301>(acc[e]);
+    }
+}
+
+template <int FMT>
+__device__ __forceinline__ bool mx_desc_ok(const DSV4QMat &m, int rows, int cols)
+{
+    const int want = FMT == FMT_FP4_E8M0 ? DSV4_WFP4
+                   : FMT == FMT_FP8_F32S ? DSV4_WFP8_F32S : DSV4_WFP8;
+    const int blk_c = FMT == FMT_FP4_E8M0 ? 32 : 128;
+    const bool br = FMT == FMT_FP4_E8M0 ? m.blk_r > 0 : (m.blk_r > 0 && m.blk_r % 16 == 0);
+    return m.wdt == want && m.rows == rows && m.cols == cols && m.blk_c == blk_c && br &&
+           m.w != nullptr && m.s != nullptr && ((uintptr_t)m.w & 15u) == 0 &&
+           (FMT != FMT_FP8_F32S || ((uintptr_t)m.s & 3u) == 0);
+}
+
+__device__ __forceinline__ float qnan_f() { return __uint_as_float(0x7FC00000u); }
+
+/* ------------------------------------------------------------- GEMV --- */
+
+template <int FMT, int CPW, int NT>
+__global__ __launch_bounds__(256) void k_gemv_mx(GemvMxArgs a)
+{
+    extern __shared__ __align__(16) uint8_t lds[];
+    constexpr bool FP4 = FMT == FMT_FP4_E8M0;
+    const int lane = threadIdx.x & 63;
+    const int wave = wave_in_group();
+    const int r0 = blockIdx.x * 16;
+    const int t0 = blockIdx.y * a.tpg;
+    const int ntok = min(a.tpg, a.nt - t0);
+    const int nc = a.cols / 128;
+    const int c0 = wave * a.ncw;
+    const int ncw = max(0, min(a.ncw, nc - c0));
+    const int cb0 = ncw > 0 ? c0 : 0;                      /* loads stay inside the row */
+    const int g = lane >> 4;
+    const int row = min(r0 + (lane & 15), a.rows - 1);
+    const uint8_t *wrow = a.W + (size_t)row * a.row_bytes;
+    const size_t tab_bytes = (size_t)a.tpg * a.ncw * TAB_CHUNK + TAB_ZERO;
+    uint8_t *tab = lds + wave * tab_bytes;
+    float *red = (float *)(lds + KSLICES * tab_bytes);     /* [KSLICES][tpg][16] */
+    constexpr int UPL = (NT * CPW * 16 + 63) / 64;
+
+    XUnits<UPL> xu;
+    load_units<UPL>(xu, a.x + (size_t)t0 * a.x_ld, a.x_ld, ntok, cb0, ncw, lane);
+    DSV4_ORDER();
+    AScales<FMT, CPW> sc;
+    ld_ascales<FMT, CPW>(sc, a.S, a.sc_cols, a.blk_r, row, r0, cb0, ncw, g, a.rows - 1);
+    DSV4_ORDER();
+    AChunk<FP4> w[CPW];
+#pragma unroll
+    for (int j = 0; j < CPW; j++) ld_a<FP4>(w[j], wrow, cb0 + (j < ncw ? j : 0), g);
+    DSV4_ORDER();
+    store_units<UPL>(tab, xu, ntok, ncw, lane);
+    v4f acc = mma_rows<FMT, CPW>(w, sc, lds_bsrc(tab, ntok, ncw, lane), ncw);
+    sum_parts(acc);
+    const int col = lane & 15;
+    if ((col & 3) == 0 && (col >> 2) < ntok) {
+#pragma unroll
+        for (int e = 0; e < 4; e++) red[(wave * a.tpg + (col >> 2)) * 16 + 4 * g + e] = acc[e];
+    }
+    __syncthreads();
+    const int tid = threadIdx.x;
+    if (tid < ntok * 16) {
+        const int t = tid >> 4, rr = tid & 15;
+        float s = red[t * 16 + rr];
+#pragma unroll
+        for (int k = 1; k < KSLICES; k++) s += red[(k * a.tpg + t) * 16 + rr];
+        if (r0 + rr < a.rows) a.y[(size_t)(t0 + t) * a.y_ld + r0 + rr] = s;
+    }
+}
+
+/* ----------------------------------------------------- expert gate/up --- */
+
+/* Eight waves: two 16-row tiles of w1 and w3 x four quarters of K. One
+ * workgroup per (slot, 32-row group). Writes mid = SwiGLU(w1.x, w3.x) and,
+ * when a.msplit is set, the split table of mid for the down projection. */
+template <int FMT, int CPW>
+__device__ __forceinline__ void gateup_mx_body(const GateUpMxArgs &a)
+{
+    extern __shared__ __align__(16) uint8_t lds[];
+    constexpr bool FP4 = FMT == FMT_FP4_E8M0;
+    const int lane = threadIdx.x & 63;
+    const int wave = wave_in_group();
+    const int tile = wave >> 2, slice = wave & 3;
+    const int groups = a.inter / 32;
+    const int slot = blockIdx.x / groups;
+    const int j0 = (blockIdx.x - slot * groups) * 32;        /* first mid row of the group */
+    const int nc = a.hidden / 128;
+    const int c0 = slice * a.ncw;
+    const int ncw = max(0, min(a.ncw, nc - c0));
+    const int cb0 = ncw > 0 ? c0 : 0;                      /* loads stay inside the row */
+    const int g = lane >> 4;
+    const int r0 = j0 + 16 * tile;
+    const int row = r0 + (lane & 15);
+    const size_t tab_bytes = (size_t)a.ncw * TAB_CHUNK + TAB_ZERO;
+    uint8_t *tab = lds + wave * tab_bytes;
+    float *red = (float *)(lds + 8 * tab_bytes);               /* [2 tiles][4][2 mats][16] */
+    float *mid = a.mid + (size_t)slot * a.mid_ld;
+    constexpr int UPL = (CPW * 16 + 63) / 64;
+
+    DSV4ExpertW e;
+    unsigned bad = 0;
+    if (a.use_direct) {
+        e = a.direct;
+    } else {
+        const int id = ld_uniform(a.idx, slot);
+        if (id < 0 || id >= a.n_experts) bad = ST_BAD_EXPERT_ID;
+        else e = ld_uniform(a.table, id);
+    }
+    if (!bad && (!mx_desc_ok<FMT>(e.w1, a.inter, a.hidden) || !mx_desc_ok<FMT>(e.w3, a.inter, a.hidden)))
+        bad = ST_BAD_DESCRIPTOR;
+    if (bad) {
+        if (threadIdx.x == 0) atomicOr(a.status, bad);
+        if (threadIdx.x < 32) mid[j0 + threadIdx.x] = qnan_f();
+        /* NaN block scales (E8M0 255) make the down projection of this slot NaN */
+        if (a.msplit && threadIdx.x < NPART)
+            *(int *)(a.msplit + (size_t)slot * a.msplit_ld + (size_t)(j0 >> 7) * TAB_CHUNK +
+                     TAB_DATA + (((j0 >> 5) & 3) * NPART + threadIdx.x) * 4) = 255;
+        return;
+    }
+    const int row_bytes = FP4 ? a.hidden / 2 : a.hidden;
+    const int sc_cols = FP4 ? a.hidden / 32 : a.hidden / 128;
+    const uint8_t *w1r = (const uint8_t *)e.w1.w + (size_t)row * row_bytes;
+    const uint8_t *w3r = (const uint8_t *)e.w3.w + (size_t)row * row_bytes;
+
+    XUnits<UPL> xu;
+    load_units<UPL>(xu, a.x, 0, 1, cb0, ncw, lane);
+    DSV4_ORDER();
+    AScales<FMT, CPW> s1, s3;
+    ld_ascales<FMT, CPW>(s1, e.w1.s, sc_cols, e.w1.blk_r, row, r0, cb0, ncw, g, a.inter - 1);
+    ld_ascales<FMT, CPW>(s3, e.w3.s, sc_cols, e.w3.blk_r, row, r0, cb0, ncw, g, a.inter - 1);
+    DSV4_ORDER();
+    AChunk<FP4> w1[CPW], w3[CPW];
+#pragma unroll
+    for (int j = 0; j < CPW; j++) {
+        const int c = cb0 + (j < ncw ? j : 0);
+        ld_a<FP4>(w1[j], w1r, c, g);
+        ld_a<FP4>(w3[j], w3r, c, g);
+    }
+    DSV4_ORDER();
+    store_units<UPL>(tab, xu, 1, ncw, lane);
+    const BSrc bs = lds_bsrc(tab, 1, ncw, lane);
+    v4f gacc = mma_rows<FMT, CPW>(w1, s1, bs, ncw);
+    v4f uacc = mma_rows<FMT, CPW>(w3, s3, bs, ncw);
+    sum_parts(gacc);
+    sum_parts(uacc);
+    if ((lane & 15) == 0) {
+#pragma unroll
+        for (int e2 = 0; e2 < 4; e2++) {
+            red[((tile * 4 + slice) * 2 + 0) * 16 + 4 * g + e2] = gacc[e2];
+            red[((tile * 4 + slice) * 2 + 1) * 16 + 4 * g + e2] = uacc[e2];
+        }
+    }
+    __syncthreads();
+    if (wave != 0) return;
+
+    /* lanes 0..31: mid row j0 + lane; lanes 32..63 carry zeros through the
+     * block reductions below */
+    float v = 0.0f;
+    if (lane < 32) {
+        const int t = lane >> 4, rr = lane & 15;
+        float gs = red[((t * 4 + 0) * 2 + 0) * 16 + rr], us = red[((t * 4 + 0) * 2 + 1) * 16 + rr];
+#pragma unroll
+        for (int k = 1; k < 4; k++) {
+            gs += red[((t * 4 + k) * 2 + 0) * 16 + rr];
+            us += red[((t * 4 + k) * 2 + 1) * 16 + rr];
+        }
+        v = dev_swiglu(gs, us, a.limit);
+        mid[j0 + lane] = v;
+    }
+    if (!a.msplit) return;
+
+    /* split of the 32-element block j0 / 32 of mid, in the down projection's
+     * table layout (chunk j0 / 128, block (j0 / 32) % 4) */
+    uint8_t *cb = a.msplit + (size_t)slot * a.msplit_ld + (size_t)(j0 >> 7) * TAB_CHUNK;
+    const int b4 = (j0 >> 5) & 3;
+    const int kk = 32 * b4 + (lane & 31);
+    uint8_t *dst = cb + ((kk & 63) >> 4) * NPART * 32 + (kk >> 6) * 16 + (kk & 15);
+#pragma unroll
+    for (int p = 0; p < NPART; p++) {
+        float m = fabsf(v);
+#pragma unroll
+        for (int o = 1; o < 32; o <<= 1) m = fmaxf(m, __shfl_xor(m, o));
+        const int E = part_e8m0(m);
+        const int ex = E - E8M0_ONE;
+        const uint32_t q = (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(ldexpf(v, -ex), 0.0f, 0, false) & 0xFFu;
+        if (lane < 32) dst[p * 32] = (uint8_t)q;
+        if (lane == 0) *(int *)(cb + TAB_DATA + (b4 * NPART + p) * 4) = E;
+        v -= ldexpf(__builtin_amdgcn_cvt_pk_f32_fp8((int)q, false)[0], ex);
+    }
+}
+
+/* Four waves per SIMD (two workgroups per CU, every workgroup of a 6-expert
+ * decode resident at once) for FP4 with up to eight chunks per wave; the
+ * larger variants keep their registers. */
+template <int FMT, int CPW>
+__global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) void k_gateup_mx(GateUpMxArgs a)
+{
+    gateup_mx_body<FMT, CPW>(a);
+}
+
+template <int FMT, int CPW>
+__global__ __launch_bounds__(512) void k_gateup_mx_wide(GateUpMxArgs a)
+{
+    gateup_mx_body<FMT, CPW>(a);
+}
+
+/* ------------------------------------------------- routed down + combine --- */
+
+/* One workgroup per 16 output rows; two waves per routed expert k, each over
+ * half of the inter dimension, reading the split table that k_gateup_mx wrote
+ * for slot k. After the barrier the first 16 lanes combine in k order:
+ * out = 0; out += w[k] * y_k (product and sum separately rounded); out += shared. */
+template <int CPW>
+__global__ __launch_bounds__(1024) void k_down_mx(DownMxArgs a)
+{
+    __shared__ float ylds[16][2][16];
+    const int lane = threadIdx.x & 63;
+    const int wave = wave_in_group();
+    const int k = wave >> 1, half = wave & 1;
+    const int r0 = blockIdx.x * 16;
+    const int nc = a.inter / 128;
+    const int c0 = half * a.ncw;
+    const int ncw = max(0, min(a.ncw, nc - c0));
+    const int cb0 = ncw > 0 ? c0 : 0;                      /* loads stay inside the row */
+    const int g = lane >> 4, col = lane & 15;
+    const int row = min(r0 + col, a.hidden - 1);
+    const int row_bytes = a.inter / 2, sc_cols = a.inter / 32;
+
+    unsigned bad = 0;
+    DSV4QMat m;
+    const int id = ld_uniform(a.idx, k);
+    if (id < 0 || id >= a.n_experts) bad = ST_BAD_EXPERT_ID;
+    else {
+        m = ld_uniform(a.table, id).w2;
+        if (!mx_desc_ok<FMT_FP4_E8M0>(m, a.hidden, a.inter)) bad = ST_BAD_DESCRIPTOR;
+    }
+    float mine[4] = {qnan_f(), qnan_f(), qnan_f(), qnan_f()};
+    if (!bad) {
+        /* B: columns 0..3 are the four parts of slot k's mid */
+        const uint8_t *tb = a.msplit + (size_t)k * a.msplit_ld;
+        const uint8_t *zero = (const uint8_t *)g_zero_operand;
+        const bool live = col < NPART;
+        const uint8_t *bd = live ? tb + (g * NPART + col) * 32 : zero;
+        const uint8_t *bsc = live ? tb + TAB_DATA + (g * NPART + col) * 4 : zero + 32;
+        const int step = live ? TAB_CHUNK : 0;
+        v8i bv[CPW];
+        int bsv[CPW];
+#pragma unroll
+        for (int j = 0; j < CPW; j++) {
+            /* slots past the wave's chunks read the zero operand (adds zero) */
+            const uint8_t *pd = j < ncw ? bd + (size_t)(cb0 + j) * step : zero;
+            const uint8_t *ps = j < ncw ? bsc + (size_t)(cb0 + j) * step : zero + 32;
+            const u32x4 lo = *gptr((const u32x4 *)pd);
+            const u32x4 hi = *gptr((const u32x4 *)(pd + 16));
+            bv[j][0] = (int)lo.x; bv[j][1] = (int)lo.y; bv[j][2] = (int)lo.z; bv[j][3] = (int)lo.w;
+            bv[j][4] = (int)hi.x; bv[j][5] = (int)hi.y; bv[j][6] = (int)hi.z; bv[j][7] = (int)hi.w;
+            bsv[j] = *gptr((const int *)ps);
+        }
+        DSV4_ORDER();
+        AScales<FMT_FP4_E8M0, CPW> sc;
+        ld_ascales<FMT_FP4_E8M0, CPW>(sc, m.s, sc_cols, m.blk_r, row, r0, cb0, ncw, g, a.hidden - 1);
+        DSV4_ORDER();
+        AChunk<true> w[CPW];
+        const uint8_t *wrow = (const uint8_t *)m.w + (size_t)row * row_bytes;
+#pragma unroll
+        for (int j = 0; j < CPW; j++) ld_a<true>(w[j], wrow, cb0 + (j < ncw ? j : 0), g);
+        DSV4_ORDER();
+        v4f acc = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int j = 0; j < CPW; j++) acc = mfma_a<true>(w[j], bv[j], acc, (int)sc.v[j], bsv[j]);
+        sum_parts(acc);
+#pragma unroll
+        for (int e = 0; e < 4; e++) mine[e] = acc[e];
+    } else if (threadIdx.x == 64 * wave && half == 0) {
+        atomicOr(a.status, bad);
+    }
+    if (col == 0) {
+#pragma unroll
+        for (int e = 0; e < 4; e++) ylds[k][half][4 * g + e] = mine[e];
+    }
+    __syncthreads();
+    if (wave != 0 || lane >= 16 || r0 + lane >= a.hidden) return;
+    float o = 0.0f;
+    for (int kk = 0; kk < a.topk; kk++) {
+        const float y = ylds[kk][0][lane] + ylds[kk][1][lane];
+        o = __fadd_rn(o, __fmul_rn(ld_uniform(a.w, kk), y));
+    }
+    if (a.shared) o = __fadd_rn(o, a.shared[r0 + lane]);
+    a.out[r0 + lane] = o;
+}
+
+/* ------------------------------------------ FP4 chunk-pair kernels --- */
+
+/* One MFMA covers 8 weight rows x 2 chunks: A rows 0-7 are the tile's rows at
+ * chunk 2m, A rows 8-15 the same rows at chunk 2m + 1, so each load
+ * instruction reads 128 contiguous bytes (one cache line) of 8 rows. B
+ * columns 0-3 are the activation parts of chunk 2m, columns 4-7 those of
+ * chunk 2m + 1, columns 8-15 zero. Of the 16 x 16 result, rows 0-7 x columns
+ * 0-3 (even chunks) and rows 8-15 x columns 4-7 (odd chunks) are the wanted
+ * partial dot products; the two cross blocks are discarded. After the
+ * column sums, lane 16 q (q = 0, 1) holds rows 4 q + e of the even chunks and
+ * lane 16 q + 4 (q = 2, 3) rows 4 (q - 2) + e of the odd chunks.
+ * Lane geometry: A row r8 = lane & 7, chunk parity par = (lane >> 3) & 1,
+ * 32-element block g = lane >> 4. */
+
+template <int NP>
+struct APairs {
+    u32x4 q[NP];
+    uint32_t s[NP];
+};
+
+/* A operand and E8M0 scale of NP chunk pairs starting at chunk c0 of row
+ * `row` (FP4, rows row_bytes apart, scale rows sc_cols bytes apart). The
+ * scales of a row's 2 NP chunks are 8 NP contiguous bytes: with NP >= 2,
+ * NP / 2 lanes per row load them as 16-byte pieces and every lane fetches
+ * its two candidate dwords from the loading lane. */
+template <int NP>
+__device__ __forceinline__ void ld_pairs_scales(APairs<NP> &a, const uint8_t *S, int sc_cols, int blk_r,
+                                                int row, int tile_row0, int row_max, int c0, int lane)
+{
+    const int par = (lane >> 3) & 1, g = lane >> 4;
+    bool wide = NP >= 2 && (sc_cols & 15) == 0 && ((4 * c0) & 15) == 0 && ((uintptr_t)S & 15u) == 0;
+    wide = __builtin_amdgcn_readfirstlane((int)wide) != 0;
+    if constexpr (NP >= 2) {
+        if (wide) {
+            constexpr int NPC = NP / 2;                       /* 16-byte pieces per row */
+            const int L = lane % (8 * NPC);
+            const int rl = min(tile_row0 + L / NPC, row_max);
+            const u32x4 piece = *gptr((const u32x4 *)(S + (size_t)(rl / blk_r) * sc_cols + 4 * c0 + 16 * (L % NPC)));
+#pragma unroll
+            for (int m = 0; m < NP; m++) {
+                const int src = ((lane & 7) * NPC + m / 2) * 4;
+                const uint32_t d0 = (uint32_t)__builtin_amdgcn_ds_bpermute(src, (int)piece[2 * (m & 1)]);
+                const uint32_t d1 = (uint32_t)__builtin_amdgcn_ds_bpermute(src, (int)piece[2 * (m & 1) + 1]);
+                a.s[m] = ((par ? d1 : d0) >> (8 * g)) & 0xFFu;
+            }
+            return;
+        }
+    }
+#pragma unroll
+    for (int m = 0; m < NP; m++)
+        a.s[m] = ld_u8(S, (size_t)(row / blk_r) * sc_cols + 4 * (c0 + 2 * m + par) + g);
+}
+
+template <int NP>
+__device__ __forceinline__ void ld_pairs_w(APairs<NP> &a, const uint8_t *wrow, int c0, int lane)
+{
+    const int par = (lane >> 3) & 1, g = lane >> 4;
+#pragma unroll
+    for (int m = 0; m < NP; m++) a.q[m] = ld_stream16(wrow + 64 * (c0 + 2 * m + par) + 16 * g);
+}
+
+/* B operand of pair m from a split table laid out per chunk (TAB_CHUNK bytes
+ * per chunk from `tab`, chunk index relative to the table's first chunk). */
+struct BPair {
+    const uint8_t *d, *s;   /* chunk 0 of this lane's column, or the zero operand */
+    int step;               /* bytes per chunk pair (0 for zero columns) */
+};
+
+__device__ __forceinline__ BPair bpair_src(const uint8_t *tab, int c0, const uint8_t *zero, int lane)
+{
+    const int col = lane & 15, h = lane >> 4;
+    BPair b;
+    if (col < 8) {
+        const uint8_t *cb = tab + (size_t)(c0 + (col >> 2)) * TAB_CHUNK;
+        b.d = cb + (h * NPART + (col & 3)) * 32;
+        b.s = cb + TAB_DATA + (h * NPART + (col & 3)) * 4;
+        b.step = 2 * TAB_CHUNK;
+    } else {
+        b.d = zero;
+        b.s = zero + 32;
+        b.step = 0;
+    }
+    return b;
+}
+
+/* Column sums of a chunk-pair accumulator and its wanted quadrants, written
+ * as 8 even-chunk and 8 odd-chunk row partials to dst[0..7], dst[8..15]. */
+__device__ __forceinline__ void store_pair_partials(v4f acc, float *dst, int lane)
+{
+    sum_parts(acc);
+    const int q = lane >> 4, col = lane & 15;
+    if (col == 0 && q < 2) {
+#pragma unroll
+        for (int e = 0; e < 4; e++) dst[4 * q + e] = acc[e];
+    }
+    if (col == 4 && q >= 2) {
+#pragma unroll
+        for (int e = 0; e < 4; e++) dst[8 + 4 * (q - 2) + e] = acc[e];
+    }
+}
+
+/* Gate/up + SwiGLU for FP4 experts with hidden = 512 NP. Eight waves: four
+ * 8-row tiles x two halves of K (NP chunk pairs each); one workgroup per
+ * (slot, 32-row group). The workgroup splits x once into LDS (one unit of
+ * eight elements per thread for hidden 4096) and every wave reads its half
+ * from there. Writes mid and, when a.msplit is set, mid's split table. */
+template <int NP>
+__global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) void k_gateup_px(GateUpMxArgs a)
+{
+    extern __shared__ __align__(16) uint8_t lds[];
+    constexpr int NC = 4 * NP;                         /* chunks of hidden */
+    constexpr int UPL = (NC * 16 + 511) / 512;
+    const int lane = threadIdx.x & 63;
+    const int wave = wave_in_group();
+    const int tile = wave >> 1, hh = wave & 1;
+    const int groups = a.inter / 32;
+    const int slot = blockIdx.x / groups;
+    const int j0 = (blockIdx.x - slot * groups) * 32;
+    const int r0 = j0 + 8 * tile;
+    const int row = r0 + (lane & 7);
+    const int c0 = hh * 2 * NP;
+    uint8_t *tab = lds;                                /* NC chunks + zero operand */
+    float *red = (float *)(lds + NC * TAB_CHUNK + TAB_ZERO);   /* [4 tiles][2 halves][2 mats][16] */
+    float *mid = a.mid + (size_t)slot * a.mid_ld;
+
+    DSV4ExpertW e;
+    unsigned bad = 0;
+    if (a.use_direct) {
+        e = a.direct;
+    } else {
+        const int id = ld_uniform(a.idx, slot);
+        if (id < 0 || id >= a.n_experts) bad = ST_BAD_EXPERT_ID;
+        else e = ld_uniform(a.table, id);
+    }
+    if (!bad && (!mx_desc_ok<FMT_FP4_E8M0>(e.w1, a.inter, a.hidden) ||
+                 !mx_desc_ok<FMT_FP4_E8M0>(e.w3, a.inter, a.hidden)))
+        bad = ST_BAD_DESCRIPTOR;
+    if (bad) {
+        if (threadIdx.x == 0) atomicOr(a.status, bad);
+        if (threadIdx.x < 32) mid[j0 + threadIdx.x] = qnan_f();
+        if (a.msplit && threadIdx.x < NPART)
+            *(int *)(a.msplit + (size_t)slot * a.msplit_ld + (size_t)(j0 >> 7) * TAB_CHUNK +
+                     TAB_DATA + (((j0 >> 5) & 3) * NPART + threadIdx.x) * 4) = 255;
+        return;
+    }
+    const int row_bytes = a.hidden / 2, sc_cols = a.hidden / 32;
+
+    XUnits<UPL> xu;
+    load_units<UPL, 512>(xu, a.x, 0, 1, 0, NC, (int)threadIdx.x);
+    DSV4_ORDER();
+    APairs<NP> w1, w3;
+    ld_pairs_scales<NP>(w1, (const uint8_t *)e.w1.s, sc_cols, e.w1.blk_r, row, r0, a.inter - 1, c0, lane);
+    ld_pairs_scales<NP>(w3, (const uint8_t *)e.w3.s, sc_cols, e.w3.blk_r, row, r0, a.inter - 1, c0, lane);
+    DSV4_ORDER();
+    ld_pairs_w<NP>(w1, (const uint8_t *)e.w1.w + (size_t)row * row_bytes, c0, lane);
+    ld_pairs_w<NP>(w3, (const uint8_t *)e.w3.w + (size_t)row * row_bytes, c0, lane);
+    DSV4_ORDER();
+    store_units<UPL, 512>(tab, xu, 1, NC, (int)threadIdx.x);
+    __builtin_amdgcn_s_waitcnt(0xC07F);                /* lgkmcnt(0): own LDS writes done */
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+    const BPair bp = bpair_src(tab, c0, tab + NC * TAB_CHUNK, lane);
+    v4f gacc = {0.0f, 0.0f, 0.0f, 0.0f}, uacc = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int m = 0; m < NP; m++) {
+        const u32x4 lo = *(const u32x4 *)(bp.d + m * bp.step);
+        const u32x4 hi = *(const u32x4 *)(bp.d + m * bp.step + 16);
+        const int sb = *(const int *)(bp.s + m * bp.step);
+        v8i b;
+        b[0] = (int)lo.x; b[1] = (int)lo.y; b[2] = (int)lo.z; b[3] = (int)lo.w;
+        b[4] = (int)hi.x; b[5] = (int)hi.y; b[6] = (int)hi.z; b[7] = (int)hi.w;
+        AChunk<true> c1, c3;
+        c1.q[0] = w1.q[m];
+        c3.q[0] = w3.q[m];
+        gacc = mfma_a<true>(c1, b, gacc, (int)w1.s[m], sb);
+        uacc = mfma_a<true>(c3, b, uacc, (int)w3.s[m], sb);
+    }
+    store_pair_partials(gacc, red + ((tile * 2 + hh) * 2 + 0) * 16, lane);
+    store_pair_partials(uacc, red + ((tile * 2 + hh) * 2 + 1) * 16, lane);
+    __syncthreads();
+    if (wave != 0) return;
+
+    float v = 0.0f;
+    if (lane < 32) {
+        const int t = lane >> 3, rr = lane & 7;
+        const float *p0 = red + ((t * 2 + 0) * 2) * 16, *p1 = red + ((t * 2 + 1) * 2) * 16;
+        const float gs = ((p0[rr] + p0[8 + rr]) + p1[rr]) + p1[8 + rr];
+        const float us = ((p0[16 + rr] + p0[24 + rr]) + p1[16 + rr]) + p1[24 + rr];
+        v = dev_swiglu(gs, us, a.limit);
+        mid[j0 + lane] = v;
+    }
+    if (!a.msplit) return;
+    uint8_t *cb = a.msplit + (size_t)slot * a.msplit_ld + (size_t)(j0 >> 7) * TAB_CHUNK;
+    const int b4 = (j0 >> 5) & 3;
+    const int kk = 32 * b4 + (lane & 31);
+    uint8_t *dst = cb + ((kk & 63) >> 4) * NPART * 32 + (kk >> 6) * 16 + (kk & 15);
+#pragma unroll
+    for (int p = 0; p < NPART; p++) {
+        float m = fabsf(v);
+#pragma unroll
+        for (int o = 1; o < 32; o <<= 1) m = fmaxf(m, __shfl_xor(m, o));
+        const int E = part_e8m0(m);
+        const int ex = E - E8M0_ONE;
+        const uint32_t q = (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(ldexpf(v, -ex), 0.0f, 0, false) & 0xFFu;
+        if (lane < 32) dst[p * 32] = (uint8_t)q;
+        if (lane == 0) *(int *)(cb + TAB_DATA + (b4 * NPART + p) * 4) = E;
+        v -= ldexpf(__builtin_amdgcn_cvt_pk_f32_fp8((int)q, false)[0], ex);
+    }
+}
+
+/* Routed FP4 down projections (inter = 256 NP) with the k-order combine. One
+ * workgroup per 16 output rows, two waves (8-row tiles) per routed expert k,
+ * each over all of inter, reading slot k's split table. */
+template <int NP>
+__global__ __launch_bounds__(1024) void k_down_px(DownMxArgs a)
+{
+    __shared__ float ylds[8][2][16];
+    const int lane = threadIdx.x & 63;
+    const int wave = wave_in_group();
+    const int k = wave >> 1, t = wave & 1;
+    const int r0 = blockIdx.x * 16 + 8 * t;
+    const int row = min(r0 + (lane & 7), a.hidden - 1);
+    const int row_bytes = a.inter / 2, sc_cols = a.inter / 32;
+
+    unsigned bad = 0;
+    DSV4QMat m;
+    const int id = ld_uniform(a.idx, k);
+    if (id < 0 || id >= a.n_experts) bad = ST_BAD_EXPERT_ID;
+    else {
+        m = ld_uniform(a.table, id).w2;
+        if (!mx_desc_ok<FMT_FP4_E8M0>(m, a.hidden, a.inter)) bad = ST_BAD_DESCRIPTOR;
+    }
+    float part[16];
+#pragma unroll
+    for (int i = 0; i < 16; i++) part[i] = qnan_f();
+    if (!bad) {
+        const BPair bp = bpair_src(a.msplit + (size_t)k * a.msplit_ld, 0,
+                                   (const uint8_t *)g_zero_operand, lane);
+        v8i bv[NP];
+        int bs[NP];
+#pragma unroll
+        for (int mm = 0; mm < NP; mm++) {
+            const u32x4 lo = *gptr((const u32x4 *)(bp.d + (size_t)mm * bp.step));
+            const u32x4 hi = *gptr((const u32x4 *)(bp.d + (size_t)mm * bp.step + 16));
+            bv[mm][0] = (int)lo.x; bv[mm][1] = (int)lo.y; bv[mm][2] = (int)lo.z; bv[mm][3] = (int)lo.w;
+            bv[mm][4] = (int)hi.x; bv[mm][5] = (int)hi.y; bv[mm][6] = (int)hi.z; bv[mm][7] = (int)hi.w;
+            bs[mm] = *gptr((const int *)(bp.s + (size_t)mm * bp.step));
+        }
+        DSV4_ORDER();
+        APairs<NP> w;
+        ld_pairs_scales<NP>(w, (const uint8_t *)m.s, sc_cols, m.blk_r, row, r0, a.hidden - 1, 0, lane);
+        DSV4_ORDER();
+        ld_pairs_w<NP>(w, (const uint8_t *)m.w + (size_t)row * row_bytes, 0, lane);
+        DSV4_ORDER();
+        v4f acc = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int mm = 0; mm < NP; mm++) {
+            AChunk<true> c;
+            c.q[0] = w.q[mm];
+            acc = mfma_a<true>(c, bv[mm], acc, (int)w.s[mm], bs[mm]);
+        }
+        store_pair_partials(acc, &ylds[k][t][0], lane);
+    } else {
+        if (lane == 0 && t == 0) atomicOr(a.status, bad);
+        if (lane < 16) ylds[k][t][lane] = qnan_f();
+    }
+    __syncthreads();
+    if (wave != 0 || lane >= 16 || blockIdx.x * 16 + lane >= a.hidden) return;
+    const int tt = lane >> 3, rr = lane & 7;
+    float o = 0.0f;
+    for (int kk = 0; kk < a.topk; kk++) {
+        const float y = ylds[kk][tt][rr] + ylds[kk][tt][8 + rr];
+        o = __fadd_rn(o, __fmul_rn(ld_uniform(a.w, kk), y));
+    }
+    if (a.shared) o = __fadd_rn(o, a.shared[blockIdx.x * 16 + lane]);
+    a.out[blockIdx.x * 16 + lane] = o;
+}
+
+/* ------------------------------------------------------------ launches --- */
+
+constexpr int cpw_for(int nch) { return nch <= 1 ? 1 : nch <= 2 ? 2 : nch <= 4 ? 4 : nch <= 8 ? 8 : 16; }
+
+/* Tokens per token group: at most four (sixteen B columns), and at most
+ * 16 / CPW so the four split tables of a workgroup stay near 37 KiB. */
+template <int FMT, int CPW, int NT>
+hipError_t gemv_mx_nt(GemvMxArgs a, hipStream_t st)
+{
+    a.tpg = NT;
+    const size_t tab = (size_t)NT * a.ncw * TAB_CHUNK + TAB_ZERO;
+    const size_t lds = KSLICES * tab + (size_t)KSLICES * NT * 16 * 4;
+    const dim3 grid((unsigned)((a.rows + 15) / 16), (unsigned)((a.nt + NT - 1) / NT));
+    hipLaunchKernelGGL((k_gemv_mx<FMT, CPW, NT>), grid, dim3(256), lds, st, a);
+    return hipGetLastError();
+}
+
+template <int FMT, int CPW>
+hipError_t gemv_mx_k(GemvMxArgs a, hipStream_t st)
+{
+    constexpr int TPG = CPW >= 16 ? 1 : (16 / CPW > 4 ? 4 : 16 / CPW);
+    if (a.nt == 1) return gemv_mx_nt<FMT, CPW, 1>(a, st);
+    if constexpr (TPG >= 2) {
+        if (a.nt == 2 || TPG == 2) return gemv_mx_nt<FMT, CPW, 2>(a, st);
+    }
+    if constexpr (TPG >= 4) return gemv_mx_nt<FMT, CPW, 4>(a, st);
+    return gemv_mx_nt<FMT, CPW, 1>(a, st);
+}
+
+template <int FMT>
+hipError_t gemv_mx_fmt(GemvMxArgs a, hipStream_t st)
+{
+    switch (cpw_for(a.ncw)) {
+    case 1: return gemv_mx_k<FMT, 1>(a, st);
+    case 2: return gemv_mx_k<FMT, 2>(a, st);
+    case 4: return gemv_mx_k<FMT, 4>(a, st);
+    case 8: return gemv_mx_k<FMT, 8>(a, st);
+    default:
+        if constexpr (FMT == FMT_FP4_E8M0) return gemv_mx_k<FMT, 16>(a, st);
+        return hipErrorInvalidValue;
+    }
+}
+
+template <int FMT, int CPW>
+hipError_t gateup_mx_k(const GateUpMxArgs &a, hipStream_t st)
+{
+    const size_t lds = 8 * ((size_t)a.ncw * TAB_CHUNK + TAB_ZERO) + 2 * 4 * 2 * 16 * 4;
+    const dim3 grid((unsigned)(a.nslots * (a.inter / 32)));
+    if constexpr (FMT == FMT_FP4_E8M0 && CPW <= 8)
+        hipLaunchKernelGGL((k_gateup_mx<FMT, CPW>), grid, dim3(512), lds, st, a);
+    else
+        hipLaunchKernelGGL((k_gateup_mx_wide<FMT, CPW>), grid, dim3(512), lds, st, a);
+    return hipGetLastError();
+}
+
+template <int NP>
+hipError_t gateup_px_k(const GateUpMxArgs &a, hipStream_t st)
+{
+    const size_t lds = (size_t)4 * NP * TAB_CHUNK + TAB_ZERO + 4 * 2 * 2 * 16 * 4;
+    const dim3 grid((unsigned)(a.nslots * (a.inter / 32)));
+    hipLaunchKernelGGL((k_gateup_px<NP>), grid, dim3(512), lds, st, a);
+    return hipGetLastError();
+}
+
+template <int FMT>
+hipError_t gateup_mx_fmt(const GateUpMxArgs &a, hipStream_t st)
+{
+    if constexpr (FMT == FMT_FP4_E8M0) {
+        switch (a.hidden) {                 /* chunk-pair kernel: hidden = 512 NP */
+        case 512: return gateup_px_k<1>(a, st);
+        case 1024: return gateup_px_k<2>(a, st);
+        case 2048: return gateup_px_k<4>(a, st);
+        case 4096: return gateup_px_k<8>(a, st);
+        default: break;
+        }
+    }
+    switch (cpw_for(a.ncw)) {
+    case 1: return gateup_mx_k<FMT, 1>(a, st);
+    case 2: return gateup_mx_k<FMT, 2>(a, st);
+    case 4: return gateup_mx_k<FMT, 4>(a, st);
+    case 8: return gateup_mx_k<FMT, 8>(a, st);
+    default:
+        if constexpr (FMT == FMT_FP4_E8M0) return gateup_mx_k<FMT, 16>(a, st);
+        return hipErrorInvalidValue;
+    }
+}
+
+} // namespace
+
+/* chunks per wave for a K of `cols`, 0 when the MFMA path does not take it */
+int gemv_mx_ncw(int fmt, int cols)
+{
+    if (cols <= 0 || cols % 128) return 0;
+    const int ncw = (cols / 128 + KSLICES - 1) / KSLICES;
+    return ncw <= (fmt == FMT_FP4_E8M0 ? 16 : 8) ? ncw : 0;
+}
+
+size_t mx_split_bytes(int inter) { return (size_t)(inter / 128) * TAB_CHUNK; }
+
+hipError_t gemv_mx_launch(int fmt, GemvMxArgs a, hipStream_t st)
+{
+    a.ncw = gemv_mx_ncw(fmt, a.cols);
+    if (!a.ncw || a.nt <= 0) return hipErrorInvalidValue;
+    switch (fmt) {
+    case FMT_FP8_E8M0: return gemv_mx_fmt<FMT_FP8_E8M0>(a, st);
+    case FMT_FP8_F32S: return gemv_mx_fmt<FMT_FP8_F32S>(a, st);
+    case FMT_FP4_E8M0: return gemv_mx_fmt<FMT_FP4_E8M0>(a, st);
+    default: return hipErrorInvalidValue;
+    }
+}
+
+hipError_t gateup_mx_launch(int fmt, GateUpMxArgs a, hipStream_t st)
+{
+    a.ncw = gemv_mx_ncw(fmt, a.hidden);
+    if (!a.ncw || a.inter % 128) return hipErrorInvalidValue;
+    switch (fmt) {
+    case FMT_FP8_E8M0: return gateup_mx_fmt<FMT_FP8_E8M0>(a, st);
+    case FMT_FP8_F32S: return gateup_mx_fmt<FMT_FP8_F32S>(a, st);
+    case FMT_FP4_E8M0: return gateup_mx_fmt<FMT_FP4_E8M0>(a, st);
+    default: return hipErrorInvalidValue;
+    }
+}
+
+hipError_t down_mx_launch(DownMxArgs a, hipStream_t st)
+{
+    if (a.topk < 1 || a.topk > 8 || a.inter % 128 || a.inter > 2048 || a.hidden <= 0)
+        return hipErrorInvalidValue;
+    const dim3 grid((unsigned)((a.hidden + 15) / 16)), block(128 * a.topk);
+    switch (a.inter) {                      /* chunk-pair kernel: inter = 256 NP */
+    case 256: hipLaunchKernelGGL((k_down_px<1>), grid, block, 0, st, a); return hipGetLastError();
+    case 512: hipLaunchKernelGGL((k_down_px<2>), grid, block, 0, st, a); return hipGetLastError();
+    case 1024: hipLaunchKernelGGL((k_down_px<4>), grid, block, 0, st, a); return hipGetLastError();
+    case 2048: hipLaunchKernelGGL((k_down_px<8>), grid, block, 0, st, a); return hipGetLastError();
+    default: break;
+    }
+    a.ncw = (a.inter / 128 + 1) / 2;
+    switch (cpw_for(a.ncw)) {
+    case 1: hipLaunchKernelGGL((k_down_mx<1>), grid, block, 0, st, a); break;
+    case 2: hipLaunchKernelGGL((k_down_mx<2>), grid, block, 0, st, a); break;
+    case 4: hipLaunchKernelGGL((k_down_mx<4>), grid, block, 0, st, a); break;
+    case 8: hipLaunchKernelGGL((k_down_mx<8>), grid, block, 0, st, a); break;
+    default: return hipErrorInvalidValue;      /* inter > 2048: 1024 threads cannot hold 16 chunks */
+    }
+    return hipGetLastError();
+}
+
+} // namespace dsv4

@@ -115,6 +115,65 @@ struct DownArgs {
 int down_groups(int hidden);
 hipError_t down_launch(const DownArgs &a, hipStream_t st);
 
+/* ------------------------------------------- decode on the MFMA --- */
+/* y = W . x for nt tokens (x rows x_ld floats apart, y rows y_ld apart) on
+ * the block-scaled MFMA; cols % 128 == 0, FP8 blk_r % 16 == 0, x 16-byte
+ * aligned. ncw and tpg are set by the launcher. */
+struct GemvMxArgs {
+    const uint8_t *W;
+    const void *S;
+    const float *x;
+    float *y;
+    int rows, cols, row_bytes, sc_cols, blk_r;
+    int nt, x_ld, y_ld;
+    int ncw, tpg;
+};
+/* chunks of 128 columns per wave, 0 when the MFMA path does not take `cols` */
+int gemv_mx_ncw(int fmt, int cols);
+hipError_t gemv_mx_launch(int fmt, GemvMxArgs a, hipStream_t st);
+
+/* Gate/up + SwiGLU for `nslots` experts (like GateUpArgs); also writes the
+ * split table of each slot's mid (msplit + slot * msplit_ld) when msplit is
+ * set. inter % 128 == 0, hidden % 128 == 0. */
+struct GateUpMxArgs {
+    const DSV4ExpertW *table;
+    const int *idx;
+    int n_experts;
+    DSV4ExpertW direct;
+    int use_direct;
+    int nslots;
+    const float *x;
+    float *mid;
+    int mid_ld;
+    uint8_t *msplit;
+    size_t msplit_ld;
+    int inter, hidden;
+    float limit;
+    unsigned *status;
+    int ncw;
+};
+hipError_t gateup_mx_launch(int fmt, GateUpMxArgs a, hipStream_t st);
+
+/* Routed FP4 down projections from the split tables of mid, with the k-order
+ * combine (+ shared); topk <= 8. */
+struct DownMxArgs {
+    const DSV4ExpertW *table;
+    const int *idx;
+    const float *w;
+    int n_experts;
+    int topk;
+    const uint8_t *msplit;
+    size_t msplit_ld;
+    const float *shared;
+    float *out;
+    int inter, hidden;
+    unsigned *status;
+    int ncw;
+};
+hipError_t down_mx_launch(DownMxArgs a, hipStream_t st);
+/* bytes of one slot's split table for a K of `inter` */
+size_t mx_split_bytes(int inter);
+
 /* ---------------------------------------------------- prefill GEMM --- */
 /* C[m][n] = sum_k A[m][k] W[n][k]: Aq e4m3 [M][K] with fp32 Sa [M][K/128];
  * W e4m3 [N][K] with Sw [N/128][K/128] fp32 (w_f32s) or E8M0 bytes; C bf16

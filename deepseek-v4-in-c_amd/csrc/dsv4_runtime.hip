@@ -64,7 +64,7 @@ struct State {
     hipEvent_t fork = nullptr, join = nullptr;
     unsigned *status = nullptr;          /* device status word            */
     std::map<uintptr_t, Region> regions; /* host start -> resident copy   */
-    DevBuf x, y, mid, table, small, ys, gemm_ws, moe_ws, x16;
+    DevBuf x, y, mid, table, small, ys, gemm_ws, moe_ws, x16, msplit;
 };
 
 State g;
@@ -184,12 +184,69 @@ GemvArgs gemv_args(const DSV4QMat &m, const float *x, float *y, int nt)
     return a;
 }
 
+/* The block-scaled MFMA GEMV takes matrices whose columns are whole 128-wide
+ * chunks (at most 4096 FP8 or 8192 FP4 columns), FP8 row blocks that are
+ * multiples of 16 rows, 4-byte aligned fp32 scales and 16-byte aligned x. */
+bool mx_gemv_ok(const DSV4QMat &d, int fmt, const float *x)
+{
+    if (!gemv_mx_ncw(fmt, d.cols) || !aligned16(x) || !aligned16(d.w)) return false;
+    if (fmt != FMT_FP4_E8M0 && d.blk_r % 16) return false;
+    if (fmt == FMT_FP8_F32S && ((uintptr_t)d.s & 3u)) return false;
+    return true;
+}
+
+GemvMxArgs gemv_mx_args(const DSV4QMat &m, const float *x, float *y, int nt)
+{
+    GemvMxArgs a;
+    memset(&a, 0, sizeof a);
+    a.W = (const uint8_t *)m.w;
+    a.S = m.s;
+    a.x = x;
+    a.y = y;
+    a.rows = m.rows;
+    a.cols = m.cols;
+    a.row_bytes = qmat_row_bytes(&m);
+    a.sc_cols = qmat_sc_cols(&m);
+    a.blk_r = m.blk_r;
+    a.nt = nt;
+    a.x_ld = m.cols;
+    a.y_ld = m.rows;
+    return a;
+}
+
+/* Expert shapes the MFMA gate/up takes: inter and hidden whole 128-wide
+ * chunks within the GEMV limits. */
+bool mx_expert_ok(int fmt, int inter, int hidden)
+{
+    return inter > 0 && inter % 128 == 0 && gemv_mx_ncw(fmt, hidden) && gemv_mx_ncw(fmt, inter);
+}
+
 /* Enqueue one expert (gate/up + SwiGLU -> mid, then w2 -> out) from a
  * descriptor holding device pointers. */
 int enqueue_expert(const DSV4ExpertW &e, int fmt, int inter, int hidden,
                    const float *x, float *mid, float *out, float limit,
                    hipStream_t st)
 {
+    const bool mx = mx_expert_ok(fmt, inter, hidden) && aligned16(x) && aligned16(mid) &&
+                    mx_gemv_ok(e.w2, fmt, mid) &&
+                    (fmt != FMT_FP8_F32S || (((uintptr_t)e.w1.s | (uintptr_t)e.w3.s) & 3u) == 0);
+    if (mx) {
+        GateUpMxArgs ga;
+        memset(&ga, 0, sizeof ga);
+        ga.direct = e;
+        ga.use_direct = 1;
+        ga.nslots = 1;
+        ga.x = x;
+        ga.mid = mid;
+        ga.mid_ld = inter;
+        ga.inter = inter;
+        ga.hidden = hidden;
+        ga.limit = limit;
+        ga.status = g.status;
+        HIPCHK(gateup_mx_launch(fmt, ga, st), "gate/up launch");
+        HIPCHK(gemv_mx_launch(fmt, gemv_mx_args(e.w2, mid, out, 1), st), "down launch");
+        return 0;
+    }
     GateUpArgs ga;
     memset(&ga, 0, sizeof ga);
     ga.direct = e;
@@ -225,6 +282,44 @@ int enqueue_moe(const DSV4ExpertW *table, int n_experts, const int *idx,
         if (enqueue_expert(*shared_dev, shared_fmt, shared_inter, hidden, x, smid,
                            ys, limit, st))
             return -1;
+    }
+    if (mx_expert_ok(FMT_FP4_E8M0, inter, hidden) && inter <= 2048 && topk <= 8 && aligned16(x)) {
+        /* routed experts on the block-scaled MFMA: gate/up writes each slot's
+         * mid split table, down reads it and combines in k order */
+        const size_t sl = mx_split_bytes(inter);
+        HIPCHK(g.msplit.need((size_t)topk * sl), "mid split alloc");
+        GateUpMxArgs ga;
+        memset(&ga, 0, sizeof ga);
+        ga.table = table;
+        ga.idx = idx;
+        ga.n_experts = n_experts;
+        ga.nslots = topk;
+        ga.x = x;
+        ga.mid = mid;
+        ga.mid_ld = (int)mid_ld;
+        ga.msplit = (uint8_t *)g.msplit.p;
+        ga.msplit_ld = sl;
+        ga.inter = inter;
+        ga.hidden = hidden;
+        ga.limit = limit;
+        ga.status = g.status;
+        HIPCHK(gateup_mx_launch(FMT_FP4_E8M0, ga, st), "routed gate/up launch");
+        DownMxArgs da;
+        memset(&da, 0, sizeof da);
+        da.table = table;
+        da.idx = idx;
+        da.w = w;
+        da.n_experts = n_experts;
+        da.topk = topk;
+        da.msplit = (const uint8_t *)g.msplit.p;
+        da.msplit_ld = sl;
+        da.shared = ys;
+        da.out = out;
+        da.inter = inter;
+        da.hidden = hidden;
+        da.status = g.status;
+        HIPCHK(down_mx_launch(da, st), "down/combine launch");
+        return 0;
     }
     GateUpArgs ga;
     memset(&ga, 0, sizeof ga);
@@ -302,7 +397,7 @@ void dsv4_hip_shutdown(void)
     g.regions.clear();
     g.x.release(); g.y.release(); g.mid.release();
     g.table.release(); g.small.release(); g.ys.release(); g.gemm_ws.release();
-    g.moe_ws.release(); g.x16.release();
+    g.moe_ws.release(); g.x16.release(); g.msplit.release();
     if (g.status) (void)hipFree(g.status);
     g.status = nullptr;
     if (g.stream) (void)hipStreamDestroy(g.stream);
@@ -366,8 +461,8 @@ void *dsv4_hip_device_ptr(const void *p)
 /* y = W . x for nt tokens. From MMQ_MFMA_MIN_TOKENS tokens on, matrices the
  * grouped kernel takes (rows, cols multiples of 128; FP8 with 128x128 blocks
  * or FP4 with 1x32) run as one dense fp16-MFMA GEMM (x rounded to fp16, weights
- * decoded exactly, fp32 accumulation); fewer tokens or other geometries run
- * the per-token GEMV. */
+ * decoded exactly, fp32 accumulation); fewer tokens run the block-scaled MFMA
+ * GEMV where its geometry fits, else the per-token VALU GEMV. */
 constexpr int MMQ_MFMA_MIN_TOKENS = 32;
 
 int enqueue_mmq(const DSV4QMat &d, int fmt, const float *x, float *y, int nt, hipStream_t st)
@@ -385,6 +480,10 @@ int enqueue_mmq(const DSV4QMat &d, int fmt, const float *x, float *y, int nt, hi
         const int tt = nt <= 16 ? 1 : 4;
         const long tiles = (nt + grouped_rows_per_tile(tt) - 1) / grouped_rows_per_tile(tt);
         HIPCHK(grouped_launch(fmt, false, tt, a, tiles, st), "dense MFMA launch");
+        return 0;
+    }
+    if (mx_gemv_ok(d, fmt, x)) {
+        HIPCHK(gemv_mx_launch(fmt, gemv_mx_args(d, x, y, nt), st), "gemv launch");
         return 0;
     }
     HIPCHK(gemv_launch(fmt, gemv_args(d, x, y, nt), st), "gemv launch");

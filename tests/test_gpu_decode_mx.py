@@ -1,0 +1,180 @@
+# SPDX-License-Identifier: Apache-2.0
+"""GPU parity of the block-scaled MFMA decode path (activations split into
+four e4m3 parts as the B operand, packed weights as the A operand) against the
+oracle: activation edge cases the split must survive (outlier channels, zero
+and tiny blocks, fp32 subnormals), 1-7 tokens per call, special scale bytes,
+waves without chunks, and the expert / MoE kernels at shapes that take the
+MFMA path."""
+import zlib
+
+import numpy as np
+import pytest
+import torch
+
+from conftest import REL_L2_TOL, rel_l2
+from test_gpu_decode import (DEV, Resident, _rand_fp8, bf16_x, check_close, dev_f32, dev_u8,
+                             make_fp4_expert, make_fp8_shared)
+
+pytestmark = pytest.mark.gpu
+
+
+def _x_edge(rng, n, kind):
+    x = rng.standard_normal(n).astype(np.float32)
+    if kind == "outliers":           # a few channels 10^4 x larger than the rest
+        x[rng.choice(n, 6, replace=False)] *= 1.0e4
+    elif kind == "zero_blocks":      # whole 32-blocks of zeros, and an all-zero chunk
+        x[32:64] = 0.0
+        x[256:384] = 0.0
+    elif kind == "tiny":             # fp32 subnormals and near-underflow blocks
+        x[:32] *= 1.0e-41
+        x[32:64] *= 1.0e-30
+        x[64:96] = np.float32(1.0e-45)
+    elif kind == "wide":             # magnitudes spanning 2^-60 .. 2^60 inside each block
+        x *= np.exp2(rng.integers(-60, 61, n)).astype(np.float32)
+    return x
+
+
+@pytest.mark.parametrize("kind", ["plain", "outliers", "zero_blocks", "tiny", "wide"])
+@pytest.mark.parametrize("fmt", ["fp4", "fp8", "fp8f"])
+def test_mx_gemv_activation_edges(lib, pkg, oracle, kind, fmt):
+    rows, cols = 256, 1024
+    rng = np.random.default_rng(zlib.crc32(f"{kind}/{fmt}".encode()))
+    x = _x_edge(rng, cols, kind)
+    if fmt == "fp4":
+        W = rng.integers(0, 256, rows * cols // 2).astype(np.uint8)
+        S = rng.integers(118, 134, rows * cols // 32).astype(np.uint8)
+        m = Resident(lib, pkg, pkg.DSV4_WFP4, W, S, rows, cols, 1, 32)
+        want = oracle.fp4_n(W, S, x, rows, cols, 1, 32, 1)
+    elif fmt == "fp8":
+        W = _rand_fp8(rng, rows * cols)
+        S = rng.integers(118, 134, (rows // 128) * (cols // 128)).astype(np.uint8)
+        m = Resident(lib, pkg, pkg.DSV4_WFP8, W, S, rows, cols, 128, 128)
+        want = oracle.fp8_n(W, S, x, rows, cols, 128, 128, 1)
+    else:
+        w = (rng.standard_normal((rows, cols)) * 0.02).astype(np.float32)
+        W, S = oracle.quant_fp8_blk128(w)
+        m = Resident(lib, pkg, pkg.DSV4_WFP8_F32S, W, S, rows, cols, 128, 128)
+        want = oracle.fp8f_n(W, S, x, rows, cols, 128, 128, 1)
+    y = lib.mmq_n(m.desc, x, 1)
+    m.drop()
+    check_close(y, want)
+
+
+@pytest.mark.parametrize("nt", [1, 2, 3, 4, 5, 7])
+@pytest.mark.parametrize("fmt,cols", [("fp4", 4096), ("fp8", 4096), ("fp4", 512), ("fp8", 8 * 128)])
+def test_mx_gemv_tokens(lib, pkg, oracle, nt, fmt, cols):
+    """Token groups of the MFMA GEMV: up to four tokens share the sixteen B
+    columns; more tokens are further groups of the grid."""
+    rows = 160
+    rng = np.random.default_rng(nt * 1000 + cols)
+    x = rng.standard_normal(nt * cols).astype(np.float32)
+    if fmt == "fp4":
+        W = rng.integers(0, 256, rows * cols // 2).astype(np.uint8)
+        S = rng.integers(118, 134, rows * cols // 32).astype(np.uint8)
+        m = Resident(lib, pkg, pkg.DSV4_WFP4, W, S, rows, cols, 1, 32)
+        want = oracle.fp4_n(W, S, x, rows, cols, 1, 32, nt)
+    else:
+        W = _rand_fp8(rng, rows * cols)
+        S = rng.integers(118, 134, 2 * (cols // 128)).astype(np.uint8)
+        m = Resident(lib, pkg, pkg.DSV4_WFP8, W, S, rows, cols, 128, 128)
+        want = oracle.fp8_n(W, S, x, rows, cols, 128, 128, nt)
+    y = lib.mmq_n(m.desc, x, nt)
+    m.drop()
+    for t in range(nt):
+        check_close(y[t * rows:(t + 1) * rows], want[t * rows:(t + 1) * rows])
+
+
+@pytest.mark.parametrize("cols", [128, 384, 640])
+def test_mx_gemv_idle_waves(lib, pkg, oracle, cols):
+    """K shorter than four waves' worth: some waves of a tile own no chunk."""
+    rows = 48
+    rng = np.random.default_rng(cols)
+    W = rng.integers(0, 256, rows * cols // 2).astype(np.uint8)
+    S = rng.integers(118, 134, rows * cols // 32).astype(np.uint8)
+    x = rng.standard_normal(cols).astype(np.float32)
+    m = Resident(lib, pkg, pkg.DSV4_WFP4, W, S, rows, cols, 1, 32)
+    y = lib.mmq_n(m.desc, x, 1)
+    m.drop()
+    check_close(y, oracle.fp4_n(W, S, x, rows, cols, 1, 32, 1))
+
+
+def test_mx_gemv_special_scales(lib, pkg, oracle):
+    """E8M0 scale bytes 0 (2^-127), 254 and 255 (NaN) in the hardware scale
+    operand: rows holding a 255 come out NaN, like the oracle's; the others
+    match it."""
+    rows, cols = 64, 512
+    rng = np.random.default_rng(5)
+    W = rng.integers(0, 256, rows * cols // 2).astype(np.uint8)
+    S = rng.integers(118, 134, rows * cols // 32).astype(np.uint8).reshape(rows, cols // 32)
+    S[3, 2] = 0
+    S[7, :] = 0
+    S[9, 5] = 254
+    S[11, 0] = 255
+    S[40, 15] = 255
+    S = S.reshape(-1)
+    x = rng.standard_normal(cols).astype(np.float32)
+    m = Resident(lib, pkg, pkg.DSV4_WFP4, W, S, rows, cols, 1, 32)
+    y = lib.mmq_n(m.desc, x, 1)
+    m.drop()
+    want = oracle.fp4_n(W, S, x, rows, cols, 1, 32, 1)
+    nan = np.isnan(want)
+    assert list(np.nonzero(nan)[0]) == [11, 40]
+    assert np.array_equal(np.isnan(y), nan)
+    ok = ~nan & np.isfinite(want)
+    assert rel_l2(y[ok], want[ok]) <= REL_L2_TOL
+
+
+def test_mx_expert_forward_fp8_shared_shape(lib, pkg, oracle):
+    """The FP8 (fp32-scale) expert through the MFMA gate/up and GEMV."""
+    rng = np.random.default_rng(41)
+    e, he, mats = make_fp8_shared(lib, pkg, oracle, rng, inter=512, hidden=1024)
+    x = bf16_x(5, 1024)
+    y = lib.expert_forward(e, x, 10.0)
+    check_close(y, oracle.expert_forward(he, x, 10.0))
+    for m in mats:
+        m.drop()
+
+
+@pytest.mark.parametrize("inter,hidden,topk", [(128, 512, 1), (256, 1024, 8), (2048, 4096, 6)])
+def test_mx_moe_decode_shapes(lib, pkg, oracle, inter, hidden, topk):
+    rng = np.random.default_rng(inter + topk)
+    experts = [make_fp4_expert(lib, pkg, oracle, rng, inter, hidden) for _ in range(topk)]
+    x = bf16_x(7, hidden)
+    lg = rng.standard_normal(topk)
+    w = (np.exp(lg) / np.exp(lg).sum()).astype(np.float32)
+    y = lib.moe_decode([e for e, _, _ in experts], w, x, None, 10.0)
+    acc = np.stack([oracle.expert_forward(he, x, 10.0) for _, he, _ in experts])
+    e = check_close(y, oracle.moe_combine(acc, w))
+    assert e < 1e-4
+    for _, _, mats in experts:
+        for m in mats:
+            m.drop()
+
+
+def test_mx_moe_decode_bad_descriptor_poisons(lib, pkg, oracle):
+    """A routed slot whose w1 descriptor has the wrong format raises status
+    bit 1 and turns the whole output NaN (the down projection reads NaN block
+    scales for that slot)."""
+    rng = np.random.default_rng(43)
+    inter, hidden = 128, 512
+    mats = []
+    for (r, c) in ((inter, hidden), (inter, hidden), (hidden, inter)):
+        W, S = oracle.quant_fp4_mx((rng.standard_normal((r, c)) * 0.02).astype(np.float32))
+        mats.append((dev_u8(W), dev_u8(S), r, c))
+    good = [pkg.qmat(pkg.DSV4_WFP4, w.data_ptr(), s.data_ptr(), r, c, 1, 32) for w, s, r, c in mats]
+    badw1 = pkg.qmat(pkg.DSV4_WFP8, mats[0][0].data_ptr(), mats[0][1].data_ptr(), inter, hidden, 128, 128)
+    table = bytes(pkg.ExpertW(good[0], good[1], good[2])) + bytes(pkg.ExpertW(badw1, good[1], good[2]))
+    tbl = torch.from_numpy(np.frombuffer(table, np.uint8).copy()).to(DEV)
+    x = dev_f32(rng.standard_normal(hidden))
+    w = dev_f32(np.array([0.5, 0.5], np.float32))
+    out = torch.zeros(hidden, dtype=torch.float32, device=DEV)
+    lib.status()
+    idx = torch.tensor([0, 0], dtype=torch.int32, device=DEV)
+    lib.moe_decode_dev(out.data_ptr(), x.data_ptr(), tbl.data_ptr(), 2, idx.data_ptr(),
+                       w.data_ptr(), 2, None, hidden, inter, 10.0)
+    assert lib.status() == 0 and torch.isfinite(out).all()
+    idx = torch.tensor([0, 1], dtype=torch.int32, device=DEV)
+    lib.moe_decode_dev(out.data_ptr(), x.data_ptr(), tbl.data_ptr(), 2, idx.data_ptr(),
+                       w.data_ptr(), 2, None, hidden, inter, 10.0)
+    assert lib.status() & 2
+    assert torch.isnan(out).all()
