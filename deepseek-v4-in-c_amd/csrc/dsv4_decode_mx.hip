@@ -266,6 +266,16 @@ __device__ __forceinline__ v4f mfma_a(const AChunk<FP4> &a, const v8i &b, const 
     }
 }
 
+/* FP4 A operand with its E8M0 scale in byte SEL of sa4. */
+template <int SEL>
+__device__ __forceinline__ v4f mfma_f4_sel(const u32x4 &q, const v8i &b, const v4f &c, uint32_t sa4, int sb)
+{
+    v8i av;
+    av[0] = (int)q.x; av[1] = (int)q.y; av[2] = (int)q.z; av[3] = (int)q.w;
+    av[4] = 0; av[5] = 0; av[6] = 0; av[7] = 0;
+    return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(av, b, c, 4, 0, SEL, (int)sa4, 0, sb);
+}
+
 /* The scale side of one matrix for a wave's chunk range: FP4 a byte per lane
  * and chunk (row l % 16, block 4 c + l / 16); FP8 one value per chunk for the
  * whole tile (the 16 rows lie in one row block), E8M0 byte or fp32 bits. */
@@ -663,40 +673,64 @@ __global__ __launch_bounds__(1024) void k_down_mx(DownMxArgs a)
 template <int NP>
 struct APairs {
     u32x4 q[NP];
-    uint32_t s[NP];
+    uint32_t s[(NP + 3) / 4];   /* E8M0 scale of pair m in byte m % 4 of s[m / 4] */
+    u32x4 piece;                /* this lane's 16 scale bytes on the wide path */
+    bool wide;
 };
 
-/* A operand and E8M0 scale of NP chunk pairs starting at chunk c0 of row
- * `row` (FP4, rows row_bytes apart, scale rows sc_cols bytes apart). The
- * scales of a row's 2 NP chunks are 8 NP contiguous bytes: with NP >= 2,
- * NP / 2 lanes per row load them as 16-byte pieces and every lane fetches
- * its two candidate dwords from the loading lane. */
+/* E8M0 scales of NP chunk pairs starting at chunk c0 of row `row` (FP4, scale
+ * rows sc_cols bytes apart). A row's 2 NP chunks have 8 NP contiguous scale
+ * bytes: with NP >= 2 and 16-byte aligned rows, NP / 2 lanes per row load
+ * them as 16-byte pieces here and ld_pairs_scales_finish hands every lane its
+ * bytes -- called after the weight loads are issued, so waiting for the
+ * pieces never delays them. Otherwise each lane loads its bytes directly. */
 template <int NP>
 __device__ __forceinline__ void ld_pairs_scales(APairs<NP> &a, const uint8_t *S, int sc_cols, int blk_r,
                                                 int row, int tile_row0, int row_max, int c0, int lane)
 {
     const int par = (lane >> 3) & 1, g = lane >> 4;
     bool wide = NP >= 2 && (sc_cols & 15) == 0 && ((4 * c0) & 15) == 0 && ((uintptr_t)S & 15u) == 0;
-    wide = __builtin_amdgcn_readfirstlane((int)wide) != 0;
+    a.wide = __builtin_amdgcn_readfirstlane((int)wide) != 0;
     if constexpr (NP >= 2) {
-        if (wide) {
+        if (a.wide) {
             constexpr int NPC = NP / 2;                       /* 16-byte pieces per row */
             const int L = lane % (8 * NPC);
             const int rl = min(tile_row0 + L / NPC, row_max);
-            const u32x4 piece = *gptr((const u32x4 *)(S + (size_t)(rl / blk_r) * sc_cols + 4 * c0 + 16 * (L % NPC)));
-#pragma unroll
-            for (int m = 0; m < NP; m++) {
-                const int src = ((lane & 7) * NPC + m / 2) * 4;
-                const uint32_t d0 = (uint32_t)__builtin_amdgcn_ds_bpermute(src, (int)piece[2 * (m & 1)]);
-                const uint32_t d1 = (uint32_t)__builtin_amdgcn_ds_bpermute(src, (int)piece[2 * (m & 1) + 1]);
-                a.s[m] = ((par ? d1 : d0) >> (8 * g)) & 0xFFu;
-            }
+            a.piece = *gptr((const u32x4 *)(S + (size_t)(rl / blk_r) * sc_cols + 4 * c0 + 16 * (L % NPC)));
             return;
         }
     }
+    uint32_t b[NP];
 #pragma unroll
     for (int m = 0; m < NP; m++)
-        a.s[m] = ld_u8(S, (size_t)(row / blk_r) * sc_cols + 4 * (c0 + 2 * m + par) + g);
+        b[m] = ld_u8(S, (size_t)(row / blk_r) * sc_cols + 4 * (c0 + 2 * m + par) + g);
+#pragma unroll
+    for (int i = 0; i < (NP + 3) / 4; i++) {
+        uint32_t v = 0;
+#pragma unroll
+        for (int m = 4 * i; m < 4 * i + 4 && m < NP; m++) v |= b[m] << (8 * (m & 3));
+        a.s[i] = v;
+    }
+}
+
+template <int NP>
+__device__ __forceinline__ void ld_pairs_scales_finish(APairs<NP> &a, int lane)
+{
+    if constexpr (NP >= 2) {
+        if (a.wide) {
+            constexpr int NPC = NP / 2;
+            const int par = (lane >> 3) & 1, g = lane >> 4;
+#pragma unroll
+            for (int i = 0; i < (NP + 3) / 4; i++) a.s[i] = 0;
+#pragma unroll
+            for (int m = 0; m < NP; m++) {
+                const int src = ((lane & 7) * NPC + m / 2) * 4;
+                const uint32_t d0 = (uint32_t)__builtin_amdgcn_ds_bpermute(src, (int)a.piece[2 * (m & 1)]);
+                const uint32_t d1 = (uint32_t)__builtin_amdgcn_ds_bpermute(src, (int)a.piece[2 * (m & 1) + 1]);
+                a.s[m >> 2] |= (((par ? d1 : d0) >> (8 * g)) & 0xFFu) << (8 * (m & 3));
+            }
+        }
+    }
 }
 
 template <int NP>
@@ -747,28 +781,30 @@ __device__ __forceinline__ void store_pair_partials(v4f acc, float *dst, int lan
     }
 }
 
-/* Gate/up + SwiGLU for FP4 experts with hidden = 512 NP. Eight waves: four
- * 8-row tiles x two halves of K (NP chunk pairs each); one workgroup per
- * (slot, 32-row group). The workgroup splits x once into LDS (one unit of
- * eight elements per thread for hidden 4096) and every wave reads its half
- * from there. Writes mid and, when a.msplit is set, mid's split table. */
+/* Gate/up + SwiGLU for FP4 experts with hidden = 512 NP, one item = (slot,
+ * 32-row group). Eight waves: four 8-row tiles x two halves of K (NP chunk
+ * pairs each). The workgroup splits x once into LDS (one unit of eight
+ * elements per thread for hidden 4096) and every wave reads its half from
+ * there. Writes mid and, when a.msplit is set, mid's split table. */
+constexpr int GU_LDS_TAIL = (4 * 2 * 2 * 16 + 32) * 4;
+
 template <int NP>
-__global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) void k_gateup_px(GateUpMxArgs a)
+__device__ __forceinline__ void gateup_px_item(const GateUpMxArgs &a, int item, uint8_t *lds)
 {
-    extern __shared__ __align__(16) uint8_t lds[];
     constexpr int NC = 4 * NP;                         /* chunks of hidden */
     constexpr int UPL = (NC * 16 + 511) / 512;
     const int lane = threadIdx.x & 63;
     const int wave = wave_in_group();
     const int tile = wave >> 1, hh = wave & 1;
     const int groups = a.inter / 32;
-    const int slot = blockIdx.x / groups;
-    const int j0 = (blockIdx.x - slot * groups) * 32;
+    const int slot = item / groups;
+    const int j0 = (item - slot * groups) * 32;
     const int r0 = j0 + 8 * tile;
     const int row = r0 + (lane & 7);
     const int c0 = hh * 2 * NP;
     uint8_t *tab = lds;                                /* NC chunks + zero operand */
     float *red = (float *)(lds + NC * TAB_CHUNK + TAB_ZERO);   /* [4 tiles][2 halves][2 mats][16] */
+    float *vl = red + 4 * 2 * 2 * 16;                  /* the group's 32 mid values */
     float *mid = a.mid + (size_t)slot * a.mid_ld;
 
     DSV4ExpertW e;
@@ -786,74 +822,94 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) void k
     if (bad) {
         if (threadIdx.x == 0) atomicOr(a.status, bad);
         if (threadIdx.x < 32) mid[j0 + threadIdx.x] = qnan_f();
+        /* NaN block scales (E8M0 255) make the down projection of this slot NaN */
         if (a.msplit && threadIdx.x < NPART)
             *(int *)(a.msplit + (size_t)slot * a.msplit_ld + (size_t)(j0 >> 7) * TAB_CHUNK +
                      TAB_DATA + (((j0 >> 5) & 3) * NPART + threadIdx.x) * 4) = 255;
-        return;
+    } else {
+        const int row_bytes = a.hidden / 2, sc_cols = a.hidden / 32;
+        XUnits<UPL> xu;
+        load_units<UPL, 512>(xu, a.x, 0, 1, 0, NC, (int)threadIdx.x);
+        DSV4_ORDER();
+        APairs<NP> w1, w3;
+        ld_pairs_scales<NP>(w1, (const uint8_t *)e.w1.s, sc_cols, e.w1.blk_r, row, r0, a.inter - 1, c0, lane);
+        ld_pairs_scales<NP>(w3, (const uint8_t *)e.w3.s, sc_cols, e.w3.blk_r, row, r0, a.inter - 1, c0, lane);
+        DSV4_ORDER();
+        ld_pairs_w<NP>(w1, (const uint8_t *)e.w1.w + (size_t)row * row_bytes, c0, lane);
+        ld_pairs_w<NP>(w3, (const uint8_t *)e.w3.w + (size_t)row * row_bytes, c0, lane);
+        DSV4_ORDER();
+        store_units<UPL, 512>(tab, xu, 1, NC, (int)threadIdx.x);
+        ld_pairs_scales_finish<NP>(w1, lane);
+        ld_pairs_scales_finish<NP>(w3, lane);
+        __builtin_amdgcn_s_waitcnt(0xC07F);            /* lgkmcnt(0): own LDS writes done */
+        __builtin_amdgcn_s_barrier();
+        asm volatile("" ::: "memory");
+        const BPair bp = bpair_src(tab, c0, tab + NC * TAB_CHUNK, lane);
+        v4f gacc = {0.0f, 0.0f, 0.0f, 0.0f}, uacc = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int m = 0; m < NP; m++) {
+            const u32x4 lo = *(const u32x4 *)(bp.d + m * bp.step);
+            const u32x4 hi = *(const u32x4 *)(bp.d + m * bp.step + 16);
+            const int sb = *(const int *)(bp.s + m * bp.step);
+            v8i b;
+            b[0] = (int)lo.x; b[1] = (int)lo.y; b[2] = (int)lo.z; b[3] = (int)lo.w;
+            b[4] = (int)hi.x; b[5] = (int)hi.y; b[6] = (int)hi.z; b[7] = (int)hi.w;
+            switch (m & 3) {       /* compile-time after unrolling: the scale byte select */
+            case 0: gacc = mfma_f4_sel<0>(w1.q[m], b, gacc, w1.s[m >> 2], sb);
+                    uacc = mfma_f4_sel<0>(w3.q[m], b, uacc, w3.s[m >> 2], sb); break;
+            case 1: gacc = mfma_f4_sel<1>(w1.q[m], b, gacc, w1.s[m >> 2], sb);
+                    uacc = mfma_f4_sel<1>(w3.q[m], b, uacc, w3.s[m >> 2], sb); break;
+            case 2: gacc = mfma_f4_sel<2>(w1.q[m], b, gacc, w1.s[m >> 2], sb);
+                    uacc = mfma_f4_sel<2>(w3.q[m], b, uacc, w3.s[m >> 2], sb); break;
+            default: gacc = mfma_f4_sel<3>(w1.q[m], b, gacc, w1.s[m >> 2], sb);
+                     uacc = mfma_f4_sel<3>(w3.q[m], b, uacc, w3.s[m >> 2], sb); break;
+            }
+        }
+        store_pair_partials(gacc, red + ((tile * 2 + hh) * 2 + 0) * 16, lane);
+        store_pair_partials(uacc, red + ((tile * 2 + hh) * 2 + 1) * 16, lane);
+        __syncthreads();
+        if (wave == 0) {
+            if (lane < 32) {
+                const int t = lane >> 3, rr = lane & 7;
+                const float *p0 = red + ((t * 2 + 0) * 2) * 16, *p1 = red + ((t * 2 + 1) * 2) * 16;
+                const float gs = ((p0[rr] + p0[8 + rr]) + p1[rr]) + p1[8 + rr];
+                const float us = ((p0[16 + rr] + p0[24 + rr]) + p1[16 + rr]) + p1[24 + rr];
+                const float v = dev_swiglu(gs, us, a.limit);
+                mid[j0 + lane] = v;
+                vl[lane] = v;
+            }
+            /* the 32-element block j0 / 32 of mid in four lanes of eight (one
+             * DPP quad), split like the activations, into the down
+             * projection's table (chunk j0 / 128, block (j0 / 32) % 4) */
+            if (a.msplit && lane < 4) {
+                float v8[8];
+#pragma unroll
+                for (int i = 0; i < 8; i++) v8[i] = vl[8 * lane + i];
+                uint32_t code[NPART][2];
+                int E[NPART];
+                split8(v8, code, E);
+                uint8_t *cb = a.msplit + (size_t)slot * a.msplit_ld + (size_t)(j0 >> 7) * TAB_CHUNK;
+                const int b4 = (j0 >> 5) & 3;
+                const int kk = 32 * b4 + 8 * lane;
+                const int h = (kk & 63) >> 4, half = kk >> 6;
+#pragma unroll
+                for (int p = 0; p < NPART; p++)
+                    *(uint2 *)(cb + (h * NPART + p) * 32 + half * 16 + (kk & 15)) =
+                        make_uint2(code[p][0], code[p][1]);
+                if (lane == 0) {
+#pragma unroll
+                    for (int p = 0; p < NPART; p++) *(int *)(cb + TAB_DATA + (b4 * NPART + p) * 4) = E[p];
+                }
+            }
+        }
     }
-    const int row_bytes = a.hidden / 2, sc_cols = a.hidden / 32;
+}
 
-    XUnits<UPL> xu;
-    load_units<UPL, 512>(xu, a.x, 0, 1, 0, NC, (int)threadIdx.x);
-    DSV4_ORDER();
-    APairs<NP> w1, w3;
-    ld_pairs_scales<NP>(w1, (const uint8_t *)e.w1.s, sc_cols, e.w1.blk_r, row, r0, a.inter - 1, c0, lane);
-    ld_pairs_scales<NP>(w3, (const uint8_t *)e.w3.s, sc_cols, e.w3.blk_r, row, r0, a.inter - 1, c0, lane);
-    DSV4_ORDER();
-    ld_pairs_w<NP>(w1, (const uint8_t *)e.w1.w + (size_t)row * row_bytes, c0, lane);
-    ld_pairs_w<NP>(w3, (const uint8_t *)e.w3.w + (size_t)row * row_bytes, c0, lane);
-    DSV4_ORDER();
-    store_units<UPL, 512>(tab, xu, 1, NC, (int)threadIdx.x);
-    __builtin_amdgcn_s_waitcnt(0xC07F);                /* lgkmcnt(0): own LDS writes done */
-    __builtin_amdgcn_s_barrier();
-    asm volatile("" ::: "memory");
-    const BPair bp = bpair_src(tab, c0, tab + NC * TAB_CHUNK, lane);
-    v4f gacc = {0.0f, 0.0f, 0.0f, 0.0f}, uacc = {0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-    for (int m = 0; m < NP; m++) {
-        const u32x4 lo = *(const u32x4 *)(bp.d + m * bp.step);
-        const u32x4 hi = *(const u32x4 *)(bp.d + m * bp.step + 16);
-        const int sb = *(const int *)(bp.s + m * bp.step);
-        v8i b;
-        b[0] = (int)lo.x; b[1] = (int)lo.y; b[2] = (int)lo.z; b[3] = (int)lo.w;
-        b[4] = (int)hi.x; b[5] = (int)hi.y; b[6] = (int)hi.z; b[7] = (int)hi.w;
-        AChunk<true> c1, c3;
-        c1.q[0] = w1.q[m];
-        c3.q[0] = w3.q[m];
-        gacc = mfma_a<true>(c1, b, gacc, (int)w1.s[m], sb);
-        uacc = mfma_a<true>(c3, b, uacc, (int)w3.s[m], sb);
-    }
-    store_pair_partials(gacc, red + ((tile * 2 + hh) * 2 + 0) * 16, lane);
-    store_pair_partials(uacc, red + ((tile * 2 + hh) * 2 + 1) * 16, lane);
-    __syncthreads();
-    if (wave != 0) return;
-
-    float v = 0.0f;
-    if (lane < 32) {
-        const int t = lane >> 3, rr = lane & 7;
-        const float *p0 = red + ((t * 2 + 0) * 2) * 16, *p1 = red + ((t * 2 + 1) * 2) * 16;
-        const float gs = ((p0[rr] + p0[8 + rr]) + p1[rr]) + p1[8 + rr];
-        const float us = ((p0[16 + rr] + p0[24 + rr]) + p1[16 + rr]) + p1[24 + rr];
-        v = dev_swiglu(gs, us, a.limit);
-        mid[j0 + lane] = v;
-    }
-    if (!a.msplit) return;
-    uint8_t *cb = a.msplit + (size_t)slot * a.msplit_ld + (size_t)(j0 >> 7) * TAB_CHUNK;
-    const int b4 = (j0 >> 5) & 3;
-    const int kk = 32 * b4 + (lane & 31);
-    uint8_t *dst = cb + ((kk & 63) >> 4) * NPART * 32 + (kk >> 6) * 16 + (kk & 15);
-#pragma unroll
-    for (int p = 0; p < NPART; p++) {
-        float m = fabsf(v);
-#pragma unroll
-        for (int o = 1; o < 32; o <<= 1) m = fmaxf(m, __shfl_xor(m, o));
-        const int E = part_e8m0(m);
-        const int ex = E - E8M0_ONE;
-        const uint32_t q = (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(ldexpf(v, -ex), 0.0f, 0, false) & 0xFFu;
-        if (lane < 32) dst[p * 32] = (uint8_t)q;
-        if (lane == 0) *(int *)(cb + TAB_DATA + (b4 * NPART + p) * 4) = E;
-        v -= ldexpf(__builtin_amdgcn_cvt_pk_f32_fp8((int)q, false)[0], ex);
-    }
+template <int NP>
+__global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) void k_gateup_px(GateUpMxArgs a)
+{
+    extern __shared__ __align__(16) uint8_t lds[];
+    gateup_px_item<NP>(a, (int)blockIdx.x, lds);
 }
 
 /* Routed FP4 down projections (inter = 256 NP) with the k-order combine. One
@@ -900,12 +956,16 @@ __global__ __launch_bounds__(1024) void k_down_px(DownMxArgs a)
         DSV4_ORDER();
         ld_pairs_w<NP>(w, (const uint8_t *)m.w + (size_t)row * row_bytes, 0, lane);
         DSV4_ORDER();
+        ld_pairs_scales_finish<NP>(w, lane);
         v4f acc = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
         for (int mm = 0; mm < NP; mm++) {
-            AChunk<true> c;
-            c.q[0] = w.q[mm];
-            acc = mfma_a<true>(c, bv[mm], acc, (int)w.s[mm], bs[mm]);
+            switch (mm & 3) {
+            case 0: acc = mfma_f4_sel<0>(w.q[mm], bv[mm], acc, w.s[mm >> 2], bs[mm]); break;
+            case 1: acc = mfma_f4_sel<1>(w.q[mm], bv[mm], acc, w.s[mm >> 2], bs[mm]); break;
+            case 2: acc = mfma_f4_sel<2>(w.q[mm], bv[mm], acc, w.s[mm >> 2], bs[mm]); break;
+            default: acc = mfma_f4_sel<3>(w.q[mm], bv[mm], acc, w.s[mm >> 2], bs[mm]); break;
+            }
         }
         store_pair_partials(acc, &ylds[k][t][0], lane);
     } else {
@@ -982,7 +1042,7 @@ hipError_t gateup_mx_k(const GateUpMxArgs &a, hipStream_t st)
 template <int NP>
 hipError_t gateup_px_k(const GateUpMxArgs &a, hipStream_t st)
 {
-    const size_t lds = (size_t)4 * NP * TAB_CHUNK + TAB_ZERO + 4 * 2 * 2 * 16 * 4;
+    const size_t lds = (size_t)4 * NP * TAB_CHUNK + TAB_ZERO + (4 * 2 * 2 * 16 + 32) * 4;
     const dim3 grid((unsigned)(a.nslots * (a.inter / 32)));
     hipLaunchKernelGGL((k_gateup_px<NP>), grid, dim3(512), lds, st, a);
     return hipGetLastError();
