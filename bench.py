@@ -64,6 +64,19 @@ def log(msg):
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
 
 
+def traffic_for(cfg):
+    """HBM bytes per launch of the config's measured call, from the committed
+    rocprofv3 FETCH_SIZE / WRITE_SIZE passes (profiles/traffic.json), each
+    counter scaled by what it reads for a plain 256 MiB device copy. None when
+    the summary is absent."""
+    try:
+        with open(os.path.join(ROOT, "profiles", "traffic.json")) as f:
+            t = json.load(f)
+        return int(t["configs"][str(cfg)]["traffic_bytes"])
+    except (OSError, KeyError, ValueError):
+        return None
+
+
 # ------------------------------------------------------------ workloads ----
 
 class ExpertArena:
@@ -343,7 +356,8 @@ def bench_grouped(args, torch, pkg, lib, stream, sp, K, W, cfg):
                        "tokens_per_step": n, "distinct_experts_avg": round(d_avg, 1),
                        "parallelism": "single GPU"},
             "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS,
-                         "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                         "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
+                         "traffic": traffic_for(cfg),
                          "kernel": "moe_grouped_dev call (route, fp16 convert, grouped gate/up, "
                                    "grouped down, shared gate/up + down, combine)",
                          "bytes_per_launch": round(bytes_avg), "launch_us": round(t_launch * 1e6, 3)},
@@ -367,7 +381,7 @@ def bench_grouped(args, torch, pkg, lib, stream, sp, K, W, cfg):
                        "parallelism": "single GPU"},
             "roofline": {"bound": "mfma", "achieved": round(achieved, 2), "peak": FP16_PEAK_TFLOPS,
                          "unit": "TFLOP/s", "frac": round(achieved / FP16_PEAK_TFLOPS, 4),
-                         "traffic": None,
+                         "traffic": traffic_for(cfg),
                          "kernel": "moe_grouped_dev call (route, fp16 convert, grouped gate/up, "
                                    "grouped down, shared gate/up + down, combine)",
                          "flops_per_launch": flops_step, "launch_us": round(t_launch * 1e6, 3),
@@ -494,7 +508,7 @@ def bench_cfg3(args, torch, pkg, lib, stream, sp, K, W):
         "tokens_per_s": round(M / t_step, 1),
         "roofline": {"bound": "mfma", "achieved": round(achieved, 2), "peak": FP8_PEAK_TFLOPS,
                      "unit": "TFLOP/s", "frac": round(achieved / FP8_PEAK_TFLOPS, 4),
-                     "traffic": None, "kernel": "k_gemm_fp8<true,true>",
+                     "traffic": traffic_for(3), "kernel": "k_gemm_fp8<true,true>",
                      "flops_per_launch": flops, "launch_us": round(t_gemm * 1e6, 3)},
         "step_includes": "activation quantization kernel + GEMM kernel",
         "cpu_baseline": cpu,
@@ -513,6 +527,9 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--cpu-threads", type=int, default=0)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--copy-calib", action="store_true",
+                    help="run only a plain 256 MiB device copy (the HBM-counter calibration "
+                         "kernel for rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (this build has no multi-GPU path); "
@@ -520,6 +537,16 @@ def main():
         sys.exit(2)
 
     import torch
+    if args.copy_calib:
+        n = 256 << 20
+        src = torch.ones(n, dtype=torch.uint8, device="cuda:0")
+        dst = torch.empty_like(src)
+        for _ in range(args.steps):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"copy_calib_bytes_read": n, "copy_calib_bytes_written": n,
+                          "calls": args.steps}), flush=True)
+        return
     pkg = load_pkg()
     lib = pkg.load()
     lib.check(lib.init(0), "dsv4_hip_init")
@@ -584,8 +611,8 @@ def main():
             "hbm_frac": round(value / HBM_PEAK_GBS, 4),
             "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS,
                          "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
-                         "traffic": None,
-                         "kernel": "moe_decode_dev call (k_gateup + k_down_combine)",
+                         "traffic": traffic_for(1),
+                         "kernel": "moe_decode_dev call (k_gateup_px + k_down_px)",
                          "bytes_per_launch": bytes_step,
                          "launch_us": round(t_launch * 1e6, 3)},
             "cpu_baseline": cpu,
@@ -650,7 +677,7 @@ def main():
             "roofline": {"bound": "hbm", "achieved": round(bytes_step / t_launch / 1e9, 2),
                          "peak": HBM_PEAK_GBS, "unit": "GB/s",
                          "frac": round(bytes_step / t_launch / 1e9 / HBM_PEAK_GBS, 4),
-                         "traffic": None, "kernel": "k_gemv<FP8_F32S,4,2>",
+                         "traffic": traffic_for(0), "kernel": "k_gemv_mx<FP8_F32S,8,1>",
                          "bytes_per_launch": bytes_step, "launch_us": round(t_launch * 1e6, 3)},
             "cpu_baseline": cpu,
             "wall_s": round(wall, 4),
