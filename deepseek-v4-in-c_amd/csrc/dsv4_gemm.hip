@@ -10,36 +10,38 @@
  * (src/10_compute/dsv4_matmul_fp8.c:102-155).
  *
  * SCHEDULE
- *   A workgroup of four waves (one per SIMD) owns a 128 (tokens) x 256
- *   (features) tile of C; wave (wm, wn) owns 64 tokens x 128 features. K
- *   advances in 128-wide blocks, one scale block each. Each block's A rows
- *   (128 x 128 B), W rows (256 x 128 B) and scales travel global -> LDS by
- *   direct loads (global_load_lds_dwordx4: 1 KiB per wave instruction, no
- *   VGPR round trip) into a three-buffer ring, 16-byte chunks XOR-swizzled
- *   so the MFMA operand reads are bank-conflict free. Block kb+2's loads are
- *   issued while block kb multiplies, spread over its first three feature
- *   tiles; between tiles 2 and 3 each wave waits for its own share of block
- *   kb+1 (vmcnt) and a plain s_barrier publishes it, so the next block's
- *   first operands are read while tile 3 multiplies.
- *   The MFMA is v_mfma_scale_f32_32x32x64_f8f6f4 with both hardware scales
- *   set to 1 (E8M0 127): W rows are its A operand and tokens its B operand,
- *   so each lane's 16 outputs of a 32 x 32 tile share one token and one 128-row
- *   weight block. The product of a 128-K block starts from zero and is then
- *   folded into the fp32 accumulator with the two fp32 block scales,
- *   acc += partial * (s_a[token][kb] * s_w[nb][kb]) -- fp32 scales cannot ride
- *   in the E8M0 hardware scale operands. Tile t's MFMAs are issued before
- *   tile t-1's promotion, so the VALU works in the matrix unit's shadow.
+ *   A workgroup of eight waves (two per SIMD) owns a 128 (tokens) x 256
+ *   (features) tile of C; wave (wm, wn) owns tokens 64 wm .. +63 and features
+ *   64 wn .. +63. K advances in 128-wide blocks, one scale block each.
+ *   Each block's A rows (128 x 128 B), W rows (256 x 128 B) and token scales
+ *   travel global -> LDS by direct loads (global_load_lds_dwordx4: 1 KiB per
+ *   wave instruction, 8 rows x 128 B, no VGPR round trip) into a three-stage
+ *   ring, 16-byte chunks XOR-swizzled so the operand reads are bank-conflict
+ *   free. Block kb's MFMAs run from registers. After its first two, every
+ *   wave waits for its own loads of stage kb+1 and a plain s_barrier
+ *   publishes it and frees stage kb, which the loads of block kb+3 refill one
+ *   per MFMA slot; block kb+1's operands are read meanwhile: the token
+ *   operands into a second register set, each weight operand into its own
+ *   registers right after its last use (feature-group-major MFMA order).
+ *   The MFMA is v_mfma_scale_f32_16x16x128_f8f6f4 with both hardware scales
+ *   set to 1 (E8M0 127): one instruction per 16 features x 16 tokens x one
+ *   128-K block, W rows as its A operand and tokens as its B operand, so each
+ *   lane's four outputs share one token and one 128-row weight block. The
+ *   product starts from zero and is folded into the fp32 accumulator two
+ *   MFMAs later with the two fp32 block scales, acc += p * (s_a[token][kb] *
+ *   s_w[nb][kb]) -- fp32 scales cannot ride in the E8M0 hardware scale
+ *   operands. Every MFMA slot is fenced, so the promotion never waits on an
+ *   MFMA still in the pipe; the other wave of the SIMD fills the matrix
+ *   unit while this one promotes, reads LDS or waits at the barrier.
+ *   Operand layout of the MFMA (measured on gfx950): lane l supplies row
+ *   l % 16 with k in [16 (l/16), +16) in bytes 0-15 and [64 + 16 (l/16), +16)
+ *   in bytes 16-31; result element e of lane l is row 4 (l/16) + e, column
+ *   l % 16.
  *   The finished tile is staged through LDS and written as whole 16-byte
  *   pieces of contiguous rows.
- *   Operand layout of the FP8 MFMA (measured on gfx950): lane l supplies row
- *   l % 32 with k in [16 (l/32), +16) in bytes 0-15 and [32 + 16 (l/32), +16) in
- *   bytes 16-31 of each 64-wide k step; accumulator element e of lane l is
- *   row 8 (e/4) + 4 (l/32) + e % 4, column l % 32.
  *
  * Bound: MFMA (2 M N K flops; 68.7 GFLOP at 2048 x 4096 x 4096).
  */
-#include <type_traits>
-
 #include "dsv4_internal.h"
 
 namespace dsv4 {
@@ -47,40 +49,44 @@ namespace dsv4 {
 namespace {
 
 typedef int v8i __attribute__((ext_vector_type(8)));
-typedef float v16f __attribute__((ext_vector_type(16)));
+typedef float v4f __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) void lds_void;
 
-constexpr int GM = 128;          /* tokens per workgroup tile            */
-constexpr int GN = 256;          /* features per workgroup tile          */
-constexpr int GK = 128;          /* k per stage = one scale block        */
-constexpr int NSTAGE = 3;        /* LDS ring: stage kb+2 loads while kb multiplies */
+constexpr int GM = 128;          /* tokens per workgroup tile                */
+constexpr int GN = 256;          /* features per workgroup tile              */
+constexpr int GK = 128;          /* k per block = one scale block            */
+constexpr int NWAVE = 8;
+constexpr int NSTAGE = 3;        /* block kb+3 loads while kb+1 is read      */
 /* one stage: A rows and W rows of 128 bytes (16-byte chunks XOR-swizzled),
- * the tile's token scales, the two weight-block scales, a landing pad */
+ * the block's 128 token scales, a pad where the waves without a scale load
+ * land theirs */
 constexpr int ST_A = 0;
 constexpr int ST_W = GM * GK;
 constexpr int ST_SA = ST_W + GN * GK;
-constexpr int ST_SW = ST_SA + GM * 4;
-constexpr int ST_PAD = ST_SW + 256;
+constexpr int ST_PAD = ST_SA + GM * 4;
 constexpr int STAGE = ST_PAD + 256;
-constexpr int LDS_BYTES = NSTAGE * STAGE;
-constexpr int VMEM_PER_STAGE = 13;   /* per wave: 4 A + 8 W + 1 scale load */
+constexpr int RING_BYTES = NSTAGE * STAGE;   /* 149,760 B */
+constexpr int VM_STAGE = 7;      /* loads per wave per block: 2 A + 4 W + 1 scale */
 constexpr int E8M0_ONE = 127;
+
+/* s_waitcnt immediate: vmcnt n (six bits, split 3:0 and 15:14), expcnt 7,
+ * lgkmcnt 0 (lgkm0) or 15 (no wait) */
+constexpr int waitcnt(int vm, bool lgkm0)
+{
+    return (vm & 15) | ((vm >> 4) << 14) | 0x70 | (lgkm0 ? 0 : 0xF00);
+}
+
+constexpr int lds_bytes(bool out_bf16)
+{
+    const int stage_out = GM * GN * (out_bf16 ? 2 : 4);
+    return RING_BYTES > stage_out ? RING_BYTES : stage_out;
+}
+static_assert(RING_BYTES <= 160 * 1024 && GM * GN * 4 <= 160 * 1024, "LDS of one CU");
 
 /* Physical 16-byte slot of logical chunk c in staged row r. Sixteen lanes
  * reading the same chunk of sixteen consecutive rows hit sixteen different
  * 16-byte bank groups. */
 __device__ __forceinline__ int swz(int r, int c) { return c ^ ((r >> 1) & 7); }
-
-__device__ __forceinline__ v8i lds_operand(const uint8_t *rowp, int row, int ks, int g)
-{
-    const int c0 = 4 * ks + g;
-    const u32x4 lo = *(const u32x4 *)(rowp + 16 * swz(row, c0));
-    const u32x4 hi = *(const u32x4 *)(rowp + 16 * swz(row, c0 + 2));
-    v8i v;
-    v[0] = (int)lo.x; v[1] = (int)lo.y; v[2] = (int)lo.z; v[3] = (int)lo.w;
-    v[4] = (int)hi.x; v[5] = (int)hi.y; v[6] = (int)hi.z; v[7] = (int)hi.w;
-    return v;
-}
 
 __device__ __forceinline__ uint32_t f32_to_bf16_bits(float f)
 {
@@ -99,41 +105,207 @@ __device__ __forceinline__ void dma4(const void *src, uint8_t *dst)
     __builtin_amdgcn_global_load_lds(gptr(src), (lds_void *)dst, 4, 0, 0);
 }
 
-/* Output staging. After the K loop the workgroup's 128 x 256 tile is written
- * to LDS (rows of GN elements, 16-byte chunk c of row r stored at chunk
- * c ^ (r % 32), so the 32 tokens of a fragment store and the consecutive
- * chunks of a row read land in distinct banks), then copied to C in whole
- * 16-byte pieces of contiguous rows. */
-template <bool OUT_BF16>
-__device__ __forceinline__ void stage_frag(uint8_t *lds, const v16f &acc, int t0, int f0, int col, int g)
+/* Per-lane offsets, fixed for the whole call; the K block only moves the
+ * wave-uniform bases. Direct-load instruction j of the workgroup fills staged
+ * rows 8j .. 8j+7 of A (j < 16) or W: lane l row 8j + l/8, slot l%8, which
+ * holds logical chunk swz(row, l%8). Wave w issues A instructions 2w, 2w+1
+ * and W instructions 4w .. 4w+3. */
+struct Plan {
+    uint32_t a[2], w[4];    /* global byte offsets from column 0            */
+    uint32_t s;             /* Sa byte offset of this lane's token (waves 0, 1) */
+    int w_lo, w_hi;         /* LDS: chunks l/16, l/16 + 4 of weight row l%16 of the wave */
+    int b_lo, b_hi;         /* LDS: the same of token row l%16 of the wave  */
+    int sa;                 /* LDS: scale of the wave's token l%16          */
+};
+
+__device__ __forceinline__ Plan make_plan(const GemmArgs &a, int m0, int n0, int wave, int lane)
 {
-    constexpr int EB = OUT_BF16 ? 2 : 4;
-    const int r = t0 + col;
-    uint8_t *row = lds + r * (GN * EB);
+    Plan d;
+    const int r8 = lane >> 3, p = lane & 7;
 #pragma unroll
-    for (int q = 0; q < 4; q++) {
-        const int f = f0 + 8 * q + 4 * g;              /* 4 consecutive features */
-        const int c = (f * EB) >> 4, off = (f * EB) & 15;
-        uint8_t *dst = row + 16 * (c ^ (r & 31)) + off;
-        if constexpr (OUT_BF16) {
-            uint2 pk;
-            pk.x = f32_to_bf16_bits(acc[4 * q]) | (f32_to_bf16_bits(acc[4 * q + 1]) << 16);
-            pk.y = f32_to_bf16_bits(acc[4 * q + 2]) | (f32_to_bf16_bits(acc[4 * q + 3]) << 16);
-            *(uint2 *)dst = pk;
-        } else {
-            *(f32x4 *)dst = f32x4{acc[4 * q], acc[4 * q + 1], acc[4 * q + 2], acc[4 * q + 3]};
-        }
+    for (int i = 0; i < 2; i++) {
+        const int r = 8 * (2 * wave + i) + r8;
+        d.a[i] = (uint32_t)min(m0 + r, a.M - 1) * (uint32_t)a.K + 16u * (uint32_t)swz(r, p);
+    }
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const int r = 8 * (4 * wave + i) + r8;
+        d.w[i] = (uint32_t)min(n0 + r, a.N - 1) * (uint32_t)a.K + 16u * (uint32_t)swz(r, p);
+    }
+    d.s = (uint32_t)min(m0 + 64 * (wave & 1) + lane, a.M - 1) * (uint32_t)a.sa_tok * 4u;
+    /* operand rows 16q + r16 of a wave share the swizzle of r16 */
+    const int wm = wave & 1, wn = wave >> 1, r16 = lane & 15, g = lane >> 4;
+    d.w_lo = ST_W + (64 * wn + r16) * GK + 16 * swz(r16, g);
+    d.w_hi = ST_W + (64 * wn + r16) * GK + 16 * swz(r16, g + 4);
+    d.b_lo = ST_A + (64 * wm + r16) * GK + 16 * swz(r16, g);
+    d.b_hi = ST_A + (64 * wm + r16) * GK + 16 * swz(r16, g + 4);
+    d.sa = ST_SA + 4 * (64 * wm + r16);
+    return d;
+}
+
+/* Load j (0..6) of block kb into stage st: A (j < 2), W (2..5), the token
+ * scales (6: waves 0, 1 load 64 each; the other waves repeat wave 0's into
+ * the pad, so every wave issues the same count and one vmcnt value serves
+ * all). */
+__device__ __forceinline__ void issue_one(const GemmArgs &a, const Plan &d, uint8_t *st, int kb,
+                                          int wave, int j)
+{
+    const size_t kofs = (size_t)kb * GK;
+    if (j < 2) {
+        dma16(a.Aq + kofs + d.a[j], st + ST_A + 1024 * (2 * wave + j));
+    } else if (j < 6) {
+        dma16(a.W + kofs + d.w[j - 2], st + ST_W + 1024 * (4 * wave + j - 2));
+    } else {
+        const uint8_t *sb = (const uint8_t *)a.Sa + (size_t)kb * (size_t)a.sa_kb * 4u;
+        dma4(sb + d.s, st + (wave < 2 ? ST_SA + 256 * wave : ST_PAD));
     }
 }
 
+__device__ __forceinline__ void issue(const GemmArgs &a, const Plan &d, uint8_t *st, int kb, int wave)
+{
+#pragma unroll
+    for (int j = 0; j < VM_STAGE; j++) issue_one(a, d, st, kb, wave, j);
+}
+
+__device__ __forceinline__ v8i lds_op(const uint8_t *p_lo, const uint8_t *p_hi)
+{
+    const u32x4 lo = *(const u32x4 *)p_lo;
+    const u32x4 hi = *(const u32x4 *)p_hi;
+    v8i v;
+    v[0] = (int)lo.x; v[1] = (int)lo.y; v[2] = (int)lo.z; v[3] = (int)lo.w;
+    v[4] = (int)hi.x; v[5] = (int)hi.y; v[6] = (int)hi.z; v[7] = (int)hi.w;
+    return v;
+}
+/* weight operand of feature group f / token operand of group t (16 rows each) */
+__device__ __forceinline__ v8i read_w(const uint8_t *st, const Plan &d, int f)
+{
+    return lds_op(st + d.w_lo + 2048 * f, st + d.w_hi + 2048 * f);
+}
+__device__ __forceinline__ v8i read_b(const uint8_t *st, const Plan &d, int t)
+{
+    return lds_op(st + d.b_lo + 2048 * t, st + d.b_hi + 2048 * t);
+}
+
+/* fp32 scale of a 128-row weight block at K block kb (wave-uniform: a scalar
+ * load) */
+template <bool WF32S>
+__device__ __forceinline__ float weight_scale(const GemmArgs &a, int nb, int kb)
+{
+    const size_t i = (size_t)nb * (size_t)(a.K / GK) + (size_t)kb;
+    if constexpr (WF32S) {
+        return ld_uniform((const float *)a.Sw + i, 0);
+    } else {
+        const uintptr_t p = (uintptr_t)a.Sw + i;
+        const uint32_t word = ld_uniform((const uint32_t *)(p & ~(uintptr_t)3), 0);
+        return dev_e8m0((word >> (8 * (p & 3))) & 0xFFu);
+    }
+}
+
+__device__ __forceinline__ v4f mfma16(const v8i &w, const v8i &b)
+{
+    const v4f zero = {0.0f, 0.0f, 0.0f, 0.0f};
+    return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(w, b, zero, 0, 0, 0, E8M0_ONE, 0, E8M0_ONE);
+}
+
+__device__ __forceinline__ void promote(v4f &acc, const v4f &p, float cs)
+{
+#pragma unroll
+    for (int e = 0; e < 4; e++) acc[e] = fmaf(p[e], cs, acc[e]);
+}
+
+/* What one wave carries from block to block. */
+struct State {
+    v4f acc[4][4];              /* [feature group][token group]                */
+    v8i w[4];                   /* weight operands (replaced group by group)   */
+    float cs[4];                /* s_a * s_w of the current block per token group */
+    v4f pc[2];                  /* the previous block's last two products      */
+    float csp[2];               /* their scales                                */
+    float sw_next;              /* weight scale of the next block              */
+};
+
+/* Block kb: MFMA slot s = 4f + t multiplies weight group f by token group t;
+ * behind it the product of slot s-2 is promoted (slots 0, 1 promote the
+ * previous block's slots 14, 15): an FMA on the product of the MFMA issued
+ * just before would stall the matrix pipe. Slots 0 and 1 run from registers; then this wave's loads
+ * of stage kb+1 have landed (only block kb+2's are outstanding) and its reads
+ * of stage kb are done, and the barrier makes both true for the workgroup:
+ * stage kb+1 is read from there on (token groups into bn at slots 2..5, the
+ * scales at 6..9, weight group f into w[f] after slot 4f+3, group 3 into its
+ * own registers at slot 10) and stage kb is refilled with block kb+3 (one
+ * load per slot, 2..8). */
+template <bool WF32S>
+__device__ __forceinline__ void kblock(const GemmArgs &a, const Plan &d, uint8_t *lds, State &S,
+                                       const v8i (&b)[4], v8i (&bn)[4], int kb, int nkb, int nb,
+                                       int wave)
+{
+    const int cb = kb % NSTAGE;
+    const int nx = cb + 1 == NSTAGE ? 0 : cb + 1;
+    const uint8_t *nst = lds + nx * STAGE;
+    uint8_t *fill = lds + cb * STAGE;
+    const int kl = min(kb + 3, nkb - 1);
+    v4f p[16];
+    float sa[4];
+    v8i w3n;
+    float sw2 = 0.0f;
+#pragma unroll
+    for (int s = 0; s < 16; s++) {
+        const int f = s >> 2, t = s & 3;
+        p[s] = mfma16(S.w[f], b[t]);
+        DSV4_ORDER();
+        if (s < 2) promote(S.acc[3][2 + s], S.pc[s], S.csp[s]);
+        else promote(S.acc[(s - 2) >> 2][(s - 2) & 3], p[s - 2], S.cs[(s - 2) & 3]);
+        if (s == 1) {
+            DSV4_ORDER();
+            __builtin_amdgcn_s_waitcnt(waitcnt(VM_STAGE, true));
+            __builtin_amdgcn_s_barrier();
+            asm volatile("" ::: "memory");
+            DSV4_ORDER();
+        }
+        if (s >= 2 && s < 2 + VM_STAGE) issue_one(a, d, fill, kl, wave, s - 2);
+        if (s == 2) sw2 = weight_scale<WF32S>(a, nb, min(kb + 2, nkb - 1));
+        if (s >= 2 && s < 6) bn[s - 2] = read_b(nst, d, s - 2);
+        if (s >= 6 && s < 10) sa[s - 6] = *(const float *)(nst + d.sa + 64 * (s - 6));
+        if (s == 10) w3n = read_w(nst, d, 3);
+        if (t == 3 && f < 3) S.w[f] = read_w(nst, d, f);
+        DSV4_ORDER();
+    }
+    S.w[3] = w3n;
+    S.pc[0] = p[14];
+    S.pc[1] = p[15];
+    S.csp[0] = S.cs[2];
+    S.csp[1] = S.cs[3];
+#pragma unroll
+    for (int t = 0; t < 4; t++) S.cs[t] = sa[t] * S.sw_next;
+    S.sw_next = sw2;
+}
+
 template <bool OUT_BF16>
-__device__ __forceinline__ void write_tile(const GemmArgs &a, const uint8_t *lds, int m0, int n0,
-                                           int tid, int nthreads)
+__device__ __forceinline__ void stage_frag(uint8_t *lds, const v4f &acc, int tok, int f)
+{
+    constexpr int EB = OUT_BF16 ? 2 : 4;
+    uint8_t *row = lds + tok * (GN * EB);
+    const int c = (f * EB) >> 4, off = (f * EB) & 15;
+    uint8_t *dst = row + 16 * (c ^ (tok & 31)) + off;
+    if constexpr (OUT_BF16) {
+        uint2 pk;
+        pk.x = f32_to_bf16_bits(acc[0]) | (f32_to_bf16_bits(acc[1]) << 16);
+        pk.y = f32_to_bf16_bits(acc[2]) | (f32_to_bf16_bits(acc[3]) << 16);
+        *(uint2 *)dst = pk;
+    } else {
+        *(f32x4 *)dst = f32x4{acc[0], acc[1], acc[2], acc[3]};
+    }
+}
+
+/* Output staging: the workgroup's 128 x 256 tile sits in LDS as rows of GN
+ * elements, 16-byte chunk c of row r stored at chunk c ^ (r % 32), and is
+ * copied to C in whole 16-byte pieces of contiguous rows. */
+template <bool OUT_BF16>
+__device__ __forceinline__ void write_tile(const GemmArgs &a, const uint8_t *lds, int m0, int n0)
 {
     constexpr int EB = OUT_BF16 ? 2 : 4;
     constexpr int CPR = GN * EB / 16;                  /* 16-byte chunks per row */
     const int live = min(GN, a.N - n0) * EB / 16;       /* a 128-wide N tail uses half */
-    for (int i = tid; i < GM * CPR; i += nthreads) {
+    for (int i = threadIdx.x; i < GM * CPR; i += NWAVE * 64) {
         const int r = i / CPR, c = i % CPR;
         const int m = m0 + r;
         if (m >= a.M || c >= live) continue;
@@ -144,228 +316,8 @@ __device__ __forceinline__ void write_tile(const GemmArgs &a, const uint8_t *lds
 
 } // namespace
 
-/* The 13 direct-to-LDS loads a wave issues per K block. Instruction j of the
- * workgroup fills staged rows 8j .. 8j+7 (1 KiB): lane l row 8j + l/8, slot
- * l%8, which holds logical chunk swz(row, l%8). Per-lane byte offsets are
- * fixed; the K block only moves the wave-uniform base. */
-struct DmaPlan {
-    uint32_t a[4];      /* Aq bytes, from column 0                          */
-    uint32_t w[8];      /* W bytes, from column 0                           */
-    uint32_t s;         /* Sa (waves 0, 1) or fp32 Sw (waves 2, 3) bytes    */
-    int nb;             /* weight block row of this lane's E8M0 scale load  */
-};
-
-template <bool WF32S>
-__device__ __forceinline__ DmaPlan make_plan(const GemmArgs &a, int m0, int n0, int wave, int lane)
-{
-    DmaPlan d;
-    const int r8 = lane >> 3, p = lane & 7, nkb = a.K / GK;
-#pragma unroll
-    for (int i = 0; i < 4; i++) {
-        const int r = 8 * (wave * 4 + i) + r8;
-        const int m = min(m0 + r, a.M - 1);
-        d.a[i] = (uint32_t)m * (uint32_t)a.K + 16u * (uint32_t)swz(r, p);
-    }
-#pragma unroll
-    for (int i = 0; i < 8; i++) {
-        const int r = 8 * (wave * 8 + i) + r8;
-        const int n = min(n0 + r, a.N - 1);
-        d.w[i] = (uint32_t)n * (uint32_t)a.K + 16u * (uint32_t)swz(r, p);
-    }
-    /* waves 0, 1: 64 token scales each; wave 2: the two weight-block scales
-     * (lanes 0, 1 land in the stage, the rest in the pad); wave 3: pad only */
-    d.nb = min(n0 / 128 + (lane & 1), a.N / 128 - 1);
-    if (wave < 2) d.s = (uint32_t)min(m0 + 64 * wave + lane, a.M - 1) * (uint32_t)nkb * 4u;
-    else d.s = (uint32_t)d.nb * (uint32_t)nkb * 4u;
-    return d;
-}
-
-/* Part PART (0: A rows, 1: first half of W rows, 2: second half and the
- * scales) of the loads of K block kb into stage buffer st. */
-template <bool WF32S, int PART>
-__device__ __forceinline__ void issue_part(const GemmArgs &a, const DmaPlan &d, uint8_t *st,
-                                           int kb, int wave)
-{
-    const size_t kofs = (size_t)kb * GK;
-    if constexpr (PART == 0) {
-        const uint8_t *base = a.Aq + kofs;
-#pragma unroll
-        for (int i = 0; i < 4; i++) dma16(base + d.a[i], st + ST_A + 1024 * (wave * 4 + i));
-    } else {
-        const uint8_t *base = a.W + kofs;
-#pragma unroll
-        for (int i = 4 * (PART - 1); i < 4 * PART; i++)
-            dma16(base + d.w[i], st + ST_W + 1024 * (wave * 8 + i));
-    }
-    if constexpr (PART == 2) {
-        if (wave < 2) {
-            dma4((const uint8_t *)a.Sa + 4 * kb + d.s, st + ST_SA + 256 * wave);
-        } else if constexpr (WF32S) {
-            dma4((const uint8_t *)a.Sw + 4 * kb + d.s, st + (wave == 2 ? ST_SW : ST_PAD));
-        } else {
-            /* an E8M0 scale is one byte: load the aligned dword holding it and
-             * pick the byte when reading (load_ops) */
-            const size_t si = (size_t)d.nb * (a.K / GK) + kb;
-            dma4((const uint8_t *)a.Sw + (si & ~(size_t)3), st + (wave == 2 ? ST_SW : ST_PAD));
-        }
-    }
-}
-
-/* Operands of one K block that are read before its first MFMA: the wave's
- * token operands (both 64-wide k steps, both 32-token halves), the weight
- * operand of feature tile 0, and the two combined scales s_a * s_w. */
-struct Ops {
-    v8i b[2][2];        /* [k step][token half]  */
-    v8i w0[2];          /* [k step]              */
-    float cs[2];        /* [token half]          */
-};
-
-template <bool WF32S>
-__device__ __forceinline__ void load_ops(Ops &o, const uint8_t *stage, const GemmArgs &a,
-                                         int kb, int n0, int wm, int wn, int col, int g)
-{
-    const uint8_t *As = stage + ST_A + (wm * 64) * GK;
-    const uint8_t *Ws = stage + ST_W + (wn * 128) * GK;
-#pragma unroll
-    for (int ks = 0; ks < 2; ks++)
-#pragma unroll
-        for (int u = 0; u < 2; u++)
-            o.b[ks][u] = lds_operand(As + (u * 32 + col) * GK, u * 32 + col, ks, g);
-#pragma unroll
-    for (int ks = 0; ks < 2; ks++) o.w0[ks] = lds_operand(Ws + col * GK, col, ks, g);
-    float sw;
-    if constexpr (WF32S) {
-        sw = *(const float *)(stage + ST_SW + 4 * wn);
-    } else {
-        const int nb = min(n0 / 128 + wn, a.N / 128 - 1);
-        const int shift = 8 * (int)(((size_t)nb * (a.K / GK) + kb) & 3);
-        sw = dev_e8m0((*(const uint32_t *)(stage + ST_SW + 4 * wn) >> shift) & 0xFFu);
-    }
-    const float *sa = (const float *)(stage + ST_SA);
-#pragma unroll
-    for (int u = 0; u < 2; u++) o.cs[u] = sa[wm * 64 + u * 32 + col] * sw;
-}
-
-__device__ __forceinline__ v16f mfma(const v8i &w, const v8i &b, const v16f &c)
-{
-    return __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(w, b, c, 0, 0, 0, E8M0_ONE, 0, E8M0_ONE);
-}
-
-/* acc[u] += p[u] * cs[u] over a tile's 16 outputs per lane */
-__device__ __forceinline__ void promote(v16f (&acc)[2], const v16f (&p)[2], const float (&cs)[2])
-{
-#pragma unroll
-    for (int u = 0; u < 2; u++)
-#pragma unroll
-        for (int e = 0; e < 16; e++) acc[u][e] = fmaf(p[u][e], cs[u], acc[u][e]);
-}
-
-/* One issue slot pattern per feature tile: the next tile's operand reads
- * first, then MFMA / direct load / eight promotion FMAs, four times, so the
- * vector ALU and the load path work in the shadow of the matrix unit. */
-#define GEMM_SLOT(NVM)                                                         \
-    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);                         \
-    __builtin_amdgcn_sched_group_barrier(0x010, NVM, 0);                       \
-    __builtin_amdgcn_sched_group_barrier(0x002, 8, 0)
-#define GEMM_STEP_PATTERN(NDS, NVM_LAST)                                       \
-    do {                                                                       \
-        __builtin_amdgcn_sched_group_barrier(0x100, NDS, 0);                   \
-        GEMM_SLOT(1); GEMM_SLOT(1); GEMM_SLOT(1); GEMM_SLOT(NVM_LAST);         \
-    } while (0)
-
-/* One 128-wide K block. On entry `cur` holds block kb's first operands and
- * stage kb is visible; pp / csp are the previous block's tile-3 partial and
- * scales (zero before block 0). Tile t's MFMAs run while tile t-1 is
- * promoted. Between tiles 2 and 3 every wave has finished reading stage kb
- * and waits for its share of stage kb+1; after the barrier `nxt` is read from
- * stage kb+1 while tile 3 multiplies. Loads of block kb+2 go into the buffer
- * freed at the previous block's barrier; past the last block they repeat the
- * last block (harmless traffic that keeps every wait count constant). */
-template <bool WF32S>
-__device__ __forceinline__ void kblock(const GemmArgs &a, const DmaPlan &d, uint8_t *lds, int &buf,
-                                       int kb, int nkb, const Ops &cur, Ops &nxt,
-                                       v16f (&acc)[4][2], v16f (&pp)[2], float (&csp)[2],
-                                       const v16f &zero, int n0, int wave, int wm, int wn,
-                                       int col, int g)
-{
-    const uint8_t *stage = lds + buf * STAGE;
-    const uint8_t *Ws = stage + ST_W + (wn * 128) * GK;
-    int b1 = buf + 1; b1 = b1 == NSTAGE ? 0 : b1;
-    int b2 = b1 + 1;  b2 = b2 == NSTAGE ? 0 : b2;
-    uint8_t *dst = lds + b2 * STAGE;
-    const int kl = min(kb + 2, nkb - 1);
-    v16f p[2];
-    v8i w1[2], w2[2], w3[2];
-
-    /* tile 0 */
-#pragma unroll
-    for (int ks = 0; ks < 2; ks++) w1[ks] = lds_operand(Ws + (32 + col) * GK, 32 + col, ks, g);
-    {
-        const v16f q0 = mfma(cur.w0[0], cur.b[0][0], zero);
-        const v16f q1 = mfma(cur.w0[0], cur.b[0][1], zero);
-        issue_part<WF32S, 0>(a, d, dst, kl, wave);
-        promote(acc[3], pp, csp);
-        p[0] = mfma(cur.w0[1], cur.b[1][0], q0);
-        p[1] = mfma(cur.w0[1], cur.b[1][1], q1);
-    }
-    /* tile 1 */
-    v16f pn[2];
-#pragma unroll
-    for (int ks = 0; ks < 2; ks++) w2[ks] = lds_operand(Ws + (64 + col) * GK, 64 + col, ks, g);
-    {
-        const v16f q0 = mfma(w1[0], cur.b[0][0], zero);
-        const v16f q1 = mfma(w1[0], cur.b[0][1], zero);
-        issue_part<WF32S, 1>(a, d, dst, kl, wave);
-        promote(acc[0], p, cur.cs);
-        pn[0] = mfma(w1[1], cur.b[1][0], q0);
-        pn[1] = mfma(w1[1], cur.b[1][1], q1);
-    }
-    /* tile 2 */
-#pragma unroll
-    for (int ks = 0; ks < 2; ks++) w3[ks] = lds_operand(Ws + (96 + col) * GK, 96 + col, ks, g);
-    {
-        const v16f q0 = mfma(w2[0], cur.b[0][0], zero);
-        const v16f q1 = mfma(w2[0], cur.b[0][1], zero);
-        issue_part<WF32S, 2>(a, d, dst, kl, wave);
-        promote(acc[1], pn, cur.cs);
-        p[0] = mfma(w2[1], cur.b[1][0], q0);
-        p[1] = mfma(w2[1], cur.b[1][1], q1);
-    }
-    GEMM_SLOT(1); GEMM_SLOT(1); GEMM_SLOT(1); GEMM_SLOT(1);
-    GEMM_SLOT(1); GEMM_SLOT(1); GEMM_SLOT(1); GEMM_SLOT(1);
-    GEMM_SLOT(1); GEMM_SLOT(1); GEMM_SLOT(1); GEMM_SLOT(2);
-    DSV4_ORDER();
-    /* stage kb fully read by this wave (lgkmcnt 0); stage kb+1 landed for this
-     * wave once only block kb+2's 13 loads are outstanding (vmcnt 13). The
-     * barrier is a plain s_barrier: __syncthreads() would also drain the
-     * loads of block kb+2. */
-    __builtin_amdgcn_s_waitcnt(0x0070 | VMEM_PER_STAGE);
-    __builtin_amdgcn_s_barrier();
-    asm volatile("" ::: "memory");
-    DSV4_ORDER();
-    /* tile 3, reading block kb+1's first operands meanwhile */
-    load_ops<WF32S>(nxt, lds + b1 * STAGE, a, kb + 1, n0, wm, wn, col, g);
-    {
-        const v16f q0 = mfma(w3[0], cur.b[0][0], zero);
-        const v16f q1 = mfma(w3[0], cur.b[0][1], zero);
-        promote(acc[2], p, cur.cs);
-        pp[0] = mfma(w3[1], cur.b[1][0], q0);
-        pp[1] = mfma(w3[1], cur.b[1][1], q1);
-    }
-    __builtin_amdgcn_sched_group_barrier(0x100, 15, 0);
-#pragma unroll
-    for (int i = 0; i < 4; i++) {
-        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-        __builtin_amdgcn_sched_group_barrier(0x002, 8, 0);
-    }
-    DSV4_ORDER();
-    csp[0] = cur.cs[0];
-    csp[1] = cur.cs[1];
-    buf = b1;
-}
-
 template <bool WF32S, bool OUT_BF16>
-__global__ __launch_bounds__(256) void k_gemm_fp8(GemmArgs a)
+__global__ __launch_bounds__(512) void k_gemm_fp8(GemmArgs a)
 {
     extern __shared__ __align__(16) uint8_t lds[];
     const int lane = threadIdx.x & 63;
@@ -373,54 +325,63 @@ __global__ __launch_bounds__(256) void k_gemm_fp8(GemmArgs a)
     const int wm = wave & 1, wn = wave >> 1;
     const int m0 = blockIdx.y * GM, n0 = blockIdx.x * GN;
     const int nkb = a.K / GK;
-    const int col = lane & 31, g = lane >> 5;
-    const DmaPlan d = make_plan<WF32S>(a, m0, n0, wave, lane);
+    const int nb = min((n0 + 64 * wn) / 128, a.N / 128 - 1);
+    const Plan d = make_plan(a, m0, n0, wave, lane);
 
-    v16f acc[4][2], pp[2], zero;
+    State S;
 #pragma unroll
-    for (int e = 0; e < 16; e++) {
-        zero[e] = 0.0f;
-        pp[0][e] = 0.0f;
-        pp[1][e] = 0.0f;
+    for (int e = 0; e < 4; e++) {
+        S.pc[0][e] = 0.0f;
+        S.pc[1][e] = 0.0f;
 #pragma unroll
-        for (int t = 0; t < 4; t++) { acc[t][0][e] = 0.0f; acc[t][1][e] = 0.0f; }
+        for (int f = 0; f < 4; f++)
+#pragma unroll
+            for (int t = 0; t < 4; t++) S.acc[f][t][e] = 0.0f;
     }
-    float csp[2] = {0.0f, 0.0f};
+    S.csp[0] = 0.0f;
+    S.csp[1] = 0.0f;
 
-    /* blocks 0 and 1 (block 1 repeats block 0 when K is one block) */
-    issue_part<WF32S, 0>(a, d, lds, 0, wave);
-    issue_part<WF32S, 1>(a, d, lds, 0, wave);
-    issue_part<WF32S, 2>(a, d, lds, 0, wave);
-    const int k1 = min(1, nkb - 1);
-    issue_part<WF32S, 0>(a, d, lds + STAGE, k1, wave);
-    issue_part<WF32S, 1>(a, d, lds + STAGE, k1, wave);
-    issue_part<WF32S, 2>(a, d, lds + STAGE, k1, wave);
-    __builtin_amdgcn_s_waitcnt(0x0F70 | VMEM_PER_STAGE);
+    /* blocks 0, 1, 2 (repeating the last block when K is shorter) */
+    issue(a, d, lds, 0, wave);
+    DSV4_ORDER();
+    issue(a, d, lds + STAGE, min(1, nkb - 1), wave);
+    DSV4_ORDER();
+    issue(a, d, lds + 2 * STAGE, min(2, nkb - 1), wave);
+    DSV4_ORDER();
+    const float sw0 = weight_scale<WF32S>(a, nb, 0);
+    S.sw_next = weight_scale<WF32S>(a, nb, min(1, nkb - 1));
+    __builtin_amdgcn_s_waitcnt(waitcnt(2 * VM_STAGE, true));
     __builtin_amdgcn_s_barrier();
     asm volatile("" ::: "memory");
 
-    Ops o0, o1;
-    load_ops<WF32S>(o0, lds, a, 0, n0, wm, wn, col, g);
-    int buf = 0, kb = 0;
-    for (; kb + 1 < nkb; kb += 2) {
-        kblock<WF32S>(a, d, lds, buf, kb, nkb, o0, o1, acc, pp, csp, zero, n0, wave, wm, wn, col, g);
-        kblock<WF32S>(a, d, lds, buf, kb + 1, nkb, o1, o0, acc, pp, csp, zero, n0, wave, wm, wn, col, g);
+    v8i b0[4], b1[4];
+#pragma unroll
+    for (int q = 0; q < 4; q++) {
+        S.w[q] = read_w(lds, d, q);
+        b0[q] = read_b(lds, d, q);
+        S.cs[q] = *(const float *)(lds + d.sa + 64 * q) * sw0;
     }
-    if (kb < nkb)
-        kblock<WF32S>(a, d, lds, buf, kb, nkb, o0, o1, acc, pp, csp, zero, n0, wave, wm, wn, col, g);
-    promote(acc[3], pp, csp);
-    /* drain the trailing repeat loads before the workgroup's LDS is released */
-    __builtin_amdgcn_s_waitcnt(0x0F70);
-
-    __builtin_amdgcn_s_barrier();      /* every wave is done with the stage buffers */
+    int kb = 0;
+    for (; kb + 1 < nkb; kb += 2) {
+        kblock<WF32S>(a, d, lds, S, b0, b1, kb, nkb, nb, wave);
+        kblock<WF32S>(a, d, lds, S, b1, b0, kb + 1, nkb, nb, wave);
+    }
+    if (kb < nkb) kblock<WF32S>(a, d, lds, S, b0, b1, kb, nkb, nb, wave);
+    promote(S.acc[3][2], S.pc[0], S.csp[0]);
+    promote(S.acc[3][3], S.pc[1], S.csp[1]);
+    /* drain the trailing repeat loads and reads before the ring becomes the
+     * output staging area */
+    __builtin_amdgcn_s_waitcnt(waitcnt(0, true));
+    __builtin_amdgcn_s_barrier();
     asm volatile("" ::: "memory");
+    const int r16 = lane & 15, g = lane >> 4;
 #pragma unroll
-    for (int t = 0; t < 4; t++)
+    for (int f = 0; f < 4; f++)
 #pragma unroll
-        for (int u = 0; u < 2; u++)
-            stage_frag<OUT_BF16>(lds, acc[t][u], wm * 64 + u * 32, wn * 128 + t * 32, col, g);
+        for (int t = 0; t < 4; t++)
+            stage_frag<OUT_BF16>(lds, S.acc[f][t], 64 * wm + 16 * t + r16, 64 * wn + 16 * f + 4 * g);
     __syncthreads();
-    write_tile<OUT_BF16>(a, lds, m0, n0, threadIdx.x, 256);
+    write_tile<OUT_BF16>(a, lds, m0, n0);
 }
 
 template <bool WS, bool OB>
@@ -430,20 +391,21 @@ static hipError_t launch_gemm(const GemmArgs &a, hipStream_t st)
     if (!attr_done) {
         const hipError_t e = hipFuncSetAttribute((const void *)k_gemm_fp8<WS, OB>,
                                                  hipFuncAttributeMaxDynamicSharedMemorySize,
-                                                 LDS_BYTES);
+                                                 lds_bytes(OB));
         if (e != hipSuccess) return e;
         attr_done = true;
     }
-    const dim3 grid((unsigned)((a.N + GN - 1) / GN), (unsigned)((a.M + GM - 1) / GM)), block(256);
-    hipLaunchKernelGGL((k_gemm_fp8<WS, OB>), grid, block, LDS_BYTES, st, a);
+    const dim3 grid((unsigned)((a.N + GN - 1) / GN), (unsigned)((a.M + GM - 1) / GM)), block(512);
+    hipLaunchKernelGGL((k_gemm_fp8<WS, OB>), grid, block, lds_bytes(OB), st, a);
     return hipGetLastError();
 }
 
 hipError_t gemm_fp8_launch(const GemmArgs &a, bool w_f32s, bool out_bf16, hipStream_t st)
 {
     if (a.K % GK || a.N % 128 || a.M <= 0) return hipErrorInvalidValue;
-    /* the loads address A and W with 32-bit per-lane byte offsets */
-    if ((size_t)a.M * a.K > 0xFFFFFFFFull || (size_t)a.N * a.K > 0xFFFFFFFFull)
+    /* the loads address A, W and Sa with 32-bit per-lane byte offsets */
+    if ((size_t)a.M * a.K > 0xFFFFFFFFull || (size_t)a.N * a.K > 0xFFFFFFFFull ||
+        (size_t)a.M * a.sa_tok * 4 > 0xFFFFFFFFull)
         return hipErrorInvalidValue;
     if (w_f32s) return out_bf16 ? launch_gemm<true, true>(a, st) : launch_gemm<true, false>(a, st);
     return out_bf16 ? launch_gemm<false, true>(a, st) : launch_gemm<false, false>(a, st);

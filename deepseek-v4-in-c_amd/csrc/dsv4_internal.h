@@ -175,9 +175,10 @@ hipError_t down_mx_launch(DownMxArgs a, hipStream_t st);
 size_t mx_split_bytes(int inter);
 
 /* ---------------------------------------------------- prefill GEMM --- */
-/* C[m][n] = sum_k A[m][k] W[n][k]: Aq e4m3 [M][K] with fp32 Sa [M][K/128];
- * W e4m3 [N][K] with Sw [N/128][K/128] fp32 (w_f32s) or E8M0 bytes; C bf16
- * or fp32 [M][ldc]. K % 128 == 0, N % 128 == 0. */
+/* C[m][n] = sum_k A[m][k] W[n][k]: Aq e4m3 [M][K] with one fp32 scale per
+ * token and 128-wide K block at Sa[m * sa_tok + kb * sa_kb]; W e4m3 [N][K]
+ * with Sw [N/128][K/128] fp32 (w_f32s) or E8M0 bytes; C bf16 or fp32
+ * [M][ldc]. K % 128 == 0, N % 128 == 0. */
 struct GemmArgs {
     const uint8_t *Aq;
     const float *Sa;
@@ -185,6 +186,7 @@ struct GemmArgs {
     const void *Sw;
     void *C;
     int M, N, K, ldc;
+    int sa_tok, sa_kb;
 };
 hipError_t gemm_fp8_launch(const GemmArgs &a, bool w_f32s, bool out_bf16, hipStream_t st);
 
@@ -194,9 +196,11 @@ hipError_t quant_fp4_mx_launch(uint8_t *W, uint8_t *S, const float *w, int rows,
                                int cols, hipStream_t st);
 hipError_t quant_fp8_blk128_launch(uint8_t *W, float *S, const float *w,
                                    int rows, int cols, hipStream_t st);
-/* a is fp32, or bf16 bits when bf16_in */
+/* a is fp32, or bf16 bits when bf16_in; S is [n][k/128], or [k/128][n] when
+ * s_blk_major */
 hipError_t quant_act_fp8_1x128_launch(uint8_t *Q, float *S, const void *a,
-                                      int n, int k, bool bf16_in, hipStream_t st);
+                                      int n, int k, bool bf16_in, bool s_blk_major,
+                                      hipStream_t st);
 hipError_t quant_act_mxfp8_launch(uint8_t *Q, uint8_t *S, const float *a,
                                   int n, int k, hipStream_t st);
 hipError_t synth_normal_launch(float *out, size_t n, uint64_t seed, float sigma,

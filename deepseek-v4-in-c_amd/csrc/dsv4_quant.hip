@@ -237,8 +237,10 @@ __device__ __forceinline__ uint32_t hw_e4m3(float v)
 /* 16 lanes per 1x128 group, 8 consecutive elements per lane (one 16-byte
  * bf16 load or two fp32 loads, one 8-byte store); a 256-thread block covers
  * 16 groups. s = amax / 448 (1 if the group is all zero), q = e4m3(v / s)
- * with a correctly rounded division -- the oracle's rule. */
-template <bool BF16_IN>
+ * with a correctly rounded division -- the oracle's rule. The scale of token
+ * t, block b goes to S[t][b], or to S[b][t] (S_BLK_MAJOR: one block's scales
+ * of consecutive tokens are contiguous, as the GEMM reads them). */
+template <bool BF16_IN, bool S_BLK_MAJOR>
 __global__ __launch_bounds__(256) void k_quant_act_fp8_1x128(uint8_t *Q, float *S,
                                                             const void *a, int n, int k)
 {
@@ -268,7 +270,10 @@ __global__ __launch_bounds__(256) void k_quant_act_fp8_1x128(uint8_t *Q, float *
     for (int off = 8; off > 0; off >>= 1) m = fmaxf(m, __shfl_xor(m, off));
     const float sc = m > 0.0f ? m / 448.0f : 1.0f;
     if (!live) return;
-    if ((threadIdx.x & 15) == 0) S[e / 128] = sc;
+    if ((threadIdx.x & 15) == 0) {
+        if (S_BLK_MAJOR) S[(e % (size_t)k) / 128 * (size_t)n + e / (size_t)k] = sc;
+        else S[e / 128] = sc;
+    }
     uint2 out;
     out.x = hw_e4m3(v[0] / sc) | (hw_e4m3(v[1] / sc) << 8) | (hw_e4m3(v[2] / sc) << 16) |
             (hw_e4m3(v[3] / sc) << 24);
@@ -278,12 +283,19 @@ __global__ __launch_bounds__(256) void k_quant_act_fp8_1x128(uint8_t *Q, float *
 }
 
 hipError_t quant_act_fp8_1x128_launch(uint8_t *Q, float *S, const void *a,
-                                      int n, int k, bool bf16_in, hipStream_t st)
+                                      int n, int k, bool bf16_in, bool s_blk_major,
+                                      hipStream_t st)
 {
     const size_t lanes = (size_t)n * k / 8;
     const dim3 grid((unsigned)((lanes + 255) / 256)), block(256);
-    if (bf16_in) hipLaunchKernelGGL(k_quant_act_fp8_1x128<true>, grid, block, 0, st, Q, S, a, n, k);
-    else hipLaunchKernelGGL(k_quant_act_fp8_1x128<false>, grid, block, 0, st, Q, S, a, n, k);
+    if (bf16_in && s_blk_major)
+        hipLaunchKernelGGL((k_quant_act_fp8_1x128<true, true>), grid, block, 0, st, Q, S, a, n, k);
+    else if (bf16_in)
+        hipLaunchKernelGGL((k_quant_act_fp8_1x128<true, false>), grid, block, 0, st, Q, S, a, n, k);
+    else if (s_blk_major)
+        hipLaunchKernelGGL((k_quant_act_fp8_1x128<false, true>), grid, block, 0, st, Q, S, a, n, k);
+    else
+        hipLaunchKernelGGL((k_quant_act_fp8_1x128<false, false>), grid, block, 0, st, Q, S, a, n, k);
     return hipGetLastError();
 }
 

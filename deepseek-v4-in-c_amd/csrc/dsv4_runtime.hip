@@ -642,12 +642,15 @@ int gemm_checks(const void *C, const void *A, int M, const DSV4QMat *W, const ch
     return 0;
 }
 
+/* Sa holds one fp32 per (token, 128-wide K block), block-major [K/128][M]. */
 int enqueue_gemm(void *C, int out_bf16, const uint8_t *Aq, const float *Sa, int M,
                  const DSV4QMat *W, int fmt, hipStream_t st)
 {
     GemmArgs ga;
     ga.Aq = Aq; ga.Sa = Sa; ga.W = (const uint8_t *)W->w; ga.Sw = W->s; ga.C = C;
     ga.M = M; ga.N = W->rows; ga.K = W->cols; ga.ldc = W->rows;
+    ga.sa_tok = 1;
+    ga.sa_kb = M;
     HIPCHK(gemm_fp8_launch(ga, fmt == FMT_FP8_F32S, out_bf16 != 0, st), "gemm launch");
     return 0;
 }
@@ -665,7 +668,8 @@ int dsv4_hip_gemm_fp8_dev(void *C, int out_bf16, const void *A, int a_bf16, int 
     uint8_t *Aq = (uint8_t *)g.gemm_ws.p;
     float *Sa = (float *)(Aq + qbytes);
     hipStream_t st = (hipStream_t)stream;
-    HIPCHK(quant_act_fp8_1x128_launch(Aq, Sa, A, M, K, a_bf16 != 0, st), "activation quant launch");
+    HIPCHK(quant_act_fp8_1x128_launch(Aq, Sa, A, M, K, a_bf16 != 0, true, st),
+           "activation quant launch");
     return enqueue_gemm(C, out_bf16, Aq, Sa, M, W, fmt, st);
 }
 
@@ -913,7 +917,8 @@ int dsv4_hip_quant_act_fp8_1x128_dev(uint8_t *Q, float *S, const float *a, int n
         return fail("quant_act_fp8_1x128_dev: bad argument");
     if (((uintptr_t)Q & 7u) != 0 || ((uintptr_t)a & 15u) != 0 || ((uintptr_t)S & 3u) != 0)
         return fail("quant_act_fp8_1x128_dev: need Q 8-, a 16- and S 4-byte aligned");
-    HIPCHK(quant_act_fp8_1x128_launch(Q, S, a, n, k, false, (hipStream_t)stream), "quant launch");
+    HIPCHK(quant_act_fp8_1x128_launch(Q, S, a, n, k, false, true, (hipStream_t)stream),
+           "quant launch");
     return 0;
 }
 

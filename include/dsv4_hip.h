@@ -181,8 +181,8 @@ int  dsv4_hip_gemm_fp8_dev(void *C, int out_bf16, const void *A, int a_bf16,
                            int M, const DSV4QMat *W, void *stream);
 
 /* The same GEMM on activations the caller already quantized:
- * Aq [M][W->cols] e4m3, Sa [M][W->cols / 128] fp32 (as produced by
- * dsv4_hip_quant_act_fp8_1x128_dev). No workspace. */
+ * Aq [M][W->cols] e4m3, Sa [W->cols / 128][M] fp32, block-major (as produced
+ * by dsv4_hip_quant_act_fp8_1x128_dev). No workspace. */
 int  dsv4_hip_gemm_fp8q_dev(void *C, int out_bf16, const uint8_t *Aq,
                             const float *Sa, int M, const DSV4QMat *W,
                             void *stream);

@@ -32,8 +32,10 @@ int dsv4_hip_quant_fp4_mx_dev(uint8_t *W, uint8_t *S, const float *w,
                               int rows, int cols, void *stream);
 
 /* n x k activations (k % 128 == 0) -> e4m3 Q[n*k] + fp32 scale per 1x128
- * S[n][k/128] = groupmax/448 (1 if all zero). Q 8-byte, a 16-byte and S
- * 4-byte aligned. */
+ * group = groupmax/448 (1 if all zero), stored block-major: the scale of row
+ * r, 128-column block b is S[b * n + r] (the layout dsv4_hip_gemm_fp8q_dev
+ * reads: one block's scales of consecutive rows are contiguous). Q 8-byte,
+ * a 16-byte and S 4-byte aligned. */
 int dsv4_hip_quant_act_fp8_1x128_dev(uint8_t *Q, float *S, const float *a,
                                      int n, int k, void *stream);
 

@@ -363,7 +363,8 @@ def test_gpu_quantizers_bitexact(lib, pkg, oracle):
     Sa = torch.empty(6 * 4, dtype=torch.float32, device=DEV)
     lib.quant_act_fp8_1x128_dev(Q.data_ptr(), Sa.data_ptr(), da.data_ptr(), 6, 512)
     Qo, So = oracle.quant_act_fp8_1x128(a)
-    assert np.array_equal(Q.cpu().numpy(), Qo) and np.array_equal(bits(Sa.cpu().numpy()), bits(So))
+    got_s = np.ascontiguousarray(Sa.cpu().numpy().reshape(4, 6).T).reshape(-1)   # block-major
+    assert np.array_equal(Q.cpu().numpy(), Qo) and np.array_equal(bits(got_s), bits(So))
 
     Qm = torch.empty(6 * 512, dtype=torch.uint8, device=DEV)
     Sm = torch.empty(6 * 16, dtype=torch.uint8, device=DEV)

@@ -123,7 +123,8 @@ def test_gemm_prequantized_matches_fused(lib, pkg, oracle):
     W, S = make_weight(oracle, rng, n, k)
     fused = run_gemm(lib, pkg, A, W, S, n, k, True, out_bf16=0, a_bf16=0)
     Q, Sa = oracle.quant_act_fp8_1x128(A)
-    dW, dS, dQ, dSa = dev(W), dev(S), dev(Q), dev(Sa)
+    Sa_blk = np.ascontiguousarray(Sa.reshape(m, k // 128).T)    # the entry point's block-major layout
+    dW, dS, dQ, dSa = dev(W), dev(S), dev(Q), dev(Sa_blk)
     desc = pkg.qmat(pkg.DSV4_WFP8_F32S, dW.data_ptr(), dS.data_ptr(), n, k, 128, 128)
     C = torch.empty((m, n), dtype=torch.float32, device=DEV)
     lib.gemm_fp8q_dev(C.data_ptr(), 0, dQ.data_ptr(), dSa.data_ptr(), m, desc)
@@ -176,7 +177,8 @@ def test_act_quant_1x128_edge_cases(lib, pkg, oracle):
     lib.quant_act_fp8_1x128_dev(Q.data_ptr(), S.data_ptr(), da.data_ptr(), n, k)
     torch.cuda.synchronize()
     Qo, So = oracle.quant_act_fp8_1x128(a)
-    got_q, got_s = Q.cpu().numpy(), S.cpu().numpy()
+    got_q = Q.cpu().numpy()
+    got_s = np.ascontiguousarray(S.cpu().numpy().reshape(k // 128, n).T).reshape(-1)   # block-major
     assert np.array_equal(bits(got_s), bits(So))
     bad = np.nonzero(got_q != Qo)[0]
     assert bad.size == 0, f"{bad.size} codes differ, first at {bad[:4]}: {got_q[bad[:4]]} vs {Qo[bad[:4]]}"
