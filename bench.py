@@ -565,7 +565,21 @@ def main():
         out = torch.empty(HIDDEN, dtype=torch.float32, device="cuda:0")
         torch.cuda.synchronize()
 
+        # The router of the reference runs on the host (src/70_decode/dsv4_layer.c:57-116):
+        # the timed path takes each token's top-6 ids and weights from the host and
+        # passes the six descriptors by value (dsv4_hip_moe_decode_routed_dev). The
+        # device-routed form (ids / weights in HBM, dsv4_hip_moe_decode_dev) is timed too.
+        ex_arr = (pkg.ExpertW * N_EXPERTS)(*arena.descs)
+        ids_c = [(C.c_int * TOPK)(*[int(v) for v in idx_h[i]]) for i in range(K + W + K)]
+        wts_c = [(C.c_float * TOPK)(*[float(v) for v in w_h[i]]) for i in range(K + W + K)]
+        routed_fn = lib.lib.dsv4_hip_moe_decode_routed_dev
+
         def step(i):
+            if routed_fn(out.data_ptr(), xs.data_ptr() + 4 * HIDDEN * i, ex_arr, N_EXPERTS,
+                         ids_c[i], wts_c[i], TOPK, None, HIDDEN, INTER, C.c_float(10.0), sp):
+                lib.check(-1, "dsv4_hip_moe_decode_routed_dev")
+
+        def step_dev(i):
             lib.moe_decode_dev(out.data_ptr(), xs.data_ptr() + 4 * HIDDEN * i,
                                arena.table.data_ptr(), N_EXPERTS,
                                idx.data_ptr() + 4 * TOPK * i, wts.data_ptr() + 4 * TOPK * i,
@@ -573,20 +587,27 @@ def main():
 
         for i in range(W):
             step(i)
+            step_dev(i)
         torch.cuda.synchronize()
         assert lib.status() == 0
         log(f"timing {K} steps")
+
+        def timed(fn):
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record(stream)
+            for i in range(K):
+                fn(W + i)
+            e1.record(stream)
+            torch.cuda.synchronize()
+            return e0.elapsed_time(e1) * 1e-3 / K
+
         t0 = time.perf_counter()
-        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        e0.record(stream)
-        for i in range(K):
-            step(W + i)
-        e1.record(stream)
-        torch.cuda.synchronize()
+        t_step = timed(step)
         wall = time.perf_counter() - t0
-        t_step = e0.elapsed_time(e1) * 1e-3 / K
+        t_step_dev = timed(step_dev)
         # per-launch durations (each call bracketed by its own events)
         t_launch = time_events(torch, stream, lambda i: step(W + K + i), K)
+        t_launch_dev = time_events(torch, stream, lambda i: step_dev(W + K + i), K)
         assert lib.status() == 0
         bytes_step = TOPK * EXPERT_BYTES + 8192 + 16384
         value = bytes_step / t_step / 1e9
@@ -612,9 +633,13 @@ def main():
             "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS,
                          "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
                          "traffic": traffic_for(1),
-                         "kernel": "moe_decode_dev call (k_gateup_px + k_down_px)",
+                         "kernel": "moe_decode_routed_dev call (k_gateup_px + k_down_px)",
                          "bytes_per_launch": bytes_step,
                          "launch_us": round(t_launch * 1e6, 3)},
+            "device_routed": {"entry": "dsv4_hip_moe_decode_dev (ids and weights in HBM)",
+                              "ms_per_step": round(t_step_dev * 1e3, 5),
+                              "value": round(bytes_step / t_step_dev / 1e9, 2),
+                              "launch_us": round(t_launch_dev * 1e6, 3)},
             "cpu_baseline": cpu,
             "wall_s": round(wall, 4),
         }

@@ -368,6 +368,43 @@ __device__ __forceinline__ void sum_parts(v4f &acc)
     }
 }
 
+/* The expert of gate/up slot `slot`: by value from the kernel arguments (host
+ * routing), the direct descriptor, or table[idx[slot]]; a routing id out of
+ * range is reported. */
+__device__ __forceinline__ unsigned gateup_expert(const GateUpMxArgs &a, int slot, DSV4ExpertW &e)
+{
+    if (a.by_value) {
+        e = a.routed[slot];
+        return 0;
+    }
+    if (a.use_direct) {
+        e = a.direct;
+        return 0;
+    }
+    const int id = ld_uniform(a.idx, slot);
+    if (id < 0 || id >= a.n_experts) return ST_BAD_EXPERT_ID;
+    e = ld_uniform(a.table, id);
+    return 0;
+}
+
+/* The down matrix of routed slot k and its routing weight. */
+__device__ __forceinline__ unsigned down_expert(const DownMxArgs &a, int k, DSV4QMat &m)
+{
+    if (a.by_value) {
+        m = a.w2v[k];
+        return 0;
+    }
+    const int id = ld_uniform(a.idx, k);
+    if (id < 0 || id >= a.n_experts) return ST_BAD_EXPERT_ID;
+    m = ld_uniform(a.table, id).w2;
+    return 0;
+}
+
+__device__ __forceinline__ float route_weight(const DownMxArgs &a, int k)
+{
+    return a.by_value ? a.wv[k] : ld_uniform(a.w, k);
+}
+
 template <int FMT>
 __device__ __forceinline__ bool mx_desc_ok(const DSV4QMat &m, int rows, int cols)
 {
@@ -465,14 +502,7 @@ __device__ __forceinline__ void gateup_mx_body(const GateUpMxArgs &a)
     constexpr int UPL = (CPW * 16 + 63) / 64;
 
     DSV4ExpertW e;
-    unsigned bad = 0;
-    if (a.use_direct) {
-        e = a.direct;
-    } else {
-        const int id = ld_uniform(a.idx, slot);
-        if (id < 0 || id >= a.n_experts) bad = ST_BAD_EXPERT_ID;
-        else e = ld_uniform(a.table, id);
-    }
+    unsigned bad = gateup_expert(a, slot, e);
     if (!bad && (!mx_desc_ok<FMT>(e.w1, a.inter, a.hidden) || !mx_desc_ok<FMT>(e.w3, a.inter, a.hidden)))
         bad = ST_BAD_DESCRIPTOR;
     if (bad) {
@@ -595,12 +625,8 @@ __global__ __launch_bounds__(1024) void k_down_mx(DownMxArgs a)
 
     unsigned bad = 0;
     DSV4QMat m;
-    const int id = ld_uniform(a.idx, k);
-    if (id < 0 || id >= a.n_experts) bad = ST_BAD_EXPERT_ID;
-    else {
-        m = ld_uniform(a.table, id).w2;
-        if (!mx_desc_ok<FMT_FP4_E8M0>(m, a.hidden, a.inter)) bad = ST_BAD_DESCRIPTOR;
-    }
+    bad = down_expert(a, k, m);
+    if (!bad && !mx_desc_ok<FMT_FP4_E8M0>(m, a.hidden, a.inter)) bad = ST_BAD_DESCRIPTOR;
     float mine[4] = {qnan_f(), qnan_f(), qnan_f(), qnan_f()};
     if (!bad) {
         /* B: columns 0..3 are the four parts of slot k's mid */
@@ -650,7 +676,7 @@ __global__ __launch_bounds__(1024) void k_down_mx(DownMxArgs a)
     float o = 0.0f;
     for (int kk = 0; kk < a.topk; kk++) {
         const float y = ylds[kk][0][lane] + ylds[kk][1][lane];
-        o = __fadd_rn(o, __fmul_rn(ld_uniform(a.w, kk), y));
+        o = __fadd_rn(o, __fmul_rn(route_weight(a, kk), y));
     }
     if (a.shared) o = __fadd_rn(o, a.shared[r0 + lane]);
     a.out[r0 + lane] = o;
@@ -786,7 +812,6 @@ __device__ __forceinline__ void store_pair_partials(v4f acc, float *dst, int lan
  * pairs each). The workgroup splits x once into LDS (one unit of eight
  * elements per thread for hidden 4096) and every wave reads its half from
  * there. Writes mid and, when a.msplit is set, mid's split table. */
-constexpr int GU_LDS_TAIL = (4 * 2 * 2 * 16 + 32) * 4;
 
 template <int NP>
 __device__ __forceinline__ void gateup_px_item(const GateUpMxArgs &a, int item, uint8_t *lds)
@@ -808,14 +833,7 @@ __device__ __forceinline__ void gateup_px_item(const GateUpMxArgs &a, int item, 
     float *mid = a.mid + (size_t)slot * a.mid_ld;
 
     DSV4ExpertW e;
-    unsigned bad = 0;
-    if (a.use_direct) {
-        e = a.direct;
-    } else {
-        const int id = ld_uniform(a.idx, slot);
-        if (id < 0 || id >= a.n_experts) bad = ST_BAD_EXPERT_ID;
-        else e = ld_uniform(a.table, id);
-    }
+    unsigned bad = gateup_expert(a, slot, e);
     if (!bad && (!mx_desc_ok<FMT_FP4_E8M0>(e.w1, a.inter, a.hidden) ||
                  !mx_desc_ok<FMT_FP4_E8M0>(e.w3, a.inter, a.hidden)))
         bad = ST_BAD_DESCRIPTOR;
@@ -928,12 +946,8 @@ __global__ __launch_bounds__(1024) void k_down_px(DownMxArgs a)
 
     unsigned bad = 0;
     DSV4QMat m;
-    const int id = ld_uniform(a.idx, k);
-    if (id < 0 || id >= a.n_experts) bad = ST_BAD_EXPERT_ID;
-    else {
-        m = ld_uniform(a.table, id).w2;
-        if (!mx_desc_ok<FMT_FP4_E8M0>(m, a.hidden, a.inter)) bad = ST_BAD_DESCRIPTOR;
-    }
+    bad = down_expert(a, k, m);
+    if (!bad && !mx_desc_ok<FMT_FP4_E8M0>(m, a.hidden, a.inter)) bad = ST_BAD_DESCRIPTOR;
     float part[16];
 #pragma unroll
     for (int i = 0; i < 16; i++) part[i] = qnan_f();
@@ -978,7 +992,7 @@ __global__ __launch_bounds__(1024) void k_down_px(DownMxArgs a)
     float o = 0.0f;
     for (int kk = 0; kk < a.topk; kk++) {
         const float y = ylds[kk][tt][rr] + ylds[kk][tt][8 + rr];
-        o = __fadd_rn(o, __fmul_rn(ld_uniform(a.w, kk), y));
+        o = __fadd_rn(o, __fmul_rn(route_weight(a, kk), y));
     }
     if (a.shared) o = __fadd_rn(o, a.shared[blockIdx.x * 16 + lane]);
     a.out[blockIdx.x * 16 + lane] = o;

@@ -132,9 +132,14 @@ struct GemvMxArgs {
 int gemv_mx_ncw(int fmt, int cols);
 hipError_t gemv_mx_launch(int fmt, GemvMxArgs a, hipStream_t st);
 
+/* Routed experts whose descriptors travel by value in the kernel arguments
+ * (routing known on the host): at most this many slots. */
+constexpr int MX_ROUTED_MAX = 8;
+
 /* Gate/up + SwiGLU for `nslots` experts (like GateUpArgs); also writes the
  * split table of each slot's mid (msplit + slot * msplit_ld) when msplit is
- * set. inter % 128 == 0, hidden % 128 == 0. */
+ * set. inter % 128 == 0, hidden % 128 == 0. Slot s uses routed[s] when
+ * by_value, else direct when use_direct, else table[idx[s]]. */
 struct GateUpMxArgs {
     const DSV4ExpertW *table;
     const int *idx;
@@ -151,11 +156,14 @@ struct GateUpMxArgs {
     float limit;
     unsigned *status;
     int ncw;
+    int by_value;
+    DSV4ExpertW routed[MX_ROUTED_MAX];
 };
 hipError_t gateup_mx_launch(int fmt, GateUpMxArgs a, hipStream_t st);
 
 /* Routed FP4 down projections from the split tables of mid, with the k-order
- * combine (+ shared); topk <= 8. */
+ * combine (+ shared); topk <= 8. Slot k uses w2v[k] and weight wv[k] when
+ * by_value, else table[idx[k]].w2 and w[k]. */
 struct DownMxArgs {
     const DSV4ExpertW *table;
     const int *idx;
@@ -169,6 +177,9 @@ struct DownMxArgs {
     int inter, hidden;
     unsigned *status;
     int ncw;
+    int by_value;
+    DSV4QMat w2v[MX_ROUTED_MAX];
+    float wv[MX_ROUTED_MAX];
 };
 hipError_t down_mx_launch(DownMxArgs a, hipStream_t st);
 /* bytes of one slot's split table for a K of `inter` */

@@ -265,10 +265,14 @@ int enqueue_expert(const DSV4ExpertW &e, int fmt, int inter, int hidden,
 }
 
 /* Enqueue the decode MoE from device tables. */
+/* Routed slots come from table[idx[k]] with weights w[k] (device arrays), or,
+ * when `routed` is set, from the host arrays routed[k] / wv[k], passed by
+ * value in the kernel arguments (MFMA path only). */
 int enqueue_moe(const DSV4ExpertW *table, int n_experts, const int *idx,
                 const float *w, int topk, const DSV4ExpertW *shared_dev,
                 int shared_fmt, int shared_inter, int hidden, int inter,
-                const float *x, float *out, float limit, hipStream_t st)
+                const float *x, float *out, float limit, hipStream_t st,
+                const DSV4ExpertW *routed = nullptr, const float *wv = nullptr)
 {
     const size_t mid_ld = (size_t)((inter + 3) & ~3);
     const size_t smid_ld = (size_t)((shared_inter + 3) & ~3);
@@ -283,7 +287,12 @@ int enqueue_moe(const DSV4ExpertW *table, int n_experts, const int *idx,
                            ys, limit, st))
             return -1;
     }
-    if (mx_expert_ok(FMT_FP4_E8M0, inter, hidden) && inter <= 2048 && topk <= 8 && aligned16(x)) {
+    const bool mx = mx_expert_ok(FMT_FP4_E8M0, inter, hidden) && inter <= 2048 &&
+                    topk <= MX_ROUTED_MAX && aligned16(x);
+    if (routed && !mx)
+        return fail("moe_decode_routed_dev: needs the MFMA path (FP4 experts, hidden and inter "
+                    "multiples of 128, inter <= 2048, topk <= %d, x 16-byte aligned)", MX_ROUTED_MAX);
+    if (mx) {
         /* routed experts on the block-scaled MFMA: gate/up writes each slot's
          * mid split table, down reads it and combines in k order */
         const size_t sl = mx_split_bytes(inter);
@@ -303,6 +312,10 @@ int enqueue_moe(const DSV4ExpertW *table, int n_experts, const int *idx,
         ga.hidden = hidden;
         ga.limit = limit;
         ga.status = g.status;
+        if (routed) {
+            ga.by_value = 1;
+            for (int k = 0; k < topk; k++) ga.routed[k] = routed[k];
+        }
         HIPCHK(gateup_mx_launch(FMT_FP4_E8M0, ga, st), "routed gate/up launch");
         DownMxArgs da;
         memset(&da, 0, sizeof da);
@@ -318,6 +331,13 @@ int enqueue_moe(const DSV4ExpertW *table, int n_experts, const int *idx,
         da.inter = inter;
         da.hidden = hidden;
         da.status = g.status;
+        if (routed) {
+            da.by_value = 1;
+            for (int k = 0; k < topk; k++) {
+                da.w2v[k] = routed[k].w2;
+                da.wv[k] = wv[k];
+            }
+        }
         HIPCHK(down_mx_launch(da, st), "down/combine launch");
         return 0;
     }
@@ -625,6 +645,44 @@ int dsv4_hip_moe_decode_dev(float *out, const float *x, const DSV4ExpertW *exper
     }
     return enqueue_moe(experts, n_experts, idx, w, topk, shared, sfmt, sinter,
                        hidden, inter, x, out, limit, (hipStream_t)stream);
+}
+
+int dsv4_hip_moe_decode_routed_dev(float *out, const float *x, const DSV4ExpertW *experts,
+                                   int n_experts, const int *idx, const float *w, int topk,
+                                   const DSV4ExpertW *shared, int hidden, int inter,
+                                   float limit, void *stream)
+{
+    std::lock_guard<std::mutex> lk(g.mu);
+    if (usable()) return -1;
+    if (!out || !x || !experts || !idx || !w) return fail("moe_decode_routed_dev: NULL pointer");
+    if (topk < 1 || topk > MX_ROUTED_MAX)
+        return fail("moe_decode_routed_dev: topk %d outside 1..%d", topk, MX_ROUTED_MAX);
+    if (n_experts < 1) return fail("moe_decode_routed_dev: no experts");
+    if (!aligned16(x)) return fail("moe_decode_routed_dev: x must be 16-byte aligned");
+    DSV4ExpertW routed[MX_ROUTED_MAX];
+    float wv[MX_ROUTED_MAX];
+    for (int k = 0; k < topk; k++) {
+        const int id = idx[k];
+        if (id < 0 || id >= n_experts)
+            return fail("moe_decode_routed_dev: routing id %d of slot %d outside 0..%d", id, k,
+                        n_experts - 1);
+        int f, ei, eh;
+        if (expert_geometry(&experts[id], &f, &ei, &eh, "moe_decode_routed_dev expert")) return -1;
+        if (f != FMT_FP4_E8M0 || ei != inter || eh != hidden)
+            return fail("moe_decode_routed_dev: expert %d is not FP4 [%d x %d]", id, inter, hidden);
+        routed[k] = experts[id];
+        wv[k] = w[k];
+    }
+    int sfmt = -1, sinter = 0;
+    if (shared) {
+        int sh;
+        if (expert_geometry(shared, &sfmt, &sinter, &sh, "moe_decode_routed_dev shared")) return -1;
+        if (sh != hidden) return fail("moe_decode_routed_dev: shared hidden %d != %d", sh, hidden);
+        if (!aligned16(shared->w1.w) || !aligned16(shared->w3.w) || !aligned16(shared->w2.w))
+            return fail("moe_decode_routed_dev: shared weights must be 16-byte aligned");
+    }
+    return enqueue_moe(nullptr, n_experts, nullptr, nullptr, topk, shared, sfmt, sinter, hidden,
+                       inter, x, out, limit, (hipStream_t)stream, routed, wv);
 }
 
 /* Shared checks of the FP8 GEMM entry points; returns the weight format. */

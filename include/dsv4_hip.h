@@ -133,6 +133,22 @@ int  dsv4_hip_moe_decode_dev(float *out, const float *x,
                              const DSV4ExpertW *shared, int hidden, int inter,
                              float limit, void *stream);
 
+/* Host-routed device form, for callers whose router runs on the host as the
+ * reference's does (src/70_decode/dsv4_layer.c:57-116 picks top-k on the CPU
+ * and then calls the experts): `experts` is a HOST array of descriptors
+ * holding device pointers, idx / w are HOST arrays of topk <= 8 entries, x /
+ * out are device arrays. The topk descriptors and weights travel by value in
+ * the kernel arguments, so no device-side lookup precedes the weight stream.
+ * Same results as dsv4_hip_moe_decode_dev bit for bit. A routing id out of
+ * range, a routed expert that is not FP4 [inter x hidden] or a geometry the
+ * FP4 MFMA path does not take (hidden, inter multiples of 128, inter <= 2048)
+ * returns -1 before anything is launched. */
+int  dsv4_hip_moe_decode_routed_dev(float *out, const float *x,
+                                    const DSV4ExpertW *experts, int n_experts,
+                                    const int *idx, const float *w, int topk,
+                                    const DSV4ExpertW *shared, int hidden, int inter,
+                                    float limit, void *stream);
+
 /* ------------------------------------- grouped MoE (a13-a15, a18) ---------
  * For n tokens (batched decode or a prefill block):
  *   out[t] = sum_{k in 0..topk-1, in k order} w[t][k] * expert_{idx[t][k]}(x[t])

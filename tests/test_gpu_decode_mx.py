@@ -11,7 +11,8 @@ import numpy as np
 import pytest
 import torch
 
-from conftest import REL_L2_TOL, rel_l2
+import pyoracle as P
+from conftest import REL_L2_TOL, bits, rel_l2
 from test_gpu_decode import (DEV, Resident, _rand_fp8, bf16_x, check_close, dev_f32, dev_u8,
                              make_fp4_expert, make_fp8_shared)
 
@@ -178,3 +179,81 @@ def test_mx_moe_decode_bad_descriptor_poisons(lib, pkg, oracle):
                        w.data_ptr(), 2, None, hidden, inter, 10.0)
     assert lib.status() & 2
     assert torch.isnan(out).all()
+
+
+def _device_fp4_experts(pkg, oracle, rng, n, inter, hidden):
+    """n FP4 experts with device-resident weights: (device descriptors, host
+    experts for the oracle, tensors to keep alive)."""
+    descs, host, keep = [], [], []
+    for _ in range(n):
+        q, hm = [], []
+        for (r, c) in ((inter, hidden), (inter, hidden), (hidden, inter)):
+            W, S = oracle.quant_fp4_mx((rng.standard_normal((r, c)) * 0.02).astype(np.float32))
+            dW, dS = dev_u8(W), dev_u8(S)
+            keep += [dW, dS]
+            q.append(pkg.qmat(pkg.DSV4_WFP4, dW.data_ptr(), dS.data_ptr(), r, c, 1, 32))
+            hm.append(P.HostMat(pkg.DSV4_WFP4, W, S, r, c, 1, 32))
+        descs.append(pkg.ExpertW(q[0], q[1], q[2]))          # w1, w3, w2
+        host.append(P.HostExpert(hm[0], hm[1], hm[2]))
+    return descs, host, keep
+
+
+@pytest.mark.parametrize("inter,hidden,topk", [(256, 1024, 8), (2048, 4096, 6)])
+def test_moe_decode_routed_matches_device_routed(lib, pkg, oracle, inter, hidden, topk):
+    """The host-routed entry (descriptors and weights by value in the kernel
+    arguments) gives the device-routed entry's output bit for bit, and the
+    oracle's within 1e-4."""
+    rng = np.random.default_rng(zlib.crc32(b"routed") + inter + topk)
+    n_exp = topk + 3
+    descs, host, keep = _device_fp4_experts(pkg, oracle, rng, n_exp, inter, hidden)
+    idx = rng.choice(n_exp, topk, replace=False).astype(np.int32)
+    lg = rng.standard_normal(topk)
+    w = (np.exp(lg) / np.exp(lg).sum()).astype(np.float32)
+    xh = bf16_x(11, hidden)
+    x = dev_f32(xh)
+    arr = (pkg.ExpertW * n_exp)(*descs)
+    tbl = torch.from_numpy(np.frombuffer(b"".join(bytes(d) for d in descs), np.uint8).copy()).to(DEV)
+    didx = torch.from_numpy(idx).to(DEV)
+    dw = dev_f32(w)
+    out_r = torch.empty(hidden, dtype=torch.float32, device=DEV)
+    out_d = torch.empty(hidden, dtype=torch.float32, device=DEV)
+    lib.status()
+    lib.moe_decode_routed_dev(out_r.data_ptr(), x.data_ptr(), arr, idx, w, topk, None,
+                              hidden, inter, 10.0)
+    lib.moe_decode_dev(out_d.data_ptr(), x.data_ptr(), tbl.data_ptr(), n_exp, didx.data_ptr(),
+                       dw.data_ptr(), topk, None, hidden, inter, 10.0)
+    torch.cuda.synchronize()
+    assert lib.status() == 0
+    got = out_r.cpu().numpy()
+    assert np.array_equal(bits(got), bits(out_d.cpu().numpy()))
+    acc = np.stack([oracle.expert_forward(host[i], xh, 10.0) for i in idx])
+    assert check_close(got, oracle.moe_combine(acc, w)) < 1e-4
+
+
+def test_moe_decode_routed_rejects_bad_routing(lib, pkg, oracle):
+    """A routing id out of range or a routed expert of the wrong format is
+    refused on the host before anything is launched; the backend stays usable."""
+    rng = np.random.default_rng(zlib.crc32(b"routed-bad"))
+    inter, hidden = 128, 512
+    descs, host, keep = _device_fp4_experts(pkg, oracle, rng, 2, inter, hidden)
+    arr = (pkg.ExpertW * 2)(*descs)
+    xh = bf16_x(12, hidden)
+    x = dev_f32(xh)
+    out = torch.zeros(hidden, dtype=torch.float32, device=DEV)
+    w = np.array([0.5, 0.5], np.float32)
+    with pytest.raises(Exception, match="routing id 2 of slot 1"):
+        lib.moe_decode_routed_dev(out.data_ptr(), x.data_ptr(), arr, [0, 2], w, 2, None,
+                                  hidden, inter, 10.0)
+    bad = pkg.ExpertW(pkg.qmat(pkg.DSV4_WFP8, descs[0].w1.w, descs[0].w1.s, inter, hidden, 128, 128),
+                      descs[0].w3, descs[0].w2)
+    arr_bad = (pkg.ExpertW * 2)(descs[0], bad)
+    with pytest.raises(Exception, match="moe_decode_routed_dev"):
+        lib.moe_decode_routed_dev(out.data_ptr(), x.data_ptr(), arr_bad, [0, 1], w, 2, None,
+                                  hidden, inter, 10.0)
+    torch.cuda.synchronize()
+    assert torch.count_nonzero(out) == 0           # nothing ran
+    lib.moe_decode_routed_dev(out.data_ptr(), x.data_ptr(), arr, [1, 0], w, 2, None,
+                              hidden, inter, 10.0)
+    torch.cuda.synchronize()
+    acc = np.stack([oracle.expert_forward(host[i], xh, 10.0) for i in (1, 0)])
+    assert check_close(out.cpu().numpy(), oracle.moe_combine(acc, w)) < 1e-4
