@@ -633,7 +633,7 @@ def main():
             "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS,
                          "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
                          "traffic": traffic_for(1),
-                         "kernel": "moe_decode_routed_dev call (k_gateup_px + k_down_px)",
+                         "kernel": "moe_decode_routed_dev call (k_moe_one: gate/up and down workgroups in one launch)",
                          "bytes_per_launch": bytes_step,
                          "launch_us": round(t_launch * 1e6, 3)},
             "device_routed": {"entry": "dsv4_hip_moe_decode_dev (ids and weights in HBM)",

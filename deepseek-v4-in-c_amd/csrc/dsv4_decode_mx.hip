@@ -49,6 +49,8 @@
  */
 #include "dsv4_internal.h"
 
+#include <algorithm>
+
 namespace dsv4 {
 
 namespace {
@@ -66,6 +68,53 @@ constexpr int KSLICES = 4;                        /* waves per tile along K */
 /* The zero B operand and unit scale for columns that carry no token, in
  * kernels whose split tables live in global memory. */
 __device__ uint32_t g_zero_operand[16] = {0, 0, 0, 0, 0, 0, 0, 0, E8M0_ONE, 0, 0, 0, 0, 0, 0, 0};
+
+/* Publication of mid's split tables between the workgroups of one launch,
+ * without fences: the writer's stores are device-scope (written through the
+ * XCD's L2) and acknowledged (vmcnt) before the slot counter is bumped; the
+ * reader polls the counter and then reads the table with device-scope loads,
+ * which bypass its CU's L1 and its XCD's L2, so a line cached by the previous
+ * call is never used. */
+__device__ __forceinline__ void st_dev32(void *p, uint32_t v)
+{
+    __hip_atomic_store((uint32_t *)p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+constexpr int CPOL_SC1 = 16;                      /* buffer cache policy: device scope */
+constexpr uint32_t BUF_WORD3 = 0x00020000u;       /* raw dword buffer */
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t dev_rsrc(const void *p, uint32_t bytes)
+{
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(p), (short)0, (int)bytes, (int)BUF_WORD3);
+}
+
+/* This wave's stores acknowledged, then one more item counted; the item that
+ * completes the call raises the done flag (its add returns after every
+ * earlier add, each issued after that item's stores were acknowledged). */
+__device__ __forceinline__ void publish(const OnePub &p, int lane)
+{
+    __builtin_amdgcn_s_waitcnt(0x0F70);            /* vmcnt(0) */
+    asm volatile("" ::: "memory");
+    if (lane == 0) {
+        const unsigned old = __hip_atomic_fetch_add(p.count, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (old == p.last) __hip_atomic_store(p.done, p.epoch, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+}
+
+/* Poll the done flag until it reaches the call's epoch (wrapping compare);
+ * false after spin_max polls. */
+__device__ __forceinline__ bool wait_done(const OnePub &p, unsigned spin_max)
+{
+    for (unsigned n = 0;; n++) {
+        const unsigned v = (unsigned)__builtin_amdgcn_readfirstlane(
+            (int)__hip_atomic_load(p.done, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
+        if ((int)(v - p.epoch) >= 0) break;
+        if (n >= spin_max) return false;
+        __builtin_amdgcn_s_sleep(16);              /* ~1k cycles between polls */
+    }
+    asm volatile("" ::: "memory");                 /* the table reads stay after the poll */
+    return true;
+}
 
 template <int CTRL>
 __device__ __forceinline__ float dpp_f(float v)
@@ -814,7 +863,8 @@ __device__ __forceinline__ void store_pair_partials(v4f acc, float *dst, int lan
  * there. Writes mid and, when a.msplit is set, mid's split table. */
 
 template <int NP>
-__device__ __forceinline__ void gateup_px_item(const GateUpMxArgs &a, int item, uint8_t *lds)
+__device__ __forceinline__ void gateup_px_item(const GateUpMxArgs &a, int item, uint8_t *lds,
+                                               const OnePub *pub = nullptr)
 {
     constexpr int NC = 4 * NP;                         /* chunks of hidden */
     constexpr int UPL = (NC * 16 + 511) / 512;
@@ -842,8 +892,8 @@ __device__ __forceinline__ void gateup_px_item(const GateUpMxArgs &a, int item, 
         if (threadIdx.x < 32) mid[j0 + threadIdx.x] = qnan_f();
         /* NaN block scales (E8M0 255) make the down projection of this slot NaN */
         if (a.msplit && threadIdx.x < NPART)
-            *(int *)(a.msplit + (size_t)slot * a.msplit_ld + (size_t)(j0 >> 7) * TAB_CHUNK +
-                     TAB_DATA + (((j0 >> 5) & 3) * NPART + threadIdx.x) * 4) = 255;
+            st_dev32(a.msplit + (size_t)slot * a.msplit_ld + (size_t)(j0 >> 7) * TAB_CHUNK + TAB_DATA +
+                     (((j0 >> 5) & 3) * NPART + threadIdx.x) * 4, 255u);
     } else {
         const int row_bytes = a.hidden / 2, sc_cols = a.hidden / 32;
         XUnits<UPL> xu;
@@ -911,16 +961,19 @@ __device__ __forceinline__ void gateup_px_item(const GateUpMxArgs &a, int item, 
                 const int kk = 32 * b4 + 8 * lane;
                 const int h = (kk & 63) >> 4, half = kk >> 6;
 #pragma unroll
-                for (int p = 0; p < NPART; p++)
-                    *(uint2 *)(cb + (h * NPART + p) * 32 + half * 16 + (kk & 15)) =
-                        make_uint2(code[p][0], code[p][1]);
+                for (int p = 0; p < NPART; p++) {
+                    uint8_t *d = cb + (h * NPART + p) * 32 + half * 16 + (kk & 15);
+                    st_dev32(d, code[p][0]);
+                    st_dev32(d + 4, code[p][1]);
+                }
                 if (lane == 0) {
 #pragma unroll
-                    for (int p = 0; p < NPART; p++) *(int *)(cb + TAB_DATA + (b4 * NPART + p) * 4) = E[p];
+                    for (int p = 0; p < NPART; p++) st_dev32(cb + TAB_DATA + (b4 * NPART + p) * 4, (uint32_t)E[p]);
                 }
             }
         }
     }
+    if (pub && wave == 0) publish(*pub, lane);     /* this item's block of slot's table is out */
 }
 
 template <int NP>
@@ -996,6 +1049,140 @@ __global__ __launch_bounds__(1024) void k_down_px(DownMxArgs a)
     }
     if (a.shared) o = __fadd_rn(o, a.shared[blockIdx.x * 16 + lane]);
     a.out[blockIdx.x * 16 + lane] = o;
+}
+
+/* ------------------------------------------- one-launch decode MoE --- */
+
+typedef __attribute__((address_space(3))) void lds_void_t;
+
+/* LDS of a down workgroup of the one-launch form: the partial sums
+ * [slot][tile][16], the ready word, then per routed slot its split table in
+ * whole 1 KiB DMA rounds and a zero operand. */
+constexpr int ONE_YL_BYTES = MX_ROUTED_MAX * 2 * 16 * 4;
+constexpr int ONE_HEAD_BYTES = ONE_YL_BYTES + 64;
+__host__ __device__ constexpr int one_tab_rounds(int inter) { return (inter / 128 * TAB_CHUNK + 1023) / 1024; }
+__host__ __device__ constexpr int one_slot_lds(int inter) { return one_tab_rounds(inter) * 1024 + TAB_ZERO; }
+
+/* s_waitcnt lgkmcnt(0) + s_barrier: a workgroup barrier that leaves the
+ * weight loads in flight (__syncthreads() would drain them). */
+__device__ __forceinline__ void lds_barrier()
+{
+    __builtin_amdgcn_s_waitcnt(0xC07F);
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+}
+
+/* Down workgroup of the one-launch form: output rows 16 grp .. 16 grp + 15,
+ * wave k = routed slot k over both 8-row tiles and all of inter (inter =
+ * 256 NP). The down weights load first; wave 0 then waits for every slot's
+ * mid; each wave copies its slot's split table into LDS with device-scope
+ * loads and runs the MFMA sequence, partial sums and k-order combine of
+ * k_down_px. */
+template <int NP>
+__device__ __forceinline__ void down_one_group(const MoeOneArgs &A, int grp, uint8_t *lds)
+{
+    const DownMxArgs &a = A.dn;
+    constexpr int ROUNDS = one_tab_rounds(256 * NP), SLOT = one_slot_lds(256 * NP);
+    float(*yl)[2][16] = (float(*)[2][16])lds;
+    int *ready_ok = (int *)(lds + ONE_YL_BYTES);
+    const int lane = threadIdx.x & 63;
+    const int k = wave_in_group();
+    const int r0 = grp * 16;
+    const bool live = k < a.topk;
+    uint8_t *tab = lds + ONE_HEAD_BYTES + k * SLOT;
+    unsigned bad = 0;
+    APairs<NP> w0, w1;
+    if (live) {
+        const int row_bytes = a.inter / 2, sc_cols = a.inter / 32;
+        DSV4QMat m;
+        bad = down_expert(a, k, m);
+        if (!bad && !mx_desc_ok<FMT_FP4_E8M0>(m, a.hidden, a.inter)) bad = ST_BAD_DESCRIPTOR;
+        if (!bad) {
+            const int row0 = min(r0 + (lane & 7), a.hidden - 1), row1 = min(r0 + 8 + (lane & 7), a.hidden - 1);
+            ld_pairs_scales<NP>(w0, (const uint8_t *)m.s, sc_cols, m.blk_r, row0, r0, a.hidden - 1, 0, lane);
+            ld_pairs_scales<NP>(w1, (const uint8_t *)m.s, sc_cols, m.blk_r, row1, r0 + 8, a.hidden - 1, 0, lane);
+            DSV4_ORDER();
+            ld_pairs_w<NP>(w0, (const uint8_t *)m.w + (size_t)row0 * row_bytes, 0, lane);
+            ld_pairs_w<NP>(w1, (const uint8_t *)m.w + (size_t)row1 * row_bytes, 0, lane);
+            DSV4_ORDER();
+            ld_pairs_scales_finish<NP>(w0, lane);
+            ld_pairs_scales_finish<NP>(w1, lane);
+            if (lane < TAB_ZERO / 4)                   /* zero operand, unit scale */
+                ((uint32_t *)(tab + ROUNDS * 1024))[lane] = lane == 8 ? E8M0_ONE : 0u;
+        }
+    }
+    /* wave 0 waits for every slot's mid (each feeds every output row) and
+     * releases the workgroup; the weight loads stay in flight */
+    if (k == 0) {
+        const bool ok = wait_done(A.pub, A.spin_max);
+        if (lane == 0) *ready_ok = ok ? 1 : 0;
+    }
+    lds_barrier();
+    if (live) {
+        if (!bad && !*ready_ok) bad = ST_SYNC_TIMEOUT;
+        if (!bad) {
+            /* slot k's table, 16 bytes a lane per round (past its end: zeros) */
+            const __amdgpu_buffer_rsrc_t rt = dev_rsrc(a.msplit + (size_t)k * a.msplit_ld, (uint32_t)a.msplit_ld);
+#pragma unroll
+            for (int r = 0; r < ROUNDS; r++)
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(rt, (lds_void_t *)(tab + 1024 * r), 16,
+                                                         1024 * r + 16 * lane, 0, 0, CPOL_SC1);
+            __builtin_amdgcn_s_waitcnt(0x0F70);        /* vmcnt(0): the copy (and the weights) landed */
+            asm volatile("" ::: "memory");
+            const BPair bp = bpair_src(tab, 0, tab + ROUNDS * 1024, lane);
+            v4f acc0 = {0.0f, 0.0f, 0.0f, 0.0f}, acc1 = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+            for (int mm = 0; mm < NP; mm++) {
+                const u32x4 lo = *(const u32x4 *)(bp.d + mm * bp.step);
+                const u32x4 hi = *(const u32x4 *)(bp.d + mm * bp.step + 16);
+                const int sb = *(const int *)(bp.s + mm * bp.step);
+                v8i b;
+                b[0] = (int)lo.x; b[1] = (int)lo.y; b[2] = (int)lo.z; b[3] = (int)lo.w;
+                b[4] = (int)hi.x; b[5] = (int)hi.y; b[6] = (int)hi.z; b[7] = (int)hi.w;
+                switch (mm & 3) {
+                case 0: acc0 = mfma_f4_sel<0>(w0.q[mm], b, acc0, w0.s[mm >> 2], sb);
+                        acc1 = mfma_f4_sel<0>(w1.q[mm], b, acc1, w1.s[mm >> 2], sb); break;
+                case 1: acc0 = mfma_f4_sel<1>(w0.q[mm], b, acc0, w0.s[mm >> 2], sb);
+                        acc1 = mfma_f4_sel<1>(w1.q[mm], b, acc1, w1.s[mm >> 2], sb); break;
+                case 2: acc0 = mfma_f4_sel<2>(w0.q[mm], b, acc0, w0.s[mm >> 2], sb);
+                        acc1 = mfma_f4_sel<2>(w1.q[mm], b, acc1, w1.s[mm >> 2], sb); break;
+                default: acc0 = mfma_f4_sel<3>(w0.q[mm], b, acc0, w0.s[mm >> 2], sb);
+                         acc1 = mfma_f4_sel<3>(w1.q[mm], b, acc1, w1.s[mm >> 2], sb); break;
+                }
+            }
+            store_pair_partials(acc0, &yl[k][0][0], lane);
+            store_pair_partials(acc1, &yl[k][1][0], lane);
+        } else {
+            if (lane == 0) atomicOr(a.status, bad);
+            if (lane < 32) yl[k][lane >> 4][lane & 15] = qnan_f();
+        }
+    }
+    __syncthreads();
+    if (threadIdx.x >= 16 || r0 + (int)threadIdx.x >= a.hidden) return;
+    const int t = threadIdx.x >> 3, rr = threadIdx.x & 7;
+    float o = 0.0f;
+    for (int kk = 0; kk < a.topk; kk++) {
+        const float y = yl[kk][t][rr] + yl[kk][t][8 + rr];
+        o = __fadd_rn(o, __fmul_rn(route_weight(a, kk), y));
+    }
+    if (a.shared) o = __fadd_rn(o, a.shared[r0 + threadIdx.x]);
+    a.out[r0 + threadIdx.x] = o;
+}
+
+/* Routed FP4 decode MoE in one launch (hidden = 512 NPG, inter = 256 NPD):
+ * workgroup b < gu_blocks runs gate/up item b and publishes it; the hidden /
+ * 16 down workgroups follow. A workgroup only ever waits on workgroups of
+ * lower id, which the hardware dispatches no later than itself and which
+ * never wait, so the launch cannot deadlock whatever part of it is resident;
+ * every wait is bounded besides. */
+template <int NPG, int NPD>
+__global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) void k_moe_one(MoeOneArgs a)
+{
+    extern __shared__ __align__(16) uint8_t lds[];
+    if ((int)blockIdx.x < a.gu_blocks)
+        gateup_px_item<NPG>(a.gu, (int)blockIdx.x, lds, &a.pub);
+    else
+        down_one_group<NPD>(a, (int)blockIdx.x - a.gu_blocks, lds);
 }
 
 /* ------------------------------------------------------------ launches --- */
@@ -1142,6 +1329,56 @@ hipError_t down_mx_launch(DownMxArgs a, hipStream_t st)
     default: return hipErrorInvalidValue;      /* inter > 2048: 1024 threads cannot hold 16 chunks */
     }
     return hipGetLastError();
+}
+
+bool moe_one_ok(int hidden, int inter, int topk, int cus)
+{
+    if (!(hidden == 512 || hidden == 1024 || hidden == 2048 || hidden == 4096)) return false;
+    if (!(inter == 256 || inter == 512 || inter == 1024 || inter == 2048)) return false;
+    if (topk < 1 || topk > MX_ROUTED_MAX || cus < 1) return false;
+    /* down workgroups: every routed slot's table in LDS, two workgroups per CU */
+    return ONE_HEAD_BYTES + (long)topk * one_slot_lds(inter) <= 80L * 1024;
+}
+
+template <int NPG, int NPD>
+static hipError_t moe_one_k(const MoeOneArgs &a, hipStream_t st)
+{
+    const size_t lds = std::max<size_t>((size_t)4 * NPG * TAB_CHUNK + TAB_ZERO + (4 * 2 * 2 * 16 + 32) * 4,
+                                        (size_t)ONE_HEAD_BYTES + (size_t)a.dn.topk * one_slot_lds(256 * NPD));
+    const unsigned grid = (unsigned)(a.gu_blocks + a.dn.hidden / 16);
+    if (lds > 64 * 1024) {
+        const hipError_t e = hipFuncSetAttribute((const void *)k_moe_one<NPG, NPD>,
+                                                 hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+        if (e != hipSuccess) return e;
+    }
+    hipLaunchKernelGGL((k_moe_one<NPG, NPD>), dim3(grid), dim3(512), lds, st, a);
+    return hipGetLastError();
+}
+
+template <int NPG>
+static hipError_t moe_one_d(const MoeOneArgs &a, hipStream_t st)
+{
+    switch (a.dn.inter) {
+    case 256: return moe_one_k<NPG, 1>(a, st);
+    case 512: return moe_one_k<NPG, 2>(a, st);
+    case 1024: return moe_one_k<NPG, 4>(a, st);
+    default: return moe_one_k<NPG, 8>(a, st);
+    }
+}
+
+hipError_t moe_one_launch(MoeOneArgs a, int cus, hipStream_t st)
+{
+    if (!moe_one_ok(a.gu.hidden, a.gu.inter, a.gu.nslots, cus) || a.dn.hidden != a.gu.hidden ||
+        a.dn.inter != a.gu.inter || a.dn.topk != a.gu.nslots || !a.gu.msplit || !a.pub.count ||
+        !a.pub.done)
+        return hipErrorInvalidValue;
+    a.gu_blocks = a.gu.nslots * (a.gu.inter / 32);
+    switch (a.gu.hidden) {
+    case 512: return moe_one_d<1>(a, st);
+    case 1024: return moe_one_d<2>(a, st);
+    case 2048: return moe_one_d<4>(a, st);
+    default: return moe_one_d<8>(a, st);
+    }
 }
 
 } // namespace dsv4

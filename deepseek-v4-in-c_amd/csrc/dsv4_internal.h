@@ -27,6 +27,8 @@ enum {
     ST_SCALE_RANGE = 1u << 2,     /* FP4 E8M0 scale byte outside 104..140:
                                      the grouped path's fp16 decode is not
                                      exact for that block                   */
+    ST_SYNC_TIMEOUT = 1u << 3,    /* a one-launch decode MoE waited past its
+                                     spin limit for a slot's mid             */
 };
 
 /* Map a descriptor to the kernel format, or -1 when the GPU path does not
@@ -182,6 +184,27 @@ struct DownMxArgs {
     float wv[MX_ROUTED_MAX];
 };
 hipError_t down_mx_launch(DownMxArgs a, hipStream_t st);
+
+/* Gate/up and down of the routed FP4 experts in one launch: workgroups
+ * [0, gu_blocks) run the gate/up items; each item adds one to *count once its
+ * block of mid's split table is out, and the item that takes *count to `last`
+ * writes `epoch` to *done. The hidden / 16 down workgroups after them load
+ * their down weights at once and wait (spin_max polls at most) until *done
+ * reaches epoch. *count and *done only grow, across calls. */
+struct OnePub {
+    unsigned *count, *done;
+    unsigned last, epoch;
+};
+struct MoeOneArgs {
+    GateUpMxArgs gu;
+    DownMxArgs dn;
+    OnePub pub;
+    int gu_blocks;
+    unsigned spin_max;
+};
+/* whether one launch takes this geometry on a device of `cus` CUs */
+bool moe_one_ok(int hidden, int inter, int topk, int cus);
+hipError_t moe_one_launch(MoeOneArgs a, int cus, hipStream_t st);
 /* bytes of one slot's split table for a K of `inter` */
 size_t mx_split_bytes(int inter);
 

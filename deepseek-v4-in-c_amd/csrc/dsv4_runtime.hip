@@ -18,6 +18,7 @@
 #include <vector>
 
 #include <stdarg.h>
+#include <stdlib.h>
 #include <stdio.h>
 #include <string.h>
 
@@ -63,6 +64,9 @@ struct State {
     hipStream_t side = nullptr;          /* concurrent work of one call (shared expert) */
     hipEvent_t fork = nullptr, join = nullptr;
     unsigned *status = nullptr;          /* device status word            */
+    unsigned *pub = nullptr;             /* one-launch decode: item counter, done flag (own line) */
+    unsigned pub_count = 0, pub_epoch = 0;     /* their values after the last enqueued call */
+    int cus = 0;
     std::map<uintptr_t, Region> regions; /* host start -> resident copy   */
     DevBuf x, y, mid, table, small, ys, gemm_ws, moe_ws, x16, msplit;
 };
@@ -316,7 +320,6 @@ int enqueue_moe(const DSV4ExpertW *table, int n_experts, const int *idx,
             ga.by_value = 1;
             for (int k = 0; k < topk; k++) ga.routed[k] = routed[k];
         }
-        HIPCHK(gateup_mx_launch(FMT_FP4_E8M0, ga, st), "routed gate/up launch");
         DownMxArgs da;
         memset(&da, 0, sizeof da);
         da.table = table;
@@ -338,6 +341,27 @@ int enqueue_moe(const DSV4ExpertW *table, int n_experts, const int *idx,
                 da.wv[k] = wv[k];
             }
         }
+        /* one launch: the down workgroups' weight stream overlaps gate/up
+         * and there is no second launch ramp; DSV4_HIP_DECODE_LAUNCHES=2
+         * keeps the two-launch form (same bits) */
+        const char *nl = getenv("DSV4_HIP_DECODE_LAUNCHES");
+        if (!(nl && atoi(nl) == 2) && moe_one_ok(hidden, inter, topk, g.cus)) {
+            MoeOneArgs oa;
+            memset(&oa, 0, sizeof oa);
+            oa.gu = ga;
+            oa.dn = da;
+            const unsigned items = (unsigned)(topk * (inter / 32));
+            oa.pub.count = g.pub;
+            oa.pub.done = g.pub + 32;
+            oa.pub.last = g.pub_count + items - 1;
+            oa.pub.epoch = g.pub_epoch + 1;
+            oa.spin_max = 1u << 20;
+            HIPCHK(moe_one_launch(oa, g.cus, st), "one-launch decode MoE");
+            g.pub_count += items;
+            g.pub_epoch += 1;
+            return 0;
+        }
+        HIPCHK(gateup_mx_launch(FMT_FP4_E8M0, ga, st), "routed gate/up launch");
         HIPCHK(down_mx_launch(da, st), "down/combine launch");
         return 0;
     }
@@ -401,6 +425,10 @@ int dsv4_hip_init(int device)
         return fail("event creation failed");
     if (hipMalloc((void **)&g.status, 256) != hipSuccess) return fail("status alloc failed");
     if (hipMemset(g.status, 0, 256) != hipSuccess) return fail("status clear failed");
+    if (hipMalloc((void **)&g.pub, 256) != hipSuccess) return fail("counter alloc failed");
+    if (hipMemset(g.pub, 0, 256) != hipSuccess) return fail("counter clear failed");
+    g.pub_count = g.pub_epoch = 0;
+    g.cus = prop.multiProcessorCount;
 
     g.device = device;
     g.ready = 1;
@@ -420,6 +448,8 @@ void dsv4_hip_shutdown(void)
     g.moe_ws.release(); g.x16.release(); g.msplit.release();
     if (g.status) (void)hipFree(g.status);
     g.status = nullptr;
+    if (g.pub) (void)hipFree(g.pub);
+    g.pub = nullptr;
     if (g.stream) (void)hipStreamDestroy(g.stream);
     if (g.side) (void)hipStreamDestroy(g.side);
     if (g.fork) (void)hipEventDestroy(g.fork);

@@ -126,7 +126,11 @@ int  dsv4_hip_moe_decode(float *out, const float *x,
  * pointers) indexed by expert id; idx / w are device arrays of topk entries.
  * `shared` is a HOST descriptor holding device pointers (or NULL). Every
  * routed expert must be DSV4_WFP4 [inter x hidden] / [hidden x inter] with
- * 1x32 blocks. */
+ * 1x32 blocks. With hidden in {512, 1024, 2048, 4096}, inter in {256, 512,
+ * 1024, 2048} and topk <= 8 the routed experts run as one launch (gate/up
+ * and down workgroups in one grid, mid handed over through a device counter);
+ * the environment variable DSV4_HIP_DECODE_LAUNCHES=2 selects the two-launch
+ * form, which gives the same bits. */
 int  dsv4_hip_moe_decode_dev(float *out, const float *x,
                              const DSV4ExpertW *experts, int n_experts,
                              const int *idx, const float *w, int topk,
@@ -207,8 +211,10 @@ int  dsv4_hip_gemm_fp8q_dev(void *C, int out_bf16, const uint8_t *Aq,
  * routing id is out of range (bit 0) or an expert descriptor in the device
  * table does not match the expected format and geometry (bit 1); the affected
  * outputs are NaN. Bit 2: the grouped MoE met an FP4 scale byte outside
- * 104..140, whose blocks it cannot decode exactly. Synchronises the library's
- * streams. 0 ok, -1 no device. */
+ * 104..140, whose blocks it cannot decode exactly. Bit 3: a one-launch decode
+ * MoE gave up waiting for its gate/up half (about a second; only possible
+ * when other work keeps its workgroups from running), its output is NaN.
+ * Synchronises the library's streams. 0 ok, -1 no device. */
 int  dsv4_hip_status(unsigned *bits);
 
 #ifdef __cplusplus

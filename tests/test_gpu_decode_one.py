@@ -1,0 +1,155 @@
+"""The one-launch decode MoE (gate/up and down workgroups of one grid, mid's
+split tables published through per-slot counters) against the two-launch form
+of the same kernels and against the oracle.
+
+The reference decodes one token's MoE as six `dsv4_expert_forward` calls
+summed in k order (src/70_decode/dsv4_layer.c:57-116, src/10_compute/dsv4_ops.c:85-93);
+both GPU forms compute the same MFMA sequence, so they must agree bit for bit.
+Consecutive calls reuse the split-table buffers and the counters: a stale
+cached table line or a wrong counter target shows up as a mismatch in a later
+call, not the first."""
+import os
+import zlib
+
+import numpy as np
+import pytest
+import torch
+
+import pyoracle as P
+from conftest import bits
+from test_gpu_decode import DEV, bf16_x, check_close, dev_f32, dev_u8
+from test_gpu_decode_mx import _device_fp4_experts
+
+pytestmark = pytest.mark.gpu
+
+ENV = "DSV4_HIP_DECODE_LAUNCHES"
+
+
+def _device_fp8_shared(pkg, oracle, rng, inter, hidden):
+    q, hm, keep = [], [], []
+    for (r, c) in ((inter, hidden), (inter, hidden), (hidden, inter)):
+        W, S = oracle.quant_fp8_blk128((rng.standard_normal((r, c)) * 0.02).astype(np.float32))
+        dW, dS = dev_u8(W), dev_f32(S)
+        keep += [dW, dS]
+        q.append(pkg.qmat(pkg.DSV4_WFP8_F32S, dW.data_ptr(), dS.data_ptr(), r, c, 128, 128))
+        hm.append(P.HostMat(pkg.DSV4_WFP8_F32S, W, S, r, c, 128, 128))
+    return pkg.ExpertW(q[0], q[1], q[2]), P.HostExpert(hm[0], hm[1], hm[2]), keep
+
+
+class _Setup:
+    def __init__(self, pkg, oracle, seed, inter, hidden, topk, n_exp, shared=False):
+        self.rng = np.random.default_rng(seed)
+        self.inter, self.hidden, self.topk, self.n_exp = inter, hidden, topk, n_exp
+        self.descs, self.host, self.keep = _device_fp4_experts(pkg, oracle, self.rng, n_exp, inter, hidden)
+        self.tbl = torch.from_numpy(np.frombuffer(b"".join(bytes(d) for d in self.descs),
+                                                  np.uint8).copy()).to(DEV)
+        self.shared = self.hshared = None
+        if shared:
+            self.shared, self.hshared, k2 = _device_fp8_shared(pkg, oracle, self.rng, inter, hidden)
+            self.keep += k2
+
+    def draw(self, seed):
+        idx = self.rng.choice(self.n_exp, self.topk, replace=False).astype(np.int32)
+        lg = self.rng.standard_normal(self.topk)
+        w = (np.exp(lg) / np.exp(lg).sum()).astype(np.float32)
+        return idx, w, bf16_x(seed, self.hidden)
+
+    def run(self, lib, idx, w, xh, out=None):
+        didx = torch.from_numpy(idx).to(DEV)
+        dw, x = dev_f32(w), dev_f32(xh)
+        if out is None:
+            out = torch.empty(self.hidden, dtype=torch.float32, device=DEV)
+        lib.moe_decode_dev(out.data_ptr(), x.data_ptr(), self.tbl.data_ptr(), self.n_exp,
+                           didx.data_ptr(), dw.data_ptr(), self.topk, self.shared, self.hidden,
+                           self.inter, 10.0)
+        return out, (didx, dw, x)
+
+    def want(self, oracle, idx, w, xh):
+        acc = np.stack([oracle.expert_forward(self.host[i], xh, 10.0) for i in idx])
+        y = oracle.moe_combine(acc, w)
+        if self.hshared is not None:
+            y = (y + oracle.expert_forward(self.hshared, xh, 10.0)).astype(np.float32)
+        return y
+
+
+@pytest.mark.parametrize("inter,hidden,topk", [(2048, 4096, 6), (256, 1024, 8), (512, 2048, 3),
+                                               (1024, 512, 1)])
+def test_one_launch_matches_two_launch(lib, pkg, oracle, monkeypatch, inter, hidden, topk):
+    """Twelve calls enqueued back to back on the one-launch form, each with its
+    own routing and token, then the same twelve on the two-launch form: bit for
+    bit equal, status clear, and the first and last against the oracle."""
+    s = _Setup(pkg, oracle, zlib.crc32(b"one") + inter + topk, inter, hidden, topk, topk + 4)
+    calls = [s.draw(100 + i) for i in range(12)]
+    lib.status()
+    monkeypatch.delenv(ENV, raising=False)
+    one = [s.run(lib, *c) for c in calls]
+    torch.cuda.synchronize()
+    assert lib.status() == 0
+    monkeypatch.setenv(ENV, "2")
+    two = [s.run(lib, *c) for c in calls]
+    torch.cuda.synchronize()
+    assert lib.status() == 0
+    for i, ((o1, _), (o2, _)) in enumerate(zip(one, two)):
+        assert np.array_equal(bits(o1.cpu().numpy()), bits(o2.cpu().numpy())), f"call {i}"
+    for i in (0, len(calls) - 1):
+        assert check_close(one[i][0].cpu().numpy(), s.want(oracle, *calls[i])) < 1e-4
+
+
+def test_one_launch_with_shared_expert(lib, pkg, oracle, monkeypatch):
+    """An FP8 shared expert (fp32 128x128 scales) added in the combine: both
+    forms agree bit for bit and match the oracle."""
+    s = _Setup(pkg, oracle, zlib.crc32(b"one-shared"), 2048, 4096, 6, 10, shared=True)
+    c = s.draw(7)
+    monkeypatch.delenv(ENV, raising=False)
+    o1, _ = s.run(lib, *c)
+    monkeypatch.setenv(ENV, "2")
+    o2, _ = s.run(lib, *c)
+    torch.cuda.synchronize()
+    assert lib.status() == 0
+    g = o1.cpu().numpy()
+    assert np.array_equal(bits(g), bits(o2.cpu().numpy()))
+    assert check_close(g, s.want(oracle, *c)) < 1e-4
+
+
+def test_one_launch_bad_id_then_good(lib, pkg, oracle, monkeypatch):
+    """A routing id out of range on the device: status bit 0 and a NaN output;
+    the gate/up items of that slot still publish, so the next call's counter
+    targets hold and its output is exact."""
+    monkeypatch.delenv(ENV, raising=False)
+    s = _Setup(pkg, oracle, zlib.crc32(b"one-bad"), 512, 2048, 4, 6)
+    idx, w, xh = s.draw(3)
+    bad = idx.copy()
+    bad[2] = s.n_exp + 5
+    lib.status()
+    o, _ = s.run(lib, bad, w, xh)
+    torch.cuda.synchronize()
+    assert lib.status() & 1
+    assert np.isnan(o.cpu().numpy()).all()
+    o, _ = s.run(lib, idx, w, xh)
+    torch.cuda.synchronize()
+    assert lib.status() == 0
+    assert check_close(o.cpu().numpy(), s.want(oracle, idx, w, xh)) < 1e-4
+
+
+def test_one_launch_host_routed(lib, pkg, oracle, monkeypatch):
+    """The host-routed entry (descriptors by value) on the one-launch form
+    equals its two-launch form bit for bit over consecutive calls."""
+    s = _Setup(pkg, oracle, zlib.crc32(b"one-routed"), 2048, 4096, 6, 9)
+    arr = (pkg.ExpertW * s.n_exp)(*s.descs)
+    calls = [s.draw(40 + i) for i in range(4)]
+    outs = {}
+    for mode in ("1", "2"):
+        monkeypatch.setenv(ENV, mode)
+        res = []
+        for idx, w, xh in calls:
+            x = dev_f32(xh)
+            out = torch.empty(s.hidden, dtype=torch.float32, device=DEV)
+            lib.moe_decode_routed_dev(out.data_ptr(), x.data_ptr(), arr, idx, w, s.topk, None,
+                                      s.hidden, s.inter, 10.0)
+            res.append((out, x))
+        torch.cuda.synchronize()
+        outs[mode] = [bits(o.cpu().numpy()) for o, _ in res]
+    assert lib.status() == 0
+    for i in range(len(calls)):
+        assert np.array_equal(outs["1"][i], outs["2"][i]), f"call {i}"
+    assert check_close(res[0][0].cpu().numpy(), s.want(oracle, *calls[0])) < 1e-4

@@ -268,3 +268,50 @@ def test_grouped_config2_shape_sampled(lib, pkg, oracle):
     want = oracle_tokens(oracle, experts, shared, x, idx, w, tokens)
     e = rel_l2(got[tokens], want)
     assert e <= REL_L2_TOL, f"rel L2 {e:.3e} (max abs {max_abs(got[tokens], want):.3e})"
+
+
+@pytest.mark.parametrize("n,topk,ne,zipf,hidden,inter", [
+    (60, 4, 5, None, 1024, 512),     # buckets of ~48 rows: several token tiles each
+    (64, 8, 8, None, 512, 256),      # 64-row buckets: whole tiles
+    (3, 2, 40, None, 2048, 1024),    # one-row buckets, most experts idle
+    (50, 6, 24, 1.1, 4096, 2048),    # config-2 geometry, skewed buckets
+])
+def test_grouped_bucket_shapes(lib, pkg, oracle, n, topk, ne, zipf, hidden, inter):
+    """Buckets spanning several token tiles, full tiles, one-row buckets with
+    most experts idle, and the real expert geometry under skewed routing:
+    against the per-token oracle, and bit-identical across two calls."""
+    gen = torch.Generator().manual_seed(n * 13 + ne)
+    dgen = torch.Generator(device=DEV).manual_seed(n * 13 + ne)
+    rng = np.random.default_rng(n * 5 + topk)
+    experts = [DevExpert(lib, pkg, "fp4", inter, hidden, dgen) for _ in range(ne)]
+    x = bf16_rows(gen, n, hidden)
+    idx, w = routing(rng, n, topk, ne, zipf=zipf)
+    lib.status()
+    got = run_dev(lib, experts, None, x, idx, w, hidden, inter)
+    again = run_dev(lib, experts, None, x, idx, w, hidden, inter)
+    assert lib.status() == 0
+    assert np.array_equal(bits(got), bits(again))
+    tokens = list(range(n)) if n <= 8 else sorted(rng.choice(n, 8, replace=False).tolist())
+    want = oracle_tokens(oracle, experts, None, x, idx, w, tokens)
+    e = rel_l2(got[tokens], want)
+    assert e <= REL_L2_TOL, f"rel L2 {e:.3e} (max abs {max_abs(got[tokens], want):.3e})"
+
+
+def test_grouped_bad_id_real_width(lib, pkg, oracle):
+    """A routing id out of range at hidden 512 (whole 256-wide K stages):
+    status bit 0, that token NaN, the others exact."""
+    gen = torch.Generator().manual_seed(21)
+    dgen = torch.Generator(device=DEV).manual_seed(21)
+    rng = np.random.default_rng(21)
+    hidden, inter, ne, n, topk = 512, 256, 4, 6, 2
+    experts = [DevExpert(lib, pkg, "fp4", inter, hidden, dgen) for _ in range(ne)]
+    x = bf16_rows(gen, n, hidden)
+    idx, w = routing(rng, n, topk, ne)
+    lib.status()
+    idx[4, 0] = -3
+    got = run_dev(lib, experts, None, x, idx, w, hidden, inter)
+    assert lib.status() & 1
+    assert np.isnan(got[4]).all()
+    ok = [t for t in range(n) if t != 4]
+    want = oracle_tokens(oracle, experts, None, x, idx, w, ok)
+    assert rel_l2(got[ok], want) <= REL_L2_TOL
