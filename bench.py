@@ -151,16 +151,19 @@ def make_shared_fp8(torch, pkg, lib, seed):
 
 
 def time_events(torch, stream, fn, n):
-    """Average duration of fn() over n calls, each bracketed by its own HIP
-    events on `stream` (the stream the kernels are launched on)."""
-    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
-           for _ in range(n)]
-    for i, (a, b) in enumerate(evs):
-        a.record(stream)
+    """Average duration of one fn() call over n calls enqueued back to back on
+    `stream` (the stream the kernels are launched on), from one pair of HIP
+    events around the n calls. Events around every single call would add a
+    drain and a release between calls that back-to-back calls do not pay
+    (about 2 us on a 21 us call), and would disagree with the kernel
+    durations rocprofv3 reports."""
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    a.record(stream)
+    for i in range(n):
         fn(i)
-        b.record(stream)
+    b.record(stream)
     torch.cuda.synchronize()
-    return float(np.mean([a.elapsed_time(b) for a, b in evs])) * 1e-3
+    return a.elapsed_time(b) * 1e-3 / n
 
 
 # --------------------------------------------------------- CPU baseline ----
@@ -605,7 +608,7 @@ def main():
         t_step = timed(step)
         wall = time.perf_counter() - t0
         t_step_dev = timed(step_dev)
-        # per-launch durations (each call bracketed by its own events)
+        # average launch durations on fresh weight sets
         t_launch = time_events(torch, stream, lambda i: step(W + K + i), K)
         t_launch_dev = time_events(torch, stream, lambda i: step_dev(W + K + i), K)
         assert lib.status() == 0
