@@ -355,7 +355,9 @@ int enqueue_moe(const DSV4ExpertW *table, int n_experts, const int *idx,
             oa.pub.done = g.pub + 32;
             oa.pub.last = g.pub_count + items - 1;
             oa.pub.epoch = g.pub_epoch + 1;
-            oa.spin_max = 1u << 20;
+            /* DSV4_HIP_DECODE_SPIN: most polls of a down workgroup's wait (default 2^20) */
+            const char *sp = getenv("DSV4_HIP_DECODE_SPIN");
+            oa.spin_max = sp ? (unsigned)strtoul(sp, nullptr, 10) : 1u << 20;
             HIPCHK(moe_one_launch(oa, g.cus, st), "one-launch decode MoE");
             g.pub_count += items;
             g.pub_epoch += 1;

@@ -130,7 +130,8 @@ int  dsv4_hip_moe_decode(float *out, const float *x,
  * 1024, 2048} and topk <= 8 the routed experts run as one launch (gate/up
  * and down workgroups in one grid, mid handed over through a device counter);
  * the environment variable DSV4_HIP_DECODE_LAUNCHES=2 selects the two-launch
- * form, which gives the same bits. */
+ * form, which gives the same bits; DSV4_HIP_DECODE_SPIN bounds the down
+ * workgroups' wait in polls (default 2^20, about a second). */
 int  dsv4_hip_moe_decode_dev(float *out, const float *x,
                              const DSV4ExpertW *experts, int n_experts,
                              const int *idx, const float *w, int topk,

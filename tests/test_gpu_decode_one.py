@@ -1,6 +1,6 @@
 """The one-launch decode MoE (gate/up and down workgroups of one grid, mid's
-split tables published through per-slot counters) against the two-launch form
-of the same kernels and against the oracle.
+split tables published through an item counter and a done flag) against the
+two-launch form of the same kernels and against the oracle.
 
 The reference decodes one token's MoE as six `dsv4_expert_forward` calls
 summed in k order (src/70_decode/dsv4_layer.c:57-116, src/10_compute/dsv4_ops.c:85-93);
@@ -8,7 +8,6 @@ both GPU forms compute the same MFMA sequence, so they must agree bit for bit.
 Consecutive calls reuse the split-table buffers and the counters: a stale
 cached table line or a wrong counter target shows up as a mismatch in a later
 call, not the first."""
-import os
 import zlib
 
 import numpy as np
@@ -153,3 +152,37 @@ def test_one_launch_host_routed(lib, pkg, oracle, monkeypatch):
     for i in range(len(calls)):
         assert np.array_equal(outs["1"][i], outs["2"][i]), f"call {i}"
     assert check_close(res[0][0].cpu().numpy(), s.want(oracle, *calls[0])) < 1e-4
+
+
+def test_one_launch_wait_timeout_then_recovers(lib, pkg, oracle, monkeypatch):
+    """The down workgroups' wait forced to give up from the host
+    (DSV4_HIP_DECODE_SPIN=0: one poll, before the gate/up half can be done
+    for the workgroups dispatched first): status bit 3 and NaN rows where
+    the wait gave up, every other row bit-identical to the two-launch form;
+    the gate/up items still publish, so the next call with the default limit
+    is exact."""
+    s = _Setup(pkg, oracle, zlib.crc32(b"one-timeout"), 2048, 4096, 6, 8)
+    idx, w, xh = s.draw(5)
+    monkeypatch.setenv(ENV, "2")
+    ref, _ = s.run(lib, idx, w, xh)
+    torch.cuda.synchronize()
+    want = bits(ref.cpu().numpy())
+    monkeypatch.delenv(ENV, raising=False)
+    lib.status()
+    monkeypatch.setenv("DSV4_HIP_DECODE_SPIN", "0")
+    o, _ = s.run(lib, idx, w, xh)
+    torch.cuda.synchronize()
+    st = lib.status()
+    got = o.cpu().numpy()
+    nan = np.isnan(got)
+    if st & 8:
+        assert nan.any()
+        assert np.array_equal(bits(got[~nan]), want[~nan])
+    else:
+        assert st == 0 and np.array_equal(bits(got), want)
+    assert st & ~8 == 0
+    monkeypatch.delenv("DSV4_HIP_DECODE_SPIN")
+    o, _ = s.run(lib, idx, w, xh)
+    torch.cuda.synchronize()
+    assert lib.status() == 0
+    assert np.array_equal(bits(o.cpu().numpy()), want)
