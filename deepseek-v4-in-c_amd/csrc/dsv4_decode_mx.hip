@@ -1331,11 +1331,11 @@ hipError_t down_mx_launch(DownMxArgs a, hipStream_t st)
     return hipGetLastError();
 }
 
-bool moe_one_ok(int hidden, int inter, int topk, int cus)
+bool moe_one_ok(int hidden, int inter, int topk)
 {
     if (!(hidden == 512 || hidden == 1024 || hidden == 2048 || hidden == 4096)) return false;
     if (!(inter == 256 || inter == 512 || inter == 1024 || inter == 2048)) return false;
-    if (topk < 1 || topk > MX_ROUTED_MAX || cus < 1) return false;
+    if (topk < 1 || topk > MX_ROUTED_MAX) return false;
     /* down workgroups: every routed slot's table in LDS, two workgroups per CU */
     return ONE_HEAD_BYTES + (long)topk * one_slot_lds(inter) <= 80L * 1024;
 }
@@ -1366,9 +1366,9 @@ static hipError_t moe_one_d(const MoeOneArgs &a, hipStream_t st)
     }
 }
 
-hipError_t moe_one_launch(MoeOneArgs a, int cus, hipStream_t st)
+hipError_t moe_one_launch(MoeOneArgs a, hipStream_t st)
 {
-    if (!moe_one_ok(a.gu.hidden, a.gu.inter, a.gu.nslots, cus) || a.dn.hidden != a.gu.hidden ||
+    if (!moe_one_ok(a.gu.hidden, a.gu.inter, a.gu.nslots) || a.dn.hidden != a.gu.hidden ||
         a.dn.inter != a.gu.inter || a.dn.topk != a.gu.nslots || !a.gu.msplit || !a.pub.count ||
         !a.pub.done)
         return hipErrorInvalidValue;

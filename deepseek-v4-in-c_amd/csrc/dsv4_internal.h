@@ -202,9 +202,9 @@ struct MoeOneArgs {
     int gu_blocks;
     unsigned spin_max;
 };
-/* whether one launch takes this geometry on a device of `cus` CUs */
-bool moe_one_ok(int hidden, int inter, int topk, int cus);
-hipError_t moe_one_launch(MoeOneArgs a, int cus, hipStream_t st);
+/* whether one launch takes this geometry */
+bool moe_one_ok(int hidden, int inter, int topk);
+hipError_t moe_one_launch(MoeOneArgs a, hipStream_t st);
 /* bytes of one slot's split table for a K of `inter` */
 size_t mx_split_bytes(int inter);
 

@@ -66,7 +66,6 @@ struct State {
     unsigned *status = nullptr;          /* device status word            */
     unsigned *pub = nullptr;             /* one-launch decode: item counter, done flag (own line) */
     unsigned pub_count = 0, pub_epoch = 0;     /* their values after the last enqueued call */
-    int cus = 0;
     std::map<uintptr_t, Region> regions; /* host start -> resident copy   */
     DevBuf x, y, mid, table, small, ys, gemm_ws, moe_ws, x16, msplit;
 };
@@ -345,7 +344,7 @@ int enqueue_moe(const DSV4ExpertW *table, int n_experts, const int *idx,
          * and there is no second launch ramp; DSV4_HIP_DECODE_LAUNCHES=2
          * keeps the two-launch form (same bits) */
         const char *nl = getenv("DSV4_HIP_DECODE_LAUNCHES");
-        if (!(nl && atoi(nl) == 2) && moe_one_ok(hidden, inter, topk, g.cus)) {
+        if (!(nl && atoi(nl) == 2) && moe_one_ok(hidden, inter, topk)) {
             MoeOneArgs oa;
             memset(&oa, 0, sizeof oa);
             oa.gu = ga;
@@ -358,7 +357,7 @@ int enqueue_moe(const DSV4ExpertW *table, int n_experts, const int *idx,
             /* DSV4_HIP_DECODE_SPIN: most polls of a down workgroup's wait (default 2^20) */
             const char *sp = getenv("DSV4_HIP_DECODE_SPIN");
             oa.spin_max = sp ? (unsigned)strtoul(sp, nullptr, 10) : 1u << 20;
-            HIPCHK(moe_one_launch(oa, g.cus, st), "one-launch decode MoE");
+            HIPCHK(moe_one_launch(oa, st), "one-launch decode MoE");
             g.pub_count += items;
             g.pub_epoch += 1;
             return 0;
@@ -430,7 +429,6 @@ int dsv4_hip_init(int device)
     if (hipMalloc((void **)&g.pub, 256) != hipSuccess) return fail("counter alloc failed");
     if (hipMemset(g.pub, 0, 256) != hipSuccess) return fail("counter clear failed");
     g.pub_count = g.pub_epoch = 0;
-    g.cus = prop.multiProcessorCount;
 
     g.device = device;
     g.ready = 1;
