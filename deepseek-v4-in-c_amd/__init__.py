@@ -35,7 +35,7 @@ EXPORTS = (
     "dsv4_hip_status", "dsv4_hip_gemm_fp8_dev", "dsv4_hip_gemm_fp8q_dev",
     "dsv4_hip_dequant_dev", "dsv4_hip_quant_fp8_blk128_dev",
     "dsv4_hip_quant_fp4_mx_dev", "dsv4_hip_quant_act_fp8_1x128_dev",
-    "dsv4_hip_quant_act_mxfp8_dev", "dsv4_hip_synth_normal_dev",
+    "dsv4_hip_quant_act_mxfp8_dev", "dsv4_hip_synth_normal_dev", "dsv4_hip_moe_route_dev",
 )
 # the reference-named C mirror (host/dsv4_compute_hip.c)
 MIRROR_EXPORTS = ("dsv4_mmq_n", "dsv4_mmq", "dsv4_expert_forward")
@@ -80,6 +80,7 @@ class Lib:
         if not os.path.exists(path):
             raise Dsv4Error(f"{path} is not built: run __graft_entry__.build()")
         self.path = path
+        self._registered = {}
         L = self.lib = C.CDLL(path)
         L.dsv4_hip_init.restype = _I; L.dsv4_hip_init.argtypes = [_I]
         L.dsv4_hip_shutdown.restype = None; L.dsv4_hip_shutdown.argtypes = []
@@ -123,6 +124,8 @@ class Lib:
             getattr(L, n).argtypes = [_P, _P, _P, _I, _I, _P]
         L.dsv4_hip_synth_normal_dev.restype = _I
         L.dsv4_hip_synth_normal_dev.argtypes = [_P, C.c_size_t, C.c_uint64, _F, _I, _P]
+        L.dsv4_hip_moe_route_dev.restype = _I
+        L.dsv4_hip_moe_route_dev.argtypes = [_P, _P, _P, _P, _P, _I, _I, _I, _P]
 
     # ------------------------------------------------------------ basics
     def error(self) -> str:
@@ -139,11 +142,24 @@ class Lib:
         self.lib.dsv4_hip_shutdown()
 
     def register(self, arr: np.ndarray) -> int:
+        """Upload arr once; the array is kept alive (its address cannot be
+        reused) until it is unregistered."""
         assert arr.flags["C_CONTIGUOUS"]
-        return self.lib.dsv4_hip_register(arr.ctypes.data, arr.nbytes)
+        rc = self.lib.dsv4_hip_register(arr.ctypes.data, arr.nbytes)
+        if rc == 0:
+            self._registered[arr.ctypes.data] = arr
+        return rc
 
     def unregister(self, arr: np.ndarray) -> int:
+        self._registered.pop(arr.ctypes.data, None)
         return self.lib.dsv4_hip_unregister(arr.ctypes.data)
+
+    def unregister_all(self) -> int:
+        """Drop every range this binding registered; returns how many."""
+        live = list(self._registered.values())
+        for a in live:
+            self.unregister(a)
+        return len(live)
 
     def status(self) -> int:
         v = C.c_uint(0)
@@ -267,6 +283,50 @@ class Lib:
         self.check(self.lib.dsv4_hip_synth_normal_dev(out_ptr, n, seed, float(sigma),
                                                       int(bool(round_bf16)), stream),
                    "synth_normal_dev")
+
+    def moe_route_dev(self, ex_off_ptr, ex_tok_ptr, ex_k_ptr, pos_ptr, idx_ptr, n, topk,
+                      n_experts, stream=None):
+        self.check(self.lib.dsv4_hip_moe_route_dev(ex_off_ptr, ex_tok_ptr, ex_k_ptr, pos_ptr,
+                                                   idx_ptr, n, topk, n_experts, stream),
+                   "dsv4_hip_moe_route_dev")
+
+
+class Mirror:
+    """ctypes view of libdsv4_amd.so: the reference's own compute entry points
+    (dsv4_mmq_n, dsv4_mmq, dsv4_expert_forward) running on the GPU library,
+    as a program written against src/10_compute would call them."""
+
+    def __init__(self, path: str = AMD_SO):
+        if not os.path.exists(path):
+            raise Dsv4Error(f"{path} is not built: run __graft_entry__.build()")
+        L = self.lib = C.CDLL(path)
+        L.dsv4_mmq_n.restype = None
+        L.dsv4_mmq_n.argtypes = [_P, _P, C.POINTER(QMat), _I]
+        L.dsv4_mmq.restype = None
+        L.dsv4_mmq.argtypes = [_P, _P, C.POINTER(QMat)]
+        L.dsv4_expert_forward.restype = None
+        L.dsv4_expert_forward.argtypes = [_P, _P, C.POINTER(ExpertW), _P, _P, _P, _I, _F]
+
+    def mmq(self, desc: QMat, x: np.ndarray) -> np.ndarray:
+        x = np.ascontiguousarray(x, np.float32)
+        y = np.zeros(desc.rows, np.float32)
+        self.lib.dsv4_mmq(y.ctypes.data, x.ctypes.data, C.byref(desc))
+        return y
+
+    def mmq_n(self, desc: QMat, x: np.ndarray, nt: int) -> np.ndarray:
+        x = np.ascontiguousarray(x, np.float32)
+        y = np.zeros(nt * desc.rows, np.float32)
+        self.lib.dsv4_mmq_n(y.ctypes.data, x.ctypes.data, C.byref(desc), nt)
+        return y
+
+    def expert_forward(self, e: ExpertW, x: np.ndarray, limit: float) -> np.ndarray:
+        x = np.ascontiguousarray(x, np.float32)
+        inter = e.w1.rows
+        out = np.zeros(e.w1.cols, np.float32)
+        g, u, m = (np.zeros(inter, np.float32) for _ in range(3))
+        self.lib.dsv4_expert_forward(out.ctypes.data, x.ctypes.data, C.byref(e), g.ctypes.data,
+                                     u.ctypes.data, m.ctypes.data, inter, float(limit))
+        return out
 
 
 def qmat(wdt, w_ptr, s_ptr, rows, cols, blk_r, blk_c) -> QMat:

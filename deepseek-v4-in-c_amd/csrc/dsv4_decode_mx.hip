@@ -89,27 +89,48 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t dev_rsrc(const void *p, uint32
     return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(p), (short)0, (int)bytes, (int)BUF_WORD3);
 }
 
+/* The calling workgroup's last access to the publication words: one add to
+ * the leave counter, issued after every earlier access of the caller has
+ * completed (vmcnt(0): stores acknowledged, loads and adds returned). The
+ * workgroup whose add returns total - 1 is the last of the launch; every
+ * other workgroup's accesses are then complete, so it sets the three words
+ * back to zero for the next launch. Lane 0 only. */
+__device__ __forceinline__ void leave(const OnePub &p)
+{
+    __builtin_amdgcn_s_waitcnt(0x0F70);            /* vmcnt(0) */
+    asm volatile("" ::: "memory");
+    const unsigned old = __hip_atomic_fetch_add(p.leave, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (old == p.total - 1) {
+        __hip_atomic_store(p.count, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_store(p.done, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_store(p.leave, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+}
+
 /* This wave's stores acknowledged, then one more item counted; the item that
  * completes the call raises the done flag (its add returns after every
- * earlier add, each issued after that item's stores were acknowledged). */
+ * earlier add, each issued after that item's stores were acknowledged).
+ * Then the item leaves. */
 __device__ __forceinline__ void publish(const OnePub &p, int lane)
 {
     __builtin_amdgcn_s_waitcnt(0x0F70);            /* vmcnt(0) */
     asm volatile("" ::: "memory");
     if (lane == 0) {
         const unsigned old = __hip_atomic_fetch_add(p.count, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        if (old == p.last) __hip_atomic_store(p.done, p.epoch, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (old == p.items - 1) __hip_atomic_store(p.done, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        leave(p);
     }
 }
 
-/* Poll the done flag until it reaches the call's epoch (wrapping compare);
- * false after spin_max polls. */
+/* Poll the done flag until it is set; false after spin_max polls, and at
+ * once, without reading the flag, when spin_max is 0. */
 __device__ __forceinline__ bool wait_done(const OnePub &p, unsigned spin_max)
 {
-    for (unsigned n = 0;; n++) {
+    if (spin_max == 0) return false;
+    for (unsigned n = 1;; n++) {
         const unsigned v = (unsigned)__builtin_amdgcn_readfirstlane(
             (int)__hip_atomic_load(p.done, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
-        if ((int)(v - p.epoch) >= 0) break;
+        if (v != 0) break;
         if (n >= spin_max) return false;
         __builtin_amdgcn_s_sleep(16);              /* ~1k cycles between polls */
     }
@@ -1159,6 +1180,7 @@ __device__ __forceinline__ void down_one_group(const MoeOneArgs &A, int grp, uin
         }
     }
     __syncthreads();
+    if (threadIdx.x == 0) leave(A.pub);            /* wave 0's poll has returned */
     if (threadIdx.x >= 16 || r0 + (int)threadIdx.x >= a.hidden) return;
     const int t = threadIdx.x >> 3, rr = threadIdx.x & 7;
     float o = 0.0f;
@@ -1223,9 +1245,7 @@ hipError_t gemv_mx_fmt(GemvMxArgs a, hipStream_t st)
     case 2: return gemv_mx_k<FMT, 2>(a, st);
     case 4: return gemv_mx_k<FMT, 4>(a, st);
     case 8: return gemv_mx_k<FMT, 8>(a, st);
-    default:
-        if constexpr (FMT == FMT_FP4_E8M0) return gemv_mx_k<FMT, 16>(a, st);
-        return hipErrorInvalidValue;
+    default: return gemv_mx_k<FMT, 16>(a, st);
     }
 }
 
@@ -1275,12 +1295,21 @@ hipError_t gateup_mx_fmt(const GateUpMxArgs &a, hipStream_t st)
 
 } // namespace
 
-/* chunks per wave for a K of `cols`, 0 when the MFMA path does not take it */
+/* chunks per wave for a K of `cols` (at most 8192 FP8 or FP4 columns), 0
+ * when the MFMA path does not take it */
 int gemv_mx_ncw(int fmt, int cols)
 {
+    (void)fmt;
     if (cols <= 0 || cols % 128) return 0;
     const int ncw = (cols / 128 + KSLICES - 1) / KSLICES;
-    return ncw <= (fmt == FMT_FP4_E8M0 ? 16 : 8) ? ncw : 0;
+    return ncw <= 16 ? ncw : 0;
+}
+
+/* the gate/up kernels take up to 8 FP8 chunks per wave (4096 columns) */
+int gateup_mx_ncw(int fmt, int cols)
+{
+    const int ncw = gemv_mx_ncw(fmt, cols);
+    return fmt == FMT_FP4_E8M0 || ncw <= 8 ? ncw : 0;
 }
 
 size_t mx_split_bytes(int inter) { return (size_t)(inter / 128) * TAB_CHUNK; }
@@ -1299,7 +1328,7 @@ hipError_t gemv_mx_launch(int fmt, GemvMxArgs a, hipStream_t st)
 
 hipError_t gateup_mx_launch(int fmt, GateUpMxArgs a, hipStream_t st)
 {
-    a.ncw = gemv_mx_ncw(fmt, a.hidden);
+    a.ncw = gateup_mx_ncw(fmt, a.hidden);
     if (!a.ncw || a.inter % 128) return hipErrorInvalidValue;
     switch (fmt) {
     case FMT_FP8_E8M0: return gateup_mx_fmt<FMT_FP8_E8M0>(a, st);
@@ -1347,10 +1376,15 @@ static hipError_t moe_one_k(const MoeOneArgs &a, hipStream_t st)
     const size_t lds = std::max<size_t>((size_t)4 * NPG * TAB_CHUNK + TAB_ZERO + (4 * 2 * 2 * 16 + 32) * 4,
                                         (size_t)ONE_HEAD_BYTES + (size_t)a.dn.topk * one_slot_lds(256 * NPD));
     const unsigned grid = (unsigned)(a.gu_blocks + a.dn.hidden / 16);
-    if (lds > 64 * 1024) {
+    /* the largest LDS any launch of this instantiation asks for, set once
+     * (not again inside a stream capture of a later call) */
+    static int lds_set = 64 * 1024;
+    if ((int)lds > lds_set) {
         const hipError_t e = hipFuncSetAttribute((const void *)k_moe_one<NPG, NPD>,
-                                                 hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+                                                 hipFuncAttributeMaxDynamicSharedMemorySize,
+                                                 (int)(80 * 1024 + ONE_HEAD_BYTES));
         if (e != hipSuccess) return e;
+        lds_set = 80 * 1024 + ONE_HEAD_BYTES;
     }
     hipLaunchKernelGGL((k_moe_one<NPG, NPD>), dim3(grid), dim3(512), lds, st, a);
     return hipGetLastError();
@@ -1371,9 +1405,11 @@ hipError_t moe_one_launch(MoeOneArgs a, hipStream_t st)
 {
     if (!moe_one_ok(a.gu.hidden, a.gu.inter, a.gu.nslots) || a.dn.hidden != a.gu.hidden ||
         a.dn.inter != a.gu.inter || a.dn.topk != a.gu.nslots || !a.gu.msplit || !a.pub.count ||
-        !a.pub.done)
+        !a.pub.done || !a.pub.leave)
         return hipErrorInvalidValue;
     a.gu_blocks = a.gu.nslots * (a.gu.inter / 32);
+    a.pub.items = (unsigned)a.gu_blocks;
+    a.pub.total = (unsigned)(a.gu_blocks + a.dn.hidden / 16);
     switch (a.gu.hidden) {
     case 512: return moe_one_d<1>(a, st);
     case 1024: return moe_one_d<2>(a, st);

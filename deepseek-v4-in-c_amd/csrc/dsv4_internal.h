@@ -18,6 +18,7 @@ enum {
     FMT_FP8_E8M0 = 0, /* DSV4_WFP8, blk_c == 128      */
     FMT_FP8_F32S = 1, /* DSV4_WFP8_F32S, blk_c == 128 */
     FMT_FP4_E8M0 = 2, /* DSV4_WFP4, blk_c == 32       */
+    FMT_BF16 = 3,     /* DSV4_WBF16, no scales, cols % 8 == 0 */
 };
 
 /* Status bits a kernel may raise in the device status word. */
@@ -29,13 +30,17 @@ enum {
                                      exact for that block                   */
     ST_SYNC_TIMEOUT = 1u << 3,    /* a one-launch decode MoE waited past its
                                      spin limit for a slot's mid             */
+    ST_F16_RANGE = 1u << 4,       /* an fp16-MFMA path met a SwiGLU output
+                                     beyond the fp16 range (|v| >= 65520)    */
 };
 
 /* Map a descriptor to the kernel format, or -1 when the GPU path does not
  * support its geometry. */
 static inline int qmat_fmt(const DSV4QMat *m)
 {
-    if (!m || m->rows <= 0 || m->cols <= 0 || m->blk_r <= 0) return -1;
+    if (!m || m->rows <= 0 || m->cols <= 0) return -1;
+    if (m->wdt == DSV4_WBF16) return (m->cols % 8) == 0 ? FMT_BF16 : -1;
+    if (m->blk_r <= 0) return -1;
     if (m->wdt == DSV4_WFP8 && m->blk_c == 128 && (m->cols % 128) == 0)
         return FMT_FP8_E8M0;
     if (m->wdt == DSV4_WFP8_F32S && m->blk_c == 128 && (m->cols % 128) == 0)
@@ -47,7 +52,7 @@ static inline int qmat_fmt(const DSV4QMat *m)
 
 static inline int qmat_row_bytes(const DSV4QMat *m)
 {
-    return m->wdt == DSV4_WFP4 ? m->cols / 2 : m->cols;
+    return m->wdt == DSV4_WFP4 ? m->cols / 2 : m->wdt == DSV4_WBF16 ? 2 * m->cols : m->cols;
 }
 
 /* scale-grid columns (entries per scale row) */
@@ -63,6 +68,7 @@ static inline size_t qmat_w_bytes(const DSV4QMat *m)
 
 static inline size_t qmat_s_bytes(const DSV4QMat *m)
 {
+    if (m->wdt == DSV4_WBF16) return 0;
     const size_t n = (size_t)((m->rows + m->blk_r - 1) / m->blk_r) *
                      (size_t)qmat_sc_cols(m);
     return m->wdt == DSV4_WFP8_F32S ? n * 4u : n;
@@ -79,6 +85,18 @@ struct GemvArgs {
     int x_ld, y_ld;     /* floats between tokens    */
 };
 hipError_t gemv_launch(int fmt, const GemvArgs &a, hipStream_t st);
+
+/* y[t*y_ld + o] = (float) sum_c (double) bf16(W[o][c]) * (double) x[t*x_ld + c]
+ * for t < nt: BF16 weights (row pitch 2 * cols bytes, 16-byte aligned, cols %
+ * 8 == 0), fp32 x and y, products and sums in fp64. */
+struct GemvBf16Args {
+    const uint16_t *W;
+    const float *x;
+    float *y;
+    int rows, cols;
+    int nt, x_ld, y_ld;
+};
+hipError_t gemv_bf16_launch(const GemvBf16Args &a, hipStream_t st);
 
 /* ---------------------------------------------------- decode MoE ------ */
 /* Gate/up + SwiGLU for `nslots` experts: slot s uses table[idx[s]] (or
@@ -132,6 +150,8 @@ struct GemvMxArgs {
 };
 /* chunks of 128 columns per wave, 0 when the MFMA path does not take `cols` */
 int gemv_mx_ncw(int fmt, int cols);
+/* the same for the gate/up kernels (FP8 hidden at most 4096) */
+int gateup_mx_ncw(int fmt, int cols);
 hipError_t gemv_mx_launch(int fmt, GemvMxArgs a, hipStream_t st);
 
 /* Routed experts whose descriptors travel by value in the kernel arguments
@@ -187,13 +207,17 @@ hipError_t down_mx_launch(DownMxArgs a, hipStream_t st);
 
 /* Gate/up and down of the routed FP4 experts in one launch: workgroups
  * [0, gu_blocks) run the gate/up items; each item adds one to *count once its
- * block of mid's split table is out, and the item that takes *count to `last`
- * writes `epoch` to *done. The hidden / 16 down workgroups after them load
- * their down weights at once and wait (spin_max polls at most) until *done
- * reaches epoch. *count and *done only grow, across calls. */
+ * block of mid's split table is out, and the item whose add returns
+ * items - 1 writes 1 to *done. The hidden / 16 down workgroups after them
+ * load their down weights at once and wait (spin_max polls at most; 0: give
+ * up without polling) until *done is 1. Every workgroup, gate/up and down,
+ * adds one to *leave as its last access to the three words; the one whose add
+ * returns items + down groups - 1 sets all three back to 0, so each launch
+ * finds them zero (a HIP graph can replay the launch). count, done and leave
+ * are on three separate 128-byte lines, zero before the first launch. */
 struct OnePub {
-    unsigned *count, *done;
-    unsigned last, epoch;
+    unsigned *count, *done, *leave;
+    unsigned items, total;
 };
 struct MoeOneArgs {
     GateUpMxArgs gu;
@@ -205,6 +229,8 @@ struct MoeOneArgs {
 /* whether one launch takes this geometry */
 bool moe_one_ok(int hidden, int inter, int topk);
 hipError_t moe_one_launch(MoeOneArgs a, hipStream_t st);
+/* the three publication words of the one-launch form: 3 lines of 128 bytes */
+constexpr size_t ONE_PUB_BYTES = 384;
 /* bytes of one slot's split table for a K of `inter` */
 size_t mx_split_bytes(int inter);
 
@@ -242,7 +268,8 @@ hipError_t synth_normal_launch(float *out, size_t n, uint64_t seed, float sigma,
 
 /* ------------------------------------------------------ grouped MoE --- */
 
-/* counting sort of the npairs = n * topk routing ids by expert */
+/* counting sort of the npairs = n * topk routing ids by expert; rows inside
+ * a bucket keep pair order (token-major, k-minor) */
 struct RouteArgs {
     const int *idx;           /* device [npairs]                          */
     int npairs, topk, n_experts;
@@ -252,12 +279,19 @@ struct RouteArgs {
     int *tile_grp;            /* [tiles] bucket (expert) of each tile     */
     int *pos;                 /* [npairs] row of each pair (-1: bad id)   */
     int *row_tok;             /* [npairs] token of each row               */
+    int *row_k;               /* [npairs] k of each row, or NULL          */
     unsigned *status;
 };
 hipError_t moe_route_launch(const RouteArgs &a, hipStream_t st);
 
-/* o[i] = fp16(x[i]), n % 8 == 0 */
-hipError_t to_f16_launch(uint16_t *o, const float *x, size_t n, hipStream_t st);
+/* Row r of x [rows][cols] (cols % 8 == 0, x 16-byte aligned) ->
+ * o[r][c] = fp16(x[r][c] * 2^ex[r]) with ex[r] the power of two that puts the
+ * row's largest finite magnitude in [2^14, 2^15) (0 for a row without one),
+ * so no finite activation overflows fp16 and every one at or above 2^-28 of
+ * the row maximum stays a normal fp16. The GEMMs that read o multiply their
+ * fp32 results by 2^-ex[r], which is exact. */
+hipError_t to_f16_rows_launch(uint16_t *o, int *ex, const float *x, int rows, int cols,
+                              hipStream_t st);
 
 /* out[row][f] for row-groups of one expert each: gate/up with SwiGLU (fp16
  * out, uses w1 and w3) or down (fp32 out). table == NULL: one group, the
@@ -270,6 +304,8 @@ struct GroupedArgs {
     DSV4QMat m1, m3;
     int nrows;                /* rows of B                                */
     const uint16_t *B;        /* fp16 [nrows][K]                          */
+    const int *bexp;          /* [nrows] power of two B row r carries (its
+                                 results are scaled by 2^-bexp[r]), or NULL */
     int K, N;
     void *out;                /* [rows][N]                                */
     float limit;

@@ -18,7 +18,9 @@
  *   k_moe_route     counting sort by expert: first row of each expert's
  *                   bucket (grp_off), prefix of its token tiles (tile_pre),
  *                   each pair's row (pos) and each row's token (row_tok).
- *   k_to_f16        x -> fp16 (round to nearest even).
+ *   k_to_f16_rows   x -> fp16 (round to nearest even) after scaling each
+ *                   row by the power of two that puts its largest magnitude
+ *                   in [2^14, 2^15); the GEMM epilogues undo it exactly.
  *   k_grouped       one wave = one work item: an expert, a slab of output
  *                   features (64 for gate/up with both w1 and w3 rows, 128 for
  *                   down) and a tile of up to 16*TT of its rows. Item ids are
@@ -33,9 +35,11 @@
  *   the status word gets ST_SCALE_RANGE); e4m3 values enter unscaled (exact)
  *   and the 128x128 block scale, E8M0 or fp32, multiplies each 128-K chunk's
  *   partial sum in fp32, as the reference's fp8_n applies it per block. The
- *   activations and
- *   the SwiGLU output enter the MFMA rounded to fp16 (relative error at most
- *   2^-11 each); everything else is fp32.
+ *   activations (row-scaled by a power of two, so no finite value overflows
+ *   and values down to 2^-28 of the row maximum stay normal) and the SwiGLU
+ *   output enter the MFMA rounded to fp16 (relative error at most 2^-11
+ *   each); a SwiGLU output beyond the fp16 range raises ST_F16_RANGE.
+ *   Everything else is fp32.
  *
  * MFMA OPERANDS (gfx950, measured): lane l supplies row l % 16 of A and of B
  *   with 8 consecutive reduction indices, lane group l / 16 selecting which 8;
@@ -117,6 +121,39 @@ __device__ __forceinline__ uint32_t f16_bits(float v)
     return (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)v);
 }
 
+/* The power of two that output row r's B row carries (0 without bexp). */
+__device__ __forceinline__ int b_row_exp(const GroupedArgs &a, int r)
+{
+    if (!a.bexp) return 0;
+    return a.bexp[a.row_tok ? a.row_tok[r] : r];
+}
+
+/* Four fp32 results of a row that carries 2^ex, brought back to scale
+ * (exact: a power-of-two multiply). */
+__device__ __forceinline__ f4v unscale4(f4v v, int ex)
+{
+    if (ex == 0) return v;
+    return f4v{ldexpf(v.x, -ex), ldexpf(v.y, -ex), ldexpf(v.z, -ex), ldexpf(v.w, -ex)};
+}
+
+/* SwiGLU of four (gate, up) pairs of a row that carries 2^ex, packed as four
+ * fp16; a finite result beyond the fp16 range raises ST_F16_RANGE in bad. */
+__device__ __forceinline__ uint2 swiglu_f16x4(const f4v &g, const f4v &u, int ex, float limit,
+                                              unsigned &bad)
+{
+    const f4v gs = unscale4(g, ex), us = unscale4(u, ex);
+    float m[4];
+#pragma unroll
+    for (int e = 0; e < 4; e++) {
+        m[e] = dev_swiglu(gs[e], us[e], limit);
+        if (__builtin_isfinite(m[e]) && __builtin_fabsf(m[e]) >= 65520.0f) bad |= ST_F16_RANGE;
+    }
+    uint2 pk;
+    pk.x = f16_bits(m[0]) | (f16_bits(m[1]) << 16);
+    pk.y = f16_bits(m[2]) | (f16_bits(m[3]) << 16);
+    return pk;
+}
+
 template <int WF>
 __device__ __forceinline__ bool qmat_matches(const DSV4QMat &m, int rows, int cols)
 {
@@ -172,35 +209,88 @@ __global__ __launch_bounds__(1024) void k_moe_route(RouteArgs a)
             a.tile_pre[E] = scan_t[tid];
         }
     }
+    /* Rows inside a bucket in pair order (token-major, k-minor), as the
+     * reference's counting sort places them: pairs go in chunks of 1024; a
+     * pair's row is its bucket's fill before the chunk, plus the pairs of the
+     * same expert in lower waves of the chunk, plus those in lower lanes of
+     * its own wave. */
+    __shared__ unsigned short wcnt[16][MAX_ROUTE_EXPERTS];
+    for (int e = tid; e < MAX_ROUTE_EXPERTS; e += 1024)
+        for (int w = 0; w < 16; w++) wcnt[w][e] = 0;
     __syncthreads();
-    /* rows inside a bucket are claimed by LDS atomics; a row's result does
-     * not depend on its slot, so the order within a bucket does not matter */
-    for (int p = tid; p < a.npairs; p += 1024) {
-        const int e = a.idx[p];
-        if ((unsigned)e < (unsigned)E) {
-            const int r = atomicAdd(&cur[e], 1);
+    const int lane = tid & 63, wv = tid >> 6;
+    const uint64_t below = lane ? (~0ull >> (64 - lane)) : 0ull;
+    for (int c0 = 0; c0 < a.npairs; c0 += 1024) {
+        const int p = c0 + tid;
+        const int e = p < a.npairs ? a.idx[p] : -1;
+        const bool ok = (unsigned)e < (unsigned)E;
+        uint64_t peers = 0;
+        for (int j = 0; j < 64; j++)
+            if (__builtin_amdgcn_readlane(e, j) == e) peers |= 1ull << j;
+        const int rank = __popcll(peers & below);
+        if (ok && rank == __popcll(peers) - 1) wcnt[wv][e] = (unsigned short)(rank + 1);
+        __syncthreads();
+        if (ok) {
+            int r = cur[e] + rank;
+            for (int w = 0; w < wv; w++) r += wcnt[w][e];
             a.pos[p] = r;
             a.row_tok[r] = p / a.topk;
-        } else {
+            if (a.row_k) a.row_k[r] = p - (p / a.topk) * a.topk;
+        } else if (p < a.npairs) {
             a.pos[p] = -1;
         }
+        __syncthreads();
+        if (tid < E) {
+            int s = 0;
+            for (int w = 0; w < 16; w++) {
+                s += wcnt[w][tid];
+                wcnt[w][tid] = 0;
+            }
+            cur[tid] += s;
+        }
+        __syncthreads();
     }
     if (bad) atomicOr(a.status, bad);
 }
 
-/* 8 floats -> 8 fp16 per thread */
-__global__ __launch_bounds__(256) void k_to_f16(uint16_t *o, const float *x, size_t n8)
+/* One workgroup per row: the row's largest finite magnitude (a fixed-order
+ * max, order does not matter), then 8 floats -> 8 fp16 per thread and unit,
+ * each multiplied by the row's power of two first (exact). The second pass
+ * re-reads the row from cache. */
+__device__ __forceinline__ float finite_abs(float v)
 {
-    const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
-    if (i >= n8) return;
-    const f32x4 a = *(const f32x4 *)(x + 8 * i);
-    const f32x4 b = *(const f32x4 *)(x + 8 * i + 4);
-    u32x4 v;
-    v.x = f16_bits(a.x) | (f16_bits(a.y) << 16);
-    v.y = f16_bits(a.z) | (f16_bits(a.w) << 16);
-    v.z = f16_bits(b.x) | (f16_bits(b.y) << 16);
-    v.w = f16_bits(b.z) | (f16_bits(b.w) << 16);
-    *(u32x4 *)(o + 8 * i) = v;
+    const float m = __builtin_fabsf(v);
+    return __builtin_isfinite(m) ? m : 0.0f;
+}
+
+__global__ __launch_bounds__(256) void k_to_f16_rows(uint16_t *o, int *ex, const float *x, int cols)
+{
+    __shared__ float wmax[4];
+    const float *xr = x + (size_t)blockIdx.x * cols;
+    uint16_t *orow = o + (size_t)blockIdx.x * cols;
+    const int units = cols / 8;
+    float m = 0.0f;
+    for (int u = threadIdx.x; u < units; u += 256) {
+        const f32x4 a = *(const f32x4 *)(xr + 8 * u), b = *(const f32x4 *)(xr + 8 * u + 4);
+        m = fmaxf(m, fmaxf(fmaxf(finite_abs(a.x), finite_abs(a.y)), fmaxf(finite_abs(a.z), finite_abs(a.w))));
+        m = fmaxf(m, fmaxf(fmaxf(finite_abs(b.x), finite_abs(b.y)), fmaxf(finite_abs(b.z), finite_abs(b.w))));
+    }
+#pragma unroll
+    for (int s = 32; s >= 1; s >>= 1) m = fmaxf(m, __shfl_xor(m, s, 64));
+    if ((threadIdx.x & 63) == 0) wmax[threadIdx.x >> 6] = m;
+    __syncthreads();
+    m = fmaxf(fmaxf(wmax[0], wmax[1]), fmaxf(wmax[2], wmax[3]));
+    const int e = m > 0.0f ? 14 - ilogbf(m) : 0;       /* m * 2^e in [2^14, 2^15) */
+    if (threadIdx.x == 0) ex[blockIdx.x] = e;
+    for (int u = threadIdx.x; u < units; u += 256) {
+        const f32x4 a = *(const f32x4 *)(xr + 8 * u), b = *(const f32x4 *)(xr + 8 * u + 4);
+        u32x4 v;
+        v.x = f16_bits(ldexpf(a.x, e)) | (f16_bits(ldexpf(a.y, e)) << 16);
+        v.y = f16_bits(ldexpf(a.z, e)) | (f16_bits(ldexpf(a.w, e)) << 16);
+        v.z = f16_bits(ldexpf(b.x, e)) | (f16_bits(ldexpf(b.y, e)) << 16);
+        v.w = f16_bits(ldexpf(b.z, e)) | (f16_bits(ldexpf(b.w, e)) << 16);
+        *(u32x4 *)(orow + 8 * u) = v;
+    }
 }
 
 /* --------------------------------------------------------- grouped GEMM --- */
@@ -405,28 +495,25 @@ __global__ __launch_bounds__(256) void k_grouped(GroupedArgs a)
 
     /* epilogue: lane holds token rr of each tile, features 4 gq .. 4 gq + 3
      * of each 16-row block */
+    unsigned range_bad = 0;
 #pragma unroll
     for (int tt = 0; tt < TT; tt++) {
         const int t = 16 * tt + rr;
         if (t >= ntok) continue;
         const size_t orow = (size_t)(r0 + t) * N;
+        const int ex = b_row_exp(a, r0 + t);
         if constexpr (SWIGLU) {
 #pragma unroll
-            for (int rb = 0; rb < 4; rb++) {
-                float m[4];
-#pragma unroll
-                for (int e = 0; e < 4; e++) m[e] = dev_swiglu(acc[rb][tt][e], acc[rb + 4][tt][e], a.limit);
-                uint2 pk;
-                pk.x = f16_bits(m[0]) | (f16_bits(m[1]) << 16);
-                pk.y = f16_bits(m[2]) | (f16_bits(m[3]) << 16);
-                *(uint2 *)((uint16_t *)a.out + orow + f0 + 16 * rb + 4 * gq) = pk;
-            }
+            for (int rb = 0; rb < 4; rb++)
+                *(uint2 *)((uint16_t *)a.out + orow + f0 + 16 * rb + 4 * gq) =
+                    swiglu_f16x4(acc[rb][tt], acc[rb + 4][tt], ex, a.limit, range_bad);
         } else {
 #pragma unroll
             for (int rb = 0; rb < RB; rb++)
-                *(f4v *)((float *)a.out + orow + f0 + 16 * rb + 4 * gq) = acc[rb][tt];
+                *(f4v *)((float *)a.out + orow + f0 + 16 * rb + 4 * gq) = unscale4(acc[rb][tt], ex);
         }
     }
+    if (range_bad) atomicOr(a.status, range_bad);
 }
 
 /* ------------------------------------------- LDS-staged grouped GEMM --- */
@@ -715,29 +802,26 @@ __global__ __launch_bounds__(512) void k_grouped2(GroupedArgs a)
     __builtin_amdgcn_s_waitcnt(0x0F70);     /* trailing repeat loads drain before exit */
     if (scale_bad) atomicOr(a.status, ST_SCALE_RANGE);
 
+    unsigned range_bad = 0;
 #pragma unroll
     for (int u = 0; u < C::TTW; u++) {
         const int t = 16 * (wt * C::TTW + u) + rr;
         if (t >= ntok) continue;
         const size_t orow = (size_t)(r0 + t) * N;
+        const int ex = b_row_exp(a, r0 + t);
         if constexpr (SWIGLU) {
             constexpr int H = C::RBW / 2;
 #pragma unroll
-            for (int i = 0; i < H; i++) {
-                float m[4];
-#pragma unroll
-                for (int e = 0; e < 4; e++) m[e] = dev_swiglu(acc[i][u][e], acc[i + H][u][e], a.limit);
-                uint2 pk;
-                pk.x = f16_bits(m[0]) | (f16_bits(m[1]) << 16);
-                pk.y = f16_bits(m[2]) | (f16_bits(m[3]) << 16);
-                *(uint2 *)((uint16_t *)a.out + orow + f0 + 16 * blk[i] + 4 * gq) = pk;
-            }
+            for (int i = 0; i < H; i++)
+                *(uint2 *)((uint16_t *)a.out + orow + f0 + 16 * blk[i] + 4 * gq) =
+                    swiglu_f16x4(acc[i][u], acc[i + H][u], ex, a.limit, range_bad);
         } else {
 #pragma unroll
             for (int i = 0; i < C::RBW; i++)
-                *(f4v *)((float *)a.out + orow + f0 + 16 * blk[i] + 4 * gq) = acc[i][u];
+                *(f4v *)((float *)a.out + orow + f0 + 16 * blk[i] + 4 * gq) = unscale4(acc[i][u], ex);
         }
     }
+    if (range_bad) atomicOr(a.status, range_bad);
 }
 
 /* ------------------------------------------- 128-token FP4 tiles (prefill) --- */
@@ -977,28 +1061,25 @@ __global__ __launch_bounds__(512) void k_grouped3(GroupedArgs a)
     __builtin_amdgcn_s_waitcnt(0x0F70);     /* trailing repeat loads drain before exit */
     if (scale_bad) atomicOr(a.status, ST_SCALE_RANGE);
 
+    unsigned range_bad = 0;
 #pragma unroll
     for (int u = 0; u < 4; u++) {
         const int t = 64 * wt + 16 * u + rr;
         if (t >= ntok) continue;
         const size_t orow = (size_t)(r0 + t) * N;
+        const int ex = b_row_exp(a, r0 + t);
         if constexpr (SWIGLU) {
 #pragma unroll
-            for (int i = 0; i < 2; i++) {
-                float m[4];
-#pragma unroll
-                for (int e = 0; e < 4; e++) m[e] = dev_swiglu(acc[i][u][e], acc[i + 2][u][e], a.limit);
-                uint2 pk;
-                pk.x = f16_bits(m[0]) | (f16_bits(m[1]) << 16);
-                pk.y = f16_bits(m[2]) | (f16_bits(m[3]) << 16);
-                *(uint2 *)((uint16_t *)a.out + orow + f0 + 16 * blk[i] + 4 * gq) = pk;
-            }
+            for (int i = 0; i < 2; i++)
+                *(uint2 *)((uint16_t *)a.out + orow + f0 + 16 * blk[i] + 4 * gq) =
+                    swiglu_f16x4(acc[i][u], acc[i + 2][u], ex, a.limit, range_bad);
         } else {
 #pragma unroll
             for (int i = 0; i < 4; i++)
-                *(f4v *)((float *)a.out + orow + f0 + 16 * blk[i] + 4 * gq) = acc[i][u];
+                *(f4v *)((float *)a.out + orow + f0 + 16 * blk[i] + 4 * gq) = unscale4(acc[i][u], ex);
         }
     }
+    if (range_bad) atomicOr(a.status, range_bad);
 }
 
 /* ------------------------------------------------------------- combine --- */
@@ -1045,11 +1126,11 @@ hipError_t moe_route_launch(const RouteArgs &a, hipStream_t st)
     return hipGetLastError();
 }
 
-hipError_t to_f16_launch(uint16_t *o, const float *x, size_t n, hipStream_t st)
+hipError_t to_f16_rows_launch(uint16_t *o, int *ex, const float *x, int rows, int cols,
+                              hipStream_t st)
 {
-    if (n % 8) return hipErrorInvalidValue;
-    const size_t n8 = n / 8;
-    hipLaunchKernelGGL(k_to_f16, dim3((unsigned)((n8 + 255) / 256)), dim3(256), 0, st, o, x, n8);
+    if (rows <= 0 || cols <= 0 || cols % 8) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(k_to_f16_rows, dim3((unsigned)rows), dim3(256), 0, st, o, ex, x, cols);
     return hipGetLastError();
 }
 

@@ -11,6 +11,16 @@
  * at once. The library is not re-entrant across host threads (one mutex
  * serialises the host-pointer calls, as the Vulkan backend's single command
  * buffer and fence do) and nothing here computes on the CPU.
+ *
+ * Kernels report bad input through a device status word. Host-pointer calls
+ * use a word of their own, read after the call's synchronisation: any bit
+ * turns the call into -1, so 0 always means the GPU produced the whole
+ * result. _dev calls use another word, read with dsv4_hip_status().
+ *
+ * DSV4_HIP_DISABLE=1 in the environment makes dsv4_hip_init() fail, which
+ * forces every caller onto its CPU path (the reference's behaviour on a
+ * machine without the GPU backend). Every entry point is one roctx range
+ * named after it, visible in rocprofv3 --marker-trace.
  */
 #include <map>
 #include <mutex>
@@ -21,6 +31,8 @@
 #include <stdlib.h>
 #include <stdio.h>
 #include <string.h>
+
+#include <rocprofiler-sdk-roctx/roctx.h>
 
 #include "dsv4_internal.h"
 #include "../../include/dsv4_hip_aux.h"
@@ -63,15 +75,23 @@ struct State {
     hipStream_t stream = nullptr;
     hipStream_t side = nullptr;          /* concurrent work of one call (shared expert) */
     hipEvent_t fork = nullptr, join = nullptr;
-    unsigned *status = nullptr;          /* device status word            */
-    unsigned *pub = nullptr;             /* one-launch decode: item counter, done flag (own line) */
-    unsigned pub_count = 0, pub_epoch = 0;     /* their values after the last enqueued call */
+    unsigned *status = nullptr;          /* status words: [0] _dev calls, [HOST_WORD] host calls */
+    unsigned *st = nullptr;              /* the word the call being enqueued raises */
+    unsigned *pub = nullptr;             /* one-launch decode: count, done, leave (own lines) */
     std::map<uintptr_t, Region> regions; /* host start -> resident copy   */
     DevBuf x, y, mid, table, small, ys, gemm_ws, moe_ws, x16, msplit;
 };
 
+constexpr int HOST_WORD = 32;            /* the host calls' word, on its own 128-byte line */
+
 State g;
 thread_local std::string g_err;
+
+/* One roctx range per entry point call. */
+struct Range {
+    explicit Range(const char *name) { roctxRangePushA(name); }
+    ~Range() { roctxRangePop(); }
+};
 
 int fail(const char *fmt, ...)
 {
@@ -103,6 +123,39 @@ int usable(void)
     return 0;
 }
 
+/* The calls that follow raise the _dev status word or the host calls' word. */
+void dev_call(void) { g.st = g.status; }
+void host_call(void) { g.st = g.status + HOST_WORD; }
+
+std::string status_text(unsigned v)
+{
+    static const char *const names[] = {
+        "routing id out of range", "expert descriptor of the wrong format",
+        "FP4 scale byte outside 104..140 on an fp16 path", "one-launch decode wait timed out",
+        "SwiGLU output beyond the fp16 range"};
+    std::string s;
+    for (unsigned b = 0; b < sizeof names / sizeof names[0]; b++)
+        if (v & (1u << b)) s += (s.empty() ? "" : "; ") + std::string(names[b]);
+    return s.empty() ? std::string("unknown bits") : s;
+}
+
+/* End of a host-pointer call whose work is enqueued on g.stream: wait for it,
+ * then read the host calls' status word; any bit makes the call -1 (its
+ * output is not the whole, valid result) and is cleared. */
+int finish_host_call(const char *what)
+{
+    unsigned v = 0;
+    HIPCHK(hipMemcpyAsync(&v, g.status + HOST_WORD, sizeof v, hipMemcpyDeviceToHost, g.stream),
+           "status read");
+    HIPCHK(hipStreamSynchronize(g.stream), what);
+    if (v) {
+        HIPCHK(hipMemsetAsync(g.status + HOST_WORD, 0, sizeof v, g.stream), "status clear");
+        HIPCHK(hipStreamSynchronize(g.stream), "status clear");
+        return fail("%s: the device raised status 0x%x (%s)", what, v, status_text(v).c_str());
+    }
+    return 0;
+}
+
 /* Device copy of [p, p + bytes) when it lies inside one registered range. */
 const void *translate(const void *p, size_t bytes)
 {
@@ -126,20 +179,23 @@ int check_qmat(const DSV4QMat *m, const char *what, int *fmt)
     if (*fmt < 0)
         return fail("%s: unsupported geometry wdt=%d %dx%d blk %dx%d", what,
                     m->wdt, m->rows, m->cols, m->blk_r, m->blk_c);
-    if (qmat_row_bytes(m) > 4096)
-        return fail("%s: rows wider than 4096 bytes are not supported", what);
+    /* FP8 up to 8192 columns, FP4 up to 16384, BF16 up to 8192 */
+    const int lim = *fmt == FMT_BF16 ? 16384 : 8192;
+    if (qmat_row_bytes(m) > lim)
+        return fail("%s: rows wider than %d bytes are not supported", what, lim);
     return 0;
 }
 
-/* Host descriptor -> descriptor with resident device pointers. */
+/* Host descriptor -> descriptor with resident device pointers (BF16 has no
+ * scales). */
 int resident(const DSV4QMat *m, DSV4QMat *out, const char *what)
 {
     int fmt;
     if (check_qmat(m, what, &fmt)) return -1;
     *out = *m;
     out->w = translate(m->w, qmat_w_bytes(m));
-    out->s = translate(m->s, qmat_s_bytes(m));
-    if (!out->w || !out->s)
+    out->s = fmt == FMT_BF16 ? nullptr : translate(m->s, qmat_s_bytes(m));
+    if (!out->w || (fmt != FMT_BF16 && !out->s))
         return fail("%s: weights or scales are not inside a registered range", what);
     if (!aligned16(out->w)) return fail("%s: weights are not 16-byte aligned", what);
     return 0;
@@ -153,6 +209,7 @@ int expert_geometry(const DSV4ExpertW *e, int *fmt, int *inter, int *hidden,
         check_qmat(&e->w2, what, &f2))
         return -1;
     if (f1 != f3 || f1 != f2) return fail("%s: w1/w3/w2 formats differ", what);
+    if (f1 == FMT_BF16) return fail("%s: experts must be FP8 or FP4", what);
     if (e->w1.rows != e->w3.rows || e->w1.cols != e->w3.cols ||
         e->w2.rows != e->w1.cols || e->w2.cols != e->w1.rows)
         return fail("%s: w1/w3/w2 shapes do not chain", what);
@@ -188,7 +245,7 @@ GemvArgs gemv_args(const DSV4QMat &m, const float *x, float *y, int nt)
 }
 
 /* The block-scaled MFMA GEMV takes matrices whose columns are whole 128-wide
- * chunks (at most 4096 FP8 or 8192 FP4 columns), FP8 row blocks that are
+ * chunks (at most 8192 FP8 or FP4 columns), FP8 row blocks that are
  * multiples of 16 rows, 4-byte aligned fp32 scales and 16-byte aligned x. */
 bool mx_gemv_ok(const DSV4QMat &d, int fmt, const float *x)
 {
@@ -221,7 +278,7 @@ GemvMxArgs gemv_mx_args(const DSV4QMat &m, const float *x, float *y, int nt)
  * chunks within the GEMV limits. */
 bool mx_expert_ok(int fmt, int inter, int hidden)
 {
-    return inter > 0 && inter % 128 == 0 && gemv_mx_ncw(fmt, hidden) && gemv_mx_ncw(fmt, inter);
+    return inter > 0 && inter % 128 == 0 && gateup_mx_ncw(fmt, hidden) && gemv_mx_ncw(fmt, inter);
 }
 
 /* Enqueue one expert (gate/up + SwiGLU -> mid, then w2 -> out) from a
@@ -245,7 +302,7 @@ int enqueue_expert(const DSV4ExpertW &e, int fmt, int inter, int hidden,
         ga.inter = inter;
         ga.hidden = hidden;
         ga.limit = limit;
-        ga.status = g.status;
+        ga.status = g.st;
         HIPCHK(gateup_mx_launch(fmt, ga, st), "gate/up launch");
         HIPCHK(gemv_mx_launch(fmt, gemv_mx_args(e.w2, mid, out, 1), st), "down launch");
         return 0;
@@ -261,45 +318,70 @@ int enqueue_expert(const DSV4ExpertW &e, int fmt, int inter, int hidden,
     ga.inter = inter;
     ga.hidden = hidden;
     ga.limit = limit;
-    ga.status = g.status;
+    ga.status = g.st;
     HIPCHK(gateup_launch(fmt, ga, st), "gate/up launch");
     HIPCHK(gemv_launch(fmt, gemv_args(e.w2, mid, out, 1), st), "down launch");
     return 0;
 }
 
+/* Device memory of one decode MoE call: the mid rows of the routed slots
+ * ([topk][mid_ld]) followed by the shared expert's, the split tables of the
+ * routed mids ([topk][mx_split_bytes(inter)]), the shared expert's output
+ * [hidden] and the one-launch publication words (ONE_PUB_BYTES, zero between
+ * launches). */
+struct MoeWs {
+    float *mid;
+    uint8_t *msplit;
+    float *ys;
+    unsigned *pub;
+};
+
+size_t moe_mid_ld(int inter) { return (size_t)((inter + 3) & ~3); }
+
 /* Enqueue the decode MoE from device tables. */
 /* Routed slots come from table[idx[k]] with weights w[k] (device arrays), or,
  * when `routed` is set, from the host arrays routed[k] / wv[k], passed by
- * value in the kernel arguments (MFMA path only). */
+ * value in the kernel arguments (MFMA path only). `ws` NULL: the library's
+ * growing buffers (allocated here when too small). */
 int enqueue_moe(const DSV4ExpertW *table, int n_experts, const int *idx,
                 const float *w, int topk, const DSV4ExpertW *shared_dev,
                 int shared_fmt, int shared_inter, int hidden, int inter,
                 const float *x, float *out, float limit, hipStream_t st,
-                const DSV4ExpertW *routed = nullptr, const float *wv = nullptr)
+                const DSV4ExpertW *routed = nullptr, const float *wv = nullptr,
+                const MoeWs *ws = nullptr)
 {
-    const size_t mid_ld = (size_t)((inter + 3) & ~3);
-    const size_t smid_ld = (size_t)((shared_inter + 3) & ~3);
-    HIPCHK(g.mid.need(((size_t)topk * mid_ld + (shared_dev ? smid_ld : 0)) * 4), "mid alloc");
-    float *mid = (float *)g.mid.p;
-    float *ys = nullptr;
-    if (shared_dev) {
-        HIPCHK(g.ys.need((size_t)hidden * 4), "shared output alloc");
-        ys = (float *)g.ys.p;
-        float *smid = mid + (size_t)topk * mid_ld;
-        if (enqueue_expert(*shared_dev, shared_fmt, shared_inter, hidden, x, smid,
-                           ys, limit, st))
-            return -1;
-    }
+    const size_t mid_ld = moe_mid_ld(inter);
     const bool mx = mx_expert_ok(FMT_FP4_E8M0, inter, hidden) && inter <= 2048 &&
                     topk <= MX_ROUTED_MAX && aligned16(x);
     if (routed && !mx)
         return fail("moe_decode_routed_dev: needs the MFMA path (FP4 experts, hidden and inter "
                     "multiples of 128, inter <= 2048, topk <= %d, x 16-byte aligned)", MX_ROUTED_MAX);
+    const size_t sl = mx ? mx_split_bytes(inter) : 0;
+    MoeWs m;
+    if (ws) {
+        m = *ws;
+    } else {
+        HIPCHK(g.mid.need(((size_t)topk * mid_ld + (shared_dev ? moe_mid_ld(shared_inter) : 0)) * 4),
+               "mid alloc");
+        if (shared_dev) HIPCHK(g.ys.need((size_t)hidden * 4), "shared output alloc");
+        if (mx) HIPCHK(g.msplit.need((size_t)topk * sl), "mid split alloc");
+        m.mid = (float *)g.mid.p;
+        m.msplit = (uint8_t *)g.msplit.p;
+        m.ys = (float *)g.ys.p;
+        m.pub = g.pub;
+    }
+    float *mid = m.mid;
+    float *ys = nullptr;
+    if (shared_dev) {
+        ys = m.ys;
+        float *smid = mid + (size_t)topk * mid_ld;
+        if (enqueue_expert(*shared_dev, shared_fmt, shared_inter, hidden, x, smid,
+                           ys, limit, st))
+            return -1;
+    }
     if (mx) {
         /* routed experts on the block-scaled MFMA: gate/up writes each slot's
          * mid split table, down reads it and combines in k order */
-        const size_t sl = mx_split_bytes(inter);
-        HIPCHK(g.msplit.need((size_t)topk * sl), "mid split alloc");
         GateUpMxArgs ga;
         memset(&ga, 0, sizeof ga);
         ga.table = table;
@@ -309,12 +391,12 @@ int enqueue_moe(const DSV4ExpertW *table, int n_experts, const int *idx,
         ga.x = x;
         ga.mid = mid;
         ga.mid_ld = (int)mid_ld;
-        ga.msplit = (uint8_t *)g.msplit.p;
+        ga.msplit = m.msplit;
         ga.msplit_ld = sl;
         ga.inter = inter;
         ga.hidden = hidden;
         ga.limit = limit;
-        ga.status = g.status;
+        ga.status = g.st;
         if (routed) {
             ga.by_value = 1;
             for (int k = 0; k < topk; k++) ga.routed[k] = routed[k];
@@ -326,13 +408,13 @@ int enqueue_moe(const DSV4ExpertW *table, int n_experts, const int *idx,
         da.w = w;
         da.n_experts = n_experts;
         da.topk = topk;
-        da.msplit = (const uint8_t *)g.msplit.p;
+        da.msplit = m.msplit;
         da.msplit_ld = sl;
         da.shared = ys;
         da.out = out;
         da.inter = inter;
         da.hidden = hidden;
-        da.status = g.status;
+        da.status = g.st;
         if (routed) {
             da.by_value = 1;
             for (int k = 0; k < topk; k++) {
@@ -349,17 +431,14 @@ int enqueue_moe(const DSV4ExpertW *table, int n_experts, const int *idx,
             memset(&oa, 0, sizeof oa);
             oa.gu = ga;
             oa.dn = da;
-            const unsigned items = (unsigned)(topk * (inter / 32));
-            oa.pub.count = g.pub;
-            oa.pub.done = g.pub + 32;
-            oa.pub.last = g.pub_count + items - 1;
-            oa.pub.epoch = g.pub_epoch + 1;
-            /* DSV4_HIP_DECODE_SPIN: most polls of a down workgroup's wait (default 2^20) */
+            oa.pub.count = m.pub;
+            oa.pub.done = m.pub + 32;
+            oa.pub.leave = m.pub + 64;
+            /* DSV4_HIP_DECODE_SPIN: most polls of a down workgroup's wait
+             * (default 2^20); 0 gives up without polling */
             const char *sp = getenv("DSV4_HIP_DECODE_SPIN");
             oa.spin_max = sp ? (unsigned)strtoul(sp, nullptr, 10) : 1u << 20;
             HIPCHK(moe_one_launch(oa, st), "one-launch decode MoE");
-            g.pub_count += items;
-            g.pub_epoch += 1;
             return 0;
         }
         HIPCHK(gateup_mx_launch(FMT_FP4_E8M0, ga, st), "routed gate/up launch");
@@ -378,7 +457,7 @@ int enqueue_moe(const DSV4ExpertW *table, int n_experts, const int *idx,
     ga.inter = inter;
     ga.hidden = hidden;
     ga.limit = limit;
-    ga.status = g.status;
+    ga.status = g.st;
     HIPCHK(gateup_launch(FMT_FP4_E8M0, ga, st), "routed gate/up launch");
     DownArgs da;
     memset(&da, 0, sizeof da);
@@ -393,7 +472,7 @@ int enqueue_moe(const DSV4ExpertW *table, int n_experts, const int *idx,
     da.out = out;
     da.inter = inter;
     da.hidden = hidden;
-    da.status = g.status;
+    da.status = g.st;
     HIPCHK(down_launch(da, st), "down/combine launch");
     return 0;
 }
@@ -405,6 +484,10 @@ extern "C" {
 int dsv4_hip_init(int device)
 {
     std::lock_guard<std::mutex> lk(g.mu);
+    Range rg("dsv4_hip_init");
+    const char *off = getenv("DSV4_HIP_DISABLE");
+    if (off && *off && strcmp(off, "0") != 0)
+        return fail("DSV4_HIP_DISABLE is set: the GPU backend is switched off");
     if (g.ready && g.device == device && !g.dead) return 0;
     if (g.ready) return fail("already initialised on device %d", g.device);
     int n = 0;
@@ -426,9 +509,9 @@ int dsv4_hip_init(int device)
         return fail("event creation failed");
     if (hipMalloc((void **)&g.status, 256) != hipSuccess) return fail("status alloc failed");
     if (hipMemset(g.status, 0, 256) != hipSuccess) return fail("status clear failed");
-    if (hipMalloc((void **)&g.pub, 256) != hipSuccess) return fail("counter alloc failed");
-    if (hipMemset(g.pub, 0, 256) != hipSuccess) return fail("counter clear failed");
-    g.pub_count = g.pub_epoch = 0;
+    if (hipMalloc((void **)&g.pub, ONE_PUB_BYTES) != hipSuccess) return fail("counter alloc failed");
+    if (hipMemset(g.pub, 0, ONE_PUB_BYTES) != hipSuccess) return fail("counter clear failed");
+    g.st = g.status;
 
     g.device = device;
     g.ready = 1;
@@ -508,25 +591,36 @@ void *dsv4_hip_device_ptr(const void *p)
     return (void *)translate(p, 1);
 }
 
-/* y = W . x for nt tokens. From MMQ_MFMA_MIN_TOKENS tokens on, matrices the
- * grouped kernel takes (rows, cols multiples of 128; FP8 with 128x128 blocks
- * or FP4 with 1x32) run as one dense fp16-MFMA GEMM (x rounded to fp16, weights
- * decoded exactly, fp32 accumulation); fewer tokens run the block-scaled MFMA
- * GEMV where its geometry fits, else the per-token VALU GEMV. */
+/* y = W . x for nt tokens. BF16 matrices run the fp64-accumulating GEMV for
+ * every nt. From MMQ_MFMA_MIN_TOKENS tokens on, packed matrices the grouped
+ * kernel takes (rows, cols multiples of 128; FP8 with 128x128 blocks or FP4
+ * with 1x32) run as one dense fp16-MFMA GEMM (x row-scaled by a power of two
+ * and rounded to fp16, weights decoded exactly, fp32 accumulation); fewer
+ * tokens run the block-scaled MFMA GEMV where its geometry fits, else the
+ * per-token VALU GEMV. */
 constexpr int MMQ_MFMA_MIN_TOKENS = 32;
 
 int enqueue_mmq(const DSV4QMat &d, int fmt, const float *x, float *y, int nt, hipStream_t st)
 {
+    if (fmt == FMT_BF16) {
+        GemvBf16Args b;
+        b.W = (const uint16_t *)d.w; b.x = x; b.y = y;
+        b.rows = d.rows; b.cols = d.cols; b.nt = nt; b.x_ld = d.cols; b.y_ld = d.rows;
+        HIPCHK(gemv_bf16_launch(b, st), "bf16 gemv launch");
+        return 0;
+    }
     const bool blocks = fmt == FMT_FP4_E8M0 ? d.blk_r == 1 : d.blk_r == 128;
     if (nt >= MMQ_MFMA_MIN_TOKENS && blocks && d.rows % 128 == 0 && d.cols % 128 == 0 &&
         ((uintptr_t)d.s & 3u) == 0) {
-        HIPCHK(g.x16.need((size_t)nt * d.cols * 2), "fp16 staging");
+        const size_t xb = ((size_t)nt * d.cols * 2 + 255) & ~(size_t)255;
+        HIPCHK(g.x16.need(xb + (size_t)nt * 4), "fp16 staging");
         uint16_t *x16 = (uint16_t *)g.x16.p;
-        HIPCHK(to_f16_launch(x16, x, (size_t)nt * d.cols, st), "x fp16 launch");
+        int *ex = (int *)((uint8_t *)g.x16.p + xb);
+        HIPCHK(to_f16_rows_launch(x16, ex, x, nt, d.cols, st), "x fp16 launch");
         GroupedArgs a;
         memset(&a, 0, sizeof a);
-        a.m1 = d; a.nrows = nt; a.B = x16; a.K = d.cols; a.N = d.rows; a.out = y;
-        a.status = g.status;
+        a.m1 = d; a.nrows = nt; a.B = x16; a.bexp = ex; a.K = d.cols; a.N = d.rows; a.out = y;
+        a.status = g.st;
         const int tt = nt <= 16 ? 1 : 4;
         const long tiles = (nt + grouped_rows_per_tile(tt) - 1) / grouped_rows_per_tile(tt);
         HIPCHK(grouped_launch(fmt, false, tt, a, tiles, st), "dense MFMA launch");
@@ -543,11 +637,13 @@ int enqueue_mmq(const DSV4QMat &d, int fmt, const float *x, float *y, int nt, hi
 int dsv4_hip_mmq_n(float *y, const float *x, const DSV4QMat *m, int nt)
 {
     std::lock_guard<std::mutex> lk(g.mu);
+    Range rg("dsv4_hip_mmq_n");
     if (usable()) return -1;
     if (nt <= 0) return 0;
     if (!x || !y) return fail("mmq_n: NULL x or y");
     DSV4QMat d;
     if (resident(m, &d, "mmq_n")) return -1;
+    host_call();
     const int fmt = qmat_fmt(m);
     const size_t xb = (size_t)nt * m->cols * 4, yb = (size_t)nt * m->rows * 4;
     HIPCHK(g.x.need(xb), "x staging");
@@ -555,8 +651,7 @@ int dsv4_hip_mmq_n(float *y, const float *x, const DSV4QMat *m, int nt)
     HIPCHK(hipMemcpyAsync(g.x.p, x, xb, hipMemcpyHostToDevice, g.stream), "x upload");
     if (enqueue_mmq(d, fmt, (const float *)g.x.p, (float *)g.y.p, nt, g.stream)) return -1;
     HIPCHK(hipMemcpyAsync(y, g.y.p, yb, hipMemcpyDeviceToHost, g.stream), "y download");
-    HIPCHK(hipStreamSynchronize(g.stream), "mmq_n sync");
-    return 0;
+    return finish_host_call("mmq_n");
 }
 
 int dsv4_hip_mmq(float *y, const float *x, const DSV4QMat *m)
@@ -568,12 +663,14 @@ int dsv4_hip_mmq_n_dev(float *y, const float *x, const DSV4QMat *m, int nt,
                        void *stream)
 {
     std::lock_guard<std::mutex> lk(g.mu);
+    Range rg("dsv4_hip_mmq_n_dev");
     if (usable()) return -1;
     if (nt <= 0) return 0;
     int fmt;
     if (check_qmat(m, "mmq_n_dev", &fmt)) return -1;
-    if (!x || !y || !m->w || !m->s) return fail("mmq_n_dev: NULL pointer");
+    if (!x || !y || !m->w || (fmt != FMT_BF16 && !m->s)) return fail("mmq_n_dev: NULL pointer");
     if (!aligned16(x) || !aligned16(m->w)) return fail("mmq_n_dev: x and W must be 16-byte aligned");
+    dev_call();
     return enqueue_mmq(*m, fmt, x, y, nt, (hipStream_t)stream);
 }
 
@@ -581,6 +678,7 @@ int dsv4_hip_expert_forward(float *out, const float *x, const DSV4ExpertW *e,
                             int inter, float limit)
 {
     std::lock_guard<std::mutex> lk(g.mu);
+    Range rg("dsv4_hip_expert_forward");
     if (usable()) return -1;
     if (!out || !x || !e) return fail("expert_forward: NULL pointer");
     int fmt, ei, eh;
@@ -588,6 +686,7 @@ int dsv4_hip_expert_forward(float *out, const float *x, const DSV4ExpertW *e,
     if (ei != inter) return fail("expert_forward: inter %d != w1 rows %d", inter, ei);
     DSV4ExpertW d;
     if (resident_expert(e, &d, "expert_forward")) return -1;
+    host_call();
     HIPCHK(g.x.need((size_t)eh * 4), "x staging");
     HIPCHK(g.y.need((size_t)eh * 4), "y staging");
     HIPCHK(g.mid.need((size_t)inter * 4), "mid alloc");
@@ -596,8 +695,7 @@ int dsv4_hip_expert_forward(float *out, const float *x, const DSV4ExpertW *e,
                        (float *)g.y.p, limit, g.stream))
         return -1;
     HIPCHK(hipMemcpyAsync(out, g.y.p, (size_t)eh * 4, hipMemcpyDeviceToHost, g.stream), "out download");
-    HIPCHK(hipStreamSynchronize(g.stream), "expert sync");
-    return 0;
+    return finish_host_call("expert_forward");
 }
 
 int dsv4_hip_moe_decode(float *out, const float *x, const DSV4ExpertW *const *ex,
@@ -605,6 +703,7 @@ int dsv4_hip_moe_decode(float *out, const float *x, const DSV4ExpertW *const *ex
                         float limit)
 {
     std::lock_guard<std::mutex> lk(g.mu);
+    Range rg("dsv4_hip_moe_decode");
     if (usable()) return -1;
     if (!out || !x || !ex || !w) return fail("moe_decode: NULL pointer");
     if (topk < 1 || topk > 16) return fail("moe_decode: topk %d outside 1..16", topk);
@@ -628,6 +727,7 @@ int dsv4_hip_moe_decode(float *out, const float *x, const DSV4ExpertW *const *ex
         if (sh != hidden) return fail("moe_decode: shared hidden %d != %d", sh, hidden);
         if (resident_expert(shared, &sdev, "moe_decode shared")) return -1;
     }
+    host_call();
     /* table, identity routing and weights in one small upload */
     const size_t tb = (size_t)topk * sizeof(DSV4ExpertW);
     const size_t ib = 16 * sizeof(int), wb = 16 * sizeof(float);
@@ -648,8 +748,7 @@ int dsv4_hip_moe_decode(float *out, const float *x, const DSV4ExpertW *const *ex
                     (float *)g.y.p, limit, g.stream))
         return -1;
     HIPCHK(hipMemcpyAsync(out, g.y.p, (size_t)hidden * 4, hipMemcpyDeviceToHost, g.stream), "out download");
-    HIPCHK(hipStreamSynchronize(g.stream), "moe sync");
-    return 0;
+    return finish_host_call("moe_decode");
 }
 
 int dsv4_hip_moe_decode_dev(float *out, const float *x, const DSV4ExpertW *experts,
@@ -658,7 +757,9 @@ int dsv4_hip_moe_decode_dev(float *out, const float *x, const DSV4ExpertW *exper
                             float limit, void *stream)
 {
     std::lock_guard<std::mutex> lk(g.mu);
+    Range rg("dsv4_hip_moe_decode_dev");
     if (usable()) return -1;
+    dev_call();
     if (!out || !x || !experts || !idx || !w) return fail("moe_decode_dev: NULL pointer");
     if (topk < 1 || topk > 16) return fail("moe_decode_dev: topk %d outside 1..16", topk);
     if (n_experts < 1) return fail("moe_decode_dev: no experts");
@@ -683,7 +784,9 @@ int dsv4_hip_moe_decode_routed_dev(float *out, const float *x, const DSV4ExpertW
                                    float limit, void *stream)
 {
     std::lock_guard<std::mutex> lk(g.mu);
+    Range rg("dsv4_hip_moe_decode_routed_dev");
     if (usable()) return -1;
+    dev_call();
     if (!out || !x || !experts || !idx || !w) return fail("moe_decode_routed_dev: NULL pointer");
     if (topk < 1 || topk > MX_ROUTED_MAX)
         return fail("moe_decode_routed_dev: topk %d outside 1..%d", topk, MX_ROUTED_MAX);
@@ -747,7 +850,9 @@ int dsv4_hip_gemm_fp8_dev(void *C, int out_bf16, const void *A, int a_bf16, int 
                           const DSV4QMat *W, void *stream)
 {
     std::lock_guard<std::mutex> lk(g.mu);
+    Range rg("dsv4_hip_gemm_fp8_dev");
     if (usable()) return -1;
+    dev_call();
     int fmt;
     if (gemm_checks(C, A, M, W, "gemm_fp8_dev", &fmt)) return -1;
     const int K = W->cols;
@@ -765,7 +870,9 @@ int dsv4_hip_gemm_fp8q_dev(void *C, int out_bf16, const uint8_t *Aq, const float
                            int M, const DSV4QMat *W, void *stream)
 {
     std::lock_guard<std::mutex> lk(g.mu);
+    Range rg("dsv4_hip_gemm_fp8q_dev");
     if (usable()) return -1;
+    dev_call();
     int fmt;
     if (gemm_checks(C, Aq, M, W, "gemm_fp8q_dev", &fmt)) return -1;
     if (!Sa) return fail("gemm_fp8q_dev: NULL scales");
@@ -799,7 +906,7 @@ int enqueue_moe_grouped(float *out, const float *x, int n, const DSV4ExpertW *ta
     const size_t o_tg = take((size_t)max_tiles * 4);
     const size_t o_pos = take((size_t)P * 4), o_row = take((size_t)P * 4);
     const size_t o_x16 = take((size_t)n * hidden * 2), o_mid = take((size_t)P * inter * 2);
-    const size_t o_y = take((size_t)P * hidden * 4);
+    const size_t o_y = take((size_t)P * hidden * 4), o_ex = take((size_t)n * 4);
     size_t o_smid = 0, o_ys = 0;
     if (shared) {
         o_smid = take((size_t)n * sinter * 2);
@@ -811,22 +918,25 @@ int enqueue_moe_grouped(float *out, const float *x, int n, const DSV4ExpertW *ta
     int *pos = (int *)(ws + o_pos), *row = (int *)(ws + o_row);
     uint16_t *x16 = (uint16_t *)(ws + o_x16), *mid = (uint16_t *)(ws + o_mid);
     float *y = (float *)(ws + o_y);
+    int *ex = (int *)(ws + o_ex);
 
     RouteArgs ra;
     ra.idx = idx; ra.npairs = (int)P; ra.topk = topk; ra.n_experts = n_experts;
     ra.tile_rows = trows; ra.grp_off = grp; ra.tile_pre = tp; ra.tile_grp = tg; ra.pos = pos;
     ra.row_tok = row;
-    ra.status = g.status;
+    ra.row_k = nullptr;
+    ra.status = g.st;
     HIPCHK(moe_route_launch(ra, st), "route launch");
-    HIPCHK(to_f16_launch(x16, x, (size_t)n * hidden, st), "x fp16 launch");
+    HIPCHK(to_f16_rows_launch(x16, ex, x, n, hidden, st), "x fp16 launch");
 
     GroupedArgs ga;
     memset(&ga, 0, sizeof ga);
     ga.table = table; ga.n_experts = n_experts; ga.grp_off = grp; ga.tile_pre = tp; ga.tile_grp = tg;
-    ga.row_tok = row; ga.nrows = n; ga.B = x16; ga.K = hidden; ga.N = inter; ga.out = mid;
-    ga.limit = limit; ga.status = g.status;
+    ga.row_tok = row; ga.nrows = n; ga.B = x16; ga.bexp = ex; ga.K = hidden; ga.N = inter;
+    ga.out = mid; ga.limit = limit; ga.status = g.st;
     HIPCHK(grouped_launch(FMT_FP4_E8M0, true, tt, ga, max_tiles, st), "routed gate/up launch");
-    ga.row_tok = nullptr; ga.nrows = (int)P; ga.B = mid; ga.K = inter; ga.N = hidden; ga.out = y;
+    ga.row_tok = nullptr; ga.bexp = nullptr;
+    ga.nrows = (int)P; ga.B = mid; ga.K = inter; ga.N = hidden; ga.out = y;
     HIPCHK(grouped_launch(FMT_FP4_E8M0, false, tt, ga, max_tiles, st), "routed down launch");
 
     float *ys = nullptr;
@@ -841,10 +951,10 @@ int enqueue_moe_grouped(float *out, const float *x, int n, const DSV4ExpertW *ta
         const long stiles = (n + grouped_rows_per_tile(stt) - 1) / grouped_rows_per_tile(stt);
         GroupedArgs sa;
         memset(&sa, 0, sizeof sa);
-        sa.m1 = shared->w1; sa.m3 = shared->w3; sa.nrows = n; sa.B = x16;
-        sa.K = hidden; sa.N = sinter; sa.out = smid; sa.limit = limit; sa.status = g.status;
+        sa.m1 = shared->w1; sa.m3 = shared->w3; sa.nrows = n; sa.B = x16; sa.bexp = ex;
+        sa.K = hidden; sa.N = sinter; sa.out = smid; sa.limit = limit; sa.status = g.st;
         HIPCHK(grouped_launch(sfmt, true, stt, sa, stiles, g.side), "shared gate/up launch");
-        sa.m1 = shared->w2; sa.B = smid; sa.K = sinter; sa.N = hidden; sa.out = ys;
+        sa.m1 = shared->w2; sa.B = smid; sa.bexp = nullptr; sa.K = sinter; sa.N = hidden; sa.out = ys;
         HIPCHK(grouped_launch(sfmt, false, stt, sa, stiles, g.side), "shared down launch");
         HIPCHK(hipEventRecord(g.join, g.side), "join record");
     }
@@ -893,7 +1003,9 @@ int dsv4_hip_moe_grouped_dev(float *out, const float *x, int n, const DSV4Expert
                              void *stream)
 {
     std::lock_guard<std::mutex> lk(g.mu);
+    Range rg("dsv4_hip_moe_grouped_dev");
     if (usable()) return -1;
+    dev_call();
     if (!out || !x || !experts || !idx || !w) return fail("moe_grouped_dev: NULL pointer");
     int sfmt, sinter;
     if (grouped_checks(n, topk, n_experts, hidden, inter, shared, &sfmt, &sinter, "moe_grouped_dev"))
@@ -908,6 +1020,7 @@ int dsv4_hip_moe_grouped(float *out, const float *x, int n, const int *topk_idx,
                          int n_experts, const DSV4ExpertW *shared, float limit)
 {
     std::lock_guard<std::mutex> lk(g.mu);
+    Range rg("dsv4_hip_moe_grouped");
     if (usable()) return -1;
     if (!out || !x || !topk_idx || !topk_w || !experts) return fail("moe_grouped: NULL pointer");
     if (n_experts < 1 || n_experts > 1024) return fail("moe_grouped: n_experts %d outside 1..1024", n_experts);
@@ -928,6 +1041,7 @@ int dsv4_hip_moe_grouped(float *out, const float *x, int n, const int *topk_idx,
     if (grouped_checks(n, topk, n_experts, hidden, inter, shared ? &sdev : nullptr, &sfmt, &sinter,
                        "moe_grouped"))
         return -1;
+    host_call();
     const size_t P = (size_t)n * topk;
     const size_t tb = ((size_t)n_experts * sizeof(DSV4ExpertW) + 255) & ~(size_t)255;
     const size_t ib = (P * 4 + 255) & ~(size_t)255;
@@ -944,13 +1058,40 @@ int dsv4_hip_moe_grouped(float *out, const float *x, int n, const int *topk_idx,
                             shared ? &sdev : nullptr, sfmt, sinter, hidden, inter, limit, g.stream))
         return -1;
     HIPCHK(hipMemcpyAsync(out, g.y.p, (size_t)n * hidden * 4, hipMemcpyDeviceToHost, g.stream), "out download");
-    HIPCHK(hipStreamSynchronize(g.stream), "grouped sync");
+    return finish_host_call("moe_grouped");
+}
+
+int dsv4_hip_moe_route_dev(int *ex_off, int *ex_tok, int *ex_k, int *pos, const int *idx, int n,
+                           int topk, int n_experts, void *stream)
+{
+    std::lock_guard<std::mutex> lk(g.mu);
+    Range rg("dsv4_hip_moe_route_dev");
+    if (usable()) return -1;
+    dev_call();
+    if (!ex_off || !ex_tok || !ex_k || !pos || !idx) return fail("moe_route_dev: NULL pointer");
+    if (n < 1 || topk < 1 || topk > 16 || (long)n * topk > (1L << 26))
+        return fail("moe_route_dev: bad n %d / topk %d", n, topk);
+    if (n_experts < 1 || n_experts > 1024)
+        return fail("moe_route_dev: n_experts %d outside 1..1024", n_experts);
+    const long P = (long)n * topk;
+    const int trows = 16;
+    const long max_tiles = (P + trows - 1) / trows + n_experts;
+    const size_t o_tp = 0, o_tg = (((size_t)n_experts + 1) * 4 + 255) & ~(size_t)255;
+    HIPCHK(g.small.need(o_tg + (size_t)max_tiles * 4), "route workspace");
+    RouteArgs ra;
+    ra.idx = idx; ra.npairs = (int)P; ra.topk = topk; ra.n_experts = n_experts;
+    ra.tile_rows = trows; ra.grp_off = ex_off;
+    ra.tile_pre = (int *)((uint8_t *)g.small.p + o_tp);
+    ra.tile_grp = (int *)((uint8_t *)g.small.p + o_tg);
+    ra.pos = pos; ra.row_tok = ex_tok; ra.row_k = ex_k; ra.status = g.st;
+    HIPCHK(moe_route_launch(ra, (hipStream_t)stream), "route launch");
     return 0;
 }
 
 int dsv4_hip_status(unsigned *bits)
 {
     std::lock_guard<std::mutex> lk(g.mu);
+    Range rg("dsv4_hip_status");
     if (!g.ready) return fail("not initialised");
     HIPCHK(hipDeviceSynchronize(), "status sync");
     unsigned v = 0;
@@ -968,6 +1109,7 @@ int dsv4_hip_dequant_dev(float *out, const DSV4QMat *m, void *stream)
     if (usable()) return -1;
     int fmt;
     if (check_qmat(m, "dequant_dev", &fmt)) return -1;
+    if (fmt == FMT_BF16) return fail("dequant_dev: BF16 has no packed format to decode");
     if (!out || !m->w || !m->s) return fail("dequant_dev: NULL pointer");
     if (!aligned16(m->w)) return fail("dequant_dev: W must be 16-byte aligned");
     HIPCHK(dequant_launch(fmt, *m, out, (hipStream_t)stream), "dequant launch");

@@ -11,7 +11,9 @@
  *                  ranges uploaded once with dsv4_hip_register(); the library
  *                  maps them to their resident HBM copies. These return 0 when
  *                  the GPU produced the whole result and -1 when it did not
- *                  (no device, unregistered weights, unsupported geometry) --
+ *                  (no device, unregistered weights, unsupported geometry,
+ *                  or a kernel of the call raised a status bit: bad routing
+ *                  id or descriptor, a value its arithmetic cannot carry) --
  *                  the convention of the reference's GPU backend
  *                  (src/80_prefill/dsv4_prefill_vk.h:31-41): on -1 the caller
  *                  keeps its own CPU path. Nothing in this library computes on
@@ -68,7 +70,8 @@ typedef struct {
 
 /* Select and initialise `device`. 0 ok, -1 when no usable gfx950 GPU exists
  * (the caller keeps its CPU path), mirroring dsv4_prefill_vk_init
- * (src/80_prefill/dsv4_prefill_vk.h:31-35). Idempotent. */
+ * (src/80_prefill/dsv4_prefill_vk.h:31-35). Idempotent. DSV4_HIP_DISABLE=1
+ * in the environment makes it return -1, forcing the CPU path. */
 int  dsv4_hip_init(int device);
 
 /* Release every resident copy and staging buffer. */
@@ -94,8 +97,11 @@ void *dsv4_hip_device_ptr(const void *p);
 /* ------------------------------------------------- packed matmul (a7-a9) --
  * y[t*rows + o] = sum_c x[t*cols + c] * W[o, c] for t in 0..nt-1.
  * Replaces the body of dsv4_mmq_n (src/10_compute/dsv4_matmul.h:40,
- * dsv4_matmul.c:117-127): DSV4_WFP8 (E8M0 128x128 or any blk_r x 128),
- * DSV4_WFP8_F32S and DSV4_WFP4 (E8M0 1x32). Other tags return -1. */
+ * dsv4_matmul.c:44-73): DSV4_WBF16 (no scales; products and sums in fp64
+ * with one final rounding, as bf16_n does, src/10_compute/dsv4_matmul.c:
+ * 88-113), DSV4_WFP8 (E8M0 128x128 or any blk_r x 128), DSV4_WFP8_F32S and
+ * DSV4_WFP4 (E8M0 1x32). Rows up to 8192 bytes (FP8 and BF16 8192 columns,
+ * FP4 16384). Other tags and geometries return -1. */
 int  dsv4_hip_mmq_n(float *y, const float *x, const DSV4QMat *m, int nt);
 
 /* One token: dsv4_mmq (src/10_compute/dsv4_matmul.h:43). */
@@ -131,7 +137,11 @@ int  dsv4_hip_moe_decode(float *out, const float *x,
  * and down workgroups in one grid, mid handed over through a device counter);
  * the environment variable DSV4_HIP_DECODE_LAUNCHES=2 selects the two-launch
  * form, which gives the same bits; DSV4_HIP_DECODE_SPIN bounds the down
- * workgroups' wait in polls (default 2^20, about a second). */
+ * workgroups' wait in polls (default 2^20, about a second; 0 gives up at
+ * once, status bit 3 and NaN output). The launch leaves its hand-off words
+ * zero as it found them, so it may be captured in a HIP graph and replayed;
+ * calls that overlap on one GPU (two streams at once) race on the library's
+ * workspace. */
 int  dsv4_hip_moe_decode_dev(float *out, const float *x,
                              const DSV4ExpertW *experts, int n_experts,
                              const int *idx, const float *w, int topk,
@@ -169,9 +179,11 @@ int  dsv4_hip_moe_decode_routed_dev(float *out, const float *x,
  * w2 [hidden x inter]. Shared: FP4 (1x32) or FP8 (128x128, E8M0 or fp32
  * scales). hidden, inter multiples of 128; n_experts <= 1024; topk <= 16.
  * Numerics: fp16 MFMA with fp32 accumulation; weights decoded exactly (FP4
- * scale bytes 104..140, i.e. |w| in [2^-24, 2^14), else status bit 2); x and
- * the SwiGLU output are rounded to fp16 on the way into the MFMA, a relative
- * error of at most 2^-11 per element. Tolerance: relative L2 1e-3 against the
+ * scale bytes 104..140, i.e. |w| in [2^-24, 2^14), else status bit 2); each
+ * row of x is scaled by a power of two (undone exactly on the results) and
+ * x and the SwiGLU output are rounded to fp16 on the way into the MFMA, a
+ * relative error of at most 2^-11 per element; a SwiGLU output beyond the
+ * fp16 range raises status bit 4. Tolerance: relative L2 1e-3 against the
  * reference's fp32 path (typically ~1e-4). */
 int  dsv4_hip_moe_grouped(float *out, const float *x, int n, const int *topk_idx,
                           const float *topk_w, int topk, const DSV4ExpertW *experts,
@@ -215,7 +227,9 @@ int  dsv4_hip_gemm_fp8q_dev(void *C, int out_bf16, const uint8_t *Aq,
  * 104..140, whose blocks it cannot decode exactly. Bit 3: a one-launch decode
  * MoE gave up waiting for its gate/up half (about a second; only possible
  * when other work keeps its workgroups from running), its output is NaN.
- * Synchronises the library's streams. 0 ok, -1 no device. */
+ * Bit 4: an fp16-MFMA path met a SwiGLU output beyond the fp16 range.
+ * Host-pointer calls keep a word of their own and turn any bit into -1.
+ * Synchronises the device. 0 ok, -1 no device. */
 int  dsv4_hip_status(unsigned *bits);
 
 #ifdef __cplusplus

@@ -44,6 +44,19 @@ int dsv4_hip_quant_act_fp8_1x128_dev(uint8_t *Q, float *S, const float *a,
 int dsv4_hip_quant_act_mxfp8_dev(uint8_t *Q, uint8_t *S, const float *a,
                                  int n, int k, void *stream);
 
+/* The grouped MoE's permutation on its own (the first step of
+ * dsv4_hip_moe_grouped_dev): the counting sort of the n * topk routing ids
+ * idx[n][topk] by expert, as src/80_prefill/dsv4_prefill_union.c:30-51
+ * builds ex_off / ex_tok / ex_k. ex_off [n_experts + 1] is the first row of
+ * each expert's bucket (ex_off[e + 1] - ex_off[e] = its count); ex_tok and
+ * ex_k [n * topk] the token and k of each row, rows of a bucket in
+ * token-major, k-minor order; pos [n * topk] the row of each (token, k)
+ * pair. An id outside [0, n_experts) raises status bit 0 and gets pos -1.
+ * The reference's ex_order (the order its host processes buckets in) has no
+ * counterpart: the device runs every bucket at once. */
+int dsv4_hip_moe_route_dev(int *ex_off, int *ex_tok, int *ex_k, int *pos, const int *idx,
+                           int n, int topk, int n_experts, void *stream);
+
 /* out[i] = sigma * N(0,1) sample i of stream `seed` (counter-based splitmix64
  * hash -> Box-Muller in double -> fp32), rounded to bf16 when round_bf16. */
 int dsv4_hip_synth_normal_dev(float *out, size_t n, uint64_t seed, float sigma,

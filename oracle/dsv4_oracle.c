@@ -34,6 +34,13 @@ static inline uint32_t f_bits(float f) { uint32_t u; memcpy(&u, &f, 4); return u
 
 /* ------------------------------------------------------------ decoders --- */
 
+/* src/10_compute/dsv4_dec_common.h:24-29 (bf16d): the halfword is the top
+ * of the float, widened to double (exact). */
+static inline double orc_bf16_to_f64(uint16_t h)
+{
+    return (double)bits_f((uint32_t)h << 16);
+}
+
 /* src/10_compute/dsv4_quant.h:72-86: 2^(b-127); 0 -> 2^-127 (subnormal),
  * 255 -> NaN. */
 float orc_e8m0(uint8_t b)
@@ -325,10 +332,43 @@ void orc_fp4_n(float *y, const float *x, const uint8_t *W, const uint8_t *S,
 
 /* src/10_compute/dsv4_matmul.c:96-127 (token tiling cannot change a row's
  * arithmetic, so the bodies are called on the whole block). */
+/* bf16_n (src/10_compute/dsv4_matmul.c:88-113) with its BLOCK_DOT_V tree
+ * (src/10_compute/dsv4_dec_common.h:23-61): weights and activations widened
+ * to double (both exact); four 4-lane double accumulators v0..v3 take
+ * columns i..i+3, i+4..i+7, i+8..i+11, i+12..i+15 of every 16-column step
+ * with one fma per lane; lanes are summed v0+v1 and v2+v3 first, then the
+ * four lane totals as (l0+l1)+(l2+l3); the tail past the last whole step
+ * takes one fma per column; the row total is rounded to float once. */
+void orc_bf16_n(float *y, const float *x, const uint16_t *W, int in, int out, int nt)
+{
+    for (int o = 0; o < out; o++) {
+        const uint16_t *row = W + (size_t)o * in;
+        for (int t = 0; t < nt; t++) {
+            const float *xb = x + (size_t)t * in;
+            double v[4][4] = {{0}};
+            int i = 0;
+            for (; i + 15 < in; i += 16)
+                for (int q = 0; q < 4; q++)
+                    for (int l = 0; l < 4; l++) {
+                        const int c = i + 4 * q + l;
+                        v[q][l] = fma(orc_bf16_to_f64(row[c]), (double)xb[c], v[q][l]);
+                    }
+            double bb[4];
+            for (int l = 0; l < 4; l++) bb[l] = (v[0][l] + v[1][l]) + (v[2][l] + v[3][l]);
+            double acc = (bb[0] + bb[1]) + (bb[2] + bb[3]);
+            for (; i < in; i++) acc = fma(orc_bf16_to_f64(row[i]), (double)xb[i], acc);
+            y[(size_t)t * out + o] = (float)acc;
+        }
+    }
+}
+
 int orc_mmq_n(float *y, const float *x, const DSV4QMat *m, int nt)
 {
     if (nt <= 0) return 0;
     switch (m->wdt) {
+    case DSV4_WBF16:
+        orc_bf16_n(y, x, (const uint16_t *)m->w, m->cols, m->rows, nt);
+        return 0;
     case DSV4_WFP8:
         orc_fp8_n(y, x, (const uint8_t *)m->w, (const uint8_t *)m->s,
                   m->cols, m->rows, m->blk_r, m->blk_c, nt);

@@ -39,8 +39,11 @@ void orc_fp8f_n(float *y, const float *x, const uint8_t *W, const float *S,
                 int in, int out, int blk_r, int blk_c, int nt);
 void orc_fp4_n(float *y, const float *x, const uint8_t *W, const uint8_t *S,
                int in, int out, int blk_r, int blk_c, int nt);
-/* dsv4_mmq_n dispatch over DSV4_WFP8 / DSV4_WFP8_F32S / DSV4_WFP4.
- * Returns -1 for other tags (the reference aborts). */
+/* bf16_n: src/10_compute/dsv4_matmul.c:88-113 (double widening and the
+ * BLOCK_DOT_V lane tree of src/10_compute/dsv4_dec_common.h:45-61) */
+void orc_bf16_n(float *y, const float *x, const uint16_t *W, int in, int out, int nt);
+/* dsv4_mmq_n dispatch over DSV4_WBF16 / DSV4_WFP8 / DSV4_WFP8_F32S /
+ * DSV4_WFP4. Returns -1 for other tags (the reference aborts). */
 int  orc_mmq_n(float *y, const float *x, const DSV4QMat *m, int nt);
 
 /* ---- scalar double oracle: tests/unit/test_matmul.c:54-176 ---- */

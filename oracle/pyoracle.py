@@ -58,6 +58,8 @@ def fp8_scale_grid(rows, cols, blk_r, blk_c):
 
 
 def scale_count(wdt, rows, cols, blk_r, blk_c):
+    if wdt == DSV4_WBF16:
+        return 0
     if wdt in (DSV4_WFP8, DSV4_WFP8_F32S):
         return fp8_scale_grid(rows, cols, blk_r, blk_c)
     if wdt == DSV4_WFP4:
@@ -66,6 +68,8 @@ def scale_count(wdt, rows, cols, blk_r, blk_c):
 
 
 def weight_bytes(wdt, rows, cols):
+    if wdt == DSV4_WBF16:
+        return 2 * rows * cols
     return rows * (cols // 2) if wdt == DSV4_WFP4 else rows * cols
 
 
@@ -91,6 +95,8 @@ class Oracle(_Lib):
         for n in ("orc_fp8_double", "orc_fp4_double"):
             getattr(L, n).restype = None
             getattr(L, n).argtypes = [_P, _P, _P, _P, _I, _I, _I, _I]
+        L.orc_bf16_n.restype = None
+        L.orc_bf16_n.argtypes = [_P, _P, _P, _I, _I, _I]
         L.orc_mmq_n.restype = _I; L.orc_mmq_n.argtypes = [_P, _P, C.POINTER(QMat), _I]
         L.orc_swiglu.restype = None; L.orc_swiglu.argtypes = [_P, _P, _P, _I, _F]
         L.orc_expert_forward.restype = _I
@@ -133,6 +139,14 @@ class Oracle(_Lib):
     def fp8f_n(self, W, S, x, rows, cols, blk_r=128, blk_c=128, nt=1):
         return self._body("orc_fp8f_n", W, S, x, rows, cols, blk_r, blk_c, nt,
                           DSV4_WFP8_F32S, np.float32)
+
+    def bf16_n(self, W, x, rows, cols, nt=1):
+        """W: uint16 bf16 bits [rows][cols]."""
+        _need(W, np.uint16, rows * cols, "W")
+        _need(x, np.float32, nt * cols, "x")
+        y = np.zeros(nt * rows, np.float32)
+        self.lib.orc_bf16_n(_ptr(y), _ptr(x), _ptr(W), cols, rows, nt)
+        return y
 
     def fp4_n(self, W, S, x, rows, cols, blk_r=1, blk_c=32, nt=1):
         return self._body("orc_fp4_n", W, S, x, rows, cols, blk_r, blk_c, nt,
@@ -259,6 +273,14 @@ class Reference(_Lib):
         L.dsv4_expert_forward.argtypes = [_P, _P, C.POINTER(ExpertW), _P, _P, _P, _I, _F]
         L.dsv4_matmul_fp8_f32.restype = None
         L.dsv4_matmul_fp8_f32.argtypes = [_P, _P, _P, _P, _I, _I, _I, _I]
+        L.bf16_n.restype = None
+        L.bf16_n.argtypes = [_P, _P, _P, _I, _I, _I]
+
+    def bf16_n(self, W, x, rows, cols, nt=1):
+        _need(W, np.uint16, rows * cols, "W"); _need(x, np.float32, nt * cols, "x")
+        y = np.zeros(nt * rows, np.float32)
+        self.lib.bf16_n(_ptr(y), _ptr(x), _ptr(W), cols, rows, nt)
+        return y
 
     def fp8_n(self, W, S, x, rows, cols, blk_r=128, blk_c=128, nt=1):
         _need(W, np.uint8, rows * cols, "W"); _need(x, np.float32, nt * cols, "x")
@@ -296,6 +318,13 @@ class HostMat:
     def __init__(self, wdt, W, S, rows, cols, blk_r, blk_c):
         self.wdt, self.rows, self.cols = wdt, rows, cols
         self.blk_r, self.blk_c = blk_r, blk_c
+        if wdt == DSV4_WBF16:
+            # a plain BF16 matrix: uint16 bits, no scales (s = NULL, blk 0)
+            self.W = np.ascontiguousarray(W, np.uint16)
+            _need(self.W, np.uint16, rows * cols, "W")
+            self.S = None
+            self.desc = QMat(_ptr(self.W), None, wdt, rows, cols, 0, 0)
+            return
         self.W = np.ascontiguousarray(W, np.uint8)
         sd = np.float32 if wdt == DSV4_WFP8_F32S else np.uint8
         self.S = np.ascontiguousarray(S, sd)

@@ -132,6 +132,19 @@ def main():
          W2=mats[2].W, S2=mats[2].S, x=x, dims=np.array([inter, hidden]),
          y=R.expert_forward(ex, x, 10.0))
 
+    # BF16 (bf16_n, src/10_compute/dsv4_matmul.c:88-113): 4136 columns = 258
+    # whole 16-column steps + an 8-column tail, nt = 3; bf16 values from
+    # N(0, 0.02) rounded to nearest even, plus +-0, a subnormal and large
+    # magnitudes in row 0.
+    rows, cols, nt = 70, 4136, 3
+    f = (rng.standard_normal(rows * cols) * 0.02).astype(np.float32)
+    u = f.view(np.uint32)
+    Wb = ((u + 0x7FFF + ((u >> 16) & 1)) >> 16).astype(np.uint16)
+    Wb[:6] = [0x0000, 0x8000, 0x0001, 0x7F7F, 0xFF7F, 0x3F80]
+    x = (rng.standard_normal(nt * cols)).astype(np.float32)
+    x[:6] = [1.0, 1.0, 3.0, 1e-30, 1e-30, -2.0]
+    save("bf16", W=Wb, x=x, dims=np.array([rows, cols, nt]), y=R.bf16_n(Wb, x, rows, cols, nt))
+
     with open(os.path.join(HERE, "MANIFEST.json"), "w") as f:
         json.dump({"source": "oracle/_ref/libdsv4ref.so built by oracle/Makefile",
                    "sha256_16": out}, f, indent=1, sort_keys=True)

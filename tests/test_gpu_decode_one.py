@@ -156,11 +156,11 @@ def test_one_launch_host_routed(lib, pkg, oracle, monkeypatch):
 
 def test_one_launch_wait_timeout_then_recovers(lib, pkg, oracle, monkeypatch):
     """The down workgroups' wait forced to give up from the host
-    (DSV4_HIP_DECODE_SPIN=0: one poll, before the gate/up half can be done
-    for the workgroups dispatched first): status bit 3 and NaN rows where
-    the wait gave up, every other row bit-identical to the two-launch form;
-    the gate/up items still publish, so the next call with the default limit
-    is exact."""
+    (DSV4_HIP_DECODE_SPIN=0: every down workgroup gives up without polling,
+    and every kernel still exits normally): status bit 3, and every output
+    row NaN. The hand-off words are reset by the launch's last workgroup
+    whatever the waits did, so the next calls with the default limit are
+    bit-identical to the two-launch form."""
     s = _Setup(pkg, oracle, zlib.crc32(b"one-timeout"), 2048, 4096, 6, 8)
     idx, w, xh = s.draw(5)
     monkeypatch.setenv(ENV, "2")
@@ -168,21 +168,93 @@ def test_one_launch_wait_timeout_then_recovers(lib, pkg, oracle, monkeypatch):
     torch.cuda.synchronize()
     want = bits(ref.cpu().numpy())
     monkeypatch.delenv(ENV, raising=False)
-    lib.status()
+    assert lib.status() == 0
     monkeypatch.setenv("DSV4_HIP_DECODE_SPIN", "0")
     o, _ = s.run(lib, idx, w, xh)
     torch.cuda.synchronize()
-    st = lib.status()
-    got = o.cpu().numpy()
-    nan = np.isnan(got)
-    if st & 8:
-        assert nan.any()
-        assert np.array_equal(bits(got[~nan]), want[~nan])
-    else:
-        assert st == 0 and np.array_equal(bits(got), want)
-    assert st & ~8 == 0
+    assert lib.status() == 8
+    assert np.isnan(o.cpu().numpy()).all()
     monkeypatch.delenv("DSV4_HIP_DECODE_SPIN")
-    o, _ = s.run(lib, idx, w, xh)
-    torch.cuda.synchronize()
+    for _ in range(3):
+        o, _ = s.run(lib, idx, w, xh)
+        torch.cuda.synchronize()
+        assert lib.status() == 0
+        assert np.array_equal(bits(o.cpu().numpy()), want)
+
+
+def test_one_launch_timeout_through_host_entry_returns_minus1(lib, pkg, oracle, monkeypatch):
+    """The host-pointer decode MoE reads its status word after the sync: a
+    wait that gave up makes the call -1 (its output is NaN), and the next call
+    is 0 and exact."""
+    rng = np.random.default_rng(88)
+    from test_gpu_decode import make_fp4_expert
+    mats, ex, hx = [], [], []
+    for _ in range(3):
+        e, he, m = make_fp4_expert(lib, pkg, oracle, rng)
+        ex.append(e)
+        hx.append(he)
+        mats += m
+    w = np.array([0.5, 0.3, 0.2], np.float32)
+    x = bf16_x(9, 4096)
+    monkeypatch.setenv("DSV4_HIP_DECODE_SPIN", "0")
+    with pytest.raises(pkg.Dsv4Error, match="timed out"):
+        lib.moe_decode(ex, w, x, None, 10.0)
+    monkeypatch.delenv("DSV4_HIP_DECODE_SPIN")
+    got = lib.moe_decode(ex, w, x, None, 10.0)
+    acc = np.stack([oracle.expert_forward(h, x, 10.0) for h in hx])
+    check_close(got, oracle.moe_combine(acc, w))
     assert lib.status() == 0
-    assert np.array_equal(bits(o.cpu().numpy()), want)
+    for m in mats:
+        m.drop()
+
+
+@pytest.mark.parametrize("shared", [False, True])
+def test_one_launch_graph_replays(lib, pkg, oracle, monkeypatch, shared):
+    """One device-routed decode MoE call captured in a HIP graph (through
+    torch's graph capture, on the capture stream) and replayed three times
+    for each of four routings, with eager copies of the new inputs and
+    synchronisations between replays: every replay bit-identical to the
+    eager two-launch form, status clean; an eager call afterwards too."""
+    s = _Setup(pkg, oracle, zlib.crc32(b"one-graph") + int(shared), 2048, 4096, 6, 16, shared=shared)
+    calls = [s.draw(40 + i) for i in range(4)]
+    monkeypatch.setenv(ENV, "2")
+    want = []
+    for c in calls:
+        o, _ = s.run(lib, *c)
+        torch.cuda.synchronize()
+        want.append(bits(o.cpu().numpy()))
+    monkeypatch.delenv(ENV, raising=False)
+    assert lib.status() == 0
+    idx0, w0, x0 = calls[0]
+    didx = torch.from_numpy(idx0.copy()).to(DEV)
+    dw, dx = dev_f32(w0), dev_f32(x0)
+    out = torch.empty(s.hidden, dtype=torch.float32, device=DEV)
+    st = torch.cuda.Stream()
+
+    def call(stream):
+        lib.moe_decode_dev(out.data_ptr(), dx.data_ptr(), s.tbl.data_ptr(), s.n_exp, didx.data_ptr(),
+                           dw.data_ptr(), s.topk, s.shared, s.hidden, s.inter, 10.0,
+                           stream.cuda_stream)
+
+    with torch.cuda.stream(st):
+        call(st)                     # workspaces exist before the capture
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=st):
+        call(st)
+    torch.cuda.synchronize()
+    for rep in range(3):
+        for i, (idx, w, xh) in enumerate(calls):
+            didx.copy_(torch.from_numpy(idx))
+            dw.copy_(torch.from_numpy(w))
+            dx.copy_(torch.from_numpy(xh))
+            torch.cuda.synchronize()
+            graph.replay()
+            torch.cuda.synchronize()
+            assert np.array_equal(bits(out.cpu().numpy()), want[i]), f"replay {rep} call {i}"
+    assert lib.status() == 0
+    with torch.cuda.stream(st):
+        call(st)
+    torch.cuda.synchronize()
+    assert np.array_equal(bits(out.cpu().numpy()), want[len(calls) - 1])
+    assert lib.status() == 0

@@ -315,3 +315,68 @@ def test_grouped_bad_id_real_width(lib, pkg, oracle):
     ok = [t for t in range(n) if t != 4]
     want = oracle_tokens(oracle, experts, None, x, idx, w, ok)
     assert rel_l2(got[ok], want) <= REL_L2_TOL
+
+
+def _arena_host_expert(bench, arena, e):
+    """Host copy of expert e of the benchmark's arena (cache-slot layout:
+    s1, s2, s3, w1, w2, w3) as an oracle expert."""
+    raw = arena.host_copy(torch, int(e))
+    H, I = bench.HIDDEN, bench.INTER
+    wb = [I * H // 2, H * I // 2, I * H // 2]
+    sb = [I * H // 32, H * I // 32, I * H // 32]
+    off_s = [0, sb[0], sb[0] + sb[1]]
+    off_w = [sum(sb), sum(sb) + wb[0], sum(sb) + wb[0] + wb[1]]
+    shapes = [(I, H), (H, I), (I, H)]
+    mats = [P.HostMat(P.DSV4_WFP4, raw[off_w[i]:off_w[i] + wb[i]], raw[off_s[i]:off_s[i] + sb[i]],
+                      r, c, 1, 32) for i, (r, c) in enumerate(shapes)]
+    return P.HostExpert(mats[0], mats[2], mats[1]), raw
+
+
+def test_grouped_config4_full_workload_sampled(lib, pkg, oracle):
+    """The prefill MoE layer at its full workload, generated exactly as the
+    benchmark generates it: 4096 tokens, top-6 of 256 FP4 experts
+    (2048 x 4096 / 4096 x 2048) under Zipf(1.1), FP8 shared expert with fp32
+    128x128 scales. This runs the 128-token-tile kernels at their real K-loop
+    depth and tile counts. Every output row finite; the tokens of the
+    smallest bucket, 8 tokens of the largest and 32 random tokens within
+    1e-3 of the per-token oracle."""
+    import bench
+    seed = 0xD5EED004
+    n, H, I, topk = 4096, bench.HIDDEN, bench.INTER, bench.TOPK
+    arena = bench.ExpertArena(torch, pkg, lib, bench.N_EXPERTS, seed=seed)
+    shared, keep = bench.make_shared_fp8(torch, pkg, lib, seed * 7)
+    idx, w = bench.zipf_routing(n, seed)
+    xs = torch.empty(n * H, dtype=torch.float32, device=DEV)
+    lib.synth_normal_dev(xs.data_ptr(), xs.numel(), seed ^ 0x55, 1.0, True)
+    di, dw = torch.from_numpy(idx).to(DEV), torch.from_numpy(w).to(DEV)
+    out = torch.empty((n, H), dtype=torch.float32, device=DEV)
+    lib.status()
+    lib.moe_grouped_dev(out.data_ptr(), xs.data_ptr(), n, arena.table.data_ptr(), bench.N_EXPERTS,
+                        di.data_ptr(), dw.data_ptr(), topk, shared, H, I, 10.0)
+    torch.cuda.synchronize()
+    assert lib.status() == 0
+    got = out.cpu().numpy()
+    assert np.isfinite(got).all()
+    counts = np.bincount(idx.reshape(-1), minlength=bench.N_EXPERTS)
+    used = np.nonzero(counts)[0]
+    e_small, e_big = used[np.argmin(counts[used])], int(np.argmax(counts))
+    assert counts[e_big] > 1000            # the 128-token tiles run many tiles of one expert
+    rng = np.random.default_rng(4)
+    toks_small = np.nonzero((idx == e_small).any(1))[0]
+    toks_big = rng.choice(np.nonzero((idx == e_big).any(1))[0], 8, replace=False)
+    sel = sorted(set(toks_small.tolist()) | set(toks_big.tolist()) |
+                 set(rng.choice(n, 32, replace=False).tolist()))
+    host = {}
+    for e in np.unique(idx[sel]):
+        host[int(e)] = _arena_host_expert(bench, arena, e)
+    hm = []
+    for i, (r, c) in enumerate(((I, H), (I, H), (H, I))):
+        hm.append(P.HostMat(P.DSV4_WFP8_F32S, keep[2 * i].cpu().numpy(), keep[2 * i + 1].cpu().numpy(),
+                            r, c, 128, 128))
+    hshared = P.HostExpert(hm[0], hm[1], hm[2])
+    x = xs.view(n, H)[torch.tensor(sel, device=DEV)].cpu().numpy()
+    for j, t in enumerate(sel):
+        acc = np.stack([oracle.expert_forward(host[int(e)][0], x[j], 10.0) for e in idx[t]])
+        want = oracle.moe_combine(acc, w[t], oracle.expert_forward(hshared, x[j], 10.0))
+        e = rel_l2(got[t], want)
+        assert e <= REL_L2_TOL, f"token {t}: rel L2 {e:.3e} (max abs {max_abs(got[t], want):.3e})"

@@ -54,6 +54,34 @@ def test_mmq_dispatch_matches_bodies(oracle):
     m = P.HostMat(P.DSV4_WFP8, g["W"], g["S"], rows, cols, br, bc)
     assert np.array_equal(bits(oracle.mmq_n(m, g["x"], nt)), bits(g["y"]))
     bad = P.HostMat(P.DSV4_WFP8, g["W"], g["S"], rows, cols, br, bc)
-    bad.desc.wdt = 1  # BF16 is outside this path
+    bad.desc.wdt = P.DSV4_WF32  # the reference's dsv4_mmq_n aborts on F32
     with pytest.raises(ValueError):
         oracle.mmq_n(bad, g["x"], 1)
+    g = golden("bf16")
+    rows, cols, nt = (int(v) for v in g["dims"])
+    m = P.HostMat(P.DSV4_WBF16, g["W"], None, rows, cols, 0, 0)
+    assert np.array_equal(bits(oracle.mmq_n(m, g["x"], nt)), bits(g["y"]))
+
+
+def test_bf16_fixture_bitexact(oracle):
+    """bf16_n (src/10_compute/dsv4_matmul.c:88-113): whole 16-column steps,
+    an 8-column tail, nt = 3, +-0 / subnormal / large bf16 codes."""
+    g = golden("bf16")
+    rows, cols, nt = (int(v) for v in g["dims"])
+    y = oracle.bf16_n(g["W"], g["x"], rows, cols, nt)
+    assert np.array_equal(bits(y), bits(g["y"]))
+
+
+def test_bf16_exact_integer_sums(oracle):
+    """With small-integer weights and activations every product and partial
+    sum is exact in double, so the result must be the exact dot product: a
+    dropped, repeated or misplaced column (step, lane or tail) changes it."""
+    rng = np.random.default_rng(7)
+    rows, cols, nt = 5, 16 * 7 + 5, 2
+    wi = rng.integers(-8, 9, rows * cols).astype(np.float32)
+    W = (wi.view(np.uint32) >> 16).astype(np.uint16)        # small integers are exact in bf16
+    x = rng.integers(-16, 17, nt * cols).astype(np.float32)
+    x += np.arange(nt * cols, dtype=np.float32) % 3        # breaks column symmetry
+    y = oracle.bf16_n(W, x, rows, cols, nt)
+    want = (x.reshape(nt, cols).astype(np.float64) @ wi.reshape(rows, cols).T.astype(np.float64))
+    assert np.array_equal(y.reshape(nt, rows), want.astype(np.float32))
