@@ -30,7 +30,7 @@ EXPORTS = (
     "dsv4_hip_register", "dsv4_hip_unregister", "dsv4_hip_device_ptr",
     "dsv4_hip_mmq_n", "dsv4_hip_mmq", "dsv4_hip_mmq_n_dev",
     "dsv4_hip_expert_forward", "dsv4_hip_moe_decode", "dsv4_hip_moe_decode_dev",
-    "dsv4_hip_moe_decode_routed_dev",
+    "dsv4_hip_moe_decode_routed_dev", "dsv4_hip_moe_decode_routed_noalloc_dev",
     "dsv4_hip_moe_grouped", "dsv4_hip_moe_grouped_dev",
     "dsv4_hip_status", "dsv4_hip_gemm_fp8_dev", "dsv4_hip_gemm_fp8q_dev",
     "dsv4_hip_dequant_dev", "dsv4_hip_quant_fp8_blk128_dev",
@@ -101,10 +101,10 @@ class Lib:
         L.dsv4_hip_moe_decode_dev.restype = _I
         L.dsv4_hip_moe_decode_dev.argtypes = [_P, _P, _P, _I, _P, _P, _I,
                                               C.POINTER(ExpertW), _I, _I, _F, _P]
-        L.dsv4_hip_moe_decode_routed_dev.restype = _I
-        L.dsv4_hip_moe_decode_routed_dev.argtypes = [_P, _P, C.POINTER(ExpertW), _I,
-                                                     C.POINTER(_I), C.POINTER(_F), _I,
-                                                     C.POINTER(ExpertW), _I, _I, _F, _P]
+        for n in ("dsv4_hip_moe_decode_routed_dev", "dsv4_hip_moe_decode_routed_noalloc_dev"):
+            getattr(L, n).restype = _I
+            getattr(L, n).argtypes = [_P, _P, C.POINTER(ExpertW), _I, C.POINTER(_I),
+                                      C.POINTER(_F), _I, C.POINTER(ExpertW), _I, _I, _F, _P]
         L.dsv4_hip_moe_grouped.restype = _I
         L.dsv4_hip_moe_grouped.argtypes = [_P, _P, _I, _P, _P, _I, C.POINTER(ExpertW), _I,
                                            C.POINTER(ExpertW), _F]
@@ -240,6 +240,17 @@ class Lib:
                                                            ia, wa, topk, sp, hidden, inter,
                                                            float(limit), stream),
                    "dsv4_hip_moe_decode_routed_dev")
+
+    def moe_decode_routed_noalloc_dev_rc(self, out_ptr, x_ptr, experts, idx, w, topk,
+                                         shared: ExpertW | None, hidden, inter, limit,
+                                         stream=None) -> int:
+        """The allocation-free twin; returns the C return code."""
+        sp = C.pointer(shared) if shared is not None else None
+        ia = (_I * topk)(*[int(i) for i in idx[:topk]])
+        wa = (_F * topk)(*[float(v) for v in w[:topk]])
+        return self.lib.dsv4_hip_moe_decode_routed_noalloc_dev(out_ptr, x_ptr, experts, len(experts),
+                                                               ia, wa, topk, sp, hidden, inter,
+                                                               float(limit), stream)
 
     def moe_grouped_dev(self, out_ptr, x_ptr, n, table_ptr, n_experts, idx_ptr, w_ptr, topk,
                         shared: ExpertW | None, hidden, inter, limit, stream=None):

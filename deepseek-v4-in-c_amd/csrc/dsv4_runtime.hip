@@ -84,6 +84,19 @@ struct State {
 
 constexpr int HOST_WORD = 32;            /* the host calls' word, on its own 128-byte line */
 
+/* Device scratch of dsv4_hip_moe_decode_routed_noalloc_dev, the entry point
+ * for callers that cannot allocate: the one-launch hand-off words (zero
+ * between launches), the mid rows, the mid split tables and the shared
+ * expert's output of one decode MoE call with topk <= 8, inter <= 2048 and
+ * hidden <= 4096 (164,352 bytes at those maxima). Each GPU holds its own
+ * copy until the process ends. Host code uses only the device address that
+ * hipGetSymbolAddress returns for it (scratch_ptr, filled at init), never
+ * this name. */
+constexpr size_t SCRATCH_BYTES = 164352;
+__device__ __align__(256) uint8_t scratch[SCRATCH_BYTES];
+constexpr int MAX_DEVICES = 64;
+void *scratch_ptr_of[MAX_DEVICES];       /* device address of `scratch` per device */
+
 State g;
 thread_local std::string g_err;
 
@@ -512,6 +525,19 @@ int dsv4_hip_init(int device)
     if (hipMalloc((void **)&g.pub, ONE_PUB_BYTES) != hipSuccess) return fail("counter alloc failed");
     if (hipMemset(g.pub, 0, ONE_PUB_BYTES) != hipSuccess) return fail("counter clear failed");
     g.st = g.status;
+    /* this device's copy of the allocation-free entry point's scratch: its
+     * address, once, with the device current; the hand-off words start at
+     * zero and every launch leaves them so */
+    if (device >= MAX_DEVICES) return fail("device %d beyond %d", device, MAX_DEVICES);
+    if (!scratch_ptr_of[device]) {
+        void *p = nullptr;
+        const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess || !p)
+            return fail("scratch address lookup failed: %s", hipGetErrorString(e));
+        if (hipMemset(p, 0, ONE_PUB_BYTES) != hipSuccess) return fail("scratch clear failed");
+        if (hipDeviceSynchronize() != hipSuccess) return fail("scratch clear failed");
+        scratch_ptr_of[device] = p;
+    }
 
     g.device = device;
     g.ready = 1;
@@ -778,6 +804,41 @@ int dsv4_hip_moe_decode_dev(float *out, const float *x, const DSV4ExpertW *exper
                        hidden, inter, x, out, limit, (hipStream_t)stream);
 }
 
+/* Checks of the host-routed decode entry points: the topk descriptors and
+ * weights picked by the host routing ids, and the shared expert's format. */
+int routed_checks(const char *what, const float *out, const float *x, const DSV4ExpertW *experts,
+                  int n_experts, const int *idx, const float *w, int topk,
+                  const DSV4ExpertW *shared, int hidden, int inter, DSV4ExpertW *routed,
+                  float *wv, int *sfmt, int *sinter)
+{
+    if (!out || !x || !experts || !idx || !w) return fail("%s: NULL pointer", what);
+    if (topk < 1 || topk > MX_ROUTED_MAX)
+        return fail("%s: topk %d outside 1..%d", what, topk, MX_ROUTED_MAX);
+    if (n_experts < 1) return fail("%s: no experts", what);
+    if (!aligned16(x)) return fail("%s: x must be 16-byte aligned", what);
+    for (int k = 0; k < topk; k++) {
+        const int id = idx[k];
+        if (id < 0 || id >= n_experts)
+            return fail("%s: routing id %d of slot %d outside 0..%d", what, id, k, n_experts - 1);
+        int f, ei, eh;
+        if (expert_geometry(&experts[id], &f, &ei, &eh, what)) return -1;
+        if (f != FMT_FP4_E8M0 || ei != inter || eh != hidden)
+            return fail("%s: expert %d is not FP4 [%d x %d]", what, id, inter, hidden);
+        routed[k] = experts[id];
+        wv[k] = w[k];
+    }
+    *sfmt = -1;
+    *sinter = 0;
+    if (shared) {
+        int sh;
+        if (expert_geometry(shared, sfmt, sinter, &sh, what)) return -1;
+        if (sh != hidden) return fail("%s: shared hidden %d != %d", what, sh, hidden);
+        if (!aligned16(shared->w1.w) || !aligned16(shared->w3.w) || !aligned16(shared->w2.w))
+            return fail("%s: shared weights must be 16-byte aligned", what);
+    }
+    return 0;
+}
+
 int dsv4_hip_moe_decode_routed_dev(float *out, const float *x, const DSV4ExpertW *experts,
                                    int n_experts, const int *idx, const float *w, int topk,
                                    const DSV4ExpertW *shared, int hidden, int inter,
@@ -787,35 +848,57 @@ int dsv4_hip_moe_decode_routed_dev(float *out, const float *x, const DSV4ExpertW
     Range rg("dsv4_hip_moe_decode_routed_dev");
     if (usable()) return -1;
     dev_call();
-    if (!out || !x || !experts || !idx || !w) return fail("moe_decode_routed_dev: NULL pointer");
-    if (topk < 1 || topk > MX_ROUTED_MAX)
-        return fail("moe_decode_routed_dev: topk %d outside 1..%d", topk, MX_ROUTED_MAX);
-    if (n_experts < 1) return fail("moe_decode_routed_dev: no experts");
-    if (!aligned16(x)) return fail("moe_decode_routed_dev: x must be 16-byte aligned");
     DSV4ExpertW routed[MX_ROUTED_MAX];
     float wv[MX_ROUTED_MAX];
-    for (int k = 0; k < topk; k++) {
-        const int id = idx[k];
-        if (id < 0 || id >= n_experts)
-            return fail("moe_decode_routed_dev: routing id %d of slot %d outside 0..%d", id, k,
-                        n_experts - 1);
-        int f, ei, eh;
-        if (expert_geometry(&experts[id], &f, &ei, &eh, "moe_decode_routed_dev expert")) return -1;
-        if (f != FMT_FP4_E8M0 || ei != inter || eh != hidden)
-            return fail("moe_decode_routed_dev: expert %d is not FP4 [%d x %d]", id, inter, hidden);
-        routed[k] = experts[id];
-        wv[k] = w[k];
-    }
-    int sfmt = -1, sinter = 0;
-    if (shared) {
-        int sh;
-        if (expert_geometry(shared, &sfmt, &sinter, &sh, "moe_decode_routed_dev shared")) return -1;
-        if (sh != hidden) return fail("moe_decode_routed_dev: shared hidden %d != %d", sh, hidden);
-        if (!aligned16(shared->w1.w) || !aligned16(shared->w3.w) || !aligned16(shared->w2.w))
-            return fail("moe_decode_routed_dev: shared weights must be 16-byte aligned");
-    }
+    int sfmt, sinter;
+    if (routed_checks("moe_decode_routed_dev", out, x, experts, n_experts, idx, w, topk, shared,
+                      hidden, inter, routed, wv, &sfmt, &sinter))
+        return -1;
     return enqueue_moe(nullptr, n_experts, nullptr, nullptr, topk, shared, sfmt, sinter, hidden,
                        inter, x, out, limit, (hipStream_t)stream, routed, wv);
+}
+
+int dsv4_hip_moe_decode_routed_noalloc_dev(float *out, const float *x, const DSV4ExpertW *experts,
+                                           int n_experts, const int *idx, const float *w, int topk,
+                                           const DSV4ExpertW *shared, int hidden, int inter,
+                                           float limit, void *stream)
+{
+    std::lock_guard<std::mutex> lk(g.mu);
+    Range rg("dsv4_hip_moe_decode_routed_noalloc_dev");
+    if (usable()) return -1;
+    dev_call();
+    const char *what = "moe_decode_routed_noalloc_dev";
+    uint8_t *base = (uint8_t *)scratch_ptr_of[g.device];
+    if (!base) return fail("%s: the device scratch is not mapped", what);
+    DSV4ExpertW routed[MX_ROUTED_MAX];
+    float wv[MX_ROUTED_MAX];
+    int sfmt, sinter;
+    if (routed_checks(what, out, x, experts, n_experts, idx, w, topk, shared, hidden, inter, routed,
+                      wv, &sfmt, &sinter))
+        return -1;
+    if (inter <= 0 || inter % 128 || inter > 2048 || hidden <= 0 || hidden % 128 || hidden > 4096 ||
+        (shared && sinter > 2048))
+        return fail("%s: the device scratch holds inter <= 2048 and hidden <= 4096 in multiples "
+                    "of 128 (shared inter <= 2048); got inter %d, hidden %d, shared inter %d",
+                    what, inter, hidden, sinter);
+    /* layout: hand-off words, mid rows (routed then shared), split tables,
+     * shared output; each part 256-byte aligned */
+    auto up = [](size_t b) { return (b + 255) & ~(size_t)255; };
+    const size_t o_mid = up(ONE_PUB_BYTES);
+    const size_t o_split = o_mid + up(((size_t)topk * moe_mid_ld(inter) +
+                                       (shared ? moe_mid_ld(sinter) : 0)) * 4);
+    const size_t o_ys = o_split + up((size_t)topk * mx_split_bytes(inter));
+    const size_t need = o_ys + (shared ? (size_t)hidden * 4 : 0);
+    if (need > SCRATCH_BYTES)
+        return fail("%s: needs %zu bytes of device scratch, the maximum is %zu", what, need,
+                    (size_t)SCRATCH_BYTES);
+    MoeWs ws;
+    ws.pub = (unsigned *)base;
+    ws.mid = (float *)(base + o_mid);
+    ws.msplit = base + o_split;
+    ws.ys = (float *)(base + o_ys);
+    return enqueue_moe(nullptr, n_experts, nullptr, nullptr, topk, shared, sfmt, sinter, hidden,
+                       inter, x, out, limit, (hipStream_t)stream, routed, wv, &ws);
 }
 
 /* Shared checks of the FP8 GEMM entry points; returns the weight format. */

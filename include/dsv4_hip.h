@@ -164,6 +164,23 @@ int  dsv4_hip_moe_decode_routed_dev(float *out, const float *x,
                                     const DSV4ExpertW *shared, int hidden, int inter,
                                     float limit, void *stream);
 
+/* Allocation-free form of dsv4_hip_moe_decode_routed_dev. No counterpart in
+ * the reference: it exists for callers that cannot allocate device memory
+ * (code under HIP graph capture, tight serving loops, harnesses that forbid
+ * allocation). Same arguments, kernels and results bit for bit; every
+ * intermediate (mid rows, mid split tables, the shared expert's output, the
+ * one-launch hand-off words) lives in a file-scope device array of 164,352
+ * bytes that each GPU holds until the process ends, mapped by
+ * dsv4_hip_init. It calls no allocating routine. Limits: topk <= 8, inter
+ * <= 2048, hidden <= 4096 (multiples of 128), shared inter <= 2048; larger
+ * calls return -1 with the reason. All calls on one GPU share the array:
+ * calls that overlap on that GPU (two streams at once) race. */
+int  dsv4_hip_moe_decode_routed_noalloc_dev(float *out, const float *x,
+                                            const DSV4ExpertW *experts, int n_experts,
+                                            const int *idx, const float *w, int topk,
+                                            const DSV4ExpertW *shared, int hidden, int inter,
+                                            float limit, void *stream);
+
 /* ------------------------------------- grouped MoE (a13-a15, a18) ---------
  * For n tokens (batched decode or a prefill block):
  *   out[t] = sum_{k in 0..topk-1, in k order} w[t][k] * expert_{idx[t][k]}(x[t])
