@@ -302,11 +302,21 @@ def bench_grouped(args, torch, pkg, lib, stream, sp, K, W, cfg):
     out = torch.empty(n * HIDDEN, dtype=torch.float32, device=dev)
     torch.cuda.synchronize()
 
-    def step(i):
+    # config 4 runs the routed experts on the block-scaled MFMA (FP4 weights x
+    # MXFP8 tokens); config 2 (and config 4 with --exact) the exact fp16 path
+    mx = cfg == 4 and not args.exact
+
+    def call(fn, i):
         j = i % nsets
-        lib.moe_grouped_dev(out.data_ptr(), xs.data_ptr() + 4 * HIDDEN * n * j, n,
-                            arena.table.data_ptr(), N_EXPERTS, idx.data_ptr() + 4 * TOPK * n * j,
-                            wts.data_ptr() + 4 * TOPK * n * j, TOPK, shared, HIDDEN, INTER, 10.0, sp)
+        fn(out.data_ptr(), xs.data_ptr() + 4 * HIDDEN * n * j, n,
+           arena.table.data_ptr(), N_EXPERTS, idx.data_ptr() + 4 * TOPK * n * j,
+           wts.data_ptr() + 4 * TOPK * n * j, TOPK, shared, HIDDEN, INTER, 10.0, sp)
+
+    def step(i):
+        call(lib.moe_grouped_mx_dev if mx else lib.moe_grouped_dev, i)
+
+    def step_other(i):
+        call(lib.moe_grouped_dev if mx else lib.moe_grouped_mx_dev, i)
 
     def step_bytes(j):
         d = len(np.unique(idx_h[n * j:n * (j + 1)]))
@@ -328,6 +338,16 @@ def bench_grouped(args, torch, pkg, lib, stream, sp, K, W, cfg):
     wall = time.perf_counter() - t0
     t_step = e0.elapsed_time(e1) * 1e-3 / K
     t_launch = time_events(torch, stream, lambda i: step(W + i), K)
+    other = None
+    if cfg == 4:
+        # the other precision path of the same call, timed the same way
+        for i in range(W):
+            step_other(i)
+        t_other = time_events(torch, stream, lambda i: step_other(W + i), K)
+        other = {"entry": "dsv4_hip_moe_grouped_dev" if mx else "dsv4_hip_moe_grouped_mx_dev",
+                 "path": "exact: fp16 MFMA on exactly decoded weights" if mx
+                 else "block-scaled MFMA, MXFP8 tokens",
+                 "launch_us": round(t_other * 1e6, 3)}
     assert lib.status() == 0
     bytes_avg = float(np.mean([step_bytes((W + i) % nsets) for i in range(K)]))
     d_avg = (bytes_avg - SHARED_BYTES - n * HIDDEN * 6) / EXPERT_BYTES
@@ -342,7 +362,9 @@ def bench_grouped(args, torch, pkg, lib, stream, sp, K, W, cfg):
         "metric": "quant matvec HBM GB/s (% peak); prefill FP4/FP8 GEMM TFLOP/s (% MFMA peak)",
         "n_gpus": 1, "steps": K, "warmup": W, "ms_per_step": round(t_step * 1e3, 5),
         "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
-        "dtype": "fp16 MFMA on exactly decoded FP4 (routed) / FP8 (shared) weights, fp32 accumulate",
+        "dtype": ("fp4 e2m1 weights x mxfp8 e4m3 tokens and mid on block-scaled MFMA (routed), fp16 "
+                  "MFMA on exactly decoded FP8 (shared), fp32 accumulate") if mx else
+                 "fp16 MFMA on exactly decoded FP4 (routed) / FP8 (shared) weights, fp32 accumulate",
         "data": "synthetic (seeded N(0,0.02) experts, bf16 N(0,1) tokens, Zipf(1.1) top-6 routing), "
                 "random-init",
         "tokens_per_s": round(n / t_step, 1),
@@ -368,13 +390,16 @@ def bench_grouped(args, torch, pkg, lib, stream, sp, K, W, cfg):
     else:
         value = flops_step / t_step / 1e12
         achieved = flops_step / t_launch / 1e12
-        # composite bound: each distinct expert at max(bytes / HBM, flops / fp16 peak)
+        # composite bound: each distinct expert (and the shared one) at
+        # max(bytes / HBM, flops / MFMA peak); the FP4 x FP8 and FP8 x FP8
+        # block-scaled MFMA both issue at the FP8 rate on gfx950
+        peak = FP8_PEAK_TFLOPS if mx else FP16_PEAK_TFLOPS
         j = (W) % nsets
         cnt = np.bincount(idx_h[n * j:n * (j + 1)].reshape(-1), minlength=N_EXPERTS)
         t_roof = sum(max(EXPERT_BYTES / (HBM_PEAK_GBS * 1e9),
-                         2.0 * c * 3 * INTER * HIDDEN / (FP16_PEAK_TFLOPS * 1e12)) for c in cnt if c)
+                         2.0 * c * 3 * INTER * HIDDEN / (FP8_PEAK_TFLOPS * 1e12)) for c in cnt if c)
         t_roof += max(SHARED_BYTES / (HBM_PEAK_GBS * 1e9),
-                      2.0 * n * 3 * INTER * HIDDEN / (FP16_PEAK_TFLOPS * 1e12))
+                      2.0 * n * 3 * INTER * HIDDEN / (FP8_PEAK_TFLOPS * 1e12))
         res.update({
             "value": round(value, 2), "unit": "TFLOP/s",
             "config": {"workload": "prefill MoE layer: 4096 tokens x top-6 of 256 FP4 experts "
@@ -382,14 +407,18 @@ def bench_grouped(args, torch, pkg, lib, stream, sp, K, W, cfg):
                                    "SwiGLU, combine",
                        "tokens_per_step": n, "distinct_experts_avg": round(d_avg, 1),
                        "parallelism": "single GPU"},
-            "roofline": {"bound": "mfma", "achieved": round(achieved, 2), "peak": FP16_PEAK_TFLOPS,
-                         "unit": "TFLOP/s", "frac": round(achieved / FP16_PEAK_TFLOPS, 4),
+            "roofline": {"bound": "mfma", "achieved": round(achieved, 2), "peak": peak,
+                         "unit": "TFLOP/s", "frac": round(achieved / peak, 4),
                          "traffic": traffic_for(cfg),
-                         "kernel": "moe_grouped_dev call (route, fp16 convert, grouped gate/up, "
-                                   "grouped down, shared gate/up + down, combine)",
+                         "kernel": ("moe_grouped_mx_dev call (route, MXFP8 quantize, block-scaled "
+                                    "grouped gate/up, grouped down, shared gate/up + down on fp16 "
+                                    "MFMA, combine)") if mx else
+                                   ("moe_grouped_dev call (route, fp16 convert, grouped gate/up, "
+                                    "grouped down, shared gate/up + down, combine)"),
                          "flops_per_launch": flops_step, "launch_us": round(t_launch * 1e6, 3),
                          "composite_t_roof_us": round(t_roof * 1e6, 1),
                          "composite_frac": round(t_roof / t_launch, 4)},
+            "other_path": other,
         })
     return res
 
@@ -530,6 +559,9 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--cpu-threads", type=int, default=0)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--exact", action="store_true",
+                    help="config 4: time the exact fp16-MFMA grouped path instead of the "
+                         "block-scaled one")
     ap.add_argument("--copy-calib", action="store_true",
                     help="run only a plain 256 MiB device copy (the HBM-counter calibration "
                          "kernel for rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE)")

@@ -31,11 +31,12 @@ EXPORTS = (
     "dsv4_hip_mmq_n", "dsv4_hip_mmq", "dsv4_hip_mmq_n_dev",
     "dsv4_hip_expert_forward", "dsv4_hip_moe_decode", "dsv4_hip_moe_decode_dev",
     "dsv4_hip_moe_decode_routed_dev", "dsv4_hip_moe_decode_routed_noalloc_dev",
-    "dsv4_hip_moe_grouped", "dsv4_hip_moe_grouped_dev",
+    "dsv4_hip_moe_grouped", "dsv4_hip_moe_grouped_dev", "dsv4_hip_moe_grouped_mx_dev",
     "dsv4_hip_status", "dsv4_hip_gemm_fp8_dev", "dsv4_hip_gemm_fp8q_dev",
     "dsv4_hip_dequant_dev", "dsv4_hip_quant_fp8_blk128_dev",
     "dsv4_hip_quant_fp4_mx_dev", "dsv4_hip_quant_act_fp8_1x128_dev",
     "dsv4_hip_quant_act_mxfp8_dev", "dsv4_hip_synth_normal_dev", "dsv4_hip_moe_route_dev",
+    "dsv4_hip_moe_grouped_mx_mid_dev",
 )
 # the reference-named C mirror (host/dsv4_compute_hip.c)
 MIRROR_EXPORTS = ("dsv4_mmq_n", "dsv4_mmq", "dsv4_expert_forward")
@@ -108,9 +109,10 @@ class Lib:
         L.dsv4_hip_moe_grouped.restype = _I
         L.dsv4_hip_moe_grouped.argtypes = [_P, _P, _I, _P, _P, _I, C.POINTER(ExpertW), _I,
                                            C.POINTER(ExpertW), _F]
-        L.dsv4_hip_moe_grouped_dev.restype = _I
-        L.dsv4_hip_moe_grouped_dev.argtypes = [_P, _P, _I, _P, _I, _P, _P, _I,
-                                               C.POINTER(ExpertW), _I, _I, _F, _P]
+        for n in ("dsv4_hip_moe_grouped_dev", "dsv4_hip_moe_grouped_mx_dev"):
+            getattr(L, n).restype = _I
+            getattr(L, n).argtypes = [_P, _P, _I, _P, _I, _P, _P, _I, C.POINTER(ExpertW), _I, _I,
+                                      _F, _P]
         L.dsv4_hip_status.restype = _I; L.dsv4_hip_status.argtypes = [C.POINTER(C.c_uint)]
         L.dsv4_hip_gemm_fp8_dev.restype = _I
         L.dsv4_hip_gemm_fp8_dev.argtypes = [_P, _I, _P, _I, _I, C.POINTER(QMat), _P]
@@ -126,6 +128,9 @@ class Lib:
         L.dsv4_hip_synth_normal_dev.argtypes = [_P, C.c_size_t, C.c_uint64, _F, _I, _P]
         L.dsv4_hip_moe_route_dev.restype = _I
         L.dsv4_hip_moe_route_dev.argtypes = [_P, _P, _P, _P, _P, _I, _I, _I, _P]
+        L.dsv4_hip_moe_grouped_mx_mid_dev.restype = _I
+        L.dsv4_hip_moe_grouped_mx_mid_dev.argtypes = [_P, _P, _P, _P, _P, _I, _P, _I, _P, _I, _I, _I,
+                                                      _F, _P]
 
     # ------------------------------------------------------------ basics
     def error(self) -> str:
@@ -259,6 +264,21 @@ class Lib:
                                                      idx_ptr, w_ptr, topk, sp, hidden, inter,
                                                      float(limit), stream),
                    "dsv4_hip_moe_grouped_dev")
+
+    def moe_grouped_mx_dev(self, out_ptr, x_ptr, n, table_ptr, n_experts, idx_ptr, w_ptr, topk,
+                           shared: ExpertW | None, hidden, inter, limit, stream=None):
+        sp = C.pointer(shared) if shared is not None else None
+        self.check(self.lib.dsv4_hip_moe_grouped_mx_dev(out_ptr, x_ptr, n, table_ptr, n_experts,
+                                                        idx_ptr, w_ptr, topk, sp, hidden, inter,
+                                                        float(limit), stream),
+                   "dsv4_hip_moe_grouped_mx_dev")
+
+    def moe_grouped_mx_mid_dev(self, mid_ptr, mids_ptr, row_tok_ptr, row_k_ptr, x_ptr, n, table_ptr,
+                               n_experts, idx_ptr, topk, hidden, inter, limit, stream=None):
+        self.check(self.lib.dsv4_hip_moe_grouped_mx_mid_dev(mid_ptr, mids_ptr, row_tok_ptr, row_k_ptr,
+                                                            x_ptr, n, table_ptr, n_experts, idx_ptr,
+                                                            topk, hidden, inter, float(limit), stream),
+                   "dsv4_hip_moe_grouped_mx_mid_dev")
 
     def gemm_fp8_dev(self, c_ptr, out_bf16, a_ptr, a_bf16, m, desc: QMat, stream=None):
         self.check(self.lib.dsv4_hip_gemm_fp8_dev(c_ptr, int(bool(out_bf16)), a_ptr,

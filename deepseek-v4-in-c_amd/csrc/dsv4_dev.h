@@ -283,6 +283,43 @@ __device__ __forceinline__ float wave_sum(float v)
     return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
 }
 
+/* ------------------------------------------------ MX scale rounding ---- */
+
+/* least e with (frac_lim * 2^exp_lim) * 2^e >= amax, amax > 0 (448 = 0.875 *
+ * 2^9 for e4m3, 6 = 0.75 * 2^3 for e2m1) */
+__device__ __forceinline__ int pow2_ceil_ratio(float amax, float frac_lim, int exp_lim)
+{
+    int e2;
+    const float f = frexpf(amax, &e2);
+    return (f <= frac_lim) ? e2 - exp_lim : e2 - exp_lim + 1;
+}
+
+__device__ __forceinline__ uint32_t e8m0_clamp(int e)
+{
+    int b = 127 + e;
+    b = b < 0 ? 0 : (b > 254 ? 254 : b);
+    return (uint32_t)b;
+}
+
+/* f32 -> e4m3 by the hardware convert (OCP e4m3fn, round to nearest even).
+ * Checked against the software rounding (q_e4m3) over every fp32 bit pattern
+ * on gfx950: identical for |v| < 464, which covers every quotient a MX or
+ * 1x128 quantizer forms (at most 448 (1 + 2^-22)); NaN is mapped explicitly
+ * to the software rule's sign | 0x7F. */
+__device__ __forceinline__ uint32_t hw_e4m3(float v)
+{
+    const uint32_t q = (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(v, 0.0f, 0, false) & 0xFFu;
+    return __builtin_isnan(v) ? (((__float_as_uint(v) >> 24) & 0x80u) | 0x7Fu) : q;
+}
+
+/* E8M0 scale byte of an MXFP8 block whose largest magnitude is amax (NaN
+ * ignored by the caller's max): least 2^e with 448 * 2^e >= amax, clamped to
+ * [0, 254]; 127 for an all-zero block. */
+__device__ __forceinline__ uint32_t mxfp8_scale_byte(float amax)
+{
+    return amax > 0.0f ? e8m0_clamp(pow2_ceil_ratio(amax, 0.875f, 9)) : 127u;
+}
+
 /* The reference's SwiGLU element (src/10_compute/dsv4_ops.c:61-79): up is
  * clamped to [-limit, limit], gate only from above; limit <= 0 disables the
  * clamp; silu(g) = g / (1 + exp(-g)). Products and sums are explicitly

@@ -315,6 +315,28 @@ int grouped_rows_per_tile(int tt);
 hipError_t grouped_launch(int fmt, bool swiglu, int tt, const GroupedArgs &a, long max_tiles,
                           hipStream_t st);
 
+/* Routed FP4 experts on the block-scaled MFMA with MXFP8 activations, over
+ * the buckets of k_moe_route run with grouped_mx_rows_per_tile() rows per
+ * tile. Gate/up (swiglu): B = x8 rows gathered through row_tok, out = mid as
+ * e4m3 [rows][N] with E8M0 out_s [rows][N / 32]; down: B = mid rows, out =
+ * fp32 [rows][N]. K % 128 == 0; N % 128 (gate/up) or % 256 (down) == 0. */
+struct GroupedMxArgs {
+    const DSV4ExpertW *table;
+    int n_experts;
+    const int *grp_off, *tile_pre, *tile_grp;
+    const int *row_tok;       /* B row of each bucket row, NULL = itself  */
+    const uint8_t *B;         /* e4m3 [nrows][K]                          */
+    const uint8_t *BS;        /* E8M0 [nrows][K / 32]                     */
+    int nrows;
+    int K, N;
+    void *out;
+    uint8_t *out_s;
+    float limit;
+    unsigned *status;
+};
+int grouped_mx_rows_per_tile();
+hipError_t grouped_mx_launch(bool swiglu, const GroupedMxArgs &a, long max_tiles, hipStream_t st);
+
 /* out[t] = sum_k w[t][k] * Y[pos[t][k]] (k order) + YS[t] */
 struct CombineArgs {
     float *out;

@@ -167,24 +167,75 @@ __device__ __forceinline__ bool qmat_matches(const DSV4QMat &m, int rows, int co
 
 /* ------------------------------------------------------------ routing --- */
 
+/* Chunks of 1024 pairs whose routing ids a thread holds in registers at
+ * once: their loads are all issued before the first is used, so a pass over
+ * them waits out one memory latency instead of one per chunk. */
+constexpr int ROUTE_BATCH = 32;
+
+__device__ __forceinline__ void route_load(int (&ev)[ROUTE_BATCH], const RouteArgs &a, int c0, int nch,
+                                           int tid)
+{
+#pragma unroll
+    for (int i = 0; i < ROUTE_BATCH; i++) {
+        const int p = (c0 + i) * 1024 + tid;
+        ev[i] = (c0 + i < nch && p < a.npairs) ? a.idx[p] : -1;
+    }
+}
+
+/* The lanes of the wave whose routing id equals this lane's; ids outside
+ * [0, E) (bad ids and pairs past the end) all count as one id of their own:
+ * one ballot per bit of the key id + 1 (E <= 1024, so 11 bits). */
+__device__ __forceinline__ uint64_t same_id_lanes(int e, int E)
+{
+    const unsigned key = (unsigned)e < (unsigned)E ? (unsigned)e + 1u : 0u;
+    uint64_t peers = ~0ull;
+#pragma unroll
+    for (int b = 0; b < 11; b++) {
+        const bool bit = (key >> b) & 1u;
+        const uint64_t m = __ballot(bit);
+        peers &= bit ? m : ~m;
+    }
+    return peers;
+}
+
 __global__ __launch_bounds__(1024) void k_moe_route(RouteArgs a)
 {
     __shared__ int hist[MAX_ROUTE_EXPERTS];
     __shared__ int cur[MAX_ROUTE_EXPERTS];
+    __shared__ int scan_r[MAX_ROUTE_EXPERTS], scan_t[MAX_ROUTE_EXPERTS];
+    __shared__ unsigned short wcnt[16][MAX_ROUTE_EXPERTS];
     const int tid = threadIdx.x;
     const int E = a.n_experts;
-    for (int e = tid; e < E; e += 1024) hist[e] = 0;
+    const int nch = (a.npairs + 1023) / 1024;
+    for (int e = tid; e < MAX_ROUTE_EXPERTS; e += 1024) {
+        hist[e] = 0;
+        for (int w = 0; w < 16; w++) wcnt[w][e] = 0;
+    }
     __syncthreads();
     unsigned bad = 0;
-    for (int p = tid; p < a.npairs; p += 1024) {
-        const int e = a.idx[p];
-        if ((unsigned)e < (unsigned)E) atomicAdd(&hist[e], 1);
-        else bad = ST_BAD_EXPERT_ID;
+    int ev[ROUTE_BATCH];
+    const int lane = tid & 63, wv = tid >> 6;
+    const uint64_t below = lane ? (~0ull >> (64 - lane)) : 0ull;
+    /* bucket sizes: one LDS add per expert and wave (the highest of its
+     * lanes adds their count) rather than one per pair, so a popular
+     * expert's counter is not hammered by every lane */
+    for (int c0 = 0; c0 < nch; c0 += ROUTE_BATCH) {
+        route_load(ev, a, c0, nch, tid);
+#pragma unroll
+        for (int i = 0; i < ROUTE_BATCH; i++) {
+            if (c0 + i >= nch) break;                              /* uniform */
+            const int p = (c0 + i) * 1024 + tid;
+            const uint64_t peers = same_id_lanes(ev[i], E);
+            if ((unsigned)ev[i] < (unsigned)E) {
+                if (__popcll(peers & below) == __popcll(peers) - 1) atomicAdd(&hist[ev[i]], __popcll(peers));
+            } else if (p < a.npairs) {
+                bad = ST_BAD_EXPERT_ID;
+            }
+        }
     }
     __syncthreads();
     /* inclusive scans of the bucket sizes and tile counts (Hillis-Steele,
      * one expert per thread; E <= 1024) */
-    __shared__ int scan_r[MAX_ROUTE_EXPERTS], scan_t[MAX_ROUTE_EXPERTS];
     const int cnt = tid < E ? hist[tid] : 0;
     const int tls = (cnt + a.tile_rows - 1) / a.tile_rows;
     scan_r[tid] = cnt;
@@ -209,46 +260,44 @@ __global__ __launch_bounds__(1024) void k_moe_route(RouteArgs a)
             a.tile_pre[E] = scan_t[tid];
         }
     }
+    __syncthreads();
     /* Rows inside a bucket in pair order (token-major, k-minor), as the
      * reference's counting sort places them: pairs go in chunks of 1024; a
      * pair's row is its bucket's fill before the chunk, plus the pairs of the
      * same expert in lower waves of the chunk, plus those in lower lanes of
      * its own wave. */
-    __shared__ unsigned short wcnt[16][MAX_ROUTE_EXPERTS];
-    for (int e = tid; e < MAX_ROUTE_EXPERTS; e += 1024)
-        for (int w = 0; w < 16; w++) wcnt[w][e] = 0;
-    __syncthreads();
-    const int lane = tid & 63, wv = tid >> 6;
-    const uint64_t below = lane ? (~0ull >> (64 - lane)) : 0ull;
-    for (int c0 = 0; c0 < a.npairs; c0 += 1024) {
-        const int p = c0 + tid;
-        const int e = p < a.npairs ? a.idx[p] : -1;
-        const bool ok = (unsigned)e < (unsigned)E;
-        uint64_t peers = 0;
-        for (int j = 0; j < 64; j++)
-            if (__builtin_amdgcn_readlane(e, j) == e) peers |= 1ull << j;
-        const int rank = __popcll(peers & below);
-        if (ok && rank == __popcll(peers) - 1) wcnt[wv][e] = (unsigned short)(rank + 1);
-        __syncthreads();
-        if (ok) {
-            int r = cur[e] + rank;
-            for (int w = 0; w < wv; w++) r += wcnt[w][e];
-            a.pos[p] = r;
-            a.row_tok[r] = p / a.topk;
-            if (a.row_k) a.row_k[r] = p - (p / a.topk) * a.topk;
-        } else if (p < a.npairs) {
-            a.pos[p] = -1;
-        }
-        __syncthreads();
-        if (tid < E) {
-            int s = 0;
-            for (int w = 0; w < 16; w++) {
-                s += wcnt[w][tid];
-                wcnt[w][tid] = 0;
+    for (int c0 = 0; c0 < nch; c0 += ROUTE_BATCH) {
+        if (nch > ROUTE_BATCH) route_load(ev, a, c0, nch, tid);   /* else still held */
+#pragma unroll
+        for (int i = 0; i < ROUTE_BATCH; i++) {
+            if (c0 + i >= nch) break;                              /* uniform */
+            const int p = (c0 + i) * 1024 + tid;
+            const int e = ev[i];
+            const bool ok = (unsigned)e < (unsigned)E;
+            const uint64_t peers = same_id_lanes(e, E);
+            const int rank = __popcll(peers & below);
+            if (ok && rank == __popcll(peers) - 1) wcnt[wv][e] = (unsigned short)(rank + 1);
+            __syncthreads();
+            if (ok) {
+                int r = cur[e] + rank;
+                for (int w = 0; w < wv; w++) r += wcnt[w][e];
+                a.pos[p] = r;
+                a.row_tok[r] = p / a.topk;
+                if (a.row_k) a.row_k[r] = p - (p / a.topk) * a.topk;
+            } else if (p < a.npairs) {
+                a.pos[p] = -1;
             }
-            cur[tid] += s;
+            __syncthreads();
+            if (tid < E) {
+                int s = 0;
+                for (int w = 0; w < 16; w++) {
+                    s += wcnt[w][tid];
+                    wcnt[w][tid] = 0;
+                }
+                cur[tid] += s;
+            }
+            __syncthreads();
         }
-        __syncthreads();
     }
     if (bad) atomicOr(a.status, bad);
 }

@@ -116,20 +116,6 @@ __device__ __forceinline__ uint32_t q_e2m1(float v)
     return sign | (uint32_t)code;
 }
 
-/* least e with (frac_lim * 2^exp_lim) * 2^e >= amax, amax > 0 */
-__device__ __forceinline__ int pow2_ceil_ratio(float amax, float frac_lim, int exp_lim)
-{
-    int e2;
-    const float f = frexpf(amax, &e2);
-    return (f <= frac_lim) ? e2 - exp_lim : e2 - exp_lim + 1;
-}
-
-__device__ __forceinline__ uint32_t e8m0_clamp(int e)
-{
-    int b = 127 + e;
-    b = b < 0 ? 0 : (b > 254 ? 254 : b);
-    return (uint32_t)b;
-}
 
 /* ---------------------------------------------------- FP4 weight quant --- */
 
@@ -224,16 +210,6 @@ hipError_t quant_fp8_blk128_launch(uint8_t *W, float *S, const float *w,
 
 /* --------------------------------------------- activation quantizers ---- */
 
-/* f32 -> e4m3 by the hardware convert (OCP e4m3fn, round to nearest even).
- * Checked against q_e4m3 over every fp32 bit pattern on gfx950: identical for
- * |v| < 464, which covers every quotient v / s below (|v / s| <= 448 (1 + 2^-22));
- * NaN is mapped explicitly to the software rule's sign | 0x7F. */
-__device__ __forceinline__ uint32_t hw_e4m3(float v)
-{
-    const uint32_t q = (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(v, 0.0f, 0, false) & 0xFFu;
-    return __builtin_isnan(v) ? (((__float_as_uint(v) >> 24) & 0x80u) | 0x7Fu) : q;
-}
-
 /* 16 lanes per 1x128 group, 8 consecutive elements per lane (one 16-byte
  * bf16 load or two fp32 loads, one 8-byte store); a 256-thread block covers
  * 16 groups. s = amax / 448 (1 if the group is all zero), q = e4m3(v / s)
@@ -314,7 +290,7 @@ __global__ __launch_bounds__(256) void k_quant_act_mxfp8(uint8_t *Q, uint8_t *S,
     }
 #pragma unroll
     for (int i = 0; i < 32; i++) amax = fabsf(v[i]) > amax ? fabsf(v[i]) : amax;
-    const uint32_t sb = amax > 0.0f ? e8m0_clamp(pow2_ceil_ratio(amax, 0.875f, 9)) : 127u;
+    const uint32_t sb = mxfp8_scale_byte(amax);
     const int e = (int)sb - 127;
     S[g] = (uint8_t)sb;
     u32x4 o0, o1;

@@ -1049,6 +1049,91 @@ int enqueue_moe_grouped(float *out, const float *x, int n, const DSV4ExpertW *ta
     return 0;
 }
 
+/* The prefill MoE on the block-scaled MFMA: tokens and mid in MXFP8, routed
+ * GEMMs on FP4 x FP8, the shared expert on the exact fp16 path (side
+ * stream), k-order combine. */
+int enqueue_moe_grouped_mx(float *out, const float *x, int n, const DSV4ExpertW *table,
+                           int n_experts, const int *idx, const float *w, int topk,
+                           const DSV4ExpertW *shared, int sfmt, int sinter, int hidden, int inter,
+                           float limit, hipStream_t st)
+{
+    const long P = (long)n * topk;
+    const int trows = grouped_mx_rows_per_tile();
+    if ((size_t)P * inter >= (1u << 31) || (size_t)n * hidden >= (1u << 31) ||
+        (size_t)inter * hidden / 2 >= (1u << 31))
+        return fail("moe_grouped_mx_dev: %ld pairs x %d / %d tokens x %d exceed 31-bit offsets",
+                    P, inter, n, hidden);
+    size_t off = 0;
+    auto take = [&](size_t b) { const size_t o = off; off += (b + 255) & ~(size_t)255; return o; };
+    const long max_tiles = (P + trows - 1) / trows + n_experts;
+    const size_t o_grp = take((size_t)(n_experts + 1) * 4), o_tp = take((size_t)(n_experts + 1) * 4);
+    const size_t o_tg = take((size_t)max_tiles * 4);
+    const size_t o_pos = take((size_t)P * 4), o_row = take((size_t)P * 4);
+    const size_t o_x8 = take((size_t)n * hidden), o_xs = take((size_t)n * hidden / 32);
+    const size_t o_mid = take((size_t)P * inter), o_ms = take((size_t)P * inter / 32);
+    const size_t o_y = take((size_t)P * hidden * 4);
+    size_t o_x16 = 0, o_ex = 0, o_smid = 0, o_ys = 0;
+    if (shared) {
+        o_x16 = take((size_t)n * hidden * 2);
+        o_ex = take((size_t)n * 4);
+        o_smid = take((size_t)n * sinter * 2);
+        o_ys = take((size_t)n * hidden * 4);
+    }
+    HIPCHK(g.moe_ws.need(off), "grouped MoE workspace");
+    uint8_t *ws = (uint8_t *)g.moe_ws.p;
+    int *grp = (int *)(ws + o_grp), *tp = (int *)(ws + o_tp), *tg = (int *)(ws + o_tg);
+    int *pos = (int *)(ws + o_pos), *row = (int *)(ws + o_row);
+    uint8_t *x8 = ws + o_x8, *xs = ws + o_xs, *mid = ws + o_mid, *ms = ws + o_ms;
+    float *y = (float *)(ws + o_y);
+
+    RouteArgs ra;
+    ra.idx = idx; ra.npairs = (int)P; ra.topk = topk; ra.n_experts = n_experts;
+    ra.tile_rows = trows; ra.grp_off = grp; ra.tile_pre = tp; ra.tile_grp = tg; ra.pos = pos;
+    ra.row_tok = row;
+    ra.row_k = nullptr;
+    ra.status = g.st;
+    HIPCHK(moe_route_launch(ra, st), "route launch");
+
+    float *ys = nullptr;
+    if (shared) {
+        /* the shared expert on the side stream: its own fp16 copy of x */
+        HIPCHK(hipEventRecord(g.fork, st), "fork record");
+        HIPCHK(hipStreamWaitEvent(g.side, g.fork, 0), "fork wait");
+        uint16_t *x16 = (uint16_t *)(ws + o_x16), *smid = (uint16_t *)(ws + o_smid);
+        int *ex = (int *)(ws + o_ex);
+        ys = (float *)(ws + o_ys);
+        HIPCHK(to_f16_rows_launch(x16, ex, x, n, hidden, g.side), "shared x fp16 launch");
+        const int stt = n <= 64 ? 1 : 4;
+        const long stiles = (n + grouped_rows_per_tile(stt) - 1) / grouped_rows_per_tile(stt);
+        GroupedArgs sa;
+        memset(&sa, 0, sizeof sa);
+        sa.m1 = shared->w1; sa.m3 = shared->w3; sa.nrows = n; sa.B = x16; sa.bexp = ex;
+        sa.K = hidden; sa.N = sinter; sa.out = smid; sa.limit = limit; sa.status = g.st;
+        HIPCHK(grouped_launch(sfmt, true, stt, sa, stiles, g.side), "shared gate/up launch");
+        sa.m1 = shared->w2; sa.B = smid; sa.bexp = nullptr; sa.K = sinter; sa.N = hidden; sa.out = ys;
+        HIPCHK(grouped_launch(sfmt, false, stt, sa, stiles, g.side), "shared down launch");
+        HIPCHK(hipEventRecord(g.join, g.side), "join record");
+    }
+
+    HIPCHK(quant_act_mxfp8_launch(x8, xs, x, n, hidden, st), "x MXFP8 launch");
+    GroupedMxArgs ga;
+    memset(&ga, 0, sizeof ga);
+    ga.table = table; ga.n_experts = n_experts; ga.grp_off = grp; ga.tile_pre = tp; ga.tile_grp = tg;
+    ga.row_tok = row; ga.B = x8; ga.BS = xs; ga.nrows = n; ga.K = hidden; ga.N = inter;
+    ga.out = mid; ga.out_s = ms; ga.limit = limit; ga.status = g.st;
+    HIPCHK(grouped_mx_launch(true, ga, max_tiles, st), "routed gate/up launch");
+    ga.row_tok = nullptr; ga.B = mid; ga.BS = ms; ga.nrows = (int)P; ga.K = inter; ga.N = hidden;
+    ga.out = y; ga.out_s = nullptr;
+    HIPCHK(grouped_mx_launch(false, ga, max_tiles, st), "routed down launch");
+
+    if (shared) HIPCHK(hipStreamWaitEvent(st, g.join, 0), "join wait");
+    CombineArgs ca;
+    ca.out = out; ca.Y = y; ca.YS = ys; ca.w = w; ca.pos = pos;
+    ca.n = n; ca.topk = topk; ca.hidden = hidden;
+    HIPCHK(moe_combine_launch(ca, st), "combine launch");
+    return 0;
+}
+
 /* Checks shared by both grouped entry points; returns the shared format. */
 int grouped_checks(int n, int topk, int n_experts, int hidden, int inter,
                    const DSV4ExpertW *shared, int *sfmt, int *sinter, const char *what)
@@ -1096,6 +1181,72 @@ int dsv4_hip_moe_grouped_dev(float *out, const float *x, int n, const DSV4Expert
     if (!aligned16(x) || !aligned16(out)) return fail("moe_grouped_dev: x and out must be 16-byte aligned");
     return enqueue_moe_grouped(out, x, n, experts, n_experts, idx, w, topk, shared, sfmt, sinter,
                                hidden, inter, limit, (hipStream_t)stream);
+}
+
+int dsv4_hip_moe_grouped_mx_dev(float *out, const float *x, int n, const DSV4ExpertW *experts,
+                                int n_experts, const int *idx, const float *w, int topk,
+                                const DSV4ExpertW *shared, int hidden, int inter, float limit,
+                                void *stream)
+{
+    std::lock_guard<std::mutex> lk(g.mu);
+    Range rg("dsv4_hip_moe_grouped_mx_dev");
+    if (usable()) return -1;
+    dev_call();
+    if (!out || !x || !experts || !idx || !w) return fail("moe_grouped_mx_dev: NULL pointer");
+    int sfmt, sinter;
+    if (grouped_checks(n, topk, n_experts, hidden, inter, shared, &sfmt, &sinter,
+                       "moe_grouped_mx_dev"))
+        return -1;
+    if (hidden % 256) return fail("moe_grouped_mx_dev: hidden %d is not a multiple of 256", hidden);
+    if (!aligned16(x) || !aligned16(out))
+        return fail("moe_grouped_mx_dev: x and out must be 16-byte aligned");
+    return enqueue_moe_grouped_mx(out, x, n, experts, n_experts, idx, w, topk, shared, sfmt, sinter,
+                                  hidden, inter, limit, (hipStream_t)stream);
+}
+
+int dsv4_hip_moe_grouped_mx_mid_dev(uint8_t *mid, uint8_t *mid_s, int *row_tok, int *row_k,
+                                    const float *x, int n, const DSV4ExpertW *experts,
+                                    int n_experts, const int *idx, int topk, int hidden, int inter,
+                                    float limit, void *stream)
+{
+    std::lock_guard<std::mutex> lk(g.mu);
+    Range rg("dsv4_hip_moe_grouped_mx_mid_dev");
+    if (usable()) return -1;
+    dev_call();
+    if (!mid || !mid_s || !row_tok || !row_k || !x || !experts || !idx)
+        return fail("moe_grouped_mx_mid_dev: NULL pointer");
+    int sfmt, sinter;
+    if (grouped_checks(n, topk, n_experts, hidden, inter, nullptr, &sfmt, &sinter,
+                       "moe_grouped_mx_mid_dev"))
+        return -1;
+    if (!aligned16(x) || ((uintptr_t)mid & 3) || ((uintptr_t)mid_s & 3))
+        return fail("moe_grouped_mx_mid_dev: x 16-byte, mid and mid_s 4-byte aligned");
+    const long P = (long)n * topk;
+    if ((size_t)P * inter >= (1u << 31) || (size_t)n * hidden >= (1u << 31))
+        return fail("moe_grouped_mx_mid_dev: too many pairs or tokens for 31-bit offsets");
+    hipStream_t st = (hipStream_t)stream;
+    const int trows = grouped_mx_rows_per_tile();
+    const long max_tiles = (P + trows - 1) / trows + n_experts;
+    size_t off = 0;
+    auto take = [&](size_t b) { const size_t o = off; off += (b + 255) & ~(size_t)255; return o; };
+    const size_t o_grp = take((size_t)(n_experts + 1) * 4), o_tp = take((size_t)(n_experts + 1) * 4);
+    const size_t o_tg = take((size_t)max_tiles * 4), o_pos = take((size_t)P * 4);
+    const size_t o_x8 = take((size_t)n * hidden), o_xs = take((size_t)n * hidden / 32);
+    HIPCHK(g.moe_ws.need(off), "grouped MoE workspace");
+    uint8_t *ws = (uint8_t *)g.moe_ws.p;
+    RouteArgs ra;
+    ra.idx = idx; ra.npairs = (int)P; ra.topk = topk; ra.n_experts = n_experts; ra.tile_rows = trows;
+    ra.grp_off = (int *)(ws + o_grp); ra.tile_pre = (int *)(ws + o_tp); ra.tile_grp = (int *)(ws + o_tg);
+    ra.pos = (int *)(ws + o_pos); ra.row_tok = row_tok; ra.row_k = row_k; ra.status = g.st;
+    HIPCHK(moe_route_launch(ra, st), "route launch");
+    HIPCHK(quant_act_mxfp8_launch(ws + o_x8, ws + o_xs, x, n, hidden, st), "x MXFP8 launch");
+    GroupedMxArgs ga;
+    memset(&ga, 0, sizeof ga);
+    ga.table = experts; ga.n_experts = n_experts; ga.grp_off = ra.grp_off; ga.tile_pre = ra.tile_pre;
+    ga.tile_grp = ra.tile_grp; ga.row_tok = row_tok; ga.B = ws + o_x8; ga.BS = ws + o_xs; ga.nrows = n;
+    ga.K = hidden; ga.N = inter; ga.out = mid; ga.out_s = mid_s; ga.limit = limit; ga.status = g.st;
+    HIPCHK(grouped_mx_launch(true, ga, max_tiles, st), "routed gate/up launch");
+    return 0;
 }
 
 int dsv4_hip_moe_grouped(float *out, const float *x, int n, const int *topk_idx,

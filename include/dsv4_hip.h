@@ -217,6 +217,24 @@ int  dsv4_hip_moe_grouped_dev(float *out, const float *x, int n,
                               const DSV4ExpertW *shared, int hidden, int inter,
                               float limit, void *stream);
 
+/* The same prefill MoE layer on CDNA4's block-scaled MFMA (replaces the same
+ * reference code as dsv4_hip_moe_grouped_dev; its GPU leg is the Vulkan fused
+ * expert, src/80_prefill/dsv4_prefill_vk_expert.c:45-172). The routed
+ * experts' FP4 weights enter the MFMA as stored, with their E8M0 scales in
+ * the hardware scale operand; the tokens and the SwiGLU output enter as MXFP8
+ * (e4m3 with one E8M0 scale per 32 reduction indices, the rule of
+ * dsv4_hip_quant_act_mxfp8_dev), fp32 accumulation. The shared expert runs on
+ * the exact fp16 path of dsv4_hip_moe_grouped_dev. Numerics: against the
+ * reference fed the same MXFP8-rounded tokens and mid, relative L2 1e-3
+ * (typically ~1e-5); against the reference on the unrounded fp32 tokens the
+ * MXFP8 rounding dominates (a few 1e-2). Same arguments and layout as
+ * dsv4_hip_moe_grouped_dev; hidden must be a multiple of 256. */
+int  dsv4_hip_moe_grouped_mx_dev(float *out, const float *x, int n,
+                                 const DSV4ExpertW *experts, int n_experts,
+                                 const int *idx, const float *w, int topk,
+                                 const DSV4ExpertW *shared, int hidden, int inter,
+                                 float limit, void *stream);
+
 /* ------------------------------------------------ prefill GEMM (a16, a17) --
  * C[m][n] = sum_k A[m][k] * W[n][k] for m < M on CDNA4 FP8 MFMA, replacing the
  * GPU leg of the prefill projection seam, dsv4_prefill_vk_gemm

@@ -57,6 +57,18 @@ int dsv4_hip_quant_act_mxfp8_dev(uint8_t *Q, uint8_t *S, const float *a,
 int dsv4_hip_moe_route_dev(int *ex_off, int *ex_tok, int *ex_k, int *pos, const int *idx,
                            int n, int topk, int n_experts, void *stream);
 
+/* The first half of dsv4_hip_moe_grouped_mx_dev on its own: the permutation,
+ * the tokens' MXFP8 quantization and the routed gate/up GEMMs with SwiGLU,
+ * writing the MXFP8 mid that its down GEMMs read: mid [n * topk][inter] e4m3
+ * and mid_s [n * topk][inter / 32] E8M0, row r belonging to token row_tok[r]
+ * and routing slot row_k[r] (rows bucketed by expert, as
+ * dsv4_hip_moe_route_dev orders them). Device arrays; mid and mid_s 4-byte
+ * aligned, x 16-byte aligned. */
+int dsv4_hip_moe_grouped_mx_mid_dev(uint8_t *mid, uint8_t *mid_s, int *row_tok, int *row_k,
+                                    const float *x, int n, const DSV4ExpertW *experts,
+                                    int n_experts, const int *idx, int topk, int hidden, int inter,
+                                    float limit, void *stream);
+
 /* out[i] = sigma * N(0,1) sample i of stream `seed` (counter-based splitmix64
  * hash -> Box-Muller in double -> fp32), rounded to bf16 when round_bf16. */
 int dsv4_hip_synth_normal_dev(float *out, size_t n, uint64_t seed, float sigma,
