@@ -23,17 +23,32 @@
  *   oracle for this path quantizes the same activations the same way.
  *
  * SCHEDULE
- *   One workgroup of eight waves per (bucket tile of up to 256 token rows,
- *   slab of 256 weight rows: 128 w1 rows and the matching 128 w3 rows, or
- *   256 w2 rows). Wave (wr, wt) owns weight rows 64 wr .. +63 (gate/up: 32
- *   w1 rows and the same 32 w3 rows) times tokens 128 wt .. +127: 4 x 8
- *   MFMA tiles. K advances in 128-wide stages: 256 weight rows x 64 bytes,
- *   their 256 scale dwords, 256 token rows x 128 bytes and their scale
- *   dwords go global -> LDS by buffer loads straight to LDS (1 KiB per wave
- *   instruction), three stages in flight, 16-byte chunks XOR-swizzled; token
- *   rows past the bucket's end read as zeros (an offset beyond the buffer).
- *   Block b = tile * slabs + slab: the same slab of an expert's consecutive
- *   tiles lands on the same XCD, whose L2 then serves the slab's later reads.
+ *   Work item = (bucket tile of up to 256 token rows, slab of 256 weight
+ *   rows: 128 w1 rows and the matching 128 w3 rows, or 256 w2 rows). K
+ *   advances in 128-wide stages. Two kernels split the tiles by size; each
+ *   returns at once from the other's tiles.
+ *
+ *   Thin tiles (at most 64 token rows: under Zipf routing most experts'
+ *   buckets) are bound by streaming the slab's weights, which nothing
+ *   reuses. k_grouped_mx_thin runs four waves per workgroup and two
+ *   workgroups per CU; wave w owns four 16-row weight tiles and loads their
+ *   FP4 bytes and scale dwords global -> VGPR itself, four stages ahead, so
+ *   weights never pass through LDS. Only the tile's tokens, which all four
+ *   waves multiply, are staged in LDS (buffer loads straight to LDS, a
+ *   five-slot ring, one barrier per stage).
+ *
+ *   Fat tiles (65-256 rows) are bound by the MFMA. k_grouped_mx runs eight
+ *   waves: wave (wr, wt) owns weight rows 64 wr .. +63 (gate/up: 32 w1 rows
+ *   and the same 32 w3 rows) times half of the tile's tokens. Weights,
+ *   tokens and both scale sets of a stage go global -> LDS by buffer loads
+ *   straight to LDS (1 KiB per wave instruction), three or four stages in
+ *   flight, 16-byte chunks XOR-swizzled.
+ *
+ *   In both, token rows past the bucket's end read as zeros (an offset
+ *   beyond the buffer). Work item b = tile * slabs + slab: workgroups are
+ *   dealt to the eight XCDs round robin, so the same slab of an expert's
+ *   consecutive tiles lands on one XCD, whose L2 then serves that slab's
+ *   weights to the later tiles.
  *
  * OPERANDS (gfx950, measured): of a 128-k stage, A lane l holds row l % 16,
  * k in [32 (l/16), +32) as 16 bytes (low nibble first); B lane l holds token
@@ -42,8 +57,8 @@
  * block l / 16; accumulator element e of lane l is row 4 (l/16) + e, token
  * l % 16.
  *
- * Bound: HBM (the 13.4 MB of each expert's weights) for small buckets, MFMA
- * for large ones.
+ * Bound: HBM (the 13.4 MB of each expert's weights) for thin tiles, MFMA
+ * for fat ones.
  */
 #include "dsv4_internal.h"
 
@@ -56,12 +71,20 @@ typedef float f4v __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) void lds_void;
 template <int N> struct IC { static constexpr int value = N; };
 
-/* Stage geometry for a tile of TOK token rows: 256 weight rows (64 FP4
- * bytes and one scale dword each), TOK token rows (128 e4m3 bytes and one
- * scale dword each) and a 256-byte pad where waves without a scale load
- * land theirs. The fewer the tokens, the smaller a stage and the more stages
- * in flight: a tile of few tokens streams its weights with nothing to hide
- * the latency behind but more loads. */
+/* f(IC<I>{}) for I = B .. E - 1, in order, each a compile-time constant */
+template <int B, int E, class F>
+__device__ __forceinline__ void static_for(F &&f)
+{
+    if constexpr (B < E) {
+        f(IC<B>{});
+        static_for<B + 1, E>(f);
+    }
+}
+
+/* Stage geometry of the fat kernel for a tile of TOK token rows: 256 weight
+ * rows (64 FP4 bytes and one scale dword each), TOK token rows (128 e4m3
+ * bytes and one scale dword each) and a 256-byte pad where waves without a
+ * scale load land theirs. */
 template <int TOK>
 struct GX {
     static constexpr int KS = 128;                     /* reduction indices per stage */
@@ -72,7 +95,7 @@ struct GX {
     static constexpr int OFF_BS = OFF_B + TOK * KS;
     static constexpr int OFF_PAD = OFF_BS + TOK * 4;
     static constexpr int STAGE = OFF_PAD + 256;
-    static constexpr int NST = TOK == 64 ? 6 : TOK == 128 ? 4 : 3;
+    static constexpr int NST = TOK == 128 ? 4 : 3;
     static constexpr int LDS = NST * STAGE;
     static constexpr int NW = ROWS * WB / 1024 / NWAVE;   /* 16-row weight loads per wave   */
     static constexpr int NB = TOK * KS / 1024 / NWAVE;    /* 8-row token loads per wave     */
@@ -83,8 +106,17 @@ struct GX {
     static_assert(NW * NWAVE * 1024 == ROWS * WB && NB * NWAVE * 1024 == TOK * KS, "load split");
 };
 constexpr int GX_TILE = 256;                           /* token rows per bucket tile */
-constexpr int GX_LDS = GX<64>::LDS > GX<256>::LDS ? (GX<64>::LDS > GX<128>::LDS ? GX<64>::LDS : GX<128>::LDS)
-                                                  : (GX<256>::LDS > GX<128>::LDS ? GX<256>::LDS : GX<128>::LDS);
+constexpr int GX_LDS = GX<256>::LDS > GX<128>::LDS ? GX<256>::LDS : GX<128>::LDS;
+
+/* Thin kernel: tiles of at most TH_TOK rows, TH_D stages in flight. LDS
+ * holds a ring of TH_D + 1 token stages (128 bytes per token) and two
+ * groups of the tokens' scale dwords (TH_G per token and group). */
+constexpr int TH_TOK = 64;
+constexpr int TH_D = 4;                                /* stages in flight             */
+constexpr int TH_G = 4;                                /* stages per scale group       */
+constexpr int TH_B = TH_TOK * 128;                     /* token bytes of a stage       */
+constexpr int TH_LDS = (TH_D + 1) * TH_B + 2 * 1024;   /* token ring + 2 scale groups  */
+constexpr int TH_KQ = 128 * 2 * TH_G;                  /* K granule of the thin kernel */
 
 constexpr uint32_t RSRC_WORD3 = 0x00020000u;      /* raw dword buffer, gfx9 */
 constexpr uint32_t OOB_OFFSET = 0x80000000u;      /* beyond every buffer    */
@@ -100,6 +132,14 @@ __device__ __forceinline__ void bdma16(__amdgpu_buffer_rsrc_t r, uint32_t voff, 
 __device__ __forceinline__ void bdma4(__amdgpu_buffer_rsrc_t r, uint32_t voff, int soff, uint8_t *dst)
 {
     __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_void *)dst, 4, (int)voff, soff, 0, 0);
+}
+
+/* s_waitcnt vmcnt(n), other counters untouched (gfx9 encoding, n < 64) */
+template <int N>
+__device__ __forceinline__ void wait_vm()
+{
+    static_assert(N >= 0 && N < 64, "vmcnt field");
+    __builtin_amdgcn_s_waitcnt(0x0F70 | (N & 15) | ((N >> 4) << 14));
 }
 
 /* LDS slot of logical 16-byte chunk c of staged weight row r / token row t */
@@ -120,10 +160,118 @@ __device__ __forceinline__ f4v mfma_mx(const u32x4 &a, const v8i &b, const f4v &
     return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(av, b, c, 4, 0, 0, sa, 0, sb);
 }
 
+/* B operand of token row t of a staged stage (128 swizzled bytes per row)
+ * and its scale byte for this lane's 32-element block gq */
+__device__ __forceinline__ v8i b_operand(const uint8_t *rows, int t, int gq)
+{
+    const uint8_t *brow = rows + t * 128;
+    const u32x4 lo = *(const u32x4 *)(brow + 16 * bslot(t, gq));
+    const u32x4 hi = *(const u32x4 *)(brow + 16 * bslot(t, 4 + gq));
+    v8i b;
+    b[0] = (int)lo.x; b[1] = (int)lo.y; b[2] = (int)lo.z; b[3] = (int)lo.w;
+    b[4] = (int)hi.x; b[5] = (int)hi.y; b[6] = (int)hi.z; b[7] = (int)hi.w;
+    return b;
+}
+__device__ __forceinline__ int scale_byte(uint32_t dword, int gq) { return (int)((dword >> (8 * gq)) & 0xFFu); }
+
 } // namespace
 
-/* One bucket tile (rows r0 .. r0 + ntok - 1, ntok <= TOK) against the
- * workgroup's 256 weight rows from feature f0. */
+/* Bucket tile and slab of this workgroup's work item; false past the last
+ * tile (tiles run to tile_pre[E]). */
+struct MxItem {
+    int r0, ntok, grp, f0;
+};
+template <int FEAT>
+__device__ __forceinline__ bool mx_item(const GroupedMxArgs &a, MxItem &it)
+{
+    const int nslab = a.N / FEAT;
+    const int tile = blockIdx.x / nslab, slab = blockIdx.x - tile * nslab;
+    const int E = a.n_experts;
+    if (tile >= ld_uniform(a.tile_pre, E)) return false;
+    const int grp = ld_uniform(a.tile_grp, tile);
+    const int go = ld_uniform(a.grp_off, grp), ge = ld_uniform(a.grp_off, grp + 1);
+    it.r0 = go + (tile - ld_uniform(a.tile_pre, grp)) * GX_TILE;
+    it.ntok = min(GX_TILE, ge - it.r0);
+    it.grp = grp;
+    it.f0 = slab * FEAT;
+    return true;
+}
+
+/* A tile whose expert fails the descriptor check: flag it, fill its outputs
+ * with NaN (e4m3 0x7F with a unit scale for mid). */
+template <bool SWIGLU, int FEAT, int NTHR>
+__device__ void mx_fill_bad(const GroupedMxArgs &a, const MxItem &it)
+{
+    if (threadIdx.x == 0) atomicOr(a.status, ST_BAD_DESCRIPTOR);
+    const float nan = __builtin_nanf("");
+    for (int i = threadIdx.x; i < it.ntok * FEAT; i += NTHR) {
+        const size_t o = (size_t)(it.r0 + i / FEAT) * a.N + it.f0 + i % FEAT;
+        if constexpr (SWIGLU) {
+            ((uint8_t *)a.out)[o] = 0x7F;
+            if ((i % FEAT) % 32 == 0) a.out_s[o / 32] = 127;
+        } else {
+            ((float *)a.out)[o] = nan;
+        }
+    }
+}
+
+/* One wave's results. acc[i][u] element e is token row t0 + 16 u + (lane &
+ * 15) of the tile times weight row 4 (lane >> 4) + e of the wave's row tile
+ * i. Gate/up: tiles 0, 1 are w1 rows fw + 16 i and tiles 2, 3 the w3 rows of
+ * the same features; mid = SwiGLU, quantized to MXFP8 with the 32-feature
+ * block fw .. fw + 31 (the wave's whole share of the row, spread over lanes
+ * rr, rr + 16, rr + 32, rr + 48). Down: tile i is output features
+ * fw + 16 i, written as fp32. */
+template <bool SWIGLU, int NU>
+__device__ __forceinline__ void mx_store(const GroupedMxArgs &a, const f4v (&acc)[4][NU], int r0, int ntok,
+                                         int t0, int fw)
+{
+    const int lane = threadIdx.x & 63;
+    const int rr = lane & 15, gq = lane >> 4;
+    const int N = a.N;
+#pragma unroll
+    for (int u = 0; u < NU; u++) {
+        const int t = t0 + 16 * u + rr;
+        const bool live = t < ntok;
+        const size_t row = (size_t)(r0 + (live ? t : 0));
+        if constexpr (SWIGLU) {
+            float m[2][4];
+            float amax = 0.0f;
+#pragma unroll
+            for (int i = 0; i < 2; i++)
+#pragma unroll
+                for (int e = 0; e < 4; e++) {
+                    m[i][e] = dev_swiglu(acc[i][u][e], acc[i + 2][u][e], a.limit);
+                    const float v = __builtin_fabsf(m[i][e]);
+                    amax = v > amax ? v : amax;
+                }
+            amax = fmaxf(amax, __shfl_xor(amax, 16, 64));
+            amax = fmaxf(amax, __shfl_xor(amax, 32, 64));
+            const uint32_t sbyte = mxfp8_scale_byte(amax);
+            const int se = (int)sbyte - 127;
+            if (live) {
+#pragma unroll
+                for (int i = 0; i < 2; i++) {
+                    const uint32_t q = hw_e4m3(ldexpf(m[i][0], -se)) | (hw_e4m3(ldexpf(m[i][1], -se)) << 8) |
+                                       (hw_e4m3(ldexpf(m[i][2], -se)) << 16) |
+                                       (hw_e4m3(ldexpf(m[i][3], -se)) << 24);
+                    *(uint32_t *)((uint8_t *)a.out + row * N + fw + 16 * i + 4 * gq) = q;
+                }
+                if (gq == 0) a.out_s[row * (size_t)(N / 32) + fw / 32] = (uint8_t)sbyte;
+            }
+        } else {
+            if (live) {
+#pragma unroll
+                for (int i = 0; i < 4; i++) *(f4v *)((float *)a.out + row * N + fw + 16 * i + 4 * gq) = acc[i][u];
+            }
+        }
+    }
+}
+
+/* ------------------------------------------------------------------------
+ * Fat tiles: rows r0 .. r0 + ntok - 1 (ntok <= TOK) against the
+ * workgroup's 256 weight rows from feature f0, everything staged in LDS.
+ * ---------------------------------------------------------------------- */
 template <bool SWIGLU, int TOK>
 __device__ __forceinline__ void mx_tile(const GroupedMxArgs &a, const DSV4QMat &m1, const DSV4QMat &m3,
                                         int r0, int ntok, int f0, uint8_t *lds)
@@ -137,12 +285,16 @@ __device__ __forceinline__ void mx_tile(const GroupedMxArgs &a, const DSV4QMat &
     /* ---- load plan: per-lane byte offsets into the buffers ---- */
     const uint32_t rowb = (uint32_t)K / 2, srow = (uint32_t)K / 32;
     const int nst = K / C::KS, last = nst - 1;
-    const __amdgpu_buffer_rsrc_t rw1 = buf_rsrc(m1.w, (uint32_t)N * rowb);
-    const __amdgpu_buffer_rsrc_t rs1 = buf_rsrc(m1.s, (uint32_t)N * srow);
-    const __amdgpu_buffer_rsrc_t rw3 = SWIGLU ? buf_rsrc(m3.w, (uint32_t)N * rowb) : rw1;
-    const __amdgpu_buffer_rsrc_t rs3 = SWIGLU ? buf_rsrc(m3.s, (uint32_t)N * srow) : rs1;
+    /* Waves 0-3 stage w1 rows (or w2 rows 0-127), waves 4-7 w3 rows (or w2
+     * rows 128-255), so each wave needs one weight descriptor. Descriptors
+     * are built from pointers chosen by value: a conditional between two
+     * descriptor variables compiles to a select of their addresses, which
+     * keeps them in scratch memory, and every buffer load then becomes a
+     * readfirstlane loop whose scratch reads wait out all loads in flight. */
+    static_assert(C::NW * 16 * 4 == 128, "waves 0-3 stage weight rows 0-127");
+    const bool w_up = SWIGLU && wave >= 4;
+    const __amdgpu_buffer_rsrc_t rw = buf_rsrc(w_up ? m3.w : m1.w, (uint32_t)N * rowb);
     const __amdgpu_buffer_rsrc_t rb = buf_rsrc(a.B, (uint32_t)a.nrows * (uint32_t)K);
-    const __amdgpu_buffer_rsrc_t rbs = buf_rsrc(a.BS, (uint32_t)a.nrows * srow);
     uint32_t wofs[C::NW];
 #pragma unroll
     for (int i = 0; i < C::NW; i++) {
@@ -168,12 +320,14 @@ __device__ __forceinline__ void mx_tile(const GroupedMxArgs &a, const DSV4QMat &
      * token rows 64 (w - 4) .. +63, the rest a zero load into the pad (the
      * same count of loads in every wave keeps one vmcnt value for all) */
     uint32_t sofs = OOB_OFFSET;
-    bool s_up = false;
     int s_dst = C::OFF_PAD;
+    const void *sbase = a.BS;
+    uint32_t sbytes = (uint32_t)a.nrows * srow;
     if (wave < 4) {
         const int r = 64 * wave + lane;
         const int row = f0 + (SWIGLU ? (r & 127) : r);
-        s_up = SWIGLU && r >= 128;
+        sbase = SWIGLU && wave >= 2 ? m3.s : m1.s;     /* staged rows 128-255 are w3's */
+        sbytes = (uint32_t)N * srow;
         sofs = (uint32_t)row * srow;
         s_dst = C::OFF_WS + 256 * wave;
     } else if (wave < 4 + C::NBS) {
@@ -181,18 +335,15 @@ __device__ __forceinline__ void mx_tile(const GroupedMxArgs &a, const DSV4QMat &
         if (t < ntok) sofs = (uint32_t)(a.row_tok ? a.row_tok[r0 + t] : r0 + t) * srow;
         s_dst = C::OFF_BS + 256 * (wave - 4);
     }
-    s_up = __builtin_amdgcn_readfirstlane((int)s_up) != 0;
+    const __amdgpu_buffer_rsrc_t rsc = buf_rsrc(sbase, sbytes);
     auto issue = [&](int stg, uint8_t *buf) {
 #pragma unroll
-        for (int i = 0; i < C::NW; i++) {
-            const bool up = SWIGLU && (wave * C::NW + i) >= 8;
-            bdma16(up ? rw3 : rw1, wofs[i], stg * C::WB, buf + 1024 * (wave * C::NW + i));
-        }
+        for (int i = 0; i < C::NW; i++)
+            bdma16(rw, wofs[i], stg * C::WB, buf + 1024 * (wave * C::NW + i));
 #pragma unroll
         for (int i = 0; i < C::NB; i++)
             bdma16(rb, bofs[i], stg * C::KS, buf + C::OFF_B + 1024 * (wave * C::NB + i));
-        if (wave < 4) bdma4(s_up ? rs3 : rs1, sofs, stg * 4, buf + s_dst);
-        else bdma4(rbs, sofs, stg * 4, buf + s_dst);
+        bdma4(rsc, sofs, stg * 4, buf + s_dst);
     };
 
     /* ---- this wave's share: 4 row tiles x NTMAX token groups ---- */
@@ -220,8 +371,7 @@ __device__ __forceinline__ void mx_tile(const GroupedMxArgs &a, const DSV4QMat &
             /* this wave's loads of stage st have landed (the NST - 2 later
              * stages may be in flight); the barrier makes that true for the
              * whole workgroup and frees the stage read in iteration st - 1 */
-            __builtin_amdgcn_s_waitcnt(0x0F70 | ((C::NST - 2) * C::VM & 15) |
-                                       ((((C::NST - 2) * C::VM) >> 4) << 14));
+            wait_vm<(C::NST - 2) * C::VM>();
             __builtin_amdgcn_s_barrier();
             asm volatile("" ::: "memory");
             {
@@ -237,18 +387,13 @@ __device__ __forceinline__ void mx_tile(const GroupedMxArgs &a, const DSV4QMat &
                 for (int i = 0; i < 4; i++) {
                     const int r = 16 * blk[i] + rr;
                     aw[i] = *(const u32x4 *)(buf + r * C::WB + 16 * wslot(r, gq));
-                    sa[i] = (int)((*(const uint32_t *)(buf + C::OFF_WS + 4 * r) >> (8 * gq)) & 0xFFu);
+                    sa[i] = scale_byte(*(const uint32_t *)(buf + C::OFF_WS + 4 * r), gq);
                 }
 #pragma unroll
                 for (int u = 0; u < NT; u++) {
                     const int t = HALF * wt + 16 * u + rr;
-                    const uint8_t *brow = buf + C::OFF_B + t * C::KS;
-                    const u32x4 lo = *(const u32x4 *)(brow + 16 * bslot(t, gq));
-                    const u32x4 hi = *(const u32x4 *)(brow + 16 * bslot(t, 4 + gq));
-                    const int sb = (int)((*(const uint32_t *)(buf + C::OFF_BS + 4 * t) >> (8 * gq)) & 0xFFu);
-                    v8i b;
-                    b[0] = (int)lo.x; b[1] = (int)lo.y; b[2] = (int)lo.z; b[3] = (int)lo.w;
-                    b[4] = (int)hi.x; b[5] = (int)hi.y; b[6] = (int)hi.z; b[7] = (int)hi.w;
+                    const v8i b = b_operand(buf + C::OFF_B, t, gq);
+                    const int sb = scale_byte(*(const uint32_t *)(buf + C::OFF_BS + 4 * t), gq);
 #pragma unroll
                     for (int i = 0; i < 4; i++) acc[i][u] = mfma_mx(aw[i], b, acc[i][u], sa[i], sb);
                 }
@@ -260,93 +405,193 @@ __device__ __forceinline__ void mx_tile(const GroupedMxArgs &a, const DSV4QMat &
     if constexpr (C::NTMAX >= 4) { if (ntw == 4) run(IC<4>{}); else if (ntw == 3) run(IC<3>{}); }
     if constexpr (C::NTMAX >= 2) { if (ntw == 2) run(IC<2>{}); else if (ntw == 1) run(IC<1>{}); }
     if (ntw == 0) run(IC<0>{});
-    __builtin_amdgcn_s_waitcnt(0x0F70);     /* trailing repeat loads drain before exit */
+    wait_vm<0>();                           /* trailing repeat loads drain before exit */
 
-#pragma unroll
-    for (int u = 0; u < C::NTMAX; u++) {
-        const int t = HALF * wt + 16 * u + rr;
-        const bool live = t < ntok;
-        const size_t row = (size_t)(r0 + (live ? t : 0));
-        if constexpr (SWIGLU) {
-            /* mid for features f0 + 32 wr + 16 i + 4 gq + e (i = 0, 1) of token
-             * row t; its 32-feature MXFP8 block is this wave's whole share of
-             * the row, spread over the four lanes rr, rr + 16, rr + 32, rr + 48 */
-            float m[2][4];
-            float amax = 0.0f;
-#pragma unroll
-            for (int i = 0; i < 2; i++)
-#pragma unroll
-                for (int e = 0; e < 4; e++) {
-                    m[i][e] = dev_swiglu(acc[i][u][e], acc[i + 2][u][e], a.limit);
-                    const float v = __builtin_fabsf(m[i][e]);
-                    amax = v > amax ? v : amax;
-                }
-            amax = fmaxf(amax, __shfl_xor(amax, 16, 64));
-            amax = fmaxf(amax, __shfl_xor(amax, 32, 64));
-            const uint32_t sbyte = mxfp8_scale_byte(amax);
-            const int se = (int)sbyte - 127;
-            if (live) {
-                const int fb = f0 + 32 * wr;
-#pragma unroll
-                for (int i = 0; i < 2; i++) {
-                    const uint32_t q = hw_e4m3(ldexpf(m[i][0], -se)) | (hw_e4m3(ldexpf(m[i][1], -se)) << 8) |
-                                       (hw_e4m3(ldexpf(m[i][2], -se)) << 16) |
-                                       (hw_e4m3(ldexpf(m[i][3], -se)) << 24);
-                    *(uint32_t *)((uint8_t *)a.out + row * N + fb + 16 * i + 4 * gq) = q;
-                }
-                if (gq == 0) a.out_s[row * (size_t)(N / 32) + fb / 32] = (uint8_t)sbyte;
-            }
-        } else {
-            if (live) {
-#pragma unroll
-                for (int i = 0; i < 4; i++)
-                    *(f4v *)((float *)a.out + row * N + f0 + 16 * blk[i] + 4 * gq) = acc[i][u];
-            }
-        }
-    }
+    mx_store<SWIGLU, C::NTMAX>(a, acc, r0, ntok, HALF * wt, SWIGLU ? f0 + 32 * wr : f0 + 64 * wr);
 }
 
 template <bool SWIGLU>
-__global__ __launch_bounds__(512) void k_grouped_mx(GroupedMxArgs a)
+__global__ __launch_bounds__(512) void k_grouped_mx(GroupedMxArgs a, int thin_rows)
 {
     constexpr int FEAT = SWIGLU ? 128 : 256;           /* output features per workgroup */
     extern __shared__ __align__(16) uint8_t lds[];
-    const int nslab = a.N / FEAT;
-    const int tile = blockIdx.x / nslab, slab = blockIdx.x - tile * nslab;
-    const int E = a.n_experts;
-    if (tile >= ld_uniform(a.tile_pre, E)) return;            /* whole workgroup */
-    const int grp = ld_uniform(a.tile_grp, tile);
-    const int go = ld_uniform(a.grp_off, grp), ge = ld_uniform(a.grp_off, grp + 1);
-    const int r0 = go + (tile - ld_uniform(a.tile_pre, grp)) * GX_TILE;
-    const int ntok = min(GX_TILE, ge - r0);
-    const DSV4ExpertW ex = ld_uniform(a.table, grp);
+    MxItem it;
+    if (!mx_item<FEAT>(a, it) || it.ntok <= thin_rows) return;     /* whole workgroup */
+    const DSV4ExpertW ex = ld_uniform(a.table, it.grp);
     const DSV4QMat m1 = SWIGLU ? ex.w1 : ex.w2, m3 = ex.w3;
-    const int f0 = slab * FEAT;
-    const int K = a.K, N = a.N;
-
-    if (!fp4_matches(m1, N, K) || (SWIGLU && !fp4_matches(m3, N, K))) {
-        if (threadIdx.x == 0) atomicOr(a.status, ST_BAD_DESCRIPTOR);
-        const float nan = __builtin_nanf("");
-        for (int i = threadIdx.x; i < ntok * FEAT; i += 512) {
-            const size_t o = (size_t)(r0 + i / FEAT) * N + f0 + i % FEAT;
-            if constexpr (SWIGLU) {
-                ((uint8_t *)a.out)[o] = 0x7F;                             /* e4m3 NaN */
-                if ((i % FEAT) % 32 == 0) a.out_s[o / 32] = 127;
-            } else {
-                ((float *)a.out)[o] = nan;
-            }
-        }
+    if (!fp4_matches(m1, a.N, a.K) || (SWIGLU && !fp4_matches(m3, a.N, a.K))) {
+        mx_fill_bad<SWIGLU, FEAT, 512>(a, it);
         return;
     }
-    if (ntok <= 64) mx_tile<SWIGLU, 64>(a, m1, m3, r0, ntok, f0, lds);
-    else if (ntok <= 128) mx_tile<SWIGLU, 128>(a, m1, m3, r0, ntok, f0, lds);
-    else mx_tile<SWIGLU, 256>(a, m1, m3, r0, ntok, f0, lds);
+    if (it.ntok <= 128) mx_tile<SWIGLU, 128>(a, m1, m3, it.r0, it.ntok, it.f0, lds);
+    else mx_tile<SWIGLU, 256>(a, m1, m3, it.r0, it.ntok, it.f0, lds);
+}
+
+/* ------------------------------------------------------------------------
+ * Thin tiles: rows r0 .. r0 + ntok - 1, ntok <= 16 NTG <= 64. Wave w owns
+ * row tiles i = 0..3: gate/up w1 rows f0 + 32 w + 16 i (i = 0, 1) and the
+ * w3 rows of the same features (i = 2, 3); down w2 rows f0 + 64 w + 16 i.
+ * Scales move once per group of TH_G stages: a row's 16 scale bytes of a
+ * group are one 16-byte load (lane (rr, gq) then takes byte gq of dword c for
+ * stage c of the group), the tokens' scale dwords one 4-byte-per-lane load
+ * per wave (wave w stages dword w of every token).
+ * ---------------------------------------------------------------------- */
+template <bool SWIGLU, int NTG>
+__device__ __forceinline__ void thin_tile(const GroupedMxArgs &a, const DSV4QMat &m1, const DSV4QMat &m3,
+                                          int r0, int ntok, int f0, uint8_t *lds)
+{
+    constexpr int D = TH_D, G = TH_G, U = 2 * TH_G;
+    static_assert(U % D == 0 && D <= G, "ring depth");
+    constexpr int NBL = (2 * NTG + 3) / 4;           /* 8-token loads per wave and stage */
+    constexpr int VMW = 4 + NBL;                     /* VMEM per wave and stage            */
+    constexpr int VMG = 4 + 1;                       /* + per group: weight and token scales */
+    static_assert((D - 1) * VMW + VMG < 64, "vmcnt range");
+    const int lane = threadIdx.x & 63, wave = wave_in_group();
+    const int rr = lane & 15, gq = lane >> 4;
+    const int K = a.K, N = a.N;
+    const uint32_t rowb = (uint32_t)K / 2, srow = (uint32_t)K / 32;
+    const int nst = K / 128, last = nst - 1, glast = nst / G - 1;
+
+    const __amdgpu_buffer_rsrc_t rw1 = buf_rsrc(m1.w, (uint32_t)N * rowb);
+    const __amdgpu_buffer_rsrc_t rs1 = buf_rsrc(m1.s, (uint32_t)N * srow);
+    const __amdgpu_buffer_rsrc_t rw3 = buf_rsrc(SWIGLU ? m3.w : m1.w, (uint32_t)N * rowb);
+    const __amdgpu_buffer_rsrc_t rs3 = buf_rsrc(SWIGLU ? m3.s : m1.s, (uint32_t)N * srow);
+    const __amdgpu_buffer_rsrc_t rb = buf_rsrc(a.B, (uint32_t)a.nrows * (uint32_t)K);
+    const __amdgpu_buffer_rsrc_t rbs = buf_rsrc(a.BS, (uint32_t)a.nrows * srow);
+
+    /* weights: lane (rr, gq) of tile i reads 16 bytes of row rr, k block gq */
+    uint32_t wo[4], so[4];
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const int row = f0 + (SWIGLU ? 32 * wave + 16 * (i & 1) : 64 * wave + 16 * i) + rr;
+        wo[i] = (uint32_t)row * rowb + 16u * (uint32_t)gq;
+        so[i] = (uint32_t)row * srow;
+    }
+    /* tokens: load q = NBL w + j stages token rows 8 q .. 8 q + 7 */
+    uint32_t bo[NBL];
+#pragma unroll
+    for (int j = 0; j < NBL; j++) {
+        const int q = NBL * wave + j;
+        const int t = 8 * q + lane / 8;
+        bo[j] = OOB_OFFSET;
+        if (t < ntok) bo[j] = (uint32_t)(a.row_tok ? a.row_tok[r0 + t] : r0 + t) * (uint32_t)K +
+                              16u * (uint32_t)bslot(t, lane & 7);
+    }
+    /* token scales: lane t, dword w of the group */
+    uint32_t bso = OOB_OFFSET;
+    if (lane < ntok) bso = (uint32_t)(a.row_tok ? a.row_tok[r0 + lane] : r0 + lane) * srow + 4u * (uint32_t)wave;
+    uint8_t *const gs = lds + (D + 1) * TH_B;         /* two group slots of [G][64] dwords */
+
+    f4v acc[4][NTG];
+#pragma unroll
+    for (int i = 0; i < 4; i++)
+#pragma unroll
+        for (int u = 0; u < NTG; u++) acc[i][u] = f4v{0.0f, 0.0f, 0.0f, 0.0f};
+
+    u32x4 aw[D][4];                                  /* stage s in slot s % D          */
+    u32x4 ws[2][4];                                  /* scale group g in slot g % 2    */
+
+    /* The loads of stage t: weights into slot t % D, at the first stage of a
+     * group that group's scales, then the tokens into LDS slot lslot. Stages
+     * past the last repeat it, so every wave and stage issues the same
+     * count of loads. */
+    auto issue = [&](int t, int lslot, u32x4 (&w)[4], u32x4 (&wsg)[4], uint8_t *gslot, bool group) {
+        const int tc = min(t, last);
+        w[0] = __builtin_amdgcn_raw_buffer_load_b128(rw1, wo[0], tc * 64, 0);
+        w[1] = __builtin_amdgcn_raw_buffer_load_b128(rw1, wo[1], tc * 64, 0);
+        w[2] = __builtin_amdgcn_raw_buffer_load_b128(rw3, wo[2], tc * 64, 0);
+        w[3] = __builtin_amdgcn_raw_buffer_load_b128(rw3, wo[3], tc * 64, 0);
+        if (group) {
+            const int g = min(t / G, glast);
+            wsg[0] = __builtin_amdgcn_raw_buffer_load_b128(rs1, so[0], g * 16, 0);
+            wsg[1] = __builtin_amdgcn_raw_buffer_load_b128(rs1, so[1], g * 16, 0);
+            wsg[2] = __builtin_amdgcn_raw_buffer_load_b128(rs3, so[2], g * 16, 0);
+            wsg[3] = __builtin_amdgcn_raw_buffer_load_b128(rs3, so[3], g * 16, 0);
+            bdma4(rbs, bso, g * 16, gslot + 256 * wave);
+        }
+        uint8_t *buf = lds + lslot * TH_B;
+#pragma unroll
+        for (int j = 0; j < NBL; j++) bdma16(rb, bo[j], tc * 128, buf + 1024 * (NBL * wave + j));
+    };
+
+#pragma unroll
+    for (int t = 0; t < D; t++) {
+        issue(t, t, aw[t], ws[(t / G) & 1], gs + ((t / G) & 1) * 1024, t % G == 0);
+        asm volatile("" ::: "memory");
+    }
+
+    int slot = 0;                                    /* LDS slot of the stage computed next */
+    for (int s0 = 0; s0 < nst; s0 += U) {
+        static_for<0, U>([&](auto qc) {
+            constexpr int q = decltype(qc)::value;
+            /* the loads of stage s = s0 + q were issued D stages ago; those
+             * of the D - 1 stages after it may still be in flight. After the
+             * barrier every wave's tokens of stage s are in LDS and no wave
+             * still reads the LDS slot of stage s - 1, which stage s + D
+             * reuses (likewise the scale group slot two groups back) */
+            wait_vm<(D - 1) * VMW + VMG * (((q % G) + D - 1) / G)>();
+            __builtin_amdgcn_s_barrier();
+            asm volatile("" ::: "memory");
+            const uint8_t *bb = lds + slot * TH_B;
+            constexpr int p = (q / G) & 1, c = q % G;
+            /* The scale bytes are extracted here and not earlier: an empty
+             * asm that takes each scale dword pins the extraction (and the
+             * wait for its load) behind this stage's barrier, where the
+             * scheduler would otherwise hoist it into an earlier stage and
+             * wait out the loads of the stages between. */
+            int sa[4];
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                uint32_t w = ws[p][i][c];
+                asm volatile("" : "+v"(w));
+                sa[i] = scale_byte(w, gq);
+            }
+            const uint8_t *gsl = gs + p * 1024 + 256 * c;
+#pragma unroll
+            for (int u = 0; u < NTG; u++) {
+                const int t = 16 * u + rr;
+                const v8i b = b_operand(bb, t, gq);
+                const int sb = scale_byte(*(const uint32_t *)(gsl + 4 * t), gq);
+#pragma unroll
+                for (int i = 0; i < 4; i++) acc[i][u] = mfma_mx(aw[q % D][i], b, acc[i][u], sa[i], sb);
+            }
+            asm volatile("" ::: "memory");
+            const int nslot = slot == 0 ? D : slot - 1;
+            constexpr int qn = q + D;                /* stage s + D within this or the next iteration */
+            issue(s0 + qn, nslot, aw[q % D], ws[(qn / G) & 1], gs + ((qn / G) & 1) * 1024, qn % G == 0);
+            asm volatile("" ::: "memory");
+            slot = slot == D ? 0 : slot + 1;
+        });
+    }
+    wait_vm<0>();                           /* trailing repeat loads drain before exit */
+
+    mx_store<SWIGLU, NTG>(a, acc, r0, ntok, 0, SWIGLU ? f0 + 32 * wave : f0 + 64 * wave);
+}
+
+template <bool SWIGLU>
+__global__ __launch_bounds__(256, 2) void k_grouped_mx_thin(GroupedMxArgs a, int thin_rows)
+{
+    constexpr int FEAT = SWIGLU ? 128 : 256;
+    __shared__ __align__(16) uint8_t lds[TH_LDS];
+    MxItem it;
+    if (!mx_item<FEAT>(a, it) || it.ntok > thin_rows) return;      /* whole workgroup */
+    const DSV4ExpertW ex = ld_uniform(a.table, it.grp);
+    const DSV4QMat m1 = SWIGLU ? ex.w1 : ex.w2, m3 = ex.w3;
+    if (!fp4_matches(m1, a.N, a.K) || (SWIGLU && !fp4_matches(m3, a.N, a.K))) {
+        mx_fill_bad<SWIGLU, FEAT, 256>(a, it);
+        return;
+    }
+    const int ntg = (it.ntok + 15) / 16;
+    if (ntg == 1) thin_tile<SWIGLU, 1>(a, m1, m3, it.r0, it.ntok, it.f0, lds);
+    else if (ntg == 2) thin_tile<SWIGLU, 2>(a, m1, m3, it.r0, it.ntok, it.f0, lds);
+    else if (ntg == 3) thin_tile<SWIGLU, 3>(a, m1, m3, it.r0, it.ntok, it.f0, lds);
+    else thin_tile<SWIGLU, 4>(a, m1, m3, it.r0, it.ntok, it.f0, lds);
 }
 
 int grouped_mx_rows_per_tile() { return GX_TILE; }
 
 template <bool SW>
-static hipError_t grouped_mx_k(const GroupedMxArgs &a, long items, hipStream_t st)
+static hipError_t grouped_mx_k(const GroupedMxArgs &a, long items, int thin_rows, hipStream_t st)
 {
     static bool attr_done = false;
     if (!attr_done) {
@@ -355,7 +600,8 @@ static hipError_t grouped_mx_k(const GroupedMxArgs &a, long items, hipStream_t s
         if (e != hipSuccess) return e;
         attr_done = true;
     }
-    hipLaunchKernelGGL((k_grouped_mx<SW>), dim3((unsigned)items), dim3(512), GX_LDS, st, a);
+    if (thin_rows > 0) hipLaunchKernelGGL((k_grouped_mx_thin<SW>), dim3((unsigned)items), dim3(256), 0, st, a, thin_rows);
+    hipLaunchKernelGGL((k_grouped_mx<SW>), dim3((unsigned)items), dim3(512), GX_LDS, st, a, thin_rows);
     return hipGetLastError();
 }
 
@@ -367,7 +613,8 @@ hipError_t grouped_mx_launch(bool swiglu, const GroupedMxArgs &a, long max_tiles
         (size_t)a.N * a.K / 2 >= (1u << 31))
         return hipErrorInvalidValue;
     const long items = max_tiles * (a.N / feat);
-    return swiglu ? grouped_mx_k<true>(a, items, st) : grouped_mx_k<false>(a, items, st);
+    const int thin_rows = a.K % TH_KQ == 0 ? TH_TOK : 0;   /* the thin ring runs whole groups of stages */
+    return swiglu ? grouped_mx_k<true>(a, items, thin_rows, st) : grouped_mx_k<false>(a, items, thin_rows, st);
 }
 
 } // namespace dsv4
