@@ -36,7 +36,10 @@ import ctypes as C
 import importlib.util
 import json
 import os
+import shutil
+import subprocess
 import sys
+import tempfile
 import time
 
 import numpy as np
@@ -167,120 +170,212 @@ def time_events(torch, stream, fn, n):
 
 
 # --------------------------------------------------------- CPU baseline ----
+#
+# The reference's CPU path (its src/10_compute objects compiled unchanged into
+# oracle/_ref, else this repo's C restatement) timed on the host of the GPU.
+# Each measurement runs in a child process started with OMP_NUM_THREADS,
+# OMP_PROC_BIND=spread and OMP_PLACES=cores in its environment: libgomp reads
+# them once, when it initialises, so they cannot be set from inside a process
+# that has loaded it. One child runs one thread, one all physical cores of
+# this process's CPU set; each does one warm-up unit and then at least five
+# timed units (more while the time bound allows) and reports their median.
+# The inputs are the GPU run's own tensors, handed over as .npy files.
 
-def omp_threads(n):
+def host_cpu():
+    """CPU model, sockets and cores (lscpu), and the physical cores of the CPU
+    set this process may run on."""
+    info = {}
+    env = dict(os.environ, LC_ALL="C")
     try:
-        gomp = C.CDLL("libgomp.so.1")
-        gomp.omp_set_num_threads(int(n))
-    except OSError:
-        pass
+        out = subprocess.run(["lscpu"], capture_output=True, text=True, env=env, timeout=20).stdout
+        for line in out.splitlines():
+            k, _, v = line.partition(":")
+            k, v = k.strip(), v.strip()
+            if k == "Model name":
+                info["model"] = v
+            elif k == "Socket(s)":
+                info["sockets"] = int(v)
+            elif k == "Core(s) per socket":
+                info["cores_per_socket"] = int(v)
+            elif k == "Thread(s) per core":
+                info["threads_per_core"] = int(v)
+        allowed = os.sched_getaffinity(0)
+        par = subprocess.run(["lscpu", "-p=CPU,CORE,SOCKET"], capture_output=True, text=True,
+                             env=env, timeout=20).stdout
+        cores = set()
+        for line in par.splitlines():
+            if line.startswith("#"):
+                continue
+            f = line.split(",")
+            if len(f) >= 3 and f[0].isdigit() and int(f[0]) in allowed:
+                cores.add((f[2], f[1]))
+        info["cpus_allowed"] = len(allowed)
+        info["cores_allowed"] = len(cores) if cores else len(allowed)
+    except (OSError, ValueError, subprocess.SubprocessError):
+        info.setdefault("cpus_allowed", os.cpu_count() or 1)
+        info.setdefault("cores_allowed", info["cpus_allowed"])
+    return info
 
 
-def cpu_baseline_cfg1(torch, arena, x_host, seconds, threads):
-    """The reference's CPU path on the host: dsv4_expert_forward x 6 + the
-    k-order combine, over 16 experts copied from the device arena (214 MB,
-    beyond the host LLC). Runs tokens until `seconds` elapse (min 3)."""
+def all_core_threads(info):
+    """All physical cores of the CPU set, at most the OMP_NUM_THREADS the
+    environment grants (the per-GPU share of the host)."""
+    cap = int(os.environ.get("OMP_NUM_THREADS", "0") or 0)
+    n = info.get("cores_allowed") or 1
+    return max(1, min(n, cap) if cap > 0 else n)
+
+
+def cpu_baseline(work, arrays, params, per_unit, unit, sample, seconds, threads=0):
+    """Runs `work` in two child processes (1 thread; all cores, or `threads`
+    when given) on `arrays` (name -> ndarray, written to a temporary
+    directory) and returns the cpu_baseline record: value = per_unit / median
+    unit time at all cores."""
+    info = host_cpu()
+    threads = threads or all_core_threads(info)
+    tmp = tempfile.mkdtemp(prefix="dsv4_cpu_")
+    try:
+        for k, a in arrays.items():
+            np.save(os.path.join(tmp, k + ".npy"), np.ascontiguousarray(a), allow_pickle=False)
+        runs = {}
+        for label, nthr, budget in (("one_thread", 1, 0.5 * seconds), ("all_cores", threads, 0.5 * seconds)):
+            spec = dict(params, work=work, dir=tmp, seconds=budget, min_runs=5, max_runs=200)
+            spath = os.path.join(tmp, f"spec_{label}.json")
+            with open(spath, "w") as f:
+                json.dump(spec, f)
+            env = dict(os.environ, OMP_NUM_THREADS=str(nthr), OMP_PROC_BIND="spread",
+                       OMP_PLACES="cores")
+            log(f"CPU baseline {work}: {label} ({nthr} threads)")
+            p = subprocess.run([sys.executable, os.path.abspath(__file__), "--cpu-worker", spath],
+                               capture_output=True, text=True, env=env, timeout=600)
+            if p.returncode != 0:
+                raise RuntimeError(f"CPU worker {work}/{label} failed: {p.stderr[-2000:]}")
+            r = json.loads(p.stdout.strip().splitlines()[-1])
+            r["threads"] = nthr
+            r["value"] = round(per_unit / r["median_s"], 5)
+            runs[label] = r
+    finally:
+        shutil.rmtree(tmp, ignore_errors=True)
+    a = runs["all_cores"]
+    return {"value": a["value"], "unit": unit, "cores": threads, "kind": a["kind"],
+            "sample": f"{sample}; median of {a['runs']} timed units after 1 warm-up",
+            "one_thread": runs["one_thread"], "all_cores": a,
+            "omp": {"OMP_PROC_BIND": "spread", "OMP_PLACES": "cores"}, "host": info}
+
+
+def _cpu_worker(spec_path):
+    """Child side of cpu_baseline: builds the work unit named in the spec,
+    runs it once untimed, then times units until min_runs are done and the
+    time bound is spent (or max_runs), and prints the median."""
+    with open(spec_path) as f:
+        spec = json.load(f)
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
     import pyoracle as P
     kind = "reference"
     try:
         impl = P.Reference()
-    except FileNotFoundError:
+    except (FileNotFoundError, OSError):
         impl, kind = P.Oracle(), "port"
     orc = P.Oracle()
-    omp_threads(threads)
-    n_host = 16
-    experts = []
-    keep = []
+    d = spec["dir"]
+
+    def ld(name):
+        return np.load(os.path.join(d, name + ".npy"), mmap_mode="r", allow_pickle=False)
+
     wb = [INTER * HIDDEN // 2, HIDDEN * INTER // 2, INTER * HIDDEN // 2]
     sb = [INTER * HIDDEN // 32, HIDDEN * INTER // 32, INTER * HIDDEN // 32]
     off_s = [0, sb[0], sb[0] + sb[1]]
     off_w = [sum(sb), sum(sb) + wb[0], sum(sb) + wb[0] + wb[1]]
     shapes = [(INTER, HIDDEN), (HIDDEN, INTER), (INTER, HIDDEN)]
-    for e in range(n_host):
-        raw = arena.host_copy(torch, e)
-        keep.append(raw)
-        mats = [P.HostMat(P.DSV4_WFP4, raw[off_w[i]:off_w[i] + wb[i]],
-                          raw[off_s[i]:off_s[i] + sb[i]], r, c, 1, 32)
-                for i, (r, c) in enumerate(shapes)]
-        experts.append(P.HostExpert(mats[0], mats[2], mats[1]))
-    rng = np.random.default_rng(7)
-    t0 = time.perf_counter()
-    tokens = 0
-    while True:
-        ids = rng.choice(n_host, TOPK, replace=False)
-        lg = rng.standard_normal(TOPK)
-        w = (np.exp(lg) / np.exp(lg).sum()).astype(np.float32)
-        acc = np.stack([impl.expert_forward(experts[i], x_host, 10.0) for i in ids])
-        orc.moe_combine(acc, w)
-        tokens += 1
-        el = time.perf_counter() - t0
-        if tokens >= 3 and el >= seconds:
-            break
-    gbs = tokens * (TOPK * EXPERT_BYTES + 8192 + 16384) / el / 1e9
-    return {"value": round(gbs, 3), "unit": "GB/s", "cores": threads, "kind": kind,
-            "sample": f"{tokens} tokens x top-6 over 16 host-resident FP4 experts "
-                      f"(214 MB), {el:.1f} s, OpenMP {threads} threads"}
 
+    def host_expert(raw):
+        """An expert in the reference's slot layout (scales s1 s2 s3, then
+        w1 w2 w3) as host descriptors over the slot's bytes."""
+        m = [P.HostMat(P.DSV4_WFP4, raw[off_w[i]:off_w[i] + wb[i]], raw[off_s[i]:off_s[i] + sb[i]],
+                       r, c, 1, 32) for i, (r, c) in enumerate(shapes)]
+        return P.HostExpert(m[0], m[2], m[1])
 
-def cpu_baseline_buckets(torch, arena, idx, x_host, seconds, threads, unit):
-    """The reference's prefill bucket path on the host
-    (src/80_prefill/dsv4_prefill_experts.c:60-69): per expert, its routed
-    tokens through fp4_n with nt = bucket size for w1 and w3, SwiGLU, fp4_n
-    for w2. Runs the buckets of the 8 most-loaded experts of the given routing
-    (copied from the device arena) until `seconds` elapse. Reports expert
-    bytes streamed per second (GB/s) or routed FLOP/s (TFLOP/s)."""
-    sys.path.insert(0, os.path.join(ROOT, "oracle"))
-    import pyoracle as P
-    kind = "reference"
-    try:
-        impl = P.Reference()
-    except FileNotFoundError:
-        impl, kind = P.Oracle(), "port"
-    omp_threads(threads)
-    counts = np.bincount(idx.reshape(-1), minlength=N_EXPERTS)
-    sel = np.argsort(-counts, kind="stable")[:8]
-    wb = [INTER * HIDDEN // 2, HIDDEN * INTER // 2, INTER * HIDDEN // 2]
-    sb = [INTER * HIDDEN // 32, HIDDEN * INTER // 32, INTER * HIDDEN // 32]
-    off_s = [0, sb[0], sb[0] + sb[1]]
-    off_w = [sum(sb), sum(sb) + wb[0], sum(sb) + wb[0] + wb[1]]
-    buckets = []
-    for e in sel:
-        raw = arena.host_copy(torch, int(e))
-        toks = np.nonzero((idx == e).any(1))[0]
-        X = np.ascontiguousarray(x_host[toks], np.float32)
-        mats = [(raw[off_w[i]:off_w[i] + wb[i]], raw[off_s[i]:off_s[i] + sb[i]]) for i in range(3)]
-        buckets.append((raw, mats, X, len(toks)))
-    def mmq_n(mat, X, rows, cols, nt):
+    def fp4_tiles(mat, X, rows, cols, nt):
         """dsv4_mmq_n's tiling: the fp4_n body takes at most 128 tokens
         (DSV4_MAX_BATCH, src/10_compute/dsv4_matmul.c:63-73)"""
         out = np.empty(nt * rows, np.float32)
         for o in range(0, nt, 128):
             t = min(128, nt - o)
-            out[o * rows:(o + t) * rows] = impl.fp4_n(mat[0], mat[1], X[o * cols:(o + t) * cols],
+            out[o * rows:(o + t) * rows] = impl.fp4_n(mat.W, mat.S, X[o * cols:(o + t) * cols],
                                                       rows, cols, 1, 32, t)
         return out
 
-    t0 = time.perf_counter()
-    passes = nbytes = flops = 0
-    while True:
-        for raw, mats, X, nt in buckets:
-            g = mmq_n(mats[0], X.reshape(-1), INTER, HIDDEN, nt)
-            u = mmq_n(mats[2], X.reshape(-1), INTER, HIDDEN, nt)
-            m = impl.swiglu(g, u, 10.0)
-            mmq_n(mats[1], m, HIDDEN, INTER, nt)
-            nbytes += EXPERT_BYTES
-            flops += 2.0 * nt * 3 * INTER * HIDDEN
-        passes += 1
-        el = time.perf_counter() - t0
-        if el >= seconds and passes >= 1:
-            break
-    loads = ",".join(str(b[3]) for b in buckets)
-    value = nbytes / el / 1e9 if unit == "GB/s" else flops / el / 1e12
-    return {"value": round(value, 5), "unit": unit, "cores": threads, "kind": kind,
-            "sample": f"{passes} passes over the buckets of the 8 most-loaded experts "
-                      f"(tokens {loads}) through fp4_n/SwiGLU/fp4_n, {el:.1f} s, "
-                      f"OpenMP {threads} threads"}
+    def fp4_bucket(e, X, nt):
+        g = fp4_tiles(e.w1, X, INTER, HIDDEN, nt)
+        u = fp4_tiles(e.w3, X, INTER, HIDDEN, nt)
+        return fp4_tiles(e.w2, impl.swiglu(g, u, 10.0), HIDDEN, INTER, nt)
+
+    def shared_fp8(X, nt):
+        """The FP8 shared expert through fp8_n (E8M0 block scales)."""
+        S = [ld(f"sh_s{i}") for i in range(3)]
+        Wm = [ld(f"sh_w{i}") for i in range(3)]
+        g = impl.fp8_n(Wm[0], S[0], X, INTER, HIDDEN, 128, 128, nt)
+        u = impl.fp8_n(Wm[1], S[1], X, INTER, HIDDEN, 128, 128, nt)
+        return impl.fp8_n(Wm[2], S[2], impl.swiglu(g, u, 10.0), HIDDEN, INTER, 128, 128, nt)
+
+    work = spec["work"]
+    if work == "fp8_matvec":
+        Wq, Se, x = ld("w"), ld("s"), np.ascontiguousarray(ld("x"))
+        def unit(i):
+            impl.fp8_n(Wq, Se, x, 4096, 4096, 128, 128, 1)
+    elif work == "fp8_gemm":
+        Wq, Se, X = ld("w"), ld("s"), np.ascontiguousarray(ld("x")).reshape(-1)
+        nt = X.size // 4096
+        def unit(i):
+            impl.fp8_n(Wq, Se, X, 4096, 4096, 128, 128, nt)
+    elif work == "decode_token":
+        slots = ld("experts")
+        experts = [host_expert(slots[e]) for e in range(slots.shape[0])]
+        x = np.ascontiguousarray(ld("x"))
+        rng = np.random.default_rng(7)
+        plans = [(rng.choice(len(experts), TOPK, replace=False), rng.standard_normal(TOPK))
+                 for _ in range(spec["max_runs"] + 1)]
+        def unit(i):
+            ids, lg = plans[i]
+            w = (np.exp(lg) / np.exp(lg).sum()).astype(np.float32)
+            acc = np.stack([impl.expert_forward(experts[k], x, 10.0) for k in ids])
+            orc.moe_combine(acc, w)
+    elif work == "buckets":
+        slots = ld("experts")
+        experts = [host_expert(slots[e]) for e in range(slots.shape[0])]
+        Xs = [np.ascontiguousarray(ld(f"x{e}")).reshape(-1) for e in range(slots.shape[0])]
+        Xsh = np.ascontiguousarray(ld("x_shared")).reshape(-1)
+        nsh = Xsh.size // HIDDEN
+        def unit(i):
+            for e, X in zip(experts, Xs):
+                fp4_bucket(e, X, X.size // HIDDEN)
+            shared_fp8(Xsh, nsh)
+    else:
+        raise SystemExit(f"unknown CPU work {work}")
+
+    unit(0)                                   # warm-up
+    times = []
+    t_end = time.perf_counter() + spec["seconds"]
+    while len(times) < spec["min_runs"] or (time.perf_counter() < t_end and len(times) < spec["max_runs"]):
+        t0 = time.perf_counter()
+        unit(len(times) + 1)
+        times.append(time.perf_counter() - t0)
+    print(json.dumps({"kind": kind, "runs": len(times), "median_s": float(np.median(times)),
+                      "min_s": float(np.min(times)), "max_s": float(np.max(times))}), flush=True)
+
+
+def fp8_e8m0(torch, S):
+    """E8M0 block scales (the power of two at or above each fp32 scale): the
+    reference's CPU fp8_n stores E8M0 scales only."""
+    return torch.clamp(torch.ceil(torch.log2(S)) + 127, 0, 254).to(torch.uint8).cpu().numpy()
+
+
+def shared_host(torch, keep):
+    """The FP8 shared expert's weights (gate, up, down) and E8M0 scales on the host."""
+    out = {}
+    for i in range(3):
+        out[f"sh_w{i}"] = keep[2 * i].cpu().numpy()
+        out[f"sh_s{i}"] = fp8_e8m0(torch, keep[2 * i + 1])
+    return out
 
 
 def bench_grouped(args, torch, pkg, lib, stream, sp, K, W, cfg):
@@ -353,11 +448,34 @@ def bench_grouped(args, torch, pkg, lib, stream, sp, K, W, cfg):
     d_avg = (bytes_avg - SHARED_BYTES - n * HIDDEN * 6) / EXPERT_BYTES
     cpu = None
     if not args.no_cpu:
-        threads = args.cpu_threads or min(16, os.cpu_count() or 1)
+        # the reference's bucket path (src/80_prefill/dsv4_prefill_experts.c:60-69):
+        # per expert, its routed tokens through fp4_n (nt = bucket size, in
+        # tiles of 128) for w1 and w3, SwiGLU, fp4_n for w2; then the shared
+        # expert through fp8_n. Unit: the 8 most-loaded buckets of step 0 and
+        # the shared expert over its 64 tokens (config 2); the 2 most-loaded
+        # buckets cut to 128 tokens each and the shared expert over 128 tokens
+        # (config 4).
+        counts = np.bincount(idx_h[:n].reshape(-1), minlength=N_EXPERTS)
+        nsel, cap = (8, n) if cfg == 2 else (2, 128)
+        sel = np.argsort(-counts, kind="stable")[:nsel]
         x_host = xs[:n * HIDDEN].view(n, HIDDEN).cpu().numpy()
-        log(f"CPU baseline ({threads} threads, {args.cpu_seconds:.0f} s)")
-        cpu = cpu_baseline_buckets(torch, arena, idx_h[:n], x_host, args.cpu_seconds, threads,
-                                   "GB/s" if cfg == 2 else "TFLOP/s")
+        arrays = {"experts": np.stack([arena.host_copy(torch, int(e)) for e in sel])}
+        ntoks = []
+        for j, e in enumerate(sel):
+            toks = np.nonzero((idx_h[:n] == e).any(1))[0][:cap]
+            arrays[f"x{j}"] = x_host[toks]
+            ntoks.append(len(toks))
+        nsh = min(n, cap)
+        arrays["x_shared"] = x_host[:nsh]
+        arrays.update(shared_host(torch, keep))
+        if cfg == 2:
+            per_unit, unit = (nsel * EXPERT_BYTES + SHARED_BYTES) / 1e9, "GB/s"
+        else:
+            per_unit, unit = 2.0 * (sum(ntoks) + nsh) * 3 * INTER * HIDDEN / 1e12, "TFLOP/s"
+        cpu = cpu_baseline("buckets", arrays, {}, per_unit, unit,
+                           f"buckets of {nsel} experts (tokens {','.join(map(str, ntoks))}) through "
+                           f"fp4_n/SwiGLU/fp4_n plus the shared expert over {nsh} tokens through fp8_n",
+                           args.cpu_seconds, args.cpu_threads)
     res = {
         "metric": "quant matvec HBM GB/s (% peak); prefill FP4/FP8 GEMM TFLOP/s (% MFMA peak)",
         "n_gpus": 1, "steps": K, "warmup": W, "ms_per_step": round(t_step * 1e3, 5),
@@ -423,61 +541,6 @@ def bench_grouped(args, torch, pkg, lib, stream, sp, K, W, cfg):
     return res
 
 
-def cpu_baseline_cfg3(Wq, Sw_e8m0, x_sample, seconds, threads):
-    """The reference's CPU fp8_n (nt > 1 body, src/10_compute/dsv4_matmul_fp8.c:
-    102-155) on the same 4096x4096 e4m3 weight, over blocks of 128 tokens
-    (dsv4_mmq_n's tile), repeated until `seconds` elapse. The reference only
-    stores E8M0 block scales, so it runs with the power of two at or above each
-    fp32 scale; the arithmetic per token is the same."""
-    sys.path.insert(0, os.path.join(ROOT, "oracle"))
-    import pyoracle as P
-    kind = "reference"
-    try:
-        impl = P.Reference()
-    except FileNotFoundError:
-        impl, kind = P.Oracle(), "port"
-    omp_threads(threads)
-    nt = x_sample.shape[0]
-    t0 = time.perf_counter()
-    blocks = 0
-    while True:
-        impl.fp8_n(Wq, Sw_e8m0, x_sample.reshape(-1), 4096, 4096, 128, 128, nt)
-        blocks += 1
-        el = time.perf_counter() - t0
-        if el >= seconds and blocks >= 2:
-            break
-    tflops = blocks * 2.0 * nt * 4096 * 4096 / el / 1e12
-    return {"value": round(tflops, 5), "unit": "TFLOP/s", "cores": threads, "kind": kind,
-            "sample": f"{blocks} x {nt} tokens through fp8_n 4096x4096 (E8M0 scales), {el:.1f} s, "
-                      f"OpenMP {threads} threads"}
-
-
-def cpu_baseline_cfg0(Wq, Sw_e8m0, x, seconds, threads):
-    """The reference's fp8_n with nt = 1 (src/10_compute/dsv4_matmul_fp8.c:
-    57-99) on one 4096x4096 e4m3 weight (16.8 MB, beyond the host LLC),
-    repeated until `seconds` elapse. The reference stores E8M0 block scales, so
-    it runs with the power of two at or above each fp32 scale."""
-    sys.path.insert(0, os.path.join(ROOT, "oracle"))
-    import pyoracle as P
-    kind = "reference"
-    try:
-        impl = P.Reference()
-    except FileNotFoundError:
-        impl, kind = P.Oracle(), "port"
-    omp_threads(threads)
-    t0 = time.perf_counter()
-    calls = 0
-    while True:
-        impl.fp8_n(Wq, Sw_e8m0, x, 4096, 4096, 128, 128, 1)
-        calls += 1
-        el = time.perf_counter() - t0
-        if el >= seconds and calls >= 3:
-            break
-    return {"value": round(calls * 16_805_888 / el / 1e9, 3), "unit": "GB/s", "cores": threads,
-            "kind": kind, "sample": f"{calls} matvecs 4096x4096 through fp8_n (E8M0 scales), "
-                                    f"{el:.1f} s, OpenMP {threads} threads"}
-
-
 def bench_cfg3(args, torch, pkg, lib, stream, sp, K, W):
     M, N, KD = 2048, 4096, 4096
     flops = 2.0 * M * N * KD
@@ -522,12 +585,14 @@ def bench_cfg3(args, torch, pkg, lib, stream, sp, K, W):
     achieved = flops / t_gemm / 1e12
     cpu = None
     if not args.no_cpu:
-        threads = args.cpu_threads or min(16, os.cpu_count() or 1)
-        Wh = Wd.cpu().numpy()
-        Se = torch.clamp(torch.ceil(torch.log2(Sd)) + 127, 0, 254).to(torch.uint8).cpu().numpy()
-        xs = A.view(M, KD)[:128].float().cpu().numpy()
-        log(f"CPU baseline ({threads} threads, {args.cpu_seconds:.0f} s)")
-        cpu = cpu_baseline_cfg3(Wh, Se, xs, args.cpu_seconds, threads)
+        # the reference's fp8_n, nt > 1 body (src/10_compute/dsv4_matmul_fp8.c:
+        # 102-155), on the same weight with E8M0 block scales; unit: one
+        # 128-token tile (dsv4_mmq_n's tile) of the activations
+        cpu = cpu_baseline("fp8_gemm", {"w": Wd.cpu().numpy(), "s": fp8_e8m0(torch, Sd),
+                                        "x": A.view(M, KD)[:128].float().cpu().numpy()},
+                           {}, 2.0 * 128 * N * KD / 1e12, "TFLOP/s",
+                           "128 tokens x 4096x4096 e4m3 (E8M0 block scales) through fp8_n",
+                           args.cpu_seconds, args.cpu_threads)
     return {
         "metric": "quant matvec HBM GB/s (% peak); prefill FP4/FP8 GEMM TFLOP/s (% MFMA peak)",
         "value": round(value, 2), "unit": "TFLOP/s", "n_gpus": 1, "steps": K, "warmup": W,
@@ -562,10 +627,15 @@ def main():
     ap.add_argument("--exact", action="store_true",
                     help="config 4: time the exact fp16-MFMA grouped path instead of the "
                          "block-scaled one")
+    ap.add_argument("--cpu-worker", metavar="SPEC",
+                    help="internal: run one CPU-baseline measurement described by SPEC and exit")
     ap.add_argument("--copy-calib", action="store_true",
                     help="run only a plain 256 MiB device copy (the HBM-counter calibration "
                          "kernel for rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE)")
     args = ap.parse_args()
+    if args.cpu_worker:
+        _cpu_worker(args.cpu_worker)
+        return
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (this build has no multi-GPU path); "
               f"got --gpus {args.gpus}", file=sys.stderr)
@@ -649,10 +719,17 @@ def main():
         achieved = bytes_step / t_launch / 1e9
         cpu = None
         if not args.no_cpu:
-            threads = args.cpu_threads or min(16, os.cpu_count() or 1)
-            x_host = xs[:HIDDEN].cpu().numpy()
-            log(f"CPU baseline ({threads} threads, {args.cpu_seconds:.0f} s)")
-            cpu = cpu_baseline_cfg1(torch, arena, x_host, args.cpu_seconds, threads)
+            # the reference's decode path on the host: dsv4_expert_forward x 6
+            # (src/10_compute/dsv4_ops.c:85-93) and the k-order combine, each
+            # unit a token routed to 6 of 64 host-resident experts (856 MB,
+            # beyond the host LLC), copied in the reference's slot layout
+            nh = 64
+            slots = arena.buf[:nh * EXPERT_BYTES].cpu().numpy().reshape(nh, EXPERT_BYTES)
+            cpu = cpu_baseline("decode_token", {"experts": slots, "x": xs[:HIDDEN].cpu().numpy()},
+                               {}, (TOPK * EXPERT_BYTES + 8192 + 16384) / 1e9, "GB/s",
+                               f"one token x top-6 of {nh} host-resident FP4 experts through "
+                               f"dsv4_expert_forward and the combine",
+                               args.cpu_seconds, args.cpu_threads)
         res = {
             "metric": "quant matvec HBM GB/s (% peak); prefill FP4/FP8 GEMM TFLOP/s (% MFMA peak)",
             "value": round(value, 2), "unit": "GB/s", "n_gpus": 1, "steps": K, "warmup": W,
@@ -721,11 +798,14 @@ def main():
         value = bytes_step / t_step / 1e9
         cpu = None
         if not args.no_cpu:
-            threads = args.cpu_threads or min(16, os.cpu_count() or 1)
-            Wh = Wd[:4096 * 4096].cpu().numpy()
-            Se = torch.clamp(torch.ceil(torch.log2(Sd[:1024])) + 127, 0, 254).to(torch.uint8).cpu().numpy()
-            log(f"CPU baseline ({threads} threads, {args.cpu_seconds:.0f} s)")
-            cpu = cpu_baseline_cfg0(Wh, Se, xs.cpu().numpy(), args.cpu_seconds, threads)
+            # the reference's fp8_n with nt = 1 (src/10_compute/dsv4_matmul_fp8.c:
+            # 57-99) on the first weight copy (16.8 MB, beyond the host LLC)
+            cpu = cpu_baseline("fp8_matvec", {"w": Wd[:4096 * 4096].cpu().numpy(),
+                                              "s": fp8_e8m0(torch, Sd[:1024]),
+                                              "x": xs.cpu().numpy()},
+                               {}, bytes_step / 1e9, "GB/s",
+                               "one 4096x4096 e4m3 matvec (E8M0 block scales) through fp8_n",
+                               args.cpu_seconds, args.cpu_threads)
         res = {
             "metric": "quant matvec HBM GB/s (% peak); prefill FP4/FP8 GEMM TFLOP/s (% MFMA peak)",
             "value": round(value, 2), "unit": "GB/s", "n_gpus": 1, "steps": K, "warmup": W,
