@@ -258,3 +258,60 @@ def test_one_launch_graph_replays(lib, pkg, oracle, monkeypatch, shared):
     torch.cuda.synchronize()
     assert np.array_equal(bits(out.cpu().numpy()), want[len(calls) - 1])
     assert lib.status() == 0
+
+
+def _host_slot_expert(raw):
+    """A device-arena expert copied to the host: scales s1 s2 s3 then weights
+    w1 w2 w3 (the reference's cache slot layout)."""
+    I, H = 2048, 4096
+    wb = [I * H // 2, H * I // 2, I * H // 2]
+    sb = [I * H // 32, H * I // 32, I * H // 32]
+    off_s = [0, sb[0], sb[0] + sb[1]]
+    off_w = [sum(sb), sum(sb) + wb[0], sum(sb) + wb[0] + wb[1]]
+    shapes = [(I, H), (H, I), (I, H)]
+    m = [P.HostMat(P.DSV4_WFP4, raw[off_w[i]:off_w[i] + wb[i]], raw[off_s[i]:off_s[i] + sb[i]], r, c, 1, 32)
+         for i, (r, c) in enumerate(shapes)]
+    return P.HostExpert(m[0], m[2], m[1])
+
+
+def test_one_launch_soak(lib, pkg, oracle, monkeypatch):
+    """A bounded soak of the one-launch hand-off: 2,000 consecutive calls,
+    each with fresh routing (top-6 of 32 full-size FP4 experts), a fresh
+    token and the FP8 shared expert, enqueued back to back on the one-launch
+    form; then the same 2,000 on the two-launch form. Every output bit for bit
+    equal (the first mismatch is reported by its call index) and the status
+    clean after each form; the first and the last call against the oracle."""
+    import bench
+    n_calls, n_exp, topk, hidden, inter = 2000, 32, 6, 4096, 2048
+    arena = bench.ExpertArena(torch, pkg, lib, n_exp, seed=0x50A4)
+    shared, keep = bench.make_shared_fp8(torch, pkg, lib, 0x50A5)
+    rng = np.random.default_rng(0x50A6)
+    idx = np.stack([rng.choice(n_exp, topk, replace=False) for _ in range(n_calls)]).astype(np.int32)
+    lg = rng.standard_normal((n_calls, topk))
+    w = (np.exp(lg) / np.exp(lg).sum(1, keepdims=True)).astype(np.float32)
+    didx, dw = torch.from_numpy(idx).to(DEV), torch.from_numpy(w).to(DEV)
+    xs = torch.empty(n_calls * hidden, dtype=torch.float32, device=DEV)
+    lib.synth_normal_dev(xs.data_ptr(), xs.numel(), 0x50A7, 1.0, True)
+    outs = {}
+    lib.status()
+    for mode in ("1", "2"):
+        monkeypatch.setenv(ENV, mode)
+        o = torch.empty((n_calls, hidden), dtype=torch.float32, device=DEV)
+        for i in range(n_calls):
+            lib.moe_decode_dev(o[i].data_ptr(), xs.data_ptr() + 4 * hidden * i, arena.table.data_ptr(),
+                               n_exp, didx.data_ptr() + 4 * topk * i, dw.data_ptr() + 4 * topk * i, topk,
+                               shared, hidden, inter, 10.0)
+        torch.cuda.synchronize()
+        assert lib.status() == 0, f"status after the {'one' if mode == '1' else 'two'}-launch form"
+        outs[mode] = bits(o.cpu().numpy())
+    same = (outs["1"] == outs["2"]).all(1)
+    assert same.all(), f"first mismatch at call {int(np.argmin(same))} of {n_calls}"
+    hsh = P.HostExpert(*[P.HostMat(P.DSV4_WFP8_F32S, keep[2 * i].cpu().numpy(), keep[2 * i + 1].cpu().numpy(),
+                                   r, c, 128, 128)
+                         for i, (r, c) in enumerate(((inter, hidden), (inter, hidden), (hidden, inter)))])
+    for i in (0, n_calls - 1):
+        xh = xs[i * hidden:(i + 1) * hidden].cpu().numpy()
+        acc = np.stack([oracle.expert_forward(_host_slot_expert(arena.host_copy(torch, int(e))), xh, 10.0)
+                        for e in idx[i]])
+        want = (oracle.moe_combine(acc, w[i]) + oracle.expert_forward(hsh, xh, 10.0)).astype(np.float32)
+        assert check_close(outs["1"][i].view(np.float32), want) < 1e-4
