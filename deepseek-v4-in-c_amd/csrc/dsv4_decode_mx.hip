@@ -90,21 +90,35 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t dev_rsrc(const void *p, uint32
 }
 
 /* The calling workgroup's last access to the publication words: one add to
- * the leave counter, issued after every earlier access of the caller has
- * completed (vmcnt(0): stores acknowledged, loads and adds returned). The
- * workgroup whose add returns total - 1 is the last of the launch; every
- * other workgroup's accesses are then complete, so it sets the three words
- * back to zero for the next launch. Lane 0 only. */
+ * its group's leave counter, issued after every earlier access of the
+ * caller has completed (vmcnt(0): stores acknowledged, loads and adds
+ * returned). The workgroup whose add completes its group adds one to the top
+ * counter; the one whose add completes the top counter is the last of the
+ * launch, every other workgroup's accesses are then complete, so it sets all
+ * the words back to zero for the next launch. Lane 0 only. */
 __device__ __forceinline__ void leave(const OnePub &p)
 {
+    /* The leave counter is split in ONE_LEAVE_GROUPS group counters (by
+     * workgroup id) and a top counter: the last leaver of a group adds once
+     * to the top counter, and the last top add does the reset. All the
+     * workgroups of a launch end at about the same time; one counter for
+     * them all serialised their adds (2.5 us of a 21 us launch). */
     __builtin_amdgcn_s_waitcnt(0x0F70);            /* vmcnt(0) */
     asm volatile("" ::: "memory");
-    const unsigned old = __hip_atomic_fetch_add(p.leave, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    if (old == p.total - 1) {
-        __hip_atomic_store(p.count, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        __hip_atomic_store(p.done, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        __hip_atomic_store(p.leave, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    }
+    const unsigned grp = blockIdx.x % ONE_LEAVE_GROUPS;
+    const unsigned in_grp = (p.total - grp + ONE_LEAVE_GROUPS - 1) / ONE_LEAVE_GROUPS;
+    const unsigned groups = p.total < ONE_LEAVE_GROUPS ? p.total : ONE_LEAVE_GROUPS;
+    unsigned *top = p.leave + ONE_LEAVE_GROUPS * ONE_PUB_LINE_WORDS;
+    const unsigned old = __hip_atomic_fetch_add(p.leave + grp * ONE_PUB_LINE_WORDS, 1u, __ATOMIC_RELAXED,
+                                                __HIP_MEMORY_SCOPE_AGENT);
+    if (old != in_grp - 1) return;
+    const unsigned told = __hip_atomic_fetch_add(top, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (told != groups - 1) return;
+    __hip_atomic_store(p.count, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __hip_atomic_store(p.done, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    for (unsigned g = 0; g < ONE_LEAVE_GROUPS; g++)
+        __hip_atomic_store(p.leave + g * ONE_PUB_LINE_WORDS, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __hip_atomic_store(top, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 /* This wave's stores acknowledged, then one more item counted; the item that
@@ -1133,13 +1147,19 @@ __device__ __forceinline__ void down_one_group(const MoeOneArgs &A, int grp, uin
                 ((uint32_t *)(tab + ROUNDS * 1024))[lane] = lane == 8 ? E8M0_ONE : 0u;
         }
     }
-    /* wave 0 waits for every slot's mid (each feeds every output row) and
-     * releases the workgroup; the weight loads stay in flight */
-    if (k == 0) {
+    /* One wave waits for every slot's mid (each feeds every output row) and
+     * releases the workgroup; the weight loads stay in flight. With fewer
+     * than eight slots the poll falls to wave 7, which has no slot: it has
+     * issued no weight loads, so its poll returns as soon as the flag is set
+     * (a wave's loads return in issue order), and its add to the leave
+     * counter runs while the slot waves multiply. */
+    const int pw = a.topk < 8 ? 7 : 0;
+    if (k == pw) {
         const bool ok = wait_done(A.pub, A.spin_max);
         if (lane == 0) *ready_ok = ok ? 1 : 0;
     }
     lds_barrier();
+    if (pw != 0 && k == pw && lane == 0) leave(A.pub);   /* its poll was its last access */
     if (live) {
         if (!bad && !*ready_ok) bad = ST_SYNC_TIMEOUT;
         if (!bad) {
@@ -1180,7 +1200,7 @@ __device__ __forceinline__ void down_one_group(const MoeOneArgs &A, int grp, uin
         }
     }
     __syncthreads();
-    if (threadIdx.x == 0) leave(A.pub);            /* wave 0's poll has returned */
+    if (pw == 0 && threadIdx.x == 0) leave(A.pub); /* wave 0's poll has returned */
     if (threadIdx.x >= 16 || r0 + (int)threadIdx.x >= a.hidden) return;
     const int t = threadIdx.x >> 3, rr = threadIdx.x & 7;
     float o = 0.0f;

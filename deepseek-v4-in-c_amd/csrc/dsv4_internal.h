@@ -211,14 +211,19 @@ hipError_t down_mx_launch(DownMxArgs a, hipStream_t st);
  * items - 1 writes 1 to *done. The hidden / 16 down workgroups after them
  * load their down weights at once and wait (spin_max polls at most; 0: give
  * up without polling) until *done is 1. Every workgroup, gate/up and down,
- * adds one to *leave as its last access to the three words; the one whose add
- * returns items + down groups - 1 sets all three back to 0, so each launch
- * finds them zero (a HIP graph can replay the launch). count, done and leave
- * are on three separate 128-byte lines, zero before the first launch. */
+ * leaves as its last access to the words: it adds one to the leave counter
+ * of its group (workgroup id % ONE_LEAVE_GROUPS, at leave + group *
+ * ONE_PUB_LINE_WORDS), the last leaver of a group adds one to the top
+ * counter (after the group counters), and the last top add sets every word
+ * back to 0, so each launch finds them zero (a HIP graph can replay the
+ * launch). Every word is on its own 128-byte line, zero before the first
+ * launch: count, done, the group counters, the top counter. */
 struct OnePub {
     unsigned *count, *done, *leave;
     unsigned items, total;
 };
+constexpr int ONE_PUB_LINE_WORDS = 32;    /* one 128-byte line per word */
+constexpr int ONE_LEAVE_GROUPS = 8;
 struct MoeOneArgs {
     GateUpMxArgs gu;
     DownMxArgs dn;
@@ -229,8 +234,9 @@ struct MoeOneArgs {
 /* whether one launch takes this geometry */
 bool moe_one_ok(int hidden, int inter, int topk);
 hipError_t moe_one_launch(MoeOneArgs a, hipStream_t st);
-/* the three publication words of the one-launch form: 3 lines of 128 bytes */
-constexpr size_t ONE_PUB_BYTES = 384;
+/* the publication words of the one-launch form: count, done, the group
+ * leave counters and the top counter, a 128-byte line each */
+constexpr size_t ONE_PUB_BYTES = (size_t)(2 + ONE_LEAVE_GROUPS + 1) * ONE_PUB_LINE_WORDS * 4;
 /* bytes of one slot's split table for a K of `inter` */
 size_t mx_split_bytes(int inter);
 

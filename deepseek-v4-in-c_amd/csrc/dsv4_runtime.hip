@@ -88,11 +88,11 @@ constexpr int HOST_WORD = 32;            /* the host calls' word, on its own 128
  * for callers that cannot allocate: the one-launch hand-off words (zero
  * between launches), the mid rows, the mid split tables and the shared
  * expert's output of one decode MoE call with topk <= 8, inter <= 2048 and
- * hidden <= 4096 (164,352 bytes at those maxima). Each GPU holds its own
+ * hidden <= 4096 (165,376 bytes at those maxima). Each GPU holds its own
  * copy until the process ends. Host code uses only the device address that
  * hipGetSymbolAddress returns for it (scratch_ptr, filled at init), never
  * this name. */
-constexpr size_t SCRATCH_BYTES = 164352;
+constexpr size_t SCRATCH_BYTES = 165376;
 __device__ __align__(256) uint8_t scratch[SCRATCH_BYTES];
 constexpr int MAX_DEVICES = 64;
 void *scratch_ptr_of[MAX_DEVICES];       /* device address of `scratch` per device */
@@ -445,8 +445,8 @@ int enqueue_moe(const DSV4ExpertW *table, int n_experts, const int *idx,
             oa.gu = ga;
             oa.dn = da;
             oa.pub.count = m.pub;
-            oa.pub.done = m.pub + 32;
-            oa.pub.leave = m.pub + 64;
+            oa.pub.done = m.pub + ONE_PUB_LINE_WORDS;
+            oa.pub.leave = m.pub + 2 * ONE_PUB_LINE_WORDS;
             /* DSV4_HIP_DECODE_SPIN: most polls of a down workgroup's wait
              * (default 2^20); 0 gives up without polling */
             const char *sp = getenv("DSV4_HIP_DECODE_SPIN");
