@@ -17,7 +17,9 @@
  * PIPELINE (one stream, no host round trip)
  *   k_moe_route     counting sort by expert: first row of each expert's
  *                   bucket (grp_off), prefix of its token tiles (tile_pre),
- *                   each pair's row (pos) and each row's token (row_tok).
+ *                   each pair's row (pos) and each row's token (row_tok);
+ *                   one launch, each workgroup placing its own chunks of
+ *                   1024 pairs after counting all of them.
  *   k_to_f16_rows   x -> fp16 (round to nearest even) after scaling each
  *                   row by the power of two that puts its largest magnitude
  *                   in [2^14, 2^15); the GEMM epilogues undo it exactly.
@@ -171,6 +173,7 @@ __device__ __forceinline__ bool qmat_matches(const DSV4QMat &m, int rows, int co
  * once: their loads are all issued before the first is used, so a pass over
  * them waits out one memory latency instead of one per chunk. */
 constexpr int ROUTE_BATCH = 32;
+constexpr int ROUTE_MAX_BLOCKS = 256;
 
 __device__ __forceinline__ void route_load(int (&ev)[ROUTE_BATCH], const RouteArgs &a, int c0, int nch,
                                            int tid)
@@ -198,17 +201,36 @@ __device__ __forceinline__ uint64_t same_id_lanes(int e, int E)
     return peers;
 }
 
-__global__ __launch_bounds__(1024) void k_moe_route(RouteArgs a)
+/* The wave's count of this lane's expert when this lane is the highest of
+ * that expert's lanes, else 0: one LDS add per expert and wave rather than
+ * one per pair, so a popular expert's counter is not hammered by every lane.
+ * Called by every lane of the wave (it ballots). */
+__device__ __forceinline__ int route_leader_count(int e, int E, uint64_t below)
 {
-    __shared__ int hist[MAX_ROUTE_EXPERTS];
+    const uint64_t peers = same_id_lanes(e, E);
+    const int n = __popcll(peers);
+    return ((unsigned)e < (unsigned)E && __popcll(peers & below) == n - 1) ? n : 0;
+}
+
+/* Stable counting sort of the pairs by expert, in one launch of up to
+ * ROUTE_MAX_BLOCKS workgroups. Pairs go in chunks of 1024; workgroup b places
+ * chunks [b * cpb, (b + 1) * cpb). Every workgroup counts every pair (the
+ * bucket sizes, and how many of each expert precede its first chunk), so no
+ * workgroup waits for another; workgroup 0 also writes grp_off, tile_pre and
+ * tile_grp and reports bad ids. */
+__global__ __launch_bounds__(1024) void k_moe_route(RouteArgs a, int cpb)
+{
+    __shared__ int hist[MAX_ROUTE_EXPERTS], before[MAX_ROUTE_EXPERTS];
     __shared__ int cur[MAX_ROUTE_EXPERTS];
     __shared__ int scan_r[MAX_ROUTE_EXPERTS], scan_t[MAX_ROUTE_EXPERTS];
     __shared__ unsigned short wcnt[16][MAX_ROUTE_EXPERTS];
     const int tid = threadIdx.x;
     const int E = a.n_experts;
     const int nch = (a.npairs + 1023) / 1024;
+    const int c_lo = blockIdx.x * cpb, c_hi = min(nch, c_lo + cpb);
     for (int e = tid; e < MAX_ROUTE_EXPERTS; e += 1024) {
         hist[e] = 0;
+        before[e] = 0;
         for (int w = 0; w < 16; w++) wcnt[w][e] = 0;
     }
     __syncthreads();
@@ -216,19 +238,17 @@ __global__ __launch_bounds__(1024) void k_moe_route(RouteArgs a)
     int ev[ROUTE_BATCH];
     const int lane = tid & 63, wv = tid >> 6;
     const uint64_t below = lane ? (~0ull >> (64 - lane)) : 0ull;
-    /* bucket sizes: one LDS add per expert and wave (the highest of its
-     * lanes adds their count) rather than one per pair, so a popular
-     * expert's counter is not hammered by every lane */
     for (int c0 = 0; c0 < nch; c0 += ROUTE_BATCH) {
         route_load(ev, a, c0, nch, tid);
 #pragma unroll
         for (int i = 0; i < ROUTE_BATCH; i++) {
             if (c0 + i >= nch) break;                              /* uniform */
             const int p = (c0 + i) * 1024 + tid;
-            const uint64_t peers = same_id_lanes(ev[i], E);
-            if ((unsigned)ev[i] < (unsigned)E) {
-                if (__popcll(peers & below) == __popcll(peers) - 1) atomicAdd(&hist[ev[i]], __popcll(peers));
-            } else if (p < a.npairs) {
+            const int n = route_leader_count(ev[i], E, below);
+            if (n) {
+                atomicAdd(&hist[ev[i]], n);
+                if (c0 + i < c_lo) atomicAdd(&before[ev[i]], n);
+            } else if ((unsigned)ev[i] >= (unsigned)E && p < a.npairs) {
                 bad = ST_BAD_EXPERT_ID;
             }
         }
@@ -249,28 +269,39 @@ __global__ __launch_bounds__(1024) void k_moe_route(RouteArgs a)
         scan_t[tid] += xt;
         __syncthreads();
     }
+    /* each tile's bucket: the first expert whose inclusive tile prefix
+     * exceeds it, tiles spread over every workgroup's threads */
+    for (int t = blockIdx.x * 1024 + tid; t < scan_t[E - 1]; t += gridDim.x * 1024) {
+        int lo = 0, hi = E - 1;
+        while (lo < hi) {
+            const int mid = (lo + hi) >> 1;
+            if (scan_t[mid] > t) hi = mid;
+            else lo = mid + 1;
+        }
+        a.tile_grp[t] = lo;
+    }
     if (tid < E) {
         const int o = scan_r[tid] - cnt;
-        a.grp_off[tid] = o;
-        a.tile_pre[tid] = scan_t[tid] - tls;
-        cur[tid] = o;
-        for (int t = scan_t[tid] - tls; t < scan_t[tid]; t++) a.tile_grp[t] = tid;
-        if (tid == E - 1) {
-            a.grp_off[E] = scan_r[tid];
-            a.tile_pre[E] = scan_t[tid];
+        cur[tid] = o + before[tid];
+        if (blockIdx.x == 0) {
+            a.grp_off[tid] = o;
+            a.tile_pre[tid] = scan_t[tid] - tls;
+            if (tid == E - 1) {
+                a.grp_off[E] = scan_r[tid];
+                a.tile_pre[E] = scan_t[tid];
+            }
         }
     }
     __syncthreads();
     /* Rows inside a bucket in pair order (token-major, k-minor), as the
-     * reference's counting sort places them: pairs go in chunks of 1024; a
-     * pair's row is its bucket's fill before the chunk, plus the pairs of the
-     * same expert in lower waves of the chunk, plus those in lower lanes of
-     * its own wave. */
-    for (int c0 = 0; c0 < nch; c0 += ROUTE_BATCH) {
-        if (nch > ROUTE_BATCH) route_load(ev, a, c0, nch, tid);   /* else still held */
+     * reference's counting sort places them: a pair's row is its bucket's
+     * start, plus the pairs of the same expert in earlier chunks, plus those
+     * in lower waves of its chunk, plus those in lower lanes of its wave. */
+    for (int c0 = c_lo; c0 < c_hi; c0 += ROUTE_BATCH) {
+        route_load(ev, a, c0, c_hi, tid);
 #pragma unroll
         for (int i = 0; i < ROUTE_BATCH; i++) {
-            if (c0 + i >= nch) break;                              /* uniform */
+            if (c0 + i >= c_hi) break;                             /* uniform */
             const int p = (c0 + i) * 1024 + tid;
             const int e = ev[i];
             const bool ok = (unsigned)e < (unsigned)E;
@@ -299,7 +330,7 @@ __global__ __launch_bounds__(1024) void k_moe_route(RouteArgs a)
             __syncthreads();
         }
     }
-    if (bad) atomicOr(a.status, bad);
+    if (bad && blockIdx.x == 0) atomicOr(a.status, bad);
 }
 
 /* One workgroup per row: the row's largest finite magnitude (a fixed-order
@@ -1171,7 +1202,10 @@ __global__ __launch_bounds__(256) void k_moe_combine(CombineArgs a)
 hipError_t moe_route_launch(const RouteArgs &a, hipStream_t st)
 {
     if (a.n_experts < 1 || a.n_experts > MAX_ROUTE_EXPERTS) return hipErrorInvalidValue;
-    hipLaunchKernelGGL(k_moe_route, dim3(1), dim3(1024), 0, st, a);
+    const int nch = (a.npairs + 1023) / 1024;
+    const int cpb = nch > ROUTE_MAX_BLOCKS ? (nch + ROUTE_MAX_BLOCKS - 1) / ROUTE_MAX_BLOCKS : 1;
+    const int blocks = nch > 0 ? (nch + cpb - 1) / cpb : 1;
+    hipLaunchKernelGGL(k_moe_route, dim3(blocks), dim3(1024), 0, st, a, cpb);
     return hipGetLastError();
 }
 

@@ -349,6 +349,7 @@ def test_drop_in_decode_layer_sequence(lib, pkg, oracle):
 
 @pytest.mark.parametrize("n,topk,ne,zipf", [
     (64, 6, 256, 1.1), (4096, 6, 256, 1.1), (1000, 8, 1024, None), (5, 2, 3, None), (1, 1, 1, None),
+    (45000, 6, 256, 1.1),    # 264 chunks of 1024 pairs: two chunks per workgroup
 ])
 def test_route_matches_union_prepare(lib, oracle, n, topk, ne, zipf):
     """ex_off, ex_tok and ex_k of the device counting sort equal the

@@ -6,6 +6,8 @@ body of src/10_compute/dsv4_matmul_fp8.c:102-155) run on the activations the
 GPU multiplies: quantized with the same 1x128 e4m3 rule and dequantized with
 one fp32 multiply (q * s). Tolerance: relative L2 1e-3 on fp32 output; bf16
 output is compared with bf16(oracle) at the same bound."""
+import zlib
+
 import numpy as np
 import pytest
 import torch
@@ -114,6 +116,33 @@ def test_gemm_config_shape_row_sample(lib, pkg, oracle):
     want = bf16_round(oracle_gemm(oracle, np.ascontiguousarray(A[rows]), W, S, n, k, True))
     assert np.all(np.isfinite(got))
     assert rel_l2(got[rows], want) <= REL_L2_TOL
+
+
+# The prefill attention side's FP8 projections at their real shapes
+# (src/00_base/dsv4_weights.h:68-98; called through src/80_prefill/
+# dsv4_prefill_proj.c:36-75 and dsv4_prefill_attn.c:26-110), with the
+# checkpoint's E8M0 block scales: (rows, cols) = (N, K).
+PROJECTIONS = {
+    "wq_a": (1024, 4096), "wq_b": (32768, 1024), "wkv": (512, 4096),
+    "wo_a_group": (1024, 4096), "wo_b": (4096, 8192), "idx_wq_b": (8192, 1024),
+}
+
+
+@pytest.mark.parametrize("name", sorted(PROJECTIONS))
+def test_gemm_prefill_projection_shapes(lib, pkg, oracle, name):
+    """300 tokens (not a tile multiple) through each projection, bf16 in and
+    out as the prefill path runs them; 12 seeded rows against the oracle."""
+    n, k = PROJECTIONS[name]
+    rng = np.random.default_rng(zlib.crc32(name.encode()))
+    m = 300
+    A = bf16_round(rng.standard_normal((m, k)).astype(np.float32))
+    W, S = make_weight(oracle, rng, n, k, f32s=False)
+    got = run_gemm(lib, pkg, A, W, S, n, k, False, out_bf16=1, a_bf16=1)
+    rows = np.sort(rng.choice(m, 12, replace=False))
+    want = bf16_round(oracle_gemm(oracle, np.ascontiguousarray(A[rows]), W, S, n, k, False))
+    assert np.all(np.isfinite(got))
+    e = rel_l2(got[rows], want)
+    assert e <= REL_L2_TOL, f"{name}: rel L2 {e:.3e}"
 
 
 def test_gemm_prequantized_matches_fused(lib, pkg, oracle):
