@@ -480,8 +480,9 @@ def bench_grouped(args, torch, pkg, lib, stream, sp, K, W, cfg):
         "metric": "quant matvec HBM GB/s (% peak); prefill FP4/FP8 GEMM TFLOP/s (% MFMA peak)",
         "n_gpus": 1, "steps": K, "warmup": W, "ms_per_step": round(t_step * 1e3, 5),
         "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
-        "dtype": ("fp4 e2m1 weights x mxfp8 e4m3 tokens and mid on block-scaled MFMA (routed), fp16 "
-                  "MFMA on exactly decoded FP8 (shared), fp32 accumulate") if mx else
+        "dtype": ("fp4 e2m1 weights x mxfp8 e4m3 tokens and mid on block-scaled MFMA (routed), fp8 "
+                  "e4m3 weights x e4m3 1x128 tokens and mid on the FP8 GEMM (shared), fp32 accumulate")
+                 if mx else
                  "fp16 MFMA on exactly decoded FP4 (routed) / FP8 (shared) weights, fp32 accumulate",
         "data": "synthetic (seeded N(0,0.02) experts, bf16 N(0,1) tokens, Zipf(1.1) top-6 routing), "
                 "random-init",
@@ -529,8 +530,8 @@ def bench_grouped(args, torch, pkg, lib, stream, sp, K, W, cfg):
                          "unit": "TFLOP/s", "frac": round(achieved / peak, 4),
                          "traffic": traffic_for(cfg),
                          "kernel": ("moe_grouped_mx_dev call (route, MXFP8 quantize, block-scaled "
-                                    "grouped gate/up, grouped down, shared gate/up + down on fp16 "
-                                    "MFMA, combine)") if mx else
+                                    "grouped gate/up, grouped down, shared 1x128 FP8 quantize, gate and up "
+                                    "GEMMs, SwiGLU + quantize, down GEMM on the side stream, combine)") if mx else
                                    ("moe_grouped_dev call (route, fp16 convert, grouped gate/up, "
                                     "grouped down, shared gate/up + down, combine)"),
                          "flops_per_launch": flops_step, "launch_us": round(t_launch * 1e6, 3),

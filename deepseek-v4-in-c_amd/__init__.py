@@ -36,7 +36,7 @@ EXPORTS = (
     "dsv4_hip_dequant_dev", "dsv4_hip_quant_fp8_blk128_dev",
     "dsv4_hip_quant_fp4_mx_dev", "dsv4_hip_quant_act_fp8_1x128_dev",
     "dsv4_hip_quant_act_mxfp8_dev", "dsv4_hip_synth_normal_dev", "dsv4_hip_moe_route_dev",
-    "dsv4_hip_moe_grouped_mx_mid_dev",
+    "dsv4_hip_moe_grouped_mx_mid_dev", "dsv4_hip_shared_fp8q_mid_dev",
 )
 # the reference-named C mirror (host/dsv4_compute_hip.c)
 MIRROR_EXPORTS = ("dsv4_mmq_n", "dsv4_mmq", "dsv4_expert_forward")
@@ -131,6 +131,8 @@ class Lib:
         L.dsv4_hip_moe_grouped_mx_mid_dev.restype = _I
         L.dsv4_hip_moe_grouped_mx_mid_dev.argtypes = [_P, _P, _P, _P, _P, _I, _P, _I, _P, _I, _I, _I,
                                                       _F, _P]
+        L.dsv4_hip_shared_fp8q_mid_dev.restype = _I
+        L.dsv4_hip_shared_fp8q_mid_dev.argtypes = [_P, _P, _P, _I, _P, _I, _F, _P]
 
     # ------------------------------------------------------------ basics
     def error(self) -> str:
@@ -279,6 +281,11 @@ class Lib:
                                                             x_ptr, n, table_ptr, n_experts, idx_ptr,
                                                             topk, hidden, inter, float(limit), stream),
                    "dsv4_hip_moe_grouped_mx_mid_dev")
+
+    def shared_fp8q_mid_dev(self, mid_ptr, mids_ptr, x_ptr, n, shared: ExpertW, hidden, limit, stream=None):
+        self.check(self.lib.dsv4_hip_shared_fp8q_mid_dev(mid_ptr, mids_ptr, x_ptr, n, C.byref(shared), hidden,
+                                                         float(limit), stream),
+                   "dsv4_hip_shared_fp8q_mid_dev")
 
     def gemm_fp8_dev(self, c_ptr, out_bf16, a_ptr, a_bf16, m, desc: QMat, stream=None):
         self.check(self.lib.dsv4_hip_gemm_fp8_dev(c_ptr, int(bool(out_bf16)), a_ptr,

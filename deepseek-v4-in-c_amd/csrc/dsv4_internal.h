@@ -267,6 +267,10 @@ hipError_t quant_fp8_blk128_launch(uint8_t *W, float *S, const float *w,
 hipError_t quant_act_fp8_1x128_launch(uint8_t *Q, float *S, const void *a,
                                       int n, int k, bool bf16_in, bool s_blk_major,
                                       hipStream_t st);
+/* Q, S (block-major [k/128][n]) = the 1x128 e4m3 quantization of
+ * SwiGLU(gate, up) over [n][k] fp32 rows (k % 128 == 0). */
+hipError_t swiglu_quant_fp8_launch(uint8_t *Q, float *S, const float *gate, const float *up, int n, int k,
+                                   float limit, hipStream_t st);
 hipError_t quant_act_mxfp8_launch(uint8_t *Q, uint8_t *S, const float *a,
                                   int n, int k, hipStream_t st);
 hipError_t synth_normal_launch(float *out, size_t n, uint64_t seed, float sigma,

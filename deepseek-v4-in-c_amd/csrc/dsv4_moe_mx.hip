@@ -143,7 +143,7 @@ __device__ __forceinline__ void wait_vm()
 }
 
 /* LDS slot of logical 16-byte chunk c of staged weight row r / token row t */
-__device__ __forceinline__ int wslot(int r, int c) { return c ^ ((r >> 2) & 3); }
+__device__ __forceinline__ int wslot(int r, int c) { return c ^ ((r >> 1) & 3); }
 __device__ __forceinline__ int bslot(int t, int c) { return c ^ (t & 7); }
 
 __device__ __forceinline__ bool fp4_matches(const DSV4QMat &m, int rows, int cols)

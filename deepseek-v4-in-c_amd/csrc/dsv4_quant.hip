@@ -216,6 +216,29 @@ hipError_t quant_fp8_blk128_launch(uint8_t *W, float *S, const float *w,
  * with a correctly rounded division -- the oracle's rule. The scale of token
  * t, block b goes to S[t][b], or to S[b][t] (S_BLK_MAJOR: one block's scales
  * of consecutive tokens are contiguous, as the GEMM reads them). */
+template <bool S_BLK_MAJOR>
+__device__ __forceinline__ void quant8_1x128(const float (&v)[8], uint8_t *Q, float *S, size_t e, bool live,
+                                             int n, int k)
+{
+    float m = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 8; i++) m = fmaxf(m, fabsf(v[i]));
+#pragma unroll
+    for (int off = 8; off > 0; off >>= 1) m = fmaxf(m, __shfl_xor(m, off));
+    const float sc = m > 0.0f ? m / 448.0f : 1.0f;
+    if (!live) return;
+    if ((threadIdx.x & 15) == 0) {
+        if (S_BLK_MAJOR) S[(e % (size_t)k) / 128 * (size_t)n + e / (size_t)k] = sc;
+        else S[e / 128] = sc;
+    }
+    uint2 out;
+    out.x = hw_e4m3(v[0] / sc) | (hw_e4m3(v[1] / sc) << 8) | (hw_e4m3(v[2] / sc) << 16) |
+            (hw_e4m3(v[3] / sc) << 24);
+    out.y = hw_e4m3(v[4] / sc) | (hw_e4m3(v[5] / sc) << 8) | (hw_e4m3(v[6] / sc) << 16) |
+            (hw_e4m3(v[7] / sc) << 24);
+    *(uint2 *)(Q + e) = out;
+}
+
 template <bool BF16_IN, bool S_BLK_MAJOR>
 __global__ __launch_bounds__(256) void k_quant_act_fp8_1x128(uint8_t *Q, float *S,
                                                             const void *a, int n, int k)
@@ -239,23 +262,35 @@ __global__ __launch_bounds__(256) void k_quant_act_fp8_1x128(uint8_t *Q, float *
         v[0] = x0.x; v[1] = x0.y; v[2] = x0.z; v[3] = x0.w;
         v[4] = x1.x; v[5] = x1.y; v[6] = x1.z; v[7] = x1.w;
     }
-    float m = 0.0f;
-#pragma unroll
-    for (int i = 0; i < 8; i++) m = fmaxf(m, fabsf(v[i]));
-#pragma unroll
-    for (int off = 8; off > 0; off >>= 1) m = fmaxf(m, __shfl_xor(m, off));
-    const float sc = m > 0.0f ? m / 448.0f : 1.0f;
-    if (!live) return;
-    if ((threadIdx.x & 15) == 0) {
-        if (S_BLK_MAJOR) S[(e % (size_t)k) / 128 * (size_t)n + e / (size_t)k] = sc;
-        else S[e / 128] = sc;
-    }
-    uint2 out;
-    out.x = hw_e4m3(v[0] / sc) | (hw_e4m3(v[1] / sc) << 8) | (hw_e4m3(v[2] / sc) << 16) |
-            (hw_e4m3(v[3] / sc) << 24);
-    out.y = hw_e4m3(v[4] / sc) | (hw_e4m3(v[5] / sc) << 8) | (hw_e4m3(v[6] / sc) << 16) |
-            (hw_e4m3(v[7] / sc) << 24);
-    *(uint2 *)(Q + e) = out;
+    quant8_1x128<S_BLK_MAJOR>(v, Q, S, e, live, n, k);
+}
+
+/* mid = SwiGLU(gate, up) (the reference's clamp, dev_swiglu) of [n][k] fp32
+ * rows, quantized by the rule above with block-major scales: the shared
+ * expert's mid on its way into the down GEMM. */
+__global__ __launch_bounds__(256) void k_swiglu_quant_fp8_1x128(uint8_t *Q, float *S, const float *g,
+                                                               const float *u, int n, int k, float limit)
+{
+    const size_t e0 = ((size_t)blockIdx.x * 256 + threadIdx.x) * 8;
+    const bool live = e0 < (size_t)n * k;
+    const size_t e = live ? e0 : 0;
+    const f32x4 g0 = *(const f32x4 *)(g + e), g1 = *(const f32x4 *)(g + e + 4);
+    const f32x4 u0 = *(const f32x4 *)(u + e), u1 = *(const f32x4 *)(u + e + 4);
+    float v[8];
+    v[0] = dev_swiglu(g0.x, u0.x, limit); v[1] = dev_swiglu(g0.y, u0.y, limit);
+    v[2] = dev_swiglu(g0.z, u0.z, limit); v[3] = dev_swiglu(g0.w, u0.w, limit);
+    v[4] = dev_swiglu(g1.x, u1.x, limit); v[5] = dev_swiglu(g1.y, u1.y, limit);
+    v[6] = dev_swiglu(g1.z, u1.z, limit); v[7] = dev_swiglu(g1.w, u1.w, limit);
+    quant8_1x128<true>(v, Q, S, e, live, n, k);
+}
+
+hipError_t swiglu_quant_fp8_launch(uint8_t *Q, float *S, const float *gate, const float *up, int n, int k,
+                                   float limit, hipStream_t st)
+{
+    const size_t lanes = (size_t)n * k / 8;
+    hipLaunchKernelGGL(k_swiglu_quant_fp8_1x128, dim3((unsigned)((lanes + 255) / 256)), dim3(256), 0, st,
+                       Q, S, gate, up, n, k, limit);
+    return hipGetLastError();
 }
 
 hipError_t quant_act_fp8_1x128_launch(uint8_t *Q, float *S, const void *a,

@@ -1049,9 +1049,29 @@ int enqueue_moe_grouped(float *out, const float *x, int n, const DSV4ExpertW *ta
     return 0;
 }
 
+/* An FP8 shared expert over n tokens as the reference's GPU prefill runs it
+ * (src/80_prefill/dsv4_prefill_moe.c:40-58): x quantized 1x128 to e4m3 (xq,
+ * xs), the w1 and w3 GEMMs into fp32 gate and up, SwiGLU with mid's 1x128
+ * quantization in one pass (mq, ms block-major), and the w2 GEMM into ys;
+ * ys == NULL stops after mid. */
+int enqueue_shared_fp8q(float *ys, uint8_t *mq, float *ms, const float *x, int n, const DSV4ExpertW *sh,
+                        int sfmt, int sinter, int hidden, float limit, uint8_t *xq, float *xs, float *gate,
+                        float *up, hipStream_t st)
+{
+    HIPCHK(quant_act_fp8_1x128_launch(xq, xs, x, n, hidden, false, true, st), "shared x FP8 launch");
+    if (enqueue_gemm(gate, 0, xq, xs, n, &sh->w1, sfmt, st) || enqueue_gemm(up, 0, xq, xs, n, &sh->w3, sfmt, st))
+        return -1;
+    HIPCHK(swiglu_quant_fp8_launch(mq, ms, gate, up, n, sinter, limit, st), "shared mid FP8 launch");
+    if (ys && enqueue_gemm(ys, 0, mq, ms, n, &sh->w2, sfmt, st)) return -1;
+    return 0;
+}
+
 /* The prefill MoE on the block-scaled MFMA: tokens and mid in MXFP8, routed
- * GEMMs on FP4 x FP8, the shared expert on the exact fp16 path (side
- * stream), k-order combine. */
+ * GEMMs on FP4 x FP8, k-order combine. The shared expert runs on the side
+ * stream: an FP8 one as the reference's GPU prefill runs it, through the FP8
+ * GEMM with the 1x128 activation quantization (w1 and w3, SwiGLU and mid's
+ * quantization in one pass, w2; src/80_prefill/dsv4_prefill_moe.c:40-58 over
+ * dsv4_prefill_proj.c:17-27), an FP4 one on the exact fp16 path. */
 int enqueue_moe_grouped_mx(float *out, const float *x, int n, const DSV4ExpertW *table,
                            int n_experts, const int *idx, const float *w, int topk,
                            const DSV4ExpertW *shared, int sfmt, int sinter, int hidden, int inter,
@@ -1072,8 +1092,18 @@ int enqueue_moe_grouped_mx(float *out, const float *x, int n, const DSV4ExpertW 
     const size_t o_x8 = take((size_t)n * hidden), o_xs = take((size_t)n * hidden / 32);
     const size_t o_mid = take((size_t)P * inter), o_ms = take((size_t)P * inter / 32);
     const size_t o_y = take((size_t)P * hidden * 4);
+    const bool sh_fp8 = shared && (sfmt == FMT_FP8_E8M0 || sfmt == FMT_FP8_F32S);
     size_t o_x16 = 0, o_ex = 0, o_smid = 0, o_ys = 0;
-    if (shared) {
+    size_t o_sxq = 0, o_sxs = 0, o_sg = 0, o_su = 0, o_smq = 0, o_sms = 0;
+    if (sh_fp8) {
+        o_sxq = take((size_t)n * hidden);
+        o_sxs = take((size_t)n * (hidden / 128) * 4);
+        o_sg = take((size_t)n * sinter * 4);
+        o_su = take((size_t)n * sinter * 4);
+        o_smq = take((size_t)n * sinter);
+        o_sms = take((size_t)n * (sinter / 128) * 4);
+        o_ys = take((size_t)n * hidden * 4);
+    } else if (shared) {
         o_x16 = take((size_t)n * hidden * 2);
         o_ex = take((size_t)n * 4);
         o_smid = take((size_t)n * sinter * 2);
@@ -1095,8 +1125,17 @@ int enqueue_moe_grouped_mx(float *out, const float *x, int n, const DSV4ExpertW 
     HIPCHK(moe_route_launch(ra, st), "route launch");
 
     float *ys = nullptr;
-    if (shared) {
-        /* the shared expert on the side stream: its own fp16 copy of x */
+    if (sh_fp8) {
+        HIPCHK(hipEventRecord(g.fork, st), "fork record");
+        HIPCHK(hipStreamWaitEvent(g.side, g.fork, 0), "fork wait");
+        ys = (float *)(ws + o_ys);
+        if (enqueue_shared_fp8q(ys, ws + o_smq, (float *)(ws + o_sms), x, n, shared, sfmt, sinter, hidden, limit,
+                                ws + o_sxq, (float *)(ws + o_sxs), (float *)(ws + o_sg), (float *)(ws + o_su),
+                                g.side))
+            return -1;
+        HIPCHK(hipEventRecord(g.join, g.side), "join record");
+    } else if (shared) {
+        /* an FP4 shared expert on the side stream: its own fp16 copy of x */
         HIPCHK(hipEventRecord(g.fork, st), "fork record");
         HIPCHK(hipStreamWaitEvent(g.side, g.fork, 0), "fork wait");
         uint16_t *x16 = (uint16_t *)(ws + o_x16), *smid = (uint16_t *)(ws + o_smid);
@@ -1247,6 +1286,32 @@ int dsv4_hip_moe_grouped_mx_mid_dev(uint8_t *mid, uint8_t *mid_s, int *row_tok, 
     ga.K = hidden; ga.N = inter; ga.out = mid; ga.out_s = mid_s; ga.limit = limit; ga.status = g.st;
     HIPCHK(grouped_mx_launch(true, ga, max_tiles, st), "routed gate/up launch");
     return 0;
+}
+
+int dsv4_hip_shared_fp8q_mid_dev(uint8_t *mid, float *mid_s, const float *x, int n,
+                                 const DSV4ExpertW *shared, int hidden, float limit, void *stream)
+{
+    std::lock_guard<std::mutex> lk(g.mu);
+    Range rg("dsv4_hip_shared_fp8q_mid_dev");
+    if (usable()) return -1;
+    dev_call();
+    const char *what = "shared_fp8q_mid_dev";
+    if (!mid || !mid_s || !x || !shared) return fail("%s: NULL pointer", what);
+    if (!aligned16(x) || ((uintptr_t)mid & 7u)) return fail("%s: x must be 16- and mid 8-byte aligned", what);
+    int sfmt, sinter;
+    if (grouped_checks(n, 1, 1, hidden, 128, shared, &sfmt, &sinter, what)) return -1;
+    if (sfmt != FMT_FP8_E8M0 && sfmt != FMT_FP8_F32S) return fail("%s: the shared expert must be FP8", what);
+    if ((size_t)n * hidden >= (1u << 31) || (size_t)n * sinter >= (1u << 31))
+        return fail("%s: %d tokens exceed 31-bit offsets", what, n);
+    size_t off = 0;
+    auto take = [&](size_t b) { const size_t o = off; off += (b + 255) & ~(size_t)255; return o; };
+    const size_t o_xq = take((size_t)n * hidden), o_xs = take((size_t)n * (hidden / 128) * 4);
+    const size_t o_g = take((size_t)n * sinter * 4), o_u = take((size_t)n * sinter * 4);
+    HIPCHK(g.moe_ws.need(off), "shared workspace");
+    uint8_t *ws = (uint8_t *)g.moe_ws.p;
+    return enqueue_shared_fp8q(nullptr, mid, mid_s, x, n, shared, sfmt, sinter, hidden, limit, ws + o_xq,
+                               (float *)(ws + o_xs), (float *)(ws + o_g), (float *)(ws + o_u),
+                               (hipStream_t)stream);
 }
 
 int dsv4_hip_moe_grouped(float *out, const float *x, int n, const int *topk_idx,

@@ -69,6 +69,14 @@ int dsv4_hip_moe_grouped_mx_mid_dev(uint8_t *mid, uint8_t *mid_s, int *row_tok, 
                                     int n_experts, const int *idx, int topk, int hidden, int inter,
                                     float limit, void *stream);
 
+/* The FP8 shared expert's mid as dsv4_hip_moe_grouped_mx_dev computes it on
+ * its side stream: x [n][hidden] quantized 1x128 to e4m3, the w1 / w3 FP8
+ * GEMMs, SwiGLU (clamp `limit`) and mid's own 1x128 quantization: mid
+ * [n][inter] e4m3 and mid_s [inter / 128][n] fp32 scales (block-major).
+ * Device arrays; x 16-byte and mid 8-byte aligned. */
+int dsv4_hip_shared_fp8q_mid_dev(uint8_t *mid, float *mid_s, const float *x, int n,
+                                 const DSV4ExpertW *shared, int hidden, float limit, void *stream);
+
 /* out[i] = sigma * N(0,1) sample i of stream `seed` (counter-based splitmix64
  * hash -> Box-Muller in double -> fp32), rounded to bf16 when round_bf16. */
 int dsv4_hip_synth_normal_dev(float *out, size_t n, uint64_t seed, float sigma,

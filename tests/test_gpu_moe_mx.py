@@ -10,9 +10,14 @@ fp32, and fed to the reference's CPU arithmetic restated: fp4_n for w1 / w3
 (src/10_compute/dsv4_matmul_fp4.c:46-162), dsv4_swiglu
 (src/10_compute/dsv4_ops.c:61-79), the same quantization of mid, fp4_n for
 w2, and the k-order combine with the shared expert (exact fp32 path) added
-unweighted (src/80_prefill/dsv4_prefill_union_run.c:109-121). Tolerance:
-relative L2 1e-3 per token. Against the oracle on the unquantized tokens the
-error is the MXFP8 rounding itself; it is reported, and bounded loosely."""
+unweighted (src/80_prefill/dsv4_prefill_union_run.c:109-121). An FP8
+shared expert runs, as in the reference's GPU prefill
+(src/80_prefill/dsv4_prefill_moe.c:40-58), through the FP8 GEMM with the
+1x128 activation quantization: its oracle quantizes x and mid with that rule
+(orc_quant_act_fp8_1x128) and feeds the dequantized values to fp8_n; an FP4
+shared expert runs exactly. Tolerance: relative L2 1e-3 per token. Against
+the oracle on the unquantized tokens the error is the rounding of the
+activations itself; it is reported, and bounded loosely."""
 import numpy as np
 import pytest
 import torch
@@ -36,6 +41,53 @@ def mx_dequant(oracle, Q, S, k):
     v = _E4M3["t"][Q].reshape(k // 32, 32)
     sc = np.ldexp(np.float32(1.0), S.astype(np.int32) - 127).astype(np.float32)
     return np.ascontiguousarray((v * sc[:, None]).reshape(k), np.float32)
+
+
+def fp8_dequant(oracle, Q, S, k):
+    """1x128 e4m3 codes and fp32 scales of one row -> fp32 (q * s)."""
+    if "t" not in _E4M3:
+        _E4M3["t"] = np.array([oracle.e4m3(b) for b in range(256)], np.float32)
+    v = _E4M3["t"][Q].reshape(k // 128, 128)
+    return np.ascontiguousarray((v * S.reshape(k // 128, 1)).reshape(k), np.float32)
+
+
+def is_fp8(hs):
+    return hs is not None and hs.w1.wdt in (P.DSV4_WFP8, P.DSV4_WFP8_F32S)
+
+
+def shared_stages(oracle, hs, xt, limit, gq, gs):
+    """The FP8 shared expert as the MX call runs it, in two stages like the
+    routed mid. Stage 1: the GPU's mid codes gq (scales gs) against the
+    oracle's 1x128 quantization of dsv4_swiglu(fp8_n(w1, x'), fp8_n(w3, x')),
+    x' being x quantized and dequantized by the same rule: equal codes but
+    for pairs of fp32 values that straddle a rounding tie (one grid step,
+    three in the subnormal range), and the fp32 scales within 1e-3.
+    Stage 2: fp8_n(w2) on the GPU's own dequantized mid. Returns (shared
+    output, codes, differing codes)."""
+    Qx, Sx = oracle.quant_act_fp8_1x128(xt[None, :])
+    xq = fp8_dequant(oracle, Qx, Sx, hs.hidden)
+    m = oracle.swiglu(oracle.mmq_n(hs.w1, xq), oracle.mmq_n(hs.w3, xq), limit)
+    Qm, Sm = oracle.quant_act_fp8_1x128(m[None, :])
+    # fp32 scales (amax / 448): they carry the largest element's rounding
+    rel_s = np.abs(Sm - gs) / np.maximum(np.abs(Sm), np.float32(1e-30))
+    assert np.all(rel_s <= 1e-3), f"shared mid scale {np.max(rel_s):.2e} apart"
+    po, pg = grid_pos(Qm), grid_pos(gq)
+    d = np.abs(po - pg)
+    sub = np.minimum(np.abs(po), np.abs(pg)) < 8
+    assert np.all((d <= 1) | (sub & (d <= 3))), f"shared mid codes {np.max(d)} grid steps apart"
+    return oracle.mmq_n(hs.w2, fp8_dequant(oracle, gq, gs, hs.inter)), Qm.size, int(np.sum(d != 0))
+
+
+def gpu_shared_mid(lib, shared, dx, n, hidden, limit):
+    """The FP8 shared expert's mid as the MX call computes it: codes [n][inter]
+    and scales [n][inter / 128] (token-major)."""
+    inter = shared.he.inter
+    mq = torch.empty(n * inter, dtype=torch.uint8, device=DEV)
+    msc = torch.empty(n * inter // 128, dtype=torch.float32, device=DEV)
+    lib.shared_fp8q_mid_dev(mq.data_ptr(), msc.data_ptr(), dx.data_ptr(), n, shared.desc, hidden, limit)
+    torch.cuda.synchronize()
+    return (mq.cpu().numpy().reshape(n, inter),
+            np.ascontiguousarray(msc.cpu().numpy().reshape(inter // 128, n).T))
 
 
 def gpu_mid(lib, tbl_ptr, n_exp, dx, di, n, topk, hidden, inter, limit):
@@ -64,7 +116,7 @@ def grid_pos(q):
 
 
 def check_mx(oracle, hexperts, hshared, x, idx, w, got, mid, ms, pos, tokens, limit=10.0,
-             strict=True):
+             strict=True, smid=None):
     """Stage 1 (gate/up): the GPU's mid codes equal the oracle's MXFP8
     quantization of the oracle's SwiGLU on the dequantized tokens, except
     where the two fp32 values (the MFMA and the AVX2 tree sum in different
@@ -76,17 +128,25 @@ def check_mx(oracle, hexperts, hshared, x, idx, w, got, mid, ms, pos, tokens, li
     steps for mid values near the clamp; then each dequantized row is held
     to 2e-2 of the oracle's instead.
     Stage 2 (down + combine): the oracle's fp4_n on the GPU's own mid, k-order
-    combine and shared expert, against the GPU output at 1e-3 per token.
+    combine and shared expert, against the GPU output at 1e-3 per token. An
+    FP8 shared expert is checked the same way on its own mid (smid, from
+    gpu_shared_mid); an FP4 one exactly.
     Also reported: the error against the oracle on unquantized tokens."""
     n, topk = idx.shape
     hidden = x.shape[1]
     ncode = nbad = nscale = nsbad = 0
+    sh_code = sh_bad = 0
+    assert is_fp8(hshared) == (smid is not None)
     outs, exact = [], []
     for t in tokens:
         Qx, Sx = oracle.quant_act_mxfp8(x[t:t + 1])
         xq = mx_dequant(oracle, Qx, Sx, hidden)
         xt = np.ascontiguousarray(x[t], np.float32)
-        sh = oracle.expert_forward(hshared, xt, limit) if hshared is not None else None
+        sh = sh_exact = oracle.expert_forward(hshared, xt, limit) if hshared is not None else None
+        if smid is not None:
+            sh, c, b = shared_stages(oracle, hshared, xt, limit, smid[0][t], smid[1][t])
+            sh_code += c
+            sh_bad += b
         acc, acc_exact = [], []
         for k in range(topk):
             he = hexperts[int(idx[t, k])]
@@ -111,9 +171,15 @@ def check_mx(oracle, hexperts, hshared, x, idx, w, got, mid, ms, pos, tokens, li
             acc.append(oracle.mmq_n(he.w2, mx_dequant(oracle, mid[r], ms[r], he.inter)))
             acc_exact.append(oracle.expert_forward(he, xt, limit))
         outs.append(oracle.moe_combine(np.stack(acc), w[t], sh))
-        exact.append(oracle.moe_combine(np.stack(acc_exact), w[t], sh))
+        exact.append(oracle.moe_combine(np.stack(acc_exact), w[t], sh_exact))
     assert nbad <= max(2, (1e-3 if strict else 3e-2) * ncode), f"{nbad} of {ncode} mid codes differ"
     assert nsbad <= max(1, 1e-2 * nscale), f"{nsbad} of {nscale} mid scale bytes differ"
+    # The FP8 x FP8 MFMA keeps ~14 bits below a group's largest product, so
+    # the shared gate / up sit ~1.5e-5 (relative L2) from the fp32 tree, about
+    # three times the routed FP4 x FP8 path; more of them straddle an e4m3
+    # tie. Each differing code is still one grid step off (checked above) and
+    # stage 2 runs on the GPU's own mid.
+    assert sh_bad <= max(2, 1e-2 * sh_code), f"{sh_bad} of {sh_code} shared mid codes differ"
     for j, t in enumerate(tokens):
         e = rel_l2(got[t], outs[j])
         assert e <= REL_L2_TOL, f"token {t}: rel L2 {e:.3e} (max abs {max_abs(got[t], outs[j]):.3e})"
@@ -122,7 +188,8 @@ def check_mx(oracle, hexperts, hshared, x, idx, w, got, mid, ms, pos, tokens, li
 
 
 def run_mx(lib, experts, shared, x, idx, w, hidden, inter, limit=10.0):
-    """(full output, GPU mid, mid scales, pair -> row)"""
+    """(full output, GPU mid, mid scales, pair -> row, the FP8 shared
+    expert's mid or None)"""
     n, topk = idx.shape
     tbl = table_of(experts)
     dx = torch.from_numpy(np.ascontiguousarray(x, np.float32)).to(DEV)
@@ -133,32 +200,34 @@ def run_mx(lib, experts, shared, x, idx, w, hidden, inter, limit=10.0):
                            inter, limit)
     torch.cuda.synchronize()
     mid, ms, pos = gpu_mid(lib, tbl.data_ptr(), len(experts), dx, di, n, topk, hidden, inter, limit)
-    return out.cpu().numpy(), mid, ms, pos
+    smid = gpu_shared_mid(lib, shared, dx, n, hidden, limit) if shared is not None and is_fp8(shared.he) else None
+    return out.cpu().numpy(), mid, ms, pos, smid
 
 
 @pytest.mark.parametrize("n,topk,ne,zipf,hidden,inter,with_shared", [
-    (48, 6, 8, None, 512, 256, True),       # one tile per expert, shared expert
-    (600, 4, 5, None, 1024, 512, False),    # ~480 rows per bucket: two 256-row tiles, the last partial
-    (7, 2, 40, None, 512, 256, True),       # one-row buckets, most experts idle
-    (256, 6, 24, 1.1, 2048, 1024, False),   # skewed buckets
+    (48, 6, 8, None, 512, 256, "fp8f32"),   # one tile per expert, FP8 shared expert (fp32 scales)
+    (600, 4, 5, None, 1024, 512, None),     # ~480 rows per bucket: two 256-row tiles, the last partial
+    (7, 2, 40, None, 512, 256, "fp8e8m0"),  # one-row buckets, most experts idle, E8M0 FP8 shared
+    (256, 6, 24, 1.1, 2048, 1024, None),    # skewed buckets
+    (130, 6, 12, None, 512, 384, "fp4"),    # FP4 shared expert (exact path), ragged token count
 ])
 def test_mx_shapes(lib, pkg, oracle, n, topk, ne, zipf, hidden, inter, with_shared):
     gen = torch.Generator().manual_seed(n + ne)
     dgen = torch.Generator(device=DEV).manual_seed(n + ne)
     rng = np.random.default_rng(n * 3 + topk)
     experts = [DevExpert(lib, pkg, "fp4", inter, hidden, dgen) for _ in range(ne)]
-    shared = DevExpert(lib, pkg, "fp8f32", inter, hidden, dgen) if with_shared else None
+    shared = DevExpert(lib, pkg, with_shared, inter, hidden, dgen) if with_shared else None
     x = bf16_rows(gen, n, hidden)
     idx, w = routing(rng, n, topk, ne, zipf=zipf)
     lib.status()
-    got, mid, ms, pos = run_mx(lib, experts, shared, x, idx, w, hidden, inter)
+    got, mid, ms, pos, smid = run_mx(lib, experts, shared, x, idx, w, hidden, inter)
     again = run_mx(lib, experts, shared, x, idx, w, hidden, inter)[0]
     assert lib.status() == 0
     assert np.isfinite(got).all()
     assert np.array_equal(bits(got), bits(again))
     tokens = list(range(n)) if n <= 16 else sorted(rng.choice(n, 16, replace=False).tolist())
     check_mx(oracle, [e.he for e in experts], shared.he if shared else None, x, idx, w, got, mid, ms, pos,
-             tokens)
+             tokens, smid=smid)
 
 
 @pytest.mark.parametrize("limit", [10.0, 0.0])
@@ -171,7 +240,7 @@ def test_mx_swiglu_clamp(lib, pkg, oracle, limit):
     x = torch.randn(n, hidden, generator=torch.Generator().manual_seed(8)).bfloat16().float().numpy()
     rng = np.random.default_rng(9)
     idx, w = routing(rng, n, topk, ne)
-    got, mid, ms, pos = run_mx(lib, experts, None, x, idx, w, hidden, inter, limit)
+    got, mid, ms, pos, _ = run_mx(lib, experts, None, x, idx, w, hidden, inter, limit)
     assert lib.status() == 0
     check_mx(oracle, [e.he for e in experts], None, x, idx, w, got, mid, ms, pos, list(range(0, n, 3)),
              limit, strict=False)
@@ -187,7 +256,7 @@ def test_mx_bad_id(lib, pkg, oracle):
     idx, w = routing(rng, n, topk, ne)
     idx[3, 1] = ne + 5
     lib.status()
-    got, mid, ms, pos = run_mx(lib, experts, None, x, idx, w, hidden, inter)
+    got, mid, ms, pos, _ = run_mx(lib, experts, None, x, idx, w, hidden, inter)
     assert lib.status() & 1
     assert np.isnan(got[3]).all()
     assert pos[3 * topk + 1] == -1
@@ -219,6 +288,11 @@ def test_mx_config4_full_workload_sampled(lib, pkg, oracle):
         torch.cuda.synchronize()
         outs.append(out.cpu().numpy())
     mid, ms, pos = gpu_mid(lib, arena.table.data_ptr(), bench.N_EXPERTS, xs, di, n, topk, H, I, 10.0)
+    smq = torch.empty(n * I, dtype=torch.uint8, device=DEV)
+    sms = torch.empty(n * I // 128, dtype=torch.float32, device=DEV)
+    lib.shared_fp8q_mid_dev(smq.data_ptr(), sms.data_ptr(), xs.data_ptr(), n, shared, H, 10.0)
+    torch.cuda.synchronize()
+    smid = (smq.cpu().numpy().reshape(n, I), np.ascontiguousarray(sms.cpu().numpy().reshape(I // 128, n).T))
     assert lib.status() == 0
     got = outs[0]
     assert np.isfinite(got).all()
@@ -238,4 +312,4 @@ def test_mx_config4_full_workload_sampled(lib, pkg, oracle):
           for i, (r, c) in enumerate(((I, H), (I, H), (H, I)))]
     hshared = P.HostExpert(hm[0], hm[1], hm[2])
     x = xs.view(n, H).cpu().numpy()
-    check_mx(oracle, host, hshared, x, idx, w, got, mid, ms, pos, tokens)
+    check_mx(oracle, host, hshared, x, idx, w, got, mid, ms, pos, tokens, smid=smid)
