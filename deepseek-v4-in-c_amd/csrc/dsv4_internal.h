@@ -345,7 +345,9 @@ struct GroupedMxArgs {
     unsigned *status;
 };
 int grouped_mx_rows_per_tile();
-hipError_t grouped_mx_launch(bool swiglu, const GroupedMxArgs &a, long max_tiles, hipStream_t st);
+/* fat tiles (more than 64 token rows) on `st`, thin tiles on `st_thin` */
+hipError_t grouped_mx_launch(bool swiglu, const GroupedMxArgs &a, long max_tiles, hipStream_t st,
+                             hipStream_t st_thin);
 
 /* out[t] = sum_k w[t][k] * Y[pos[t][k]] (k order) + YS[t] */
 struct CombineArgs {

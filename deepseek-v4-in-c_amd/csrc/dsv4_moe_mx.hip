@@ -108,15 +108,18 @@ struct GX {
 constexpr int GX_TILE = 256;                           /* token rows per bucket tile */
 constexpr int GX_LDS = GX<256>::LDS > GX<128>::LDS ? GX<256>::LDS : GX<128>::LDS;
 
-/* Thin kernel: tiles of at most TH_TOK rows, TH_D stages in flight. LDS
- * holds a ring of TH_D + 1 token stages (128 bytes per token) and two
- * groups of the tokens' scale dwords (TH_G per token and group). */
+/* Thin kernel: tiles of at most TH_TOK rows. A stage covers 256 reduction
+ * indices as two 128-wide halves, TH_D stages in flight. LDS holds a ring of
+ * TH_D + 1 token stages (two halves of 128 bytes per token) and two groups
+ * of the tokens' scale dwords (one dword per half, 2 TH_G per token and
+ * group). */
 constexpr int TH_TOK = 64;
-constexpr int TH_D = 4;                                /* stages in flight             */
-constexpr int TH_G = 4;                                /* stages per scale group       */
-constexpr int TH_B = TH_TOK * 128;                     /* token bytes of a stage       */
-constexpr int TH_LDS = (TH_D + 1) * TH_B + 2 * 1024;   /* token ring + 2 scale groups  */
-constexpr int TH_KQ = 128 * 2 * TH_G;                  /* K granule of the thin kernel */
+constexpr int TH_D = 2;                                /* stages in flight             */
+constexpr int TH_G = 2;                                /* stages per scale group       */
+constexpr int TH_B = TH_TOK * 128;                     /* token bytes of a half        */
+constexpr int TH_SLOT = 2 * TH_B;                      /* token bytes of a stage       */
+constexpr int TH_LDS = (TH_D + 1) * TH_SLOT + 2 * 1024;   /* token ring + 2 scale groups */
+constexpr int TH_KQ = 256 * 2 * TH_G;                  /* K granule of the thin kernel */
 
 constexpr uint32_t RSRC_WORD3 = 0x00020000u;      /* raw dword buffer, gfx9 */
 constexpr uint32_t OOB_OFFSET = 0x80000000u;      /* beyond every buffer    */
@@ -431,9 +434,16 @@ __global__ __launch_bounds__(512) void k_grouped_mx(GroupedMxArgs a, int thin_ro
  * Thin tiles: rows r0 .. r0 + ntok - 1, ntok <= 16 NTG <= 64. Wave w owns
  * row tiles i = 0..3: gate/up w1 rows f0 + 32 w + 16 i (i = 0, 1) and the
  * w3 rows of the same features (i = 2, 3); down w2 rows f0 + 64 w + 16 i.
+ * A stage is 256 reduction indices, two 128-wide halves: 128 bytes of each
+ * weight row, one cache line. A row tile's stage is loaded by two
+ * instructions that each read 8 whole lines (rows 2 r' + j of the tile for
+ * instruction j; lane 16 g + 2 r' + h takes bytes 64 h + 16 g of its row);
+ * a lane-pair exchange (DPP) then forms the MFMA operand of each half, in
+ * which lane 16 g + r holds bytes 64 h + 16 g of row r. Half-line loads (16
+ * rows x 64 bytes per instruction) made the L2 fetch many lines twice.
  * Scales move once per group of TH_G stages: a row's 16 scale bytes of a
  * group are one 16-byte load (lane (rr, gq) then takes byte gq of dword c for
- * stage c of the group), the tokens' scale dwords one 4-byte-per-lane load
+ * half c of the group), the tokens' scale dwords one 4-byte-per-lane load
  * per wave (wave w stages dword w of every token).
  * ---------------------------------------------------------------------- */
 template <bool SWIGLU, int NTG>
@@ -442,15 +452,16 @@ __device__ __forceinline__ void thin_tile(const GroupedMxArgs &a, const DSV4QMat
 {
     constexpr int D = TH_D, G = TH_G, U = 2 * TH_G;
     static_assert(U % D == 0 && D <= G, "ring depth");
-    constexpr int NBL = (2 * NTG + 3) / 4;           /* 8-token loads per wave and stage */
-    constexpr int VMW = 4 + NBL;                     /* VMEM per wave and stage            */
+    static_assert(2 * G == 4, "a scale group is four 128-wide halves: 16 scale bytes per row, one dword per wave");
+    constexpr int NBL = (2 * NTG + 3) / 4;           /* 8-token loads per wave and half  */
+    constexpr int VMW = 8 + 2 * NBL;                 /* VMEM per wave and stage            */
     constexpr int VMG = 4 + 1;                       /* + per group: weight and token scales */
     static_assert((D - 1) * VMW + VMG < 64, "vmcnt range");
     const int lane = threadIdx.x & 63, wave = wave_in_group();
     const int rr = lane & 15, gq = lane >> 4;
     const int K = a.K, N = a.N;
     const uint32_t rowb = (uint32_t)K / 2, srow = (uint32_t)K / 32;
-    const int nst = K / 128, last = nst - 1, glast = nst / G - 1;
+    const int nst = K / 256, last = nst - 1, glast = nst / G - 1;
 
     const __amdgpu_buffer_rsrc_t rw1 = buf_rsrc(m1.w, (uint32_t)N * rowb);
     const __amdgpu_buffer_rsrc_t rs1 = buf_rsrc(m1.s, (uint32_t)N * srow);
@@ -459,15 +470,21 @@ __device__ __forceinline__ void thin_tile(const GroupedMxArgs &a, const DSV4QMat
     const __amdgpu_buffer_rsrc_t rb = buf_rsrc(a.B, (uint32_t)a.nrows * (uint32_t)K);
     const __amdgpu_buffer_rsrc_t rbs = buf_rsrc(a.BS, (uint32_t)a.nrows * srow);
 
-    /* weights: lane (rr, gq) of tile i reads 16 bytes of row rr, k block gq */
-    uint32_t wo[4], so[4];
+    /* weights: instruction j of tile i, lane 16 g + 2 r' + h reads 16 bytes
+     * of row 2 r' + j at byte 64 h + 16 g of the stage's 128; scales: lane
+     * (rr, gq) the 16 scale bytes of row rr */
+    uint32_t wo[4][2], so[4];
+    const bool odd = lane & 1;
 #pragma unroll
     for (int i = 0; i < 4; i++) {
-        const int row = f0 + (SWIGLU ? 32 * wave + 16 * (i & 1) : 64 * wave + 16 * i) + rr;
-        wo[i] = (uint32_t)row * rowb + 16u * (uint32_t)gq;
-        so[i] = (uint32_t)row * srow;
+        const int base = f0 + (SWIGLU ? 32 * wave + 16 * (i & 1) : 64 * wave + 16 * i);
+#pragma unroll
+        for (int j = 0; j < 2; j++)
+            wo[i][j] = (uint32_t)(base + 2 * (rr >> 1) + j) * rowb + 64u * (uint32_t)(lane & 1) +
+                       16u * (uint32_t)gq;
+        so[i] = (uint32_t)(base + rr) * srow;
     }
-    /* tokens: load q = NBL w + j stages token rows 8 q .. 8 q + 7 */
+    /* tokens: load q = NBL w + j of a half stages token rows 8 q .. 8 q + 7 */
     uint32_t bo[NBL];
 #pragma unroll
     for (int j = 0; j < NBL; j++) {
@@ -480,7 +497,7 @@ __device__ __forceinline__ void thin_tile(const GroupedMxArgs &a, const DSV4QMat
     /* token scales: lane t, dword w of the group */
     uint32_t bso = OOB_OFFSET;
     if (lane < ntok) bso = (uint32_t)(a.row_tok ? a.row_tok[r0 + lane] : r0 + lane) * srow + 4u * (uint32_t)wave;
-    uint8_t *const gs = lds + (D + 1) * TH_B;         /* two group slots of [G][64] dwords */
+    uint8_t *const gs = lds + (D + 1) * TH_SLOT;      /* two group slots of [2 G][64] dwords */
 
     f4v acc[4][NTG];
 #pragma unroll
@@ -488,19 +505,24 @@ __device__ __forceinline__ void thin_tile(const GroupedMxArgs &a, const DSV4QMat
 #pragma unroll
         for (int u = 0; u < NTG; u++) acc[i][u] = f4v{0.0f, 0.0f, 0.0f, 0.0f};
 
-    u32x4 aw[D][4];                                  /* stage s in slot s % D          */
+    u32x4 aw[D][2][4];                               /* stage s in slot s % D: [instruction][tile] */
     u32x4 ws[2][4];                                  /* scale group g in slot g % 2    */
 
-    /* The loads of stage t: weights into slot t % D, at the first stage of a
-     * group that group's scales, then the tokens into LDS slot lslot. Stages
-     * past the last repeat it, so every wave and stage issues the same
-     * count of loads. */
-    auto issue = [&](int t, int lslot, u32x4 (&w)[4], u32x4 (&wsg)[4], uint8_t *gslot, bool group) {
+    /* The loads of stage t: weights into slot t % D (both halves of a row
+     * tile back to back), at the first stage of a group that group's scales,
+     * then the tokens of both halves into LDS slot lslot. Stages past the
+     * last repeat it, so every wave and stage issues the same count of
+     * loads. */
+    auto issue = [&](int t, int lslot, u32x4 (&w)[2][4], u32x4 (&wsg)[4], uint8_t *gslot, bool group) {
         const int tc = min(t, last);
-        w[0] = __builtin_amdgcn_raw_buffer_load_b128(rw1, wo[0], tc * 64, 0);
-        w[1] = __builtin_amdgcn_raw_buffer_load_b128(rw1, wo[1], tc * 64, 0);
-        w[2] = __builtin_amdgcn_raw_buffer_load_b128(rw3, wo[2], tc * 64, 0);
-        w[3] = __builtin_amdgcn_raw_buffer_load_b128(rw3, wo[3], tc * 64, 0);
+        w[0][0] = __builtin_amdgcn_raw_buffer_load_b128(rw1, wo[0][0], tc * 128, 0);
+        w[1][0] = __builtin_amdgcn_raw_buffer_load_b128(rw1, wo[0][1], tc * 128, 0);
+        w[0][1] = __builtin_amdgcn_raw_buffer_load_b128(rw1, wo[1][0], tc * 128, 0);
+        w[1][1] = __builtin_amdgcn_raw_buffer_load_b128(rw1, wo[1][1], tc * 128, 0);
+        w[0][2] = __builtin_amdgcn_raw_buffer_load_b128(rw3, wo[2][0], tc * 128, 0);
+        w[1][2] = __builtin_amdgcn_raw_buffer_load_b128(rw3, wo[2][1], tc * 128, 0);
+        w[0][3] = __builtin_amdgcn_raw_buffer_load_b128(rw3, wo[3][0], tc * 128, 0);
+        w[1][3] = __builtin_amdgcn_raw_buffer_load_b128(rw3, wo[3][1], tc * 128, 0);
         if (group) {
             const int g = min(t / G, glast);
             wsg[0] = __builtin_amdgcn_raw_buffer_load_b128(rs1, so[0], g * 16, 0);
@@ -509,9 +531,12 @@ __device__ __forceinline__ void thin_tile(const GroupedMxArgs &a, const DSV4QMat
             wsg[3] = __builtin_amdgcn_raw_buffer_load_b128(rs3, so[3], g * 16, 0);
             bdma4(rbs, bso, g * 16, gslot + 256 * wave);
         }
-        uint8_t *buf = lds + lslot * TH_B;
+        uint8_t *buf = lds + lslot * TH_SLOT;
 #pragma unroll
-        for (int j = 0; j < NBL; j++) bdma16(rb, bo[j], tc * 128, buf + 1024 * (NBL * wave + j));
+        for (int h = 0; h < 2; h++)
+#pragma unroll
+            for (int j = 0; j < NBL; j++)
+                bdma16(rb, bo[j], tc * 256 + h * 128, buf + h * TH_B + 1024 * (NBL * wave + j));
     };
 
 #pragma unroll
@@ -532,29 +557,50 @@ __device__ __forceinline__ void thin_tile(const GroupedMxArgs &a, const DSV4QMat
             wait_vm<(D - 1) * VMW + VMG * (((q % G) + D - 1) / G)>();
             __builtin_amdgcn_s_barrier();
             asm volatile("" ::: "memory");
-            const uint8_t *bb = lds + slot * TH_B;
-            constexpr int p = (q / G) & 1, c = q % G;
-            /* The scale bytes are extracted here and not earlier: an empty
-             * asm that takes each scale dword pins the extraction (and the
-             * wait for its load) behind this stage's barrier, where the
-             * scheduler would otherwise hoist it into an earlier stage and
-             * wait out the loads of the stages between. */
-            int sa[4];
+            constexpr int p = (q / G) & 1;
+            /* operands of both halves: an even lane keeps its own dword of
+             * instruction 0 (half 0) and takes its odd neighbour's (half 1);
+             * an odd lane keeps its own of instruction 1 (half 1) and takes
+             * its even neighbour's (half 0) */
+            u32x4 ah[2][4];
 #pragma unroll
             for (int i = 0; i < 4; i++) {
-                uint32_t w = ws[p][i][c];
-                asm volatile("" : "+v"(w));
-                sa[i] = scale_byte(w, gq);
-            }
-            const uint8_t *gsl = gs + p * 1024 + 256 * c;
+                const u32x4 &x0 = aw[q % D][0][i], &x1 = aw[q % D][1][i];
 #pragma unroll
-            for (int u = 0; u < NTG; u++) {
-                const int t = 16 * u + rr;
-                const v8i b = b_operand(bb, t, gq);
-                const int sb = scale_byte(*(const uint32_t *)(gsl + 4 * t), gq);
-#pragma unroll
-                for (int i = 0; i < 4; i++) acc[i][u] = mfma_mx(aw[q % D][i], b, acc[i][u], sa[i], sb);
+                for (int e = 0; e < 4; e++) {
+                    const uint32_t s0 = (uint32_t)__builtin_amdgcn_mov_dpp((int)x0[e], DPP_QUAD_1032, 0xF, 0xF, false);
+                    const uint32_t s1 = (uint32_t)__builtin_amdgcn_mov_dpp((int)x1[e], DPP_QUAD_1032, 0xF, 0xF, false);
+                    ah[0][i][e] = odd ? s1 : x0[e];
+                    ah[1][i][e] = odd ? x1[e] : s0;
+                }
             }
+            static_for<0, 2>([&](auto hc) {
+                constexpr int h = decltype(hc)::value;
+                constexpr int c = 2 * (q % G) + h;   /* 128-wide half within the scale group */
+                const uint8_t *bb = lds + slot * TH_SLOT + h * TH_B;
+                /* The scale bytes are extracted here and not earlier: an
+                 * empty asm that takes each scale dword pins the extraction
+                 * (and the wait for its load) behind this stage's barrier,
+                 * where the scheduler would otherwise hoist it into an
+                 * earlier stage and wait out the loads of the stages
+                 * between. */
+                int sa[4];
+#pragma unroll
+                for (int i = 0; i < 4; i++) {
+                    uint32_t w = ws[p][i][c];
+                    asm volatile("" : "+v"(w));
+                    sa[i] = scale_byte(w, gq);
+                }
+                const uint8_t *gsl = gs + p * 1024 + 256 * c;
+#pragma unroll
+                for (int u = 0; u < NTG; u++) {
+                    const int t = 16 * u + rr;
+                    const v8i b = b_operand(bb, t, gq);
+                    const int sb = scale_byte(*(const uint32_t *)(gsl + 4 * t), gq);
+#pragma unroll
+                    for (int i = 0; i < 4; i++) acc[i][u] = mfma_mx(ah[h][i], b, acc[i][u], sa[i], sb);
+                }
+            });
             asm volatile("" ::: "memory");
             const int nslot = slot == 0 ? D : slot - 1;
             constexpr int qn = q + D;                /* stage s + D within this or the next iteration */
@@ -591,7 +637,8 @@ __global__ __launch_bounds__(256, 2) void k_grouped_mx_thin(GroupedMxArgs a, int
 int grouped_mx_rows_per_tile() { return GX_TILE; }
 
 template <bool SW>
-static hipError_t grouped_mx_k(const GroupedMxArgs &a, long items, int thin_rows, hipStream_t st)
+static hipError_t grouped_mx_k(const GroupedMxArgs &a, long items, int thin_rows, hipStream_t st,
+                               hipStream_t st_thin)
 {
     static bool attr_done = false;
     if (!attr_done) {
@@ -600,12 +647,13 @@ static hipError_t grouped_mx_k(const GroupedMxArgs &a, long items, int thin_rows
         if (e != hipSuccess) return e;
         attr_done = true;
     }
-    if (thin_rows > 0) hipLaunchKernelGGL((k_grouped_mx_thin<SW>), dim3((unsigned)items), dim3(256), 0, st, a, thin_rows);
+    if (thin_rows > 0) hipLaunchKernelGGL((k_grouped_mx_thin<SW>), dim3((unsigned)items), dim3(256), 0, st_thin, a, thin_rows);
     hipLaunchKernelGGL((k_grouped_mx<SW>), dim3((unsigned)items), dim3(512), GX_LDS, st, a, thin_rows);
     return hipGetLastError();
 }
 
-hipError_t grouped_mx_launch(bool swiglu, const GroupedMxArgs &a, long max_tiles, hipStream_t st)
+hipError_t grouped_mx_launch(bool swiglu, const GroupedMxArgs &a, long max_tiles, hipStream_t st,
+                             hipStream_t st_thin)
 {
     const int feat = swiglu ? 128 : 256;
     if (!a.table || a.N % feat || a.K % 128 || max_tiles <= 0 || a.nrows <= 0 ||
@@ -614,7 +662,8 @@ hipError_t grouped_mx_launch(bool swiglu, const GroupedMxArgs &a, long max_tiles
         return hipErrorInvalidValue;
     const long items = max_tiles * (a.N / feat);
     const int thin_rows = a.K % TH_KQ == 0 ? TH_TOK : 0;   /* the thin ring runs whole groups of stages */
-    return swiglu ? grouped_mx_k<true>(a, items, thin_rows, st) : grouped_mx_k<false>(a, items, thin_rows, st);
+    return swiglu ? grouped_mx_k<true>(a, items, thin_rows, st, st_thin)
+                  : grouped_mx_k<false>(a, items, thin_rows, st, st_thin);
 }
 
 } // namespace dsv4

@@ -74,7 +74,8 @@ struct State {
     int device = -1;
     hipStream_t stream = nullptr;
     hipStream_t side = nullptr;          /* concurrent work of one call (shared expert) */
-    hipEvent_t fork = nullptr, join = nullptr;
+    hipStream_t side2 = nullptr;         /* concurrent work of one call (thin routed tiles) */
+    hipEvent_t fork = nullptr, join = nullptr, fork2 = nullptr, join2 = nullptr;
     unsigned *status = nullptr;          /* status words: [0] _dev calls, [HOST_WORD] host calls */
     unsigned *st = nullptr;              /* the word the call being enqueued raises */
     unsigned *pub = nullptr;             /* one-launch decode: count, done, leave (own lines) */
@@ -515,10 +516,13 @@ int dsv4_hip_init(int device)
                     prop.gcnArchName);
     if (hipSetDevice(device) != hipSuccess) return fail("hipSetDevice failed");
     if (hipStreamCreateWithFlags(&g.stream, hipStreamNonBlocking) != hipSuccess ||
-        hipStreamCreateWithFlags(&g.side, hipStreamNonBlocking) != hipSuccess)
+        hipStreamCreateWithFlags(&g.side, hipStreamNonBlocking) != hipSuccess ||
+        hipStreamCreateWithFlags(&g.side2, hipStreamNonBlocking) != hipSuccess)
         return fail("stream creation failed");
     if (hipEventCreateWithFlags(&g.fork, hipEventDisableTiming) != hipSuccess ||
-        hipEventCreateWithFlags(&g.join, hipEventDisableTiming) != hipSuccess)
+        hipEventCreateWithFlags(&g.join, hipEventDisableTiming) != hipSuccess ||
+        hipEventCreateWithFlags(&g.fork2, hipEventDisableTiming) != hipSuccess ||
+        hipEventCreateWithFlags(&g.join2, hipEventDisableTiming) != hipSuccess)
         return fail("event creation failed");
     if (hipMalloc((void **)&g.status, 256) != hipSuccess) return fail("status alloc failed");
     if (hipMemset(g.status, 0, 256) != hipSuccess) return fail("status clear failed");
@@ -561,10 +565,13 @@ void dsv4_hip_shutdown(void)
     g.pub = nullptr;
     if (g.stream) (void)hipStreamDestroy(g.stream);
     if (g.side) (void)hipStreamDestroy(g.side);
+    if (g.side2) (void)hipStreamDestroy(g.side2);
     if (g.fork) (void)hipEventDestroy(g.fork);
     if (g.join) (void)hipEventDestroy(g.join);
-    g.stream = g.side = nullptr;
-    g.fork = g.join = nullptr;
+    if (g.fork2) (void)hipEventDestroy(g.fork2);
+    if (g.join2) (void)hipEventDestroy(g.join2);
+    g.stream = g.side = g.side2 = nullptr;
+    g.fork = g.join = g.fork2 = g.join2 = nullptr;
     g.ready = 0;
     g.dead = 0;
     g.device = -1;
@@ -606,6 +613,7 @@ int dsv4_hip_unregister(const void *host)
     if (it == g.regions.end()) return fail("unregister: unknown range");
     (void)hipStreamSynchronize(g.stream);
     (void)hipStreamSynchronize(g.side);
+    (void)hipStreamSynchronize(g.side2);
     (void)hipFree(it->second.dev);
     g.regions.erase(it);
     return 0;
@@ -1160,10 +1168,17 @@ int enqueue_moe_grouped_mx(float *out, const float *x, int n, const DSV4ExpertW 
     ga.table = table; ga.n_experts = n_experts; ga.grp_off = grp; ga.tile_pre = tp; ga.tile_grp = tg;
     ga.row_tok = row; ga.B = x8; ga.BS = xs; ga.nrows = n; ga.K = hidden; ga.N = inter;
     ga.out = mid; ga.out_s = ms; ga.limit = limit; ga.status = g.st;
-    HIPCHK(grouped_mx_launch(true, ga, max_tiles, st), "routed gate/up launch");
+    /* thin tiles (weight streaming) on a second side stream, beside the fat
+     * tiles (MFMA) on this one; each down launch reads only mid rows its own
+     * gate/up launch wrote */
+    HIPCHK(hipEventRecord(g.fork2, st), "fork record");
+    HIPCHK(hipStreamWaitEvent(g.side2, g.fork2, 0), "fork wait");
+    HIPCHK(grouped_mx_launch(true, ga, max_tiles, st, g.side2), "routed gate/up launch");
     ga.row_tok = nullptr; ga.B = mid; ga.BS = ms; ga.nrows = (int)P; ga.K = inter; ga.N = hidden;
     ga.out = y; ga.out_s = nullptr;
-    HIPCHK(grouped_mx_launch(false, ga, max_tiles, st), "routed down launch");
+    HIPCHK(grouped_mx_launch(false, ga, max_tiles, st, g.side2), "routed down launch");
+    HIPCHK(hipEventRecord(g.join2, g.side2), "join record");
+    HIPCHK(hipStreamWaitEvent(st, g.join2, 0), "join wait");
 
     if (shared) HIPCHK(hipStreamWaitEvent(st, g.join, 0), "join wait");
     CombineArgs ca;
@@ -1284,7 +1299,7 @@ int dsv4_hip_moe_grouped_mx_mid_dev(uint8_t *mid, uint8_t *mid_s, int *row_tok, 
     ga.table = experts; ga.n_experts = n_experts; ga.grp_off = ra.grp_off; ga.tile_pre = ra.tile_pre;
     ga.tile_grp = ra.tile_grp; ga.row_tok = row_tok; ga.B = ws + o_x8; ga.BS = ws + o_xs; ga.nrows = n;
     ga.K = hidden; ga.N = inter; ga.out = mid; ga.out_s = mid_s; ga.limit = limit; ga.status = g.st;
-    HIPCHK(grouped_mx_launch(true, ga, max_tiles, st), "routed gate/up launch");
+    HIPCHK(grouped_mx_launch(true, ga, max_tiles, st, st), "routed gate/up launch");
     return 0;
 }
 
