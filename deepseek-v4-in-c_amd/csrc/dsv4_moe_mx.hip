@@ -383,23 +383,42 @@ __device__ __forceinline__ void mx_tile(const GroupedMxArgs &a, const DSV4QMat &
                 issue(min(st + C::NST - 1, last), lds + nb * C::STAGE);
             }
             if constexpr (NT > 0) {
+                /* Operands from LDS one token group ahead: the reads of
+                 * group u + 1 are issued before the MFMAs of group u, so
+                 * those MFMAs wait only for group u's reads. */
                 const uint8_t *buf = lds + (st % C::NST) * C::STAGE;
                 u32x4 aw[4];
-                int sa[4];
+                uint32_t swd[4];
 #pragma unroll
                 for (int i = 0; i < 4; i++) {
                     const int r = 16 * blk[i] + rr;
                     aw[i] = *(const u32x4 *)(buf + r * C::WB + 16 * wslot(r, gq));
-                    sa[i] = scale_byte(*(const uint32_t *)(buf + C::OFF_WS + 4 * r), gq);
+                    swd[i] = *(const uint32_t *)(buf + C::OFF_WS + 4 * r);
                 }
-#pragma unroll
-                for (int u = 0; u < NT; u++) {
-                    const int t = HALF * wt + 16 * u + rr;
-                    const v8i b = b_operand(buf + C::OFF_B, t, gq);
-                    const int sb = scale_byte(*(const uint32_t *)(buf + C::OFF_BS + 4 * t), gq);
-#pragma unroll
-                    for (int i = 0; i < 4; i++) acc[i][u] = mfma_mx(aw[i], b, acc[i][u], sa[i], sb);
+                v8i bq[2];
+                uint32_t bsd[2];
+                {
+                    const int t = HALF * wt + rr;
+                    bq[0] = b_operand(buf + C::OFF_B, t, gq);
+                    bsd[0] = *(const uint32_t *)(buf + C::OFF_BS + 4 * t);
                 }
+                DSV4_ORDER();
+                int sa[4];
+#pragma unroll
+                for (int i = 0; i < 4; i++) sa[i] = scale_byte(swd[i], gq);
+                static_for<0, NT>([&](auto uc) {
+                    constexpr int u = decltype(uc)::value;
+                    if constexpr (u + 1 < NT) {
+                        const int t = HALF * wt + 16 * (u + 1) + rr;
+                        bq[(u + 1) & 1] = b_operand(buf + C::OFF_B, t, gq);
+                        bsd[(u + 1) & 1] = *(const uint32_t *)(buf + C::OFF_BS + 4 * t);
+                    }
+                    DSV4_ORDER();
+                    const int sb = scale_byte(bsd[u & 1], gq);
+#pragma unroll
+                    for (int i = 0; i < 4; i++) acc[i][u] = mfma_mx(aw[i], bq[u & 1], acc[i][u], sa[i], sb);
+                    DSV4_ORDER();
+                });
             }
         }
     };
