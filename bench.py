@@ -434,7 +434,7 @@ def bench_grouped(args, torch, pkg, lib, stream, sp, K, W, cfg):
     t_step = e0.elapsed_time(e1) * 1e-3 / K
     t_launch = time_events(torch, stream, lambda i: step(W + i), K)
     other = None
-    if cfg == 4:
+    if cfg == 4 and not args.no_other:
         # the other precision path of the same call, timed the same way
         for i in range(W):
             step_other(i)
@@ -625,6 +625,8 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--cpu-threads", type=int, default=0)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-other", action="store_true",
+                    help="config 4: skip timing the other precision path (counter runs)")
     ap.add_argument("--exact", action="store_true",
                     help="config 4: time the exact fp16-MFMA grouped path instead of the "
                          "block-scaled one")
