@@ -95,14 +95,22 @@ __device__ __forceinline__ uint32_t f32_to_bf16_bits(float f)
     return (u + 0x7FFFu + ((u >> 16) & 1u)) >> 16;
 }
 
-/* global -> LDS, 16 (or 4) bytes per lane, lane l landing at dst + l * size */
-__device__ __forceinline__ void dma16(const void *src, uint8_t *dst)
+constexpr uint32_t RSRC_WORD3 = 0x00020000u;      /* raw dword buffer */
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t buf_rsrc(const void *p, uint32_t bytes)
 {
-    __builtin_amdgcn_global_load_lds(gptr(src), (lds_void *)dst, 16, 0, 0);
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(p), (short)0, (int)bytes, (int)RSRC_WORD3);
 }
-__device__ __forceinline__ void dma4(const void *src, uint8_t *dst)
+/* buffer -> LDS, 16 (or 4) bytes per lane at byte voff + soff, lane l landing
+ * at dst + l * size; the per-block offset soff is a scalar, so a load costs
+ * no vector instruction for its address */
+__device__ __forceinline__ void dma16(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff, uint8_t *dst)
 {
-    __builtin_amdgcn_global_load_lds(gptr(src), (lds_void *)dst, 4, 0, 0);
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_void *)dst, 16, (int)voff, (int)soff, 0, 0);
+}
+__device__ __forceinline__ void dma4(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff, uint8_t *dst)
+{
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_void *)dst, 4, (int)voff, (int)soff, 0, 0);
 }
 
 /* Per-lane offsets, fixed for the whole call; the K block only moves the
@@ -111,6 +119,7 @@ __device__ __forceinline__ void dma4(const void *src, uint8_t *dst)
  * holds logical chunk swz(row, l%8). Wave w issues A instructions 2w, 2w+1
  * and W instructions 4w .. 4w+3. */
 struct Plan {
+    __amdgpu_buffer_rsrc_t ra, rw, rs;   /* A, W and the token scales          */
     uint32_t a[2], w[4];    /* global byte offsets from column 0            */
     uint32_t s;             /* Sa byte offset of this lane's token (waves 0, 1) */
     int w_lo, w_hi;         /* LDS: chunks l/16, l/16 + 4 of weight row l%16 of the wave */
@@ -121,6 +130,9 @@ struct Plan {
 __device__ __forceinline__ Plan make_plan(const GemmArgs &a, int m0, int n0, int wave, int lane)
 {
     Plan d;
+    d.ra = buf_rsrc(a.Aq, (uint32_t)a.M * (uint32_t)a.K);
+    d.rw = buf_rsrc(a.W, (uint32_t)a.N * (uint32_t)a.K);
+    d.rs = buf_rsrc(a.Sa, (uint32_t)(a.K / GK) * (uint32_t)a.sa_kb * 4u + (uint32_t)a.M * (uint32_t)a.sa_tok * 4u);
     const int r8 = lane >> 3, p = lane & 7;
 #pragma unroll
     for (int i = 0; i < 2; i++) {
@@ -150,14 +162,13 @@ __device__ __forceinline__ Plan make_plan(const GemmArgs &a, int m0, int n0, int
 __device__ __forceinline__ void issue_one(const GemmArgs &a, const Plan &d, uint8_t *st, int kb,
                                           int wave, int j)
 {
-    const size_t kofs = (size_t)kb * GK;
+    const uint32_t kofs = (uint32_t)kb * GK;
     if (j < 2) {
-        dma16(a.Aq + kofs + d.a[j], st + ST_A + 1024 * (2 * wave + j));
+        dma16(d.ra, d.a[j], kofs, st + ST_A + 1024 * (2 * wave + j));
     } else if (j < 6) {
-        dma16(a.W + kofs + d.w[j - 2], st + ST_W + 1024 * (4 * wave + j - 2));
+        dma16(d.rw, d.w[j - 2], kofs, st + ST_W + 1024 * (4 * wave + j - 2));
     } else {
-        const uint8_t *sb = (const uint8_t *)a.Sa + (size_t)kb * (size_t)a.sa_kb * 4u;
-        dma4(sb + d.s, st + (wave < 2 ? ST_SA + 256 * wave : ST_PAD));
+        dma4(d.rs, d.s, (uint32_t)kb * (uint32_t)a.sa_kb * 4u, st + (wave < 2 ? ST_SA + 256 * wave : ST_PAD));
     }
 }
 
@@ -213,47 +224,55 @@ __device__ __forceinline__ void promote(v4f &acc, const v4f &p, float cs)
     for (int e = 0; e < 4; e++) acc[e] = fmaf(p[e], cs, acc[e]);
 }
 
-/* What one wave carries from block to block. */
+/* What one wave carries from block to block. Values a block hands to the
+ * next live in two register sets chosen by the block's parity, so nothing
+ * is copied between blocks: block kb (parity P) multiplies with weight
+ * group 3 from w3[P] and loads the next block's into w3[1 - P]; it promotes
+ * with cs[P] and writes the next block's scales to cs[1 - P]; its last two
+ * products land in pc[P], which the next block promotes in its first two
+ * slots with cs[P][2..3]. */
 struct State {
     v4f acc[4][4];              /* [feature group][token group]                */
-    v8i w[4];                   /* weight operands (replaced group by group)   */
-    float cs[4];                /* s_a * s_w of the current block per token group */
-    v4f pc[2];                  /* the previous block's last two products      */
-    float csp[2];               /* their scales                                */
+    v8i w[3];                   /* weight groups 0-2 (replaced group by group) */
+    v8i w3[2];                  /* weight group 3, by block parity             */
+    float cs[2][4];             /* s_a * s_w per token group, by block parity  */
+    v4f pc[2][2];               /* a block's last two products, by parity      */
     float sw_next;              /* weight scale of the next block              */
 };
 
-/* Block kb: MFMA slot s = 4f + t multiplies weight group f by token group t;
- * behind it the product of slot s-2 is promoted (slots 0, 1 promote the
- * previous block's slots 14, 15): an FMA on the product of the MFMA issued
- * just before would stall the matrix pipe. Slots 0 and 1 run from registers; then this wave's loads
- * of stage kb+1 have landed (only block kb+2's are outstanding) and its reads
- * of stage kb are done, and the barrier makes both true for the workgroup:
- * stage kb+1 is read from there on (token groups into bn at slots 2..5, the
- * scales at 6..9, weight group f into w[f] after slot 4f+3, group 3 into its
- * own registers at slot 10) and stage kb is refilled with block kb+3 (one
- * load per slot, 2..8). */
-template <bool WF32S>
+/* Block kb (parity P): MFMA slot s = 4f + t multiplies weight group f by
+ * token group t; behind it the product of slot s-2 is promoted (slots 0, 1
+ * promote the previous block's slots 14, 15): an FMA on the product of the
+ * MFMA issued just before would stall the matrix pipe. Slots 0 and 1 run
+ * from registers; then this wave's loads of stage kb+1 have landed (only
+ * block kb+2's are outstanding) and its reads of stage kb are done, and the
+ * barrier makes both true for the workgroup: stage kb+1 is read from there
+ * on (token groups into bn at slots 2..5, the scales at 6..9, weight group f
+ * into w[f] after slot 4f+3, group 3 into w3[1 - P] at slot 10) and stage kb
+ * is refilled with block kb+3 (one load per slot, 2..8). */
+template <bool WF32S, int P>
 __device__ __forceinline__ void kblock(const GemmArgs &a, const Plan &d, uint8_t *lds, State &S,
                                        const v8i (&b)[4], v8i (&bn)[4], int kb, int nkb, int nb,
                                        int wave)
 {
+    constexpr int Q = 1 - P;
     const int cb = kb % NSTAGE;
     const int nx = cb + 1 == NSTAGE ? 0 : cb + 1;
     const uint8_t *nst = lds + nx * STAGE;
     uint8_t *fill = lds + cb * STAGE;
     const int kl = min(kb + 3, nkb - 1);
-    v4f p[16];
+    v4f p[14];
     float sa[4];
-    v8i w3n;
     float sw2 = 0.0f;
 #pragma unroll
     for (int s = 0; s < 16; s++) {
         const int f = s >> 2, t = s & 3;
-        p[s] = mfma16(S.w[f], b[t]);
+        const v8i &wop = f < 3 ? S.w[f] : S.w3[P];
+        if (s < 14) p[s] = mfma16(wop, b[t]);
+        else S.pc[P][s - 14] = mfma16(wop, b[t]);
         DSV4_ORDER();
-        if (s < 2) promote(S.acc[3][2 + s], S.pc[s], S.csp[s]);
-        else promote(S.acc[(s - 2) >> 2][(s - 2) & 3], p[s - 2], S.cs[(s - 2) & 3]);
+        if (s < 2) promote(S.acc[3][2 + s], S.pc[Q][s], S.cs[Q][2 + s]);
+        else promote(S.acc[(s - 2) >> 2][(s - 2) & 3], p[s - 2], S.cs[P][(s - 2) & 3]);
         if (s == 1) {
             DSV4_ORDER();
             __builtin_amdgcn_s_waitcnt(waitcnt(VM_STAGE, true));
@@ -265,17 +284,12 @@ __device__ __forceinline__ void kblock(const GemmArgs &a, const Plan &d, uint8_t
         if (s == 2) sw2 = weight_scale<WF32S>(a, nb, min(kb + 2, nkb - 1));
         if (s >= 2 && s < 6) bn[s - 2] = read_b(nst, d, s - 2);
         if (s >= 6 && s < 10) sa[s - 6] = *(const float *)(nst + d.sa + 64 * (s - 6));
-        if (s == 10) w3n = read_w(nst, d, 3);
+        if (s == 10) S.w3[Q] = read_w(nst, d, 3);
         if (t == 3 && f < 3) S.w[f] = read_w(nst, d, f);
         DSV4_ORDER();
     }
-    S.w[3] = w3n;
-    S.pc[0] = p[14];
-    S.pc[1] = p[15];
-    S.csp[0] = S.cs[2];
-    S.csp[1] = S.cs[3];
 #pragma unroll
-    for (int t = 0; t < 4; t++) S.cs[t] = sa[t] * S.sw_next;
+    for (int t = 0; t < 4; t++) S.cs[Q][t] = sa[t] * S.sw_next;
     S.sw_next = sw2;
 }
 
@@ -331,15 +345,15 @@ __global__ __launch_bounds__(512) void k_gemm_fp8(GemmArgs a)
     State S;
 #pragma unroll
     for (int e = 0; e < 4; e++) {
-        S.pc[0][e] = 0.0f;
-        S.pc[1][e] = 0.0f;
+        S.pc[1][0][e] = 0.0f;
+        S.pc[1][1][e] = 0.0f;
 #pragma unroll
         for (int f = 0; f < 4; f++)
 #pragma unroll
             for (int t = 0; t < 4; t++) S.acc[f][t][e] = 0.0f;
     }
-    S.csp[0] = 0.0f;
-    S.csp[1] = 0.0f;
+    S.cs[1][2] = 0.0f;
+    S.cs[1][3] = 0.0f;
 
     /* blocks 0, 1, 2 (repeating the last block when K is shorter) */
     issue(a, d, lds, 0, wave);
@@ -357,18 +371,24 @@ __global__ __launch_bounds__(512) void k_gemm_fp8(GemmArgs a)
     v8i b0[4], b1[4];
 #pragma unroll
     for (int q = 0; q < 4; q++) {
-        S.w[q] = read_w(lds, d, q);
+        if (q < 3) S.w[q] = read_w(lds, d, q);
+        else S.w3[0] = read_w(lds, d, 3);
         b0[q] = read_b(lds, d, q);
-        S.cs[q] = *(const float *)(lds + d.sa + 64 * q) * sw0;
+        S.cs[0][q] = *(const float *)(lds + d.sa + 64 * q) * sw0;
     }
     int kb = 0;
     for (; kb + 1 < nkb; kb += 2) {
-        kblock<WF32S>(a, d, lds, S, b0, b1, kb, nkb, nb, wave);
-        kblock<WF32S>(a, d, lds, S, b1, b0, kb + 1, nkb, nb, wave);
+        kblock<WF32S, 0>(a, d, lds, S, b0, b1, kb, nkb, nb, wave);
+        kblock<WF32S, 1>(a, d, lds, S, b1, b0, kb + 1, nkb, nb, wave);
     }
-    if (kb < nkb) kblock<WF32S>(a, d, lds, S, b0, b1, kb, nkb, nb, wave);
-    promote(S.acc[3][2], S.pc[0], S.csp[0]);
-    promote(S.acc[3][3], S.pc[1], S.csp[1]);
+    if (kb < nkb) {
+        kblock<WF32S, 0>(a, d, lds, S, b0, b1, kb, nkb, nb, wave);
+        promote(S.acc[3][2], S.pc[0][0], S.cs[0][2]);
+        promote(S.acc[3][3], S.pc[0][1], S.cs[0][3]);
+    } else {
+        promote(S.acc[3][2], S.pc[1][0], S.cs[1][2]);
+        promote(S.acc[3][3], S.pc[1][1], S.cs[1][3]);
+    }
     /* drain the trailing repeat loads and reads before the ring becomes the
      * output staging area */
     __builtin_amdgcn_s_waitcnt(waitcnt(0, true));
@@ -405,7 +425,7 @@ hipError_t gemm_fp8_launch(const GemmArgs &a, bool w_f32s, bool out_bf16, hipStr
     if (a.K % GK || a.N % 128 || a.M <= 0) return hipErrorInvalidValue;
     /* the loads address A, W and Sa with 32-bit per-lane byte offsets */
     if ((size_t)a.M * a.K > 0xFFFFFFFFull || (size_t)a.N * a.K > 0xFFFFFFFFull ||
-        (size_t)a.M * a.sa_tok * 4 > 0xFFFFFFFFull)
+        (size_t)a.M * a.sa_tok * 4 + (size_t)(a.K / GK) * a.sa_kb * 4 > 0xFFFFFFFFull)
         return hipErrorInvalidValue;
     if (w_f32s) return out_bf16 ? launch_gemm<true, true>(a, st) : launch_gemm<true, false>(a, st);
     return out_bf16 ? launch_gemm<false, true>(a, st) : launch_gemm<false, false>(a, st);
