@@ -584,6 +584,33 @@ def bench_cfg3(args, torch, pkg, lib, stream, sp, K, W):
     t_gemm = time_events(torch, stream, gemm_only, K)
     value = flops / t_step / 1e12
     achieved = flops / t_gemm / 1e12
+    # the same GEMM in the checkpoint's own FP8 format: E8M0 128x128 weight
+    # scales (the power of two at or above each fp32 scale) and MXFP8 tokens,
+    # both in the MFMA's hardware scale operands (dsv4_hip_gemm_mxfp8_dev)
+    Se = torch.from_numpy(fp8_e8m0(torch, Sd)).to(dev)
+    desc_e = pkg.qmat(pkg.DSV4_WFP8, Wd.data_ptr(), Se.data_ptr(), N, KD, 128, 128)
+    Aqm = torch.empty(M * KD, dtype=torch.uint8, device=dev)
+    Asm = torch.empty(M * KD // 32, dtype=torch.uint8, device=dev)
+    lib.quant_act_mxfp8_dev(Aqm.data_ptr(), Asm.data_ptr(), af.data_ptr(), M, KD)
+
+    def step_mx(i):
+        lib.gemm_mxfp8_dev(C.data_ptr(), 1, A.data_ptr(), 1, M, desc_e, sp)
+
+    def gemm_only_mx(i):
+        lib.gemm_mxfp8q_dev(C.data_ptr(), 1, Aqm.data_ptr(), Asm.data_ptr(), M, desc_e, sp)
+
+    for i in range(W):
+        step_mx(i)
+    t_step_mx = time_events(torch, stream, step_mx, K)
+    t_gemm_mx = time_events(torch, stream, gemm_only_mx, K)
+    checkpoint = {"entry": "dsv4_hip_gemm_mxfp8_dev",
+                  "format": "e4m3 W with E8M0 128x128 scales, bf16 A quantized on the fly to MXFP8 "
+                            "(e4m3 + E8M0 per 1x32), bf16 out",
+                  "ms_per_step": round(t_step_mx * 1e3, 5),
+                  "tflops_step": round(flops / t_step_mx / 1e12, 2),
+                  "gemm_launch_us": round(t_gemm_mx * 1e6, 3),
+                  "gemm_tflops": round(flops / t_gemm_mx / 1e12, 2),
+                  "gemm_frac": round(flops / t_gemm_mx / 1e12 / FP8_PEAK_TFLOPS, 4)}
     cpu = None
     if not args.no_cpu:
         # the reference's fp8_n, nt > 1 body (src/10_compute/dsv4_matmul_fp8.c:
@@ -609,6 +636,7 @@ def bench_cfg3(args, torch, pkg, lib, stream, sp, K, W):
                      "traffic": traffic_for(3), "kernel": "k_gemm_fp8<true,true>",
                      "flops_per_launch": flops, "launch_us": round(t_gemm * 1e6, 3)},
         "step_includes": "activation quantization kernel + GEMM kernel",
+        "checkpoint_format": checkpoint,
         "cpu_baseline": cpu,
         "wall_s": round(wall, 4),
     }

@@ -33,6 +33,7 @@ EXPORTS = (
     "dsv4_hip_moe_decode_routed_dev", "dsv4_hip_moe_decode_routed_noalloc_dev",
     "dsv4_hip_moe_grouped", "dsv4_hip_moe_grouped_dev", "dsv4_hip_moe_grouped_mx_dev",
     "dsv4_hip_status", "dsv4_hip_gemm_fp8_dev", "dsv4_hip_gemm_fp8q_dev",
+    "dsv4_hip_gemm_mxfp8_dev", "dsv4_hip_gemm_mxfp8q_dev",
     "dsv4_hip_dequant_dev", "dsv4_hip_quant_fp8_blk128_dev",
     "dsv4_hip_quant_fp4_mx_dev", "dsv4_hip_quant_act_fp8_1x128_dev",
     "dsv4_hip_quant_act_mxfp8_dev", "dsv4_hip_synth_normal_dev", "dsv4_hip_moe_route_dev",
@@ -118,6 +119,10 @@ class Lib:
         L.dsv4_hip_gemm_fp8_dev.argtypes = [_P, _I, _P, _I, _I, C.POINTER(QMat), _P]
         L.dsv4_hip_gemm_fp8q_dev.restype = _I
         L.dsv4_hip_gemm_fp8q_dev.argtypes = [_P, _I, _P, _P, _I, C.POINTER(QMat), _P]
+        L.dsv4_hip_gemm_mxfp8_dev.restype = _I
+        L.dsv4_hip_gemm_mxfp8_dev.argtypes = [_P, _I, _P, _I, _I, C.POINTER(QMat), _P]
+        L.dsv4_hip_gemm_mxfp8q_dev.restype = _I
+        L.dsv4_hip_gemm_mxfp8q_dev.argtypes = [_P, _I, _P, _P, _I, C.POINTER(QMat), _P]
         L.dsv4_hip_dequant_dev.restype = _I
         L.dsv4_hip_dequant_dev.argtypes = [_P, C.POINTER(QMat), _P]
         for n in ("dsv4_hip_quant_fp8_blk128_dev", "dsv4_hip_quant_fp4_mx_dev",
@@ -296,6 +301,16 @@ class Lib:
         self.check(self.lib.dsv4_hip_gemm_fp8q_dev(c_ptr, int(bool(out_bf16)), aq_ptr, sa_ptr,
                                                    m, C.byref(desc), stream),
                    "dsv4_hip_gemm_fp8q_dev")
+
+    def gemm_mxfp8_dev(self, c_ptr, out_bf16, a_ptr, a_bf16, m, desc: QMat, stream=None):
+        self.check(self.lib.dsv4_hip_gemm_mxfp8_dev(c_ptr, int(bool(out_bf16)), a_ptr,
+                                                    int(bool(a_bf16)), m, C.byref(desc), stream),
+                   "dsv4_hip_gemm_mxfp8_dev")
+
+    def gemm_mxfp8q_dev(self, c_ptr, out_bf16, aq_ptr, as_ptr, m, desc: QMat, stream=None):
+        self.check(self.lib.dsv4_hip_gemm_mxfp8q_dev(c_ptr, int(bool(out_bf16)), aq_ptr, as_ptr,
+                                                     m, C.byref(desc), stream),
+                   "dsv4_hip_gemm_mxfp8q_dev")
 
     def dequant_dev(self, out_ptr, desc: QMat, stream=None):
         self.check(self.lib.dsv4_hip_dequant_dev(out_ptr, C.byref(desc), stream),

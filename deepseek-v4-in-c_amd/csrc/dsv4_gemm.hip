@@ -41,6 +41,11 @@
  *   pieces of contiguous rows.
  *
  * Bound: MFMA (2 M N K flops; 68.7 GFLOP at 2048 x 4096 x 4096).
+ *
+ * k_gemm_mx is the same schedule for the checkpoint's own FP8 format, E8M0
+ * 128 x 128 weight scales, with MXFP8 tokens (E8M0 per 32 reduction
+ * indices): both scales go into the MFMA's hardware scale operands, the
+ * MFMA accumulates across K blocks, and no product is promoted.
  */
 #include "dsv4_internal.h"
 
@@ -293,6 +298,71 @@ __device__ __forceinline__ void kblock(const GemmArgs &a, const Plan &d, uint8_t
     S.sw_next = sw2;
 }
 
+/* E8M0 byte of a 128 x 128 weight block (wave-uniform: a scalar load) */
+__device__ __forceinline__ int weight_byte(const GemmArgs &a, int nb, int kb)
+{
+    const uintptr_t p = (uintptr_t)a.Sw + (size_t)nb * (size_t)(a.K / GK) + (size_t)kb;
+    const uint32_t word = ld_uniform((const uint32_t *)(p & ~(uintptr_t)3), 0);
+    return (int)((word >> (8 * (p & 3))) & 0xFFu);
+}
+
+/* What one wave of the hardware-scaled GEMM carries between blocks: the
+ * accumulators (the MFMA accumulates across blocks), the operands of weight
+ * groups 0-2 and group 3 by block parity, and the E8M0 scales: the token
+ * groups' bytes of this lane's 32-element block by parity, the weight
+ * block's byte of this block and the next. */
+struct StateHw {
+    v4f acc[4][4];
+    v8i w[3];
+    v8i w3[2];
+    int tb[2][4];
+    int wb, wb_next;
+};
+
+/* Block kb (parity P) of the hardware-scaled GEMM: E8M0 weight blocks and
+ * MXFP8 tokens both ride in the MFMA's scale operands, so every slot is one
+ * MFMA accumulating into its own accumulator and no vector instruction
+ * promotes a product. Loads, barrier and operand reads follow kblock. */
+template <int P>
+__device__ __forceinline__ void kblock_hw(const GemmArgs &a, const Plan &d, uint8_t *lds, StateHw &S,
+                                          const v8i (&b)[4], v8i (&bn)[4], int kb, int nkb, int nb,
+                                          int wave, int gq)
+{
+    constexpr int Q = 1 - P;
+    const int cb = kb % NSTAGE;
+    const int nx = cb + 1 == NSTAGE ? 0 : cb + 1;
+    const uint8_t *nst = lds + nx * STAGE;
+    uint8_t *fill = lds + cb * STAGE;
+    const int kl = min(kb + 3, nkb - 1);
+    uint32_t sd[4];
+    int wb2 = 0;
+#pragma unroll
+    for (int s = 0; s < 16; s++) {
+        const int f = s >> 2, t = s & 3;
+        const v8i &wop = f < 3 ? S.w[f] : S.w3[P];
+        S.acc[f][t] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(wop, b[t], S.acc[f][t], 0, 0, 0, S.wb,
+                                                                        0, S.tb[P][t]);
+        DSV4_ORDER();
+        if (s == 1) {
+            __builtin_amdgcn_s_waitcnt(waitcnt(VM_STAGE, true));
+            __builtin_amdgcn_s_barrier();
+            asm volatile("" ::: "memory");
+            DSV4_ORDER();
+        }
+        if (s >= 2 && s < 2 + VM_STAGE) issue_one(a, d, fill, kl, wave, s - 2);
+        if (s == 2) wb2 = weight_byte(a, nb, min(kb + 2, nkb - 1));
+        if (s >= 2 && s < 6) bn[s - 2] = read_b(nst, d, s - 2);
+        if (s >= 6 && s < 10) sd[s - 6] = *(const uint32_t *)(nst + d.sa + 64 * (s - 6));
+        if (s == 10) S.w3[Q] = read_w(nst, d, 3);
+        if (t == 3 && f < 3) S.w[f] = read_w(nst, d, f);
+        DSV4_ORDER();
+    }
+#pragma unroll
+    for (int t = 0; t < 4; t++) S.tb[Q][t] = (int)((sd[t] >> (8 * gq)) & 0xFFu);
+    S.wb = S.wb_next;
+    S.wb_next = wb2;
+}
+
 template <bool OUT_BF16>
 __device__ __forceinline__ void stage_frag(uint8_t *lds, const v4f &acc, int tok, int f)
 {
@@ -404,6 +474,83 @@ __global__ __launch_bounds__(512) void k_gemm_fp8(GemmArgs a)
     write_tile<OUT_BF16>(a, lds, m0, n0);
 }
 
+/* C = A W^T with E8M0 128 x 128 weight blocks (the checkpoint's FP8 format)
+ * and MXFP8 tokens (e4m3, one E8M0 per token and 32 reduction indices); the
+ * staged scale dword of a token holds its four 32-blocks of a 128-K block. */
+template <bool OUT_BF16>
+__global__ __launch_bounds__(512) void k_gemm_mx(GemmArgs a)
+{
+    extern __shared__ __align__(16) uint8_t lds[];
+    const int lane = threadIdx.x & 63;
+    const int wave = wave_in_group();
+    const int wm = wave & 1, wn = wave >> 1;
+    const int gq = lane >> 4;
+    const int m0 = blockIdx.y * GM, n0 = blockIdx.x * GN;
+    const int nkb = a.K / GK;
+    const int nb = min((n0 + 64 * wn) / 128, a.N / 128 - 1);
+    const Plan d = make_plan(a, m0, n0, wave, lane);
+
+    StateHw S;
+#pragma unroll
+    for (int f = 0; f < 4; f++)
+#pragma unroll
+        for (int t = 0; t < 4; t++) S.acc[f][t] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+
+    issue(a, d, lds, 0, wave);
+    DSV4_ORDER();
+    issue(a, d, lds + STAGE, min(1, nkb - 1), wave);
+    DSV4_ORDER();
+    issue(a, d, lds + 2 * STAGE, min(2, nkb - 1), wave);
+    DSV4_ORDER();
+    S.wb = weight_byte(a, nb, 0);
+    S.wb_next = weight_byte(a, nb, min(1, nkb - 1));
+    __builtin_amdgcn_s_waitcnt(waitcnt(2 * VM_STAGE, true));
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+
+    v8i b0[4], b1[4];
+#pragma unroll
+    for (int q = 0; q < 4; q++) {
+        if (q < 3) S.w[q] = read_w(lds, d, q);
+        else S.w3[0] = read_w(lds, d, 3);
+        b0[q] = read_b(lds, d, q);
+        S.tb[0][q] = (int)((*(const uint32_t *)(lds + d.sa + 64 * q) >> (8 * gq)) & 0xFFu);
+    }
+    int kb = 0;
+    for (; kb + 1 < nkb; kb += 2) {
+        kblock_hw<0>(a, d, lds, S, b0, b1, kb, nkb, nb, wave, gq);
+        kblock_hw<1>(a, d, lds, S, b1, b0, kb + 1, nkb, nb, wave, gq);
+    }
+    if (kb < nkb) kblock_hw<0>(a, d, lds, S, b0, b1, kb, nkb, nb, wave, gq);
+    __builtin_amdgcn_s_waitcnt(waitcnt(0, true));
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+    const int r16 = lane & 15;
+#pragma unroll
+    for (int f = 0; f < 4; f++)
+#pragma unroll
+        for (int t = 0; t < 4; t++)
+            stage_frag<OUT_BF16>(lds, S.acc[f][t], 64 * wm + 16 * t + r16, 64 * wn + 16 * f + 4 * gq);
+    __syncthreads();
+    write_tile<OUT_BF16>(a, lds, m0, n0);
+}
+
+template <bool OB>
+static hipError_t launch_gemm_mx(const GemmArgs &a, hipStream_t st)
+{
+    static bool attr_done = false;
+    if (!attr_done) {
+        const hipError_t e = hipFuncSetAttribute((const void *)k_gemm_mx<OB>,
+                                                 hipFuncAttributeMaxDynamicSharedMemorySize,
+                                                 lds_bytes(OB));
+        if (e != hipSuccess) return e;
+        attr_done = true;
+    }
+    const dim3 grid((unsigned)((a.N + GN - 1) / GN), (unsigned)((a.M + GM - 1) / GM)), block(512);
+    hipLaunchKernelGGL((k_gemm_mx<OB>), grid, block, lds_bytes(OB), st, a);
+    return hipGetLastError();
+}
+
 template <bool WS, bool OB>
 static hipError_t launch_gemm(const GemmArgs &a, hipStream_t st)
 {
@@ -429,6 +576,15 @@ hipError_t gemm_fp8_launch(const GemmArgs &a, bool w_f32s, bool out_bf16, hipStr
         return hipErrorInvalidValue;
     if (w_f32s) return out_bf16 ? launch_gemm<true, true>(a, st) : launch_gemm<true, false>(a, st);
     return out_bf16 ? launch_gemm<false, true>(a, st) : launch_gemm<false, false>(a, st);
+}
+
+hipError_t gemm_mx_launch(const GemmArgs &a, bool out_bf16, hipStream_t st)
+{
+    if (a.K % GK || a.N % 128 || a.M <= 0 || a.sa_tok != a.K / GK || a.sa_kb != 1)
+        return hipErrorInvalidValue;
+    if ((size_t)a.M * a.K > 0xFFFFFFFFull || (size_t)a.N * a.K > 0xFFFFFFFFull)
+        return hipErrorInvalidValue;
+    return out_bf16 ? launch_gemm_mx<true>(a, st) : launch_gemm_mx<false>(a, st);
 }
 
 } // namespace dsv4

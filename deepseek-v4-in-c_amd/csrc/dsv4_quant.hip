@@ -310,18 +310,33 @@ hipError_t quant_act_fp8_1x128_launch(uint8_t *Q, float *S, const void *a,
     return hipGetLastError();
 }
 
-/* one thread per 1x32 group */
+/* one thread per 1x32 group; fp32 or bf16 (widened exactly) input */
+template <bool BF16_IN>
 __global__ __launch_bounds__(256) void k_quant_act_mxfp8(uint8_t *Q, uint8_t *S,
-                                                        const float *a, int n, int k)
+                                                        const void *a, int n, int k)
 {
     const long g = (long)blockIdx.x * blockDim.x + threadIdx.x;
     if (g >= (long)n * (k / 32)) return;
-    const float *src = a + (size_t)g * 32;
     float v[32], amax = 0.0f;
+    if constexpr (BF16_IN) {
+        const uint16_t *src = (const uint16_t *)a + (size_t)g * 32;
 #pragma unroll
-    for (int i = 0; i < 32; i += 4) {
-        const f32x4 q = *(const f32x4 *)(src + i);
-        v[i] = q.x; v[i + 1] = q.y; v[i + 2] = q.z; v[i + 3] = q.w;
+        for (int i = 0; i < 32; i += 8) {
+            const u32x4 q = *(const u32x4 *)(src + i);
+            const uint32_t w[4] = {q.x, q.y, q.z, q.w};
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                v[i + 2 * j] = __uint_as_float(w[j] << 16);
+                v[i + 2 * j + 1] = __uint_as_float(w[j] & 0xFFFF0000u);
+            }
+        }
+    } else {
+        const float *src = (const float *)a + (size_t)g * 32;
+#pragma unroll
+        for (int i = 0; i < 32; i += 4) {
+            const f32x4 q = *(const f32x4 *)(src + i);
+            v[i] = q.x; v[i + 1] = q.y; v[i + 2] = q.z; v[i + 3] = q.w;
+        }
     }
 #pragma unroll
     for (int i = 0; i < 32; i++) amax = fabsf(v[i]) > amax ? fabsf(v[i]) : amax;
@@ -340,12 +355,15 @@ __global__ __launch_bounds__(256) void k_quant_act_mxfp8(uint8_t *Q, uint8_t *S,
     *(u32x4 *)(Q + (size_t)g * 32 + 16) = o1;
 }
 
-hipError_t quant_act_mxfp8_launch(uint8_t *Q, uint8_t *S, const float *a,
-                                  int n, int k, hipStream_t st)
+hipError_t quant_act_mxfp8_launch(uint8_t *Q, uint8_t *S, const void *a,
+                                  int n, int k, hipStream_t st, bool bf16_in)
 {
     const long groups = (long)n * (k / 32);
-    hipLaunchKernelGGL(k_quant_act_mxfp8, dim3((unsigned)((groups + 255) / 256)), dim3(256), 0, st,
-                       Q, S, a, n, k);
+    const dim3 grid((unsigned)((groups + 255) / 256)), block(256);
+    if (bf16_in)
+        hipLaunchKernelGGL(k_quant_act_mxfp8<true>, grid, block, 0, st, Q, S, a, n, k);
+    else
+        hipLaunchKernelGGL(k_quant_act_mxfp8<false>, grid, block, 0, st, Q, S, a, n, k);
     return hipGetLastError();
 }
 

@@ -970,6 +970,53 @@ int dsv4_hip_gemm_fp8q_dev(void *C, int out_bf16, const uint8_t *Aq, const float
     return enqueue_gemm(C, out_bf16, Aq, Sa, M, W, fmt, (hipStream_t)stream);
 }
 
+/* The hardware-scaled GEMM: W must carry E8M0 128 x 128 block scales. */
+int enqueue_gemm_mx(void *C, int out_bf16, const uint8_t *Aq, const uint8_t *As, int M,
+                    const DSV4QMat *W, hipStream_t st)
+{
+    GemmArgs ga;
+    ga.Aq = Aq; ga.Sa = (const float *)As; ga.W = (const uint8_t *)W->w; ga.Sw = W->s; ga.C = C;
+    ga.M = M; ga.N = W->rows; ga.K = W->cols; ga.ldc = W->rows;
+    ga.sa_tok = W->cols / 128;
+    ga.sa_kb = 1;
+    HIPCHK(gemm_mx_launch(ga, out_bf16 != 0, st), "gemm launch");
+    return 0;
+}
+
+int dsv4_hip_gemm_mxfp8_dev(void *C, int out_bf16, const void *A, int a_bf16, int M,
+                            const DSV4QMat *W, void *stream)
+{
+    std::lock_guard<std::mutex> lk(g.mu);
+    Range rg("dsv4_hip_gemm_mxfp8_dev");
+    if (usable()) return -1;
+    dev_call();
+    int fmt;
+    if (gemm_checks(C, A, M, W, "gemm_mxfp8_dev", &fmt)) return -1;
+    if (fmt != FMT_FP8_E8M0) return fail("gemm_mxfp8_dev: W must carry E8M0 block scales (DSV4_WFP8)");
+    const int K = W->cols;
+    const size_t qbytes = ((size_t)M * K + 255) & ~(size_t)255;
+    HIPCHK(g.gemm_ws.need(qbytes + (size_t)M * (K / 32)), "gemm workspace");
+    uint8_t *Aq = (uint8_t *)g.gemm_ws.p;
+    uint8_t *As = Aq + qbytes;
+    hipStream_t st = (hipStream_t)stream;
+    HIPCHK(quant_act_mxfp8_launch(Aq, As, A, M, K, st, a_bf16 != 0), "activation quant launch");
+    return enqueue_gemm_mx(C, out_bf16, Aq, As, M, W, st);
+}
+
+int dsv4_hip_gemm_mxfp8q_dev(void *C, int out_bf16, const uint8_t *Aq, const uint8_t *As,
+                             int M, const DSV4QMat *W, void *stream)
+{
+    std::lock_guard<std::mutex> lk(g.mu);
+    Range rg("dsv4_hip_gemm_mxfp8q_dev");
+    if (usable()) return -1;
+    dev_call();
+    int fmt;
+    if (gemm_checks(C, Aq, M, W, "gemm_mxfp8q_dev", &fmt)) return -1;
+    if (fmt != FMT_FP8_E8M0) return fail("gemm_mxfp8q_dev: W must carry E8M0 block scales (DSV4_WFP8)");
+    if (!As) return fail("gemm_mxfp8q_dev: NULL scales");
+    return enqueue_gemm_mx(C, out_bf16, Aq, As, M, W, (hipStream_t)stream);
+}
+
 /* ------------------------------------------------------ grouped MoE --- */
 
 /* 16-row tiles when buckets are small (batched decode: few tokens per expert,

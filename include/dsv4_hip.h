@@ -255,6 +255,28 @@ int  dsv4_hip_gemm_fp8q_dev(void *C, int out_bf16, const uint8_t *Aq,
                             const float *Sa, int M, const DSV4QMat *W,
                             void *stream);
 
+/* The prefill GEMM for the checkpoint's own FP8 format: W DSV4_WFP8 with
+ * E8M0 128 x 128 block scales (src/00_base/dsv4_weights.h:34-40; the scales
+ * the reference's packer writes, tools/pack_trunk.py:219-227), replacing the
+ * same seam as dsv4_hip_gemm_fp8_dev (src/80_prefill/dsv4_prefill_vk.h:37-41,
+ * src/80_prefill/dsv4_prefill_proj.c:17-27). A [M][W->cols] fp32 (a_bf16 = 0)
+ * or bf16 (a_bf16 = 1) is quantized on the fly to MXFP8: e4m3 with one E8M0
+ * scale per token and 32 columns (the power of two that keeps the group's
+ * largest magnitude at or below 448). Both scales ride in the MFMA's
+ * hardware scale operands, so the MFMA accumulates across K. C as in
+ * dsv4_hip_gemm_fp8_dev. Numerics: against the reference fed the same
+ * MXFP8-rounded activations, relative L2 1e-3 (typically ~1e-5). 0 enqueued,
+ * -1 otherwise (also for fp32-scaled weights). */
+int  dsv4_hip_gemm_mxfp8_dev(void *C, int out_bf16, const void *A, int a_bf16,
+                             int M, const DSV4QMat *W, void *stream);
+
+/* The same on activations the caller already quantized: Aq [M][W->cols]
+ * e4m3, As [M][W->cols / 32] E8M0 bytes (as dsv4_hip_quant_act_mxfp8_dev
+ * writes them). No workspace. */
+int  dsv4_hip_gemm_mxfp8q_dev(void *C, int out_bf16, const uint8_t *Aq,
+                              const uint8_t *As, int M, const DSV4QMat *W,
+                              void *stream);
+
 /* Read and clear the device status word that the _dev kernels raise when a
  * routing id is out of range (bit 0) or an expert descriptor in the device
  * table does not match the expected format and geometry (bit 1); the affected

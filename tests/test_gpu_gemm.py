@@ -211,3 +211,116 @@ def test_act_quant_1x128_edge_cases(lib, pkg, oracle):
     assert np.array_equal(bits(got_s), bits(So))
     bad = np.nonzero(got_q != Qo)[0]
     assert bad.size == 0, f"{bad.size} codes differ, first at {bad[:4]}: {got_q[bad[:4]]} vs {Qo[bad[:4]]}"
+
+
+# ---------------------------------------------------------------------------
+# The checkpoint-format GEMM (dsv4_hip_gemm_mxfp8_dev / _mxfp8q_dev): E8M0
+# 128x128 weight scales and MXFP8 activations (e4m3 + E8M0 per 1x32), both in
+# the MFMA's hardware scale operands. The oracle is fp8_n on the weights as
+# stored, fed the activations quantized by the oracle's MXFP8 rule and
+# dequantized (q * 2^(s - 127), exact).
+
+def dequant_mx(oracle, Q, S, m, k):
+    vals = e4m3_table(oracle)[Q].reshape(m, k)
+    sc = np.ldexp(np.float32(1.0), S.astype(np.int32) - 127).astype(np.float32).reshape(m, k // 32)
+    return (vals * np.repeat(sc, 32, axis=1)).astype(np.float32)
+
+
+def run_gemm_mx(lib, pkg, A, W, S, n, k, out_bf16, a_bf16):
+    m = A.shape[0]
+    dW, dS = dev(W), dev(S)
+    desc = pkg.qmat(pkg.DSV4_WFP8, dW.data_ptr(), dS.data_ptr(), n, k, 128, 128)
+    dA = torch.from_numpy(A).to(DEV).bfloat16() if a_bf16 else dev(A.astype(np.float32))
+    C = torch.empty((m, n), dtype=torch.bfloat16 if out_bf16 else torch.float32, device=DEV)
+    lib.gemm_mxfp8_dev(C.data_ptr(), out_bf16, dA.data_ptr(), a_bf16, m, desc)
+    torch.cuda.synchronize()
+    return C.float().cpu().numpy()
+
+
+def oracle_gemm_mx(oracle, A, W, S, n, k):
+    m = A.shape[0]
+    Q, Sa = oracle.quant_act_mxfp8(np.ascontiguousarray(A, np.float32))
+    x = dequant_mx(oracle, Q, Sa, m, k).reshape(-1)
+    return oracle.fp8_n(W, S, x, n, k, 128, 128, m).reshape(m, n)
+
+
+@pytest.mark.parametrize("m,n,k", [(256, 512, 1024), (200, 384, 512), (8, 256, 256), (1, 128, 128),
+                                   (130, 640, 768)])
+def test_gemm_mx_fp32_out(lib, pkg, oracle, m, n, k):
+    rng = np.random.default_rng(m * 37 + n + 3 * k)
+    A = bf16_round(rng.standard_normal((m, k)).astype(np.float32))
+    W, S = make_weight(oracle, rng, n, k, f32s=False)
+    got = run_gemm_mx(lib, pkg, A, W, S, n, k, out_bf16=0, a_bf16=0)
+    want = oracle_gemm_mx(oracle, A, W, S, n, k)
+    e = rel_l2(got, want)
+    assert np.all(np.isfinite(got))
+    assert e <= REL_L2_TOL, f"rel L2 {e:.3e} (max abs {max_abs(got, want):.3e})"
+
+
+def test_gemm_mx_outlier_scales(lib, pkg, oracle):
+    """Activation groups spanning 2^-40 .. 2^40 and weight blocks whose E8M0
+    bytes differ by up to 2^20: every scale is a power of two the hardware
+    applies exactly, so the result still meets the bound."""
+    rng = np.random.default_rng(44)
+    m, n, k = 64, 256, 512
+    A = rng.standard_normal((m, k)).astype(np.float32)
+    A *= np.exp2(rng.integers(-40, 41, (m, k // 32))).repeat(32, axis=1).astype(np.float32)
+    A = bf16_round(A)
+    W, S = make_weight(oracle, rng, n, k, f32s=False)
+    S = np.clip(S.astype(np.int32) + rng.integers(-10, 11, S.shape), 1, 254).astype(np.uint8)
+    got = run_gemm_mx(lib, pkg, A, W, S, n, k, out_bf16=0, a_bf16=0)
+    want = oracle_gemm_mx(oracle, A, W, S, n, k)
+    assert np.all(np.isfinite(got))
+    assert rel_l2(got, want) <= REL_L2_TOL
+
+
+def test_gemm_mx_bf16_in_out(lib, pkg, oracle):
+    rng = np.random.default_rng(45)
+    m, n, k = 160, 512, 1024
+    A = bf16_round(rng.standard_normal((m, k)).astype(np.float32))
+    W, S = make_weight(oracle, rng, n, k, f32s=False)
+    a = run_gemm_mx(lib, pkg, A, W, S, n, k, out_bf16=0, a_bf16=0)
+    b = run_gemm_mx(lib, pkg, A, W, S, n, k, out_bf16=0, a_bf16=1)
+    assert np.array_equal(bits(a), bits(b))
+    got = run_gemm_mx(lib, pkg, A, W, S, n, k, out_bf16=1, a_bf16=1)
+    want = bf16_round(oracle_gemm_mx(oracle, A, W, S, n, k))
+    assert rel_l2(got, want) <= REL_L2_TOL
+
+
+def test_gemm_mx_config_shape_row_sample(lib, pkg, oracle):
+    """2048 tokens x 4096 x 4096 with the checkpoint's E8M0 weight scales;
+    24 seeded rows against the oracle."""
+    rng = np.random.default_rng(46)
+    m, n, k = 2048, 4096, 4096
+    A = bf16_round(rng.standard_normal((m, k)).astype(np.float32))
+    W, S = make_weight(oracle, rng, n, k, f32s=False)
+    got = run_gemm_mx(lib, pkg, A, W, S, n, k, out_bf16=1, a_bf16=1)
+    rows = np.sort(rng.choice(m, 24, replace=False))
+    want = bf16_round(oracle_gemm_mx(oracle, np.ascontiguousarray(A[rows]), W, S, n, k))
+    assert np.all(np.isfinite(got))
+    assert rel_l2(got[rows], want) <= REL_L2_TOL
+
+
+def test_gemm_mx_prequantized_matches_fused(lib, pkg, oracle):
+    rng = np.random.default_rng(47)
+    m, n, k = 96, 256, 384
+    A = bf16_round(rng.standard_normal((m, k)).astype(np.float32))
+    W, S = make_weight(oracle, rng, n, k, f32s=False)
+    fused = run_gemm_mx(lib, pkg, A, W, S, n, k, out_bf16=0, a_bf16=0)
+    Q, Sa = oracle.quant_act_mxfp8(A)
+    dW, dS, dQ, dSa = dev(W), dev(S), dev(Q), dev(Sa)
+    desc = pkg.qmat(pkg.DSV4_WFP8, dW.data_ptr(), dS.data_ptr(), n, k, 128, 128)
+    C = torch.empty((m, n), dtype=torch.float32, device=DEV)
+    lib.gemm_mxfp8q_dev(C.data_ptr(), 0, dQ.data_ptr(), dSa.data_ptr(), m, desc)
+    torch.cuda.synchronize()
+    assert np.array_equal(bits(C.cpu().numpy()), bits(fused))
+
+
+def test_gemm_mx_rejects_fp32_scales(lib, pkg):
+    W = torch.zeros(128 * 128, dtype=torch.uint8, device=DEV)
+    S = torch.zeros(1, dtype=torch.float32, device=DEV)
+    A = torch.zeros(128, dtype=torch.float32, device=DEV)
+    C = torch.zeros(128, dtype=torch.float32, device=DEV)
+    desc = pkg.qmat(pkg.DSV4_WFP8_F32S, W.data_ptr(), S.data_ptr(), 128, 128, 128, 128)
+    rc = lib.lib.dsv4_hip_gemm_mxfp8_dev(C.data_ptr(), 0, A.data_ptr(), 0, 1, desc, None)
+    assert rc == -1 and "E8M0" in lib.error()
