@@ -1164,31 +1164,45 @@ __global__ __launch_bounds__(512) void k_grouped3(GroupedArgs a)
 
 /* ------------------------------------------------------------- combine --- */
 
-/* 4 consecutive outputs of one token per thread */
+/* 4 consecutive outputs of one token per thread. The positions and weights
+ * of all k (topk <= 16) are read first and every Y load is issued before the
+ * first is used, so a thread waits one memory latency rather than topk
+ * dependent pairs of them; the sum stays in k order. */
 __global__ __launch_bounds__(256) void k_moe_combine(CombineArgs a)
 {
+    constexpr int KMAX = 16;
     const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
     const int q = a.hidden / 4;
     if (i >= (size_t)a.n * q) return;
     const int t = (int)(i / q), c = (int)(i - (size_t)t * q) * 4;
+    const int topk = a.topk;
+    int p[KMAX];
+    float wk[KMAX];
+#pragma unroll
+    for (int k = 0; k < KMAX; k++) {
+        p[k] = k < topk ? a.pos[(size_t)t * topk + k] : -1;
+        wk[k] = k < topk ? a.w[(size_t)t * topk + k] : 0.0f;
+    }
+    f32x4 v[KMAX];
+    const float nan = __builtin_nanf("");
+#pragma unroll
+    for (int k = 0; k < KMAX; k++) {
+        if (k < topk && p[k] >= 0) v[k] = *(const f32x4 *)(a.Y + (size_t)p[k] * a.hidden + c);
+        else v[k] = f32x4{nan, nan, nan, nan};
+    }
+    f32x4 s = {0.0f, 0.0f, 0.0f, 0.0f};
+    if (a.YS) s = *(const f32x4 *)(a.YS + (size_t)t * a.hidden + c);
     f32x4 o = {0.0f, 0.0f, 0.0f, 0.0f};
-    for (int k = 0; k < a.topk; k++) {
-        const int p = a.pos[(size_t)t * a.topk + k];
-        const float wk = a.w[(size_t)t * a.topk + k];
-        f32x4 v;
-        if (p >= 0) {
-            v = *(const f32x4 *)(a.Y + (size_t)p * a.hidden + c);
-        } else {
-            const float nan = __builtin_nanf("");
-            v = f32x4{nan, nan, nan, nan};
+#pragma unroll
+    for (int k = 0; k < KMAX; k++) {
+        if (k < topk) {
+            o.x = __fadd_rn(o.x, __fmul_rn(wk[k], v[k].x));
+            o.y = __fadd_rn(o.y, __fmul_rn(wk[k], v[k].y));
+            o.z = __fadd_rn(o.z, __fmul_rn(wk[k], v[k].z));
+            o.w = __fadd_rn(o.w, __fmul_rn(wk[k], v[k].w));
         }
-        o.x = __fadd_rn(o.x, __fmul_rn(wk, v.x));
-        o.y = __fadd_rn(o.y, __fmul_rn(wk, v.y));
-        o.z = __fadd_rn(o.z, __fmul_rn(wk, v.z));
-        o.w = __fadd_rn(o.w, __fmul_rn(wk, v.w));
     }
     if (a.YS) {
-        const f32x4 s = *(const f32x4 *)(a.YS + (size_t)t * a.hidden + c);
         o.x = __fadd_rn(o.x, s.x);
         o.y = __fadd_rn(o.y, s.y);
         o.z = __fadd_rn(o.z, s.z);

@@ -310,56 +310,53 @@ hipError_t quant_act_fp8_1x128_launch(uint8_t *Q, float *S, const void *a,
     return hipGetLastError();
 }
 
-/* one thread per 1x32 group; fp32 or bf16 (widened exactly) input */
+/* eight lanes per 1x32 group (four elements each), so a wave reads one
+ * contiguous run of eight groups; fp32 or bf16 (widened exactly) input */
 template <bool BF16_IN>
 __global__ __launch_bounds__(256) void k_quant_act_mxfp8(uint8_t *Q, uint8_t *S,
                                                         const void *a, int n, int k)
 {
-    const long g = (long)blockIdx.x * blockDim.x + threadIdx.x;
-    if (g >= (long)n * (k / 32)) return;
-    float v[32], amax = 0.0f;
-    if constexpr (BF16_IN) {
-        const uint16_t *src = (const uint16_t *)a + (size_t)g * 32;
-#pragma unroll
-        for (int i = 0; i < 32; i += 8) {
-            const u32x4 q = *(const u32x4 *)(src + i);
-            const uint32_t w[4] = {q.x, q.y, q.z, q.w};
-#pragma unroll
-            for (int j = 0; j < 4; j++) {
-                v[i + 2 * j] = __uint_as_float(w[j] << 16);
-                v[i + 2 * j + 1] = __uint_as_float(w[j] & 0xFFFF0000u);
-            }
-        }
-    } else {
-        const float *src = (const float *)a + (size_t)g * 32;
-#pragma unroll
-        for (int i = 0; i < 32; i += 4) {
-            const f32x4 q = *(const f32x4 *)(src + i);
-            v[i] = q.x; v[i + 1] = q.y; v[i + 2] = q.z; v[i + 3] = q.w;
+    const long lid = (long)blockIdx.x * blockDim.x + threadIdx.x;
+    const long g = lid >> 3;
+    const int sub = (int)(lid & 7);
+    const bool live = g < (long)n * (k / 32);
+    float v[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    if (live) {
+        if constexpr (BF16_IN) {
+            const uint2 q = *(const uint2 *)((const uint16_t *)a + (size_t)g * 32 + 4 * sub);
+            v[0] = __uint_as_float(q.x << 16);
+            v[1] = __uint_as_float(q.x & 0xFFFF0000u);
+            v[2] = __uint_as_float(q.y << 16);
+            v[3] = __uint_as_float(q.y & 0xFFFF0000u);
+        } else {
+            const f32x4 q = *(const f32x4 *)((const float *)a + (size_t)g * 32 + 4 * sub);
+            v[0] = q.x; v[1] = q.y; v[2] = q.z; v[3] = q.w;
         }
     }
+    float amax = 0.0f;
 #pragma unroll
-    for (int i = 0; i < 32; i++) amax = fabsf(v[i]) > amax ? fabsf(v[i]) : amax;
+    for (int i = 0; i < 4; i++) amax = fabsf(v[i]) > amax ? fabsf(v[i]) : amax;
+    /* group maximum over the eight lanes (NaN never wins a > compare) */
+#pragma unroll
+    for (int d = 1; d < 8; d <<= 1) {
+        const float o = __shfl_xor(amax, d, 8);
+        amax = o > amax ? o : amax;
+    }
+    if (!live) return;
     const uint32_t sb = mxfp8_scale_byte(amax);
     const int e = (int)sb - 127;
-    S[g] = (uint8_t)sb;
-    u32x4 o0, o1;
+    if (sub == 0) S[g] = (uint8_t)sb;
+    uint32_t word = 0;
 #pragma unroll
-    for (int d = 0; d < 8; d++) {
-        uint32_t word = 0;
-#pragma unroll
-        for (int b = 0; b < 4; b++) word |= q_e4m3(ldexpf(v[4 * d + b], -e)) << (8 * b);
-        if (d < 4) o0[d] = word; else o1[d - 4] = word;
-    }
-    *(u32x4 *)(Q + (size_t)g * 32) = o0;
-    *(u32x4 *)(Q + (size_t)g * 32 + 16) = o1;
+    for (int b = 0; b < 4; b++) word |= q_e4m3(ldexpf(v[b], -e)) << (8 * b);
+    *(uint32_t *)(Q + (size_t)g * 32 + 4 * sub) = word;
 }
 
 hipError_t quant_act_mxfp8_launch(uint8_t *Q, uint8_t *S, const void *a,
                                   int n, int k, hipStream_t st, bool bf16_in)
 {
-    const long groups = (long)n * (k / 32);
-    const dim3 grid((unsigned)((groups + 255) / 256)), block(256);
+    const long lanes = (long)n * (k / 32) * 8;
+    const dim3 grid((unsigned)((lanes + 255) / 256)), block(256);
     if (bf16_in)
         hipLaunchKernelGGL(k_quant_act_mxfp8<true>, grid, block, 0, st, Q, S, a, n, k);
     else
