@@ -34,6 +34,7 @@ EXPORTS = (
     "dsv4_hip_moe_grouped", "dsv4_hip_moe_grouped_dev", "dsv4_hip_moe_grouped_mx_dev",
     "dsv4_hip_status", "dsv4_hip_gemm_fp8_dev", "dsv4_hip_gemm_fp8q_dev",
     "dsv4_hip_gemm_mxfp8_dev", "dsv4_hip_gemm_mxfp8q_dev",
+    "dsv4_hip_load_experts", "dsv4_hip_free_experts",
     "dsv4_hip_dequant_dev", "dsv4_hip_quant_fp8_blk128_dev",
     "dsv4_hip_quant_fp4_mx_dev", "dsv4_hip_quant_act_fp8_1x128_dev",
     "dsv4_hip_quant_act_mxfp8_dev", "dsv4_hip_synth_normal_dev", "dsv4_hip_moe_route_dev",
@@ -123,6 +124,10 @@ class Lib:
         L.dsv4_hip_gemm_mxfp8_dev.argtypes = [_P, _I, _P, _I, _I, C.POINTER(QMat), _P]
         L.dsv4_hip_gemm_mxfp8q_dev.restype = _I
         L.dsv4_hip_gemm_mxfp8q_dev.argtypes = [_P, _I, _P, _P, _I, C.POINTER(QMat), _P]
+        L.dsv4_hip_load_experts.restype = _P
+        L.dsv4_hip_load_experts.argtypes = [C.c_char_p, C.c_char_p, _I, _I, _I, _P, _I, C.POINTER(_I)]
+        L.dsv4_hip_free_experts.restype = _I
+        L.dsv4_hip_free_experts.argtypes = [_P]
         L.dsv4_hip_dequant_dev.restype = _I
         L.dsv4_hip_dequant_dev.argtypes = [_P, C.POINTER(QMat), _P]
         for n in ("dsv4_hip_quant_fp8_blk128_dev", "dsv4_hip_quant_fp4_mx_dev",
@@ -301,6 +306,19 @@ class Lib:
         self.check(self.lib.dsv4_hip_gemm_fp8q_dev(c_ptr, int(bool(out_bf16)), aq_ptr, sa_ptr,
                                                    m, C.byref(desc), stream),
                    "dsv4_hip_gemm_fp8q_dev")
+
+    def load_experts(self, model_dir, index_dir, layer, hidden, inter, max_experts=1024):
+        """(arena, ctypes array of ExpertW with device pointers, n_experts)"""
+        table = (ExpertW * max_experts)()
+        n = _I(0)
+        arena = self.lib.dsv4_hip_load_experts(model_dir.encode(), index_dir.encode(), layer, hidden, inter,
+                                               C.cast(table, C.c_void_p), max_experts, C.byref(n))
+        if not arena:
+            raise Dsv4Error(f"dsv4_hip_load_experts: {self.error()}")
+        return arena, table, n.value
+
+    def free_experts(self, arena):
+        self.check(self.lib.dsv4_hip_free_experts(arena), "dsv4_hip_free_experts")
 
     def gemm_mxfp8_dev(self, c_ptr, out_bf16, a_ptr, a_bf16, m, desc: QMat, stream=None):
         self.check(self.lib.dsv4_hip_gemm_mxfp8_dev(c_ptr, int(bool(out_bf16)), a_ptr,

@@ -27,8 +27,14 @@
 #include <string>
 #include <vector>
 
+#include <algorithm>
+
+#include <dirent.h>
+#include <fcntl.h>
 #include <stdarg.h>
+#include <stdint.h>
 #include <stdlib.h>
+#include <unistd.h>
 #include <stdio.h>
 #include <string.h>
 
@@ -909,6 +915,64 @@ int dsv4_hip_moe_decode_routed_noalloc_dev(float *out, const float *x, const DSV
                        inter, x, out, limit, (hipStream_t)stream, routed, wv, &ws);
 }
 
+/* ------------------------------------------- checkpoint experts (f4) --- */
+
+/* experts.idx record (tools/pack_trunk.py writes "<iiqq"). */
+struct ExpLoc {
+    int32_t shard, pad;
+    int64_t off, nbytes;
+};
+static_assert(sizeof(ExpLoc) == 24, "experts.idx record");
+constexpr int EXP_TENSORS = 6;                 /* w1, w1 scales, w2, w2 scales, w3, w3 scales */
+
+/* The *.safetensors files of dir in strcmp order: shard i of the index. */
+int list_shards(const char *dir, std::vector<std::string> &out)
+{
+    DIR *d = opendir(dir);
+    if (!d) return fail("load_experts: cannot open directory %s", dir);
+    while (struct dirent *e = readdir(d)) {
+        const size_t n = strlen(e->d_name);
+        if (n >= 12 && strcmp(e->d_name + n - 12, ".safetensors") == 0)
+            out.push_back(std::string(dir) + "/" + e->d_name);
+    }
+    closedir(d);
+    if (out.empty()) return fail("load_experts: no .safetensors files in %s", dir);
+    std::sort(out.begin(), out.end(), [](const std::string &a, const std::string &b) {
+        return strcmp(a.c_str(), b.c_str()) < 0;
+    });
+    return 0;
+}
+
+/* The layer's records: n_experts x 6, in the packer's tensor order. */
+int read_expert_index(const char *index_dir, int layer, std::vector<ExpLoc> &loc, int *n_experts)
+{
+    const std::string path = std::string(index_dir) + "/experts.idx";
+    FILE *f = fopen(path.c_str(), "rb");
+    if (!f) return fail("load_experts: cannot open %s", path.c_str());
+    char magic[8];
+    int32_t nl = 0, ne = 0;
+    int rc = 0;
+    if (fread(magic, 1, 8, f) != 8 || memcmp(magic, "DSV4EXP1", 8) != 0)
+        rc = fail("load_experts: %s is not an experts index (magic DSV4EXP1)", path.c_str());
+    else if (fread(&nl, 4, 1, f) != 1 || fread(&ne, 4, 1, f) != 1 || nl <= 0 || ne <= 0)
+        rc = fail("load_experts: %s has a bad header", path.c_str());
+    else if (layer < 0 || layer >= nl)
+        rc = fail("load_experts: layer %d outside 0..%d", layer, nl - 1);
+    if (!rc) {
+        const long rec = (long)ne * EXP_TENSORS;
+        loc.resize((size_t)rec);
+        if (fseek(f, 16 + (long)layer * rec * (long)sizeof(ExpLoc), SEEK_SET) != 0 ||
+            fread(loc.data(), sizeof(ExpLoc), (size_t)rec, f) != (size_t)rec)
+            rc = fail("load_experts: %s is short for layer %d", path.c_str(), layer);
+        *n_experts = ne;
+    }
+    fclose(f);
+    return rc;
+}
+
+/* Device arenas handed out by dsv4_hip_load_experts. */
+std::map<uintptr_t, size_t> g_expert_arenas;
+
 /* Shared checks of the FP8 GEMM entry points; returns the weight format. */
 int gemm_checks(const void *C, const void *A, int M, const DSV4QMat *W, const char *what, int *fmt)
 {
@@ -980,6 +1044,131 @@ int enqueue_gemm_mx(void *C, int out_bf16, const uint8_t *Aq, const uint8_t *As,
     ga.sa_tok = W->cols / 128;
     ga.sa_kb = 1;
     HIPCHK(gemm_mx_launch(ga, out_bf16 != 0, st), "gemm launch");
+    return 0;
+}
+
+void *dsv4_hip_load_experts(const char *model_dir, const char *index_dir, int layer, int hidden,
+                            int inter, DSV4ExpertW *table, int max_experts, int *n_experts)
+{
+    std::lock_guard<std::mutex> lk(g.mu);
+    Range rg("dsv4_hip_load_experts");
+    if (!model_dir || !index_dir || !table || !n_experts) {
+        fail("load_experts: NULL argument");
+        return nullptr;
+    }
+    if (hidden <= 0 || inter <= 0 || hidden % 32 || inter % 32) {
+        fail("load_experts: hidden %d and inter %d must be positive multiples of 32", hidden, inter);
+        return nullptr;
+    }
+    /* the index and the shard list first: a bad checkpoint fails before
+     * any device memory is touched */
+    std::vector<ExpLoc> loc;
+    int ne = 0;
+    if (read_expert_index(index_dir, layer, loc, &ne)) return nullptr;
+    if (ne > max_experts) {
+        fail("load_experts: the index has %d experts, the table holds %d", ne, max_experts);
+        return nullptr;
+    }
+    std::vector<std::string> shards;
+    if (list_shards(model_dir, shards)) return nullptr;
+    /* one slot per expert as the reference's cache lays it out
+     * (src/60_cache/dsv4_cache_geom.c:14-31): scales s1 s2 s3, then weights
+     * w1 w2 w3; slots 4096-byte aligned */
+    const int64_t H = hidden, I = inter;
+    const int64_t wb[3] = {I * (H / 2), H * (I / 2), I * (H / 2)};
+    const int64_t sb[3] = {I * (H / 32), H * (I / 32), I * (H / 32)};
+    int64_t off_s[3], off_w[3], at = 0;
+    for (int i = 0; i < 3; i++) { off_s[i] = at; at += sb[i]; }
+    for (int i = 0; i < 3; i++) { off_w[i] = at; at += wb[i]; }
+    const size_t slot = (size_t)((at + 4095) / 4096 * 4096);
+    /* index order w1 w1s w2 w2s w3 w3s -> (matrix, is scale) */
+    const int mat_of[EXP_TENSORS] = {0, 0, 1, 1, 2, 2};
+    for (int e = 0; e < ne; e++)
+        for (int j = 0; j < EXP_TENSORS; j++) {
+            const ExpLoc &l = loc[(size_t)e * EXP_TENSORS + j];
+            const int64_t want = (j & 1) ? sb[mat_of[j]] : wb[mat_of[j]];
+            if (l.shard < 0 || l.shard >= (int)shards.size() || l.off < 0 || l.nbytes != want) {
+                fail("load_experts: layer %d expert %d tensor %d: shard %d, %lld bytes (want %lld, %zu shards)",
+                     layer, e, j, l.shard, (long long)l.nbytes, (long long)want, shards.size());
+                return nullptr;
+            }
+        }
+    if (usable()) return nullptr;
+    std::vector<int> fds(shards.size(), -1);
+    auto close_all = [&]() { for (int fd : fds) if (fd >= 0) close(fd); };
+    for (size_t i = 0; i < shards.size(); i++) {
+        fds[i] = open(shards[i].c_str(), O_RDONLY);
+        if (fds[i] < 0) {
+            close_all();
+            fail("load_experts: cannot open %s", shards[i].c_str());
+            return nullptr;
+        }
+    }
+    uint8_t *arena = nullptr, *stage = nullptr;
+    if (hipMalloc((void **)&arena, slot * (size_t)ne) != hipSuccess ||
+        hipHostMalloc((void **)&stage, slot, hipHostMallocDefault) != hipSuccess) {
+        if (arena) (void)hipFree(arena);
+        close_all();
+        fail("load_experts: cannot allocate %zu bytes of device arena", slot * (size_t)ne);
+        return nullptr;
+    }
+    bool ok = true;
+    for (int e = 0; e < ne && ok; e++) {
+        for (int j = 0; j < EXP_TENSORS && ok; j++) {
+            const ExpLoc &l = loc[(size_t)e * EXP_TENSORS + j];
+            uint8_t *dst = stage + ((j & 1) ? off_s[mat_of[j]] : off_w[mat_of[j]]);
+            int64_t done = 0;
+            while (done < l.nbytes) {
+                const ssize_t r = pread(fds[(size_t)l.shard], dst + done, (size_t)(l.nbytes - done),
+                                        (off_t)(l.off + done));
+                if (r <= 0) {
+                    ok = false;
+                    fail("load_experts: short read of layer %d expert %d tensor %d from %s", layer, e, j,
+                         shards[(size_t)l.shard].c_str());
+                    break;
+                }
+                done += r;
+            }
+        }
+        if (ok && hipMemcpy(arena + (size_t)e * slot, stage, (size_t)at, hipMemcpyHostToDevice) != hipSuccess) {
+            ok = false;
+            fail("load_experts: upload of expert %d failed", e);
+        }
+    }
+    close_all();
+    (void)hipHostFree(stage);
+    if (!ok) {
+        (void)hipFree(arena);
+        return nullptr;
+    }
+    const int64_t rows[3] = {I, H, I}, cols[3] = {H, I, H};
+    for (int e = 0; e < ne; e++) {
+        uint8_t *b = arena + (size_t)e * slot;
+        DSV4QMat *m[3] = {&table[e].w1, &table[e].w2, &table[e].w3};
+        for (int i = 0; i < 3; i++) {
+            memset(m[i], 0, sizeof *m[i]);
+            m[i]->wdt = DSV4_WFP4;
+            m[i]->rows = (int)rows[i];
+            m[i]->cols = (int)cols[i];
+            m[i]->blk_r = 1;
+            m[i]->blk_c = 32;
+            m[i]->w = b + off_w[i];
+            m[i]->s = b + off_s[i];
+        }
+    }
+    g_expert_arenas[(uintptr_t)arena] = slot * (size_t)ne;
+    *n_experts = ne;
+    return arena;
+}
+
+int dsv4_hip_free_experts(void *arena)
+{
+    std::lock_guard<std::mutex> lk(g.mu);
+    auto it = g_expert_arenas.find((uintptr_t)arena);
+    if (it == g_expert_arenas.end()) return fail("free_experts: not an arena of dsv4_hip_load_experts");
+    (void)hipDeviceSynchronize();
+    (void)hipFree(arena);
+    g_expert_arenas.erase(it);
     return 0;
 }
 

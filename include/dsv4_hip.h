@@ -277,6 +277,30 @@ int  dsv4_hip_gemm_mxfp8q_dev(void *C, int out_bf16, const uint8_t *Aq,
                               const uint8_t *As, int M, const DSV4QMat *W,
                               void *stream);
 
+/* ------------------------------------- checkpoint experts (loader hook) --
+ * The loader's upload-once path for the routed experts, which the reference
+ * streams from NVMe through its slot cache (src/60_cache/dsv4_cache_load.c)
+ * and which here stay resident in HBM. Reads index_dir/experts.idx (magic
+ * "DSV4EXP1", int32 n_layers and n_experts, then n_layers x n_experts x 6
+ * records {int32 shard, int32 pad, int64 offset, int64 bytes} in the order
+ * w1, w1 scales, w2, w2 scales, w3, w3 scales: src/40_io/dsv4_st.h:36-55,
+ * src/40_io/dsv4_st.c:60-84, tools/pack_trunk.py:333-346); shard i is the
+ * i-th *.safetensors file of model_dir in strcmp order
+ * (src/40_io/dsv4_st.c:88-135). Layer `layer`'s experts are uploaded into one
+ * device arena, one slot per expert laid out as the reference's cache slot
+ * (scales s1 s2 s3, then weights w1 w2 w3: src/60_cache/dsv4_cache_geom.c:
+ * 14-50), and table[0..n_experts) receives their descriptors (FP4, 1 x 32
+ * E8M0 scales, device pointers) for the _dev MoE entry points. Returns the
+ * arena, or NULL with dsv4_hip_last_error() (bad index, a tensor of the wrong
+ * size, a short read, no device memory); the index is checked before any
+ * device memory is touched. */
+void *dsv4_hip_load_experts(const char *model_dir, const char *index_dir, int layer,
+                            int hidden, int inter, DSV4ExpertW *table, int max_experts,
+                            int *n_experts);
+
+/* Release an arena of dsv4_hip_load_experts (synchronises the device). */
+int  dsv4_hip_free_experts(void *arena);
+
 /* Read and clear the device status word that the _dev kernels raise when a
  * routing id is out of range (bit 0) or an expert descriptor in the device
  * table does not match the expected format and geometry (bit 1); the affected

@@ -18,8 +18,11 @@ descriptors unchanged. Both are checked against the oracle (relative L2 1e-3
 per token), for the compact layout and for an O_DIRECT placement, with the
 experts scattered over the slots as an LRU cache leaves them.
 """
+import ctypes as C
+
 import numpy as np
 import pytest
+import torch
 
 import pyoracle as P
 from conftest import REL_L2_TOL, max_abs, rel_l2
@@ -206,3 +209,55 @@ def test_odirect_placement_rule():
     for make in LAYOUTS.values():
         toff = make()
         assert all(toff[3 + i] % 16 == 0 and toff[i] % 4 == 0 for i in range(3))
+
+
+# ---------------------------------------------------------------------------
+# Straight from the checkpoint files: dsv4_hip_load_experts reads the packer's
+# experts.idx and the shards (tests/ckpt_writer.py writes a synthetic pair in
+# that format) into one device arena of cache-layout slots; the MoE runs from
+# the descriptors it returns.
+
+@pytest.mark.gpu
+def test_load_experts_from_checkpoint(lib, pkg, oracle, tmp_path):
+    from ckpt_writer import write_checkpoint
+
+    hidden, inter, ne, layers = 512, 256, 8, 2
+    model_dir, index_dir, hosts = write_checkpoint(oracle, str(tmp_path), layers, ne, hidden, inter, seed=11)
+    arena, table, n = lib.load_experts(model_dir, index_dir, 1, hidden, inter)
+    try:
+        assert n == ne
+        # every matrix bit-exact after dequantization
+        for e in (0, 5, 7):
+            he = hosts[(1, e)]
+            for desc, hm in ((table[e].w1, he.w1), (table[e].w3, he.w3), (table[e].w2, he.w2)):
+                out = torch.empty(hm.rows * hm.cols, dtype=torch.float32, device="cuda:0")
+                lib.dequant_dev(out.data_ptr(), desc)
+                torch.cuda.synchronize()
+                want = oracle.dequant(hm) if hasattr(oracle, "dequant") else None
+                got = out.cpu().numpy().reshape(hm.rows, hm.cols)
+                if want is not None:
+                    assert np.array_equal(got.view(np.uint32), want.reshape(hm.rows, hm.cols).view(np.uint32))
+                else:
+                    x = np.eye(hm.cols, dtype=np.float32)[:8]          # rows of the dequantized matrix
+                    ref = oracle.mmq_n(hm, np.ascontiguousarray(x.reshape(-1)), 8).reshape(8, hm.rows).T
+                    assert np.array_equal(got[:, :8], ref)
+        # the decode MoE through the loaded table against the oracle
+        raw = bytes(C.string_at(C.addressof(table), C.sizeof(pkg.ExpertW) * n))
+        dtab = torch.from_numpy(np.frombuffer(raw, np.uint8).copy()).to("cuda:0")
+        rng = np.random.default_rng(5)
+        for t in range(4):
+            ids = rng.choice(ne, 6, replace=False).astype(np.int32)
+            w = rng.dirichlet(np.ones(6)).astype(np.float32)
+            x = rng.standard_normal(hidden).astype(np.float32)
+            dx, di, dw = (torch.from_numpy(a).to("cuda:0") for a in (x, ids, w))
+            out = torch.empty(hidden, dtype=torch.float32, device="cuda:0")
+            lib.moe_decode_dev(out.data_ptr(), dx.data_ptr(), dtab.data_ptr(), ne, di.data_ptr(), dw.data_ptr(),
+                               6, None, hidden, inter, 10.0)
+            torch.cuda.synchronize()
+            acc = np.stack([oracle.expert_forward(hosts[(1, int(e))], x, 10.0) for e in ids])
+            want = oracle.moe_combine(acc, w)
+            got = out.cpu().numpy()
+            assert rel_l2(got, want) <= REL_L2_TOL, f"token {t}: {rel_l2(got, want):.3e}"
+        assert lib.status() == 0
+    finally:
+        lib.free_experts(arena)
