@@ -477,6 +477,49 @@ void orc_swiglu(float *y, const float *gate, const float *up, int n, float limit
     }
 }
 
+/* ------------------------------------------------------------- router --- */
+
+/* src/10_compute/dsv4_ops.c:43-46 */
+static float orc_softplus(float x)
+{
+    return (x > 20.0f) ? x : log1pf(expf(x));
+}
+
+/* src/10_compute/dsv4_ops.c:117-157: orig = sqrt(softplus(scores)); the
+ * selection runs on orig + bias (scores becomes that biased copy), or takes
+ * tid2eid's row for hash-routed layers; top-k is descending with ties to the
+ * lower index, a candidate replacing the best only when strictly greater;
+ * the weights are the UNBIASED orig of the picks, divided by their double
+ * sum and scaled by route_scale. */
+void orc_route(int *idx, float *wts, float *scores, float *orig, const float *bias,
+               const int64_t *tid2eid, int token_id, int n_experts, int topk, float route_scale)
+{
+    for (int e = 0; e < n_experts; e++) orig[e] = sqrtf(orc_softplus(scores[e]));
+    for (int e = 0; e < n_experts; e++) scores[e] = bias ? orig[e] + bias[e] : orig[e];
+    if (tid2eid) {
+        for (int k = 0; k < topk; k++) idx[k] = (int)tid2eid[(int64_t)token_id * topk + k];
+    } else {
+        for (int k = 0; k < topk; k++) {
+            int best = -1;
+            for (int e = 0; e < n_experts; e++) {
+                int taken = 0;
+                for (int j = 0; j < k; j++)
+                    if (idx[j] == e) { taken = 1; break; }
+                if (taken) continue;
+                if (best < 0 || scores[e] > scores[best]) best = e;
+            }
+            idx[k] = best;
+        }
+    }
+    double sum = 0.0;
+    for (int k = 0; k < topk; k++) {
+        wts[k] = orig[idx[k]];
+        sum += (double)wts[k];
+    }
+    const float inv = (sum != 0.0) ? (float)(1.0 / sum) : 0.0f;
+    for (int k = 0; k < topk; k++) wts[k] = wts[k] * inv * route_scale;
+}
+
 /* src/10_compute/dsv4_ops.c:85-93 */
 int orc_expert_forward(float *out, const float *x, const DSV4ExpertW *e,
                        float *gate, float *up, float *mid, int inter,

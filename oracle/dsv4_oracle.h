@@ -52,6 +52,11 @@ void orc_fp8_double(float *y, const float *x, const uint8_t *W,
 void orc_fp4_double(float *y, const float *x, const uint8_t *W,
                     const uint8_t *S, int in, int out, int blk_r, int blk_c);
 
+/* ---- router: src/10_compute/dsv4_ops.c:43-46, 117-157 ---- */
+void orc_route(int *idx, float *wts, float *scores, float *orig, const float *bias,
+               const int64_t *tid2eid, int token_id, int n_experts, int topk,
+               float route_scale);
+
 /* ---- elementwise and expert: src/10_compute/dsv4_ops.c:61-93 ---- */
 void orc_swiglu(float *y, const float *gate, const float *up, int n,
                 float limit);

@@ -99,6 +99,8 @@ class Oracle(_Lib):
         L.orc_bf16_n.argtypes = [_P, _P, _P, _I, _I, _I]
         L.orc_mmq_n.restype = _I; L.orc_mmq_n.argtypes = [_P, _P, C.POINTER(QMat), _I]
         L.orc_swiglu.restype = None; L.orc_swiglu.argtypes = [_P, _P, _P, _I, _F]
+        L.orc_route.restype = None
+        L.orc_route.argtypes = [_P, _P, _P, _P, _P, _P, _I, _I, _I, _F]
         L.orc_expert_forward.restype = _I
         L.orc_expert_forward.argtypes = [_P, _P, C.POINTER(ExpertW), _P, _P, _P, _I, _F]
         L.orc_moe_combine.restype = None
@@ -167,6 +169,19 @@ class Oracle(_Lib):
         y = np.zeros(rows, np.float32)
         self.lib.orc_fp4_double(_ptr(y), _ptr(x), _ptr(W), _ptr(S), cols, rows, blk_r, blk_c)
         return y
+
+    def route(self, scores, topk, route_scale, bias=None, tid2eid=None, token_id=0):
+        """(idx, wts, orig) of dsv4_route on one token's raw gate outputs"""
+        sc = np.array(scores, np.float32)
+        ne = sc.size
+        orig = np.zeros(ne, np.float32)
+        idx = np.zeros(topk, np.int32)
+        wts = np.zeros(topk, np.float32)
+        b = None if bias is None else np.ascontiguousarray(bias, np.float32)
+        t = None if tid2eid is None else np.ascontiguousarray(tid2eid, np.int64)
+        self.lib.orc_route(_ptr(idx), _ptr(wts), _ptr(sc), _ptr(orig), _ptr(b) if b is not None else None,
+                           _ptr(t) if t is not None else None, token_id, ne, topk, float(route_scale))
+        return idx, wts, orig
 
     def swiglu(self, gate, up, limit):
         _need(gate, np.float32, gate.size, "gate"); _need(up, np.float32, gate.size, "up")
@@ -300,6 +315,21 @@ class Reference(_Lib):
         y = np.zeros(gate.size, np.float32)
         self.lib.dsv4_swiglu(_ptr(y), _ptr(gate), _ptr(up), gate.size, float(limit))
         return y
+
+    def route(self, scores, topk, route_scale, bias=None, tid2eid=None, token_id=0):
+        sc = np.array(scores, np.float32)
+        ne = sc.size
+        orig = np.zeros(ne, np.float32)
+        idx = np.zeros(topk, np.int32)
+        wts = np.zeros(topk, np.float32)
+        b = None if bias is None else np.ascontiguousarray(bias, np.float32)
+        t = None if tid2eid is None else np.ascontiguousarray(tid2eid, np.int64)
+        f = self.lib.dsv4_route
+        f.restype = None
+        f.argtypes = [_P, _P, _P, _P, _P, _P, _I, _I, _I, _F]
+        f(_ptr(idx), _ptr(wts), _ptr(sc), _ptr(orig), _ptr(b) if b is not None else None,
+          _ptr(t) if t is not None else None, token_id, ne, topk, float(route_scale))
+        return idx, wts, orig
 
     def expert_forward(self, expert: "HostExpert", x, limit):
         inter = expert.inter

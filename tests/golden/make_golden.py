@@ -145,6 +145,30 @@ def main():
     x[:6] = [1.0, 1.0, 3.0, 1e-30, 1e-30, -2.0]
     save("bf16", W=Wb, x=x, dims=np.array([rows, cols, nt]), y=R.bf16_n(Wb, x, rows, cols, nt))
 
+    # dsv4_route (src/10_compute/dsv4_ops.c:117-157) over 64 tokens x 256
+    # experts: raw gate outputs from -30 to 30 (both sides of softplus's
+    # threshold 20), a selection bias, exact ties (duplicated scores; ties go
+    # to the lower index), and a hash-routed (tid2eid) call.
+    rr = np.random.default_rng(7311)
+    ntok, ne, topk, scale = 64, 256, 6, 1.5
+    sc = (rr.standard_normal((ntok, ne)) * 4.0).astype(np.float32)
+    sc[0, :] = rr.uniform(-30, 30, ne).astype(np.float32)
+    sc[1, 10:20] = sc[1, 5]                            # ties
+    sc[2, :] = 1.0                                     # all equal
+    bias = (rr.standard_normal(ne) * 0.1).astype(np.float32)
+    idx_b = np.zeros((ntok, topk), np.int32); w_b = np.zeros((ntok, topk), np.float32)
+    idx_n = np.zeros((ntok, topk), np.int32); w_n = np.zeros((ntok, topk), np.float32)
+    for t in range(ntok):
+        idx_b[t], w_b[t], _ = R.route(sc[t], topk, scale, bias=bias)
+        idx_n[t], w_n[t], _ = R.route(sc[t], topk, scale)
+    tid2eid = rr.integers(0, ne, (16, topk)).astype(np.int64)
+    idx_h = np.zeros((16, topk), np.int32); w_h = np.zeros((16, topk), np.float32)
+    for t in range(16):
+        idx_h[t], w_h[t], _ = R.route(sc[t], topk, scale, tid2eid=tid2eid, token_id=t)
+    save("route", scores=sc, bias=bias, tid2eid=tid2eid, dims=np.array([ntok, ne, topk]),
+         scale=np.array([scale], np.float32), idx_b=idx_b, w_b=w_b, idx_n=idx_n, w_n=w_n,
+         idx_h=idx_h, w_h=w_h)
+
     with open(os.path.join(HERE, "MANIFEST.json"), "w") as f:
         json.dump({"source": "oracle/_ref/libdsv4ref.so built by oracle/Makefile",
                    "sha256_16": out}, f, indent=1, sort_keys=True)

@@ -85,3 +85,39 @@ def test_bf16_exact_integer_sums(oracle):
     y = oracle.bf16_n(W, x, rows, cols, nt)
     want = (x.reshape(nt, cols).astype(np.float64) @ wi.reshape(rows, cols).T.astype(np.float64))
     assert np.array_equal(y.reshape(nt, rows), want.astype(np.float32))
+
+
+def test_route_fixture_bitexact(oracle):
+    """dsv4_route: biased selection, plain selection and hash routing, with
+    ties and scores on both sides of softplus's threshold."""
+    g = golden("route")
+    ntok, ne, topk = (int(v) for v in g["dims"])
+    scale = float(g["scale"][0])
+    for t in range(ntok):
+        i, w, _ = oracle.route(g["scores"][t], topk, scale, bias=g["bias"])
+        assert np.array_equal(i, g["idx_b"][t]) and np.array_equal(bits(w), bits(g["w_b"][t])), t
+        i, w, _ = oracle.route(g["scores"][t], topk, scale)
+        assert np.array_equal(i, g["idx_n"][t]) and np.array_equal(bits(w), bits(g["w_n"][t])), t
+    for t in range(16):
+        i, w, _ = oracle.route(g["scores"][t], topk, scale, tid2eid=g["tid2eid"], token_id=t)
+        assert np.array_equal(i, g["idx_h"][t]) and np.array_equal(bits(w), bits(g["w_h"][t])), t
+
+
+def test_route_closed_forms(oracle):
+    """What the router's definition fixes: the picks are the top-k of the
+    biased scores in descending order with ties to the lower index (a stable
+    sort), the weights are the unbiased sqrt(softplus) of the picks summing to
+    route_scale, and the bias moves only the selection."""
+    rng = np.random.default_rng(9)
+    for t in range(50):
+        sc = (rng.standard_normal(256) * 3).astype(np.float32)
+        sc[rng.integers(0, 256, 8)] = sc[3]                       # ties
+        bias = (rng.standard_normal(256) * 0.2).astype(np.float32)
+        idx, w, orig = oracle.route(sc, 6, 1.5, bias=bias)
+        sp = np.where(sc > 20, sc, np.log1p(np.exp(sc.astype(np.float64)))).astype(np.float32)
+        assert np.allclose(orig, np.sqrt(sp), rtol=1e-6)
+        biased = orig + bias
+        want = np.argsort(-biased, kind="stable")[:6]
+        assert np.array_equal(idx, want)
+        assert abs(float(w.astype(np.float64).sum()) - 1.5) < 1e-5
+        assert np.allclose(w, orig[idx] / orig[idx].astype(np.float64).sum() * 1.5, rtol=1e-6)
