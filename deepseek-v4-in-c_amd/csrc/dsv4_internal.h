@@ -297,6 +297,31 @@ struct RouteArgs {
 };
 hipError_t moe_route_launch(const RouteArgs &a, hipStream_t st);
 
+/* dsv4_route for n tokens, one workgroup each: scores [n][scores_ld] fp32
+ * (the gate matvec's output) -> idx, w [n][topk], orig [n][n_experts] (may
+ * be NULL). bias [n_experts] may be NULL. With tid2eid ([n_vocab][topk]
+ * int64) the ids are tid2eid[token], token = token_ids[t] (device) or
+ * token_id when token_ids is NULL (n == 1). */
+constexpr int GATE_ROUTE_MAX_EXPERTS = 1024;
+constexpr int GATE_ROUTE_MAX_TOPK = 16;
+struct GateRouteArgs {
+    const float *scores;
+    int scores_ld;
+    int n;
+    const float *bias;
+    const int64_t *tid2eid;
+    int n_vocab;
+    const int *token_ids;
+    int token_id;
+    int n_experts, topk;
+    float route_scale;
+    int *idx;
+    float *w;
+    float *orig;
+    unsigned *status;
+};
+hipError_t gate_route_launch(const GateRouteArgs &a, hipStream_t st);
+
 /* Row r of x [rows][cols] (cols % 8 == 0, x 16-byte aligned) ->
  * o[r][c] = fp16(x[r][c] * 2^ex[r]) with ex[r] the power of two that puts the
  * row's largest finite magnitude in [2^14, 2^15) (0 for a row without one),

@@ -86,7 +86,7 @@ struct State {
     unsigned *st = nullptr;              /* the word the call being enqueued raises */
     unsigned *pub = nullptr;             /* one-launch decode: count, done, leave (own lines) */
     std::map<uintptr_t, Region> regions; /* host start -> resident copy   */
-    DevBuf x, y, mid, table, small, ys, gemm_ws, moe_ws, x16, msplit;
+    DevBuf x, y, mid, table, small, ys, gemm_ws, moe_ws, x16, msplit, route;
 };
 
 constexpr int HOST_WORD = 32;            /* the host calls' word, on its own 128-byte line */
@@ -564,7 +564,7 @@ void dsv4_hip_shutdown(void)
     g.regions.clear();
     g.x.release(); g.y.release(); g.mid.release();
     g.table.release(); g.small.release(); g.ys.release(); g.gemm_ws.release();
-    g.moe_ws.release(); g.x16.release(); g.msplit.release();
+    g.moe_ws.release(); g.x16.release(); g.msplit.release(); g.route.release();
     if (g.status) (void)hipFree(g.status);
     g.status = nullptr;
     if (g.pub) (void)hipFree(g.pub);
@@ -640,7 +640,7 @@ void *dsv4_hip_device_ptr(const void *p)
  * per-token VALU GEMV. */
 constexpr int MMQ_MFMA_MIN_TOKENS = 32;
 
-int enqueue_mmq(const DSV4QMat &d, int fmt, const float *x, float *y, int nt, hipStream_t st)
+static int enqueue_mmq(const DSV4QMat &d, int fmt, const float *x, float *y, int nt, hipStream_t st)
 {
     if (fmt == FMT_BF16) {
         GemvBf16Args b;
@@ -791,6 +791,30 @@ int dsv4_hip_moe_decode(float *out, const float *x, const DSV4ExpertW *const *ex
     return finish_host_call("moe_decode");
 }
 
+/* Checks of the device-routed decode MoE: geometry, topk and the shared
+ * expert's format. */
+static int decode_dev_checks(const char *what, const float *out, const float *x,
+                      const DSV4ExpertW *experts, int n_experts, int topk,
+                      const DSV4ExpertW *shared, int hidden, int inter, int *sfmt, int *sinter)
+{
+    if (!out || !x || !experts) return fail("%s: NULL pointer", what);
+    if (topk < 1 || topk > 16) return fail("%s: topk %d outside 1..16", what, topk);
+    if (n_experts < 1) return fail("%s: no experts", what);
+    if (hidden % 32 || inter % 32 || hidden / 2 > 4096 || inter / 2 > 2048 || hidden <= 0 || inter <= 0)
+        return fail("%s: unsupported hidden %d / inter %d", what, hidden, inter);
+    if (!aligned16(x)) return fail("%s: x must be 16-byte aligned", what);
+    *sfmt = -1;
+    *sinter = 0;
+    if (shared) {
+        int sh;
+        if (expert_geometry(shared, sfmt, sinter, &sh, what)) return -1;
+        if (sh != hidden) return fail("%s: shared hidden %d != %d", what, sh, hidden);
+        if (!aligned16(shared->w1.w) || !aligned16(shared->w3.w) || !aligned16(shared->w2.w))
+            return fail("%s: shared weights must be 16-byte aligned", what);
+    }
+    return 0;
+}
+
 int dsv4_hip_moe_decode_dev(float *out, const float *x, const DSV4ExpertW *experts,
                             int n_experts, const int *idx, const float *w, int topk,
                             const DSV4ExpertW *shared, int hidden, int inter,
@@ -800,27 +824,112 @@ int dsv4_hip_moe_decode_dev(float *out, const float *x, const DSV4ExpertW *exper
     Range rg("dsv4_hip_moe_decode_dev");
     if (usable()) return -1;
     dev_call();
-    if (!out || !x || !experts || !idx || !w) return fail("moe_decode_dev: NULL pointer");
-    if (topk < 1 || topk > 16) return fail("moe_decode_dev: topk %d outside 1..16", topk);
-    if (n_experts < 1) return fail("moe_decode_dev: no experts");
-    if (hidden % 32 || inter % 32 || hidden / 2 > 4096 || inter / 2 > 2048 || hidden <= 0 || inter <= 0)
-        return fail("moe_decode_dev: unsupported hidden %d / inter %d", hidden, inter);
-    if (!aligned16(x)) return fail("moe_decode_dev: x must be 16-byte aligned");
-    int sfmt = -1, sinter = 0;
-    if (shared) {
-        int sh;
-        if (expert_geometry(shared, &sfmt, &sinter, &sh, "moe_decode_dev shared")) return -1;
-        if (sh != hidden) return fail("moe_decode_dev: shared hidden %d != %d", sh, hidden);
-        if (!aligned16(shared->w1.w) || !aligned16(shared->w3.w) || !aligned16(shared->w2.w))
-            return fail("moe_decode_dev: shared weights must be 16-byte aligned");
-    }
+    if (!idx || !w) return fail("moe_decode_dev: NULL pointer");
+    int sfmt, sinter;
+    if (decode_dev_checks("moe_decode_dev", out, x, experts, n_experts, topk, shared, hidden,
+                          inter, &sfmt, &sinter))
+        return -1;
     return enqueue_moe(experts, n_experts, idx, w, topk, shared, sfmt, sinter,
                        hidden, inter, x, out, limit, (hipStream_t)stream);
 }
 
+/* Checks shared by the router entry points. */
+static int route_checks(const char *what, int n_experts, int topk, const int64_t *tid2eid, int n_vocab)
+{
+    if (n_experts < 1 || n_experts > GATE_ROUTE_MAX_EXPERTS)
+        return fail("%s: n_experts %d outside 1..%d", what, n_experts, GATE_ROUTE_MAX_EXPERTS);
+    if (topk < 1 || topk > GATE_ROUTE_MAX_TOPK || topk > n_experts)
+        return fail("%s: topk %d outside 1..%d", what, topk,
+                    std::min(GATE_ROUTE_MAX_TOPK, n_experts));
+    if (tid2eid && n_vocab < 1) return fail("%s: hash routing needs n_vocab >= 1", what);
+    return 0;
+}
+
+int dsv4_hip_route_dev(int *idx, float *w, float *orig, const float *scores, int n,
+                       const float *bias, const int64_t *tid2eid, int n_vocab,
+                       const int *token_ids, int n_experts, int topk, float route_scale,
+                       void *stream)
+{
+    std::lock_guard<std::mutex> lk(g.mu);
+    Range rg("dsv4_hip_route_dev");
+    if (usable()) return -1;
+    dev_call();
+    if (n < 0) return fail("route_dev: n %d < 0", n);
+    if (n == 0) return 0;
+    if (!idx || !w || !scores) return fail("route_dev: NULL pointer");
+    if (route_checks("route_dev", n_experts, topk, tid2eid, n_vocab)) return -1;
+    if (tid2eid && !token_ids) return fail("route_dev: hash routing needs token_ids");
+    GateRouteArgs a;
+    memset(&a, 0, sizeof a);
+    a.scores = scores;
+    a.scores_ld = n_experts;
+    a.n = n;
+    a.bias = bias;
+    a.tid2eid = tid2eid;
+    a.n_vocab = n_vocab;
+    a.token_ids = token_ids;
+    a.n_experts = n_experts;
+    a.topk = topk;
+    a.route_scale = route_scale;
+    a.idx = idx;
+    a.w = w;
+    a.orig = orig;
+    a.status = g.st;
+    HIPCHK(gate_route_launch(a, (hipStream_t)stream), "route launch");
+    return 0;
+}
+
+int dsv4_hip_moe_layer_dev(float *out, const float *x, const DSV4QMat *gate,
+                           const float *bias, const int64_t *tid2eid, int n_vocab, int token_id,
+                           float route_scale, const DSV4ExpertW *experts, int n_experts, int topk,
+                           const DSV4ExpertW *shared, int hidden, int inter, float limit,
+                           int *idx_out, float *w_out, void *stream)
+{
+    std::lock_guard<std::mutex> lk(g.mu);
+    Range rg("dsv4_hip_moe_layer_dev");
+    if (usable()) return -1;
+    dev_call();
+    int gfmt, sfmt, sinter;
+    if (check_qmat(gate, "moe_layer_dev gate", &gfmt)) return -1;
+    if (!gate->w || (gfmt != FMT_BF16 && !gate->s)) return fail("moe_layer_dev: NULL gate pointer");
+    if (gate->rows != n_experts || gate->cols != hidden)
+        return fail("moe_layer_dev: gate is [%d x %d], expected [%d x %d]", gate->rows,
+                    gate->cols, n_experts, hidden);
+    if (!aligned16(gate->w)) return fail("moe_layer_dev: gate weights must be 16-byte aligned");
+    if (route_checks("moe_layer_dev", n_experts, topk, tid2eid, n_vocab)) return -1;
+    if (decode_dev_checks("moe_layer_dev", out, x, experts, n_experts, topk, shared, hidden,
+                          inter, &sfmt, &sinter))
+        return -1;
+    const hipStream_t st = (hipStream_t)stream;
+    const size_t sb = ((size_t)n_experts * 4 + 255) & ~(size_t)255;
+    HIPCHK(g.route.need(sb + 2 * 256), "router workspace");
+    float *scores = (float *)g.route.p;
+    int *idx = idx_out ? idx_out : (int *)((uint8_t *)g.route.p + sb);
+    float *w = w_out ? w_out : (float *)((uint8_t *)g.route.p + sb + 256);
+    if (enqueue_mmq(*gate, gfmt, x, scores, 1, st)) return -1;
+    GateRouteArgs a;
+    memset(&a, 0, sizeof a);
+    a.scores = scores;
+    a.scores_ld = n_experts;
+    a.n = 1;
+    a.bias = bias;
+    a.tid2eid = tid2eid;
+    a.n_vocab = n_vocab;
+    a.token_id = token_id;
+    a.n_experts = n_experts;
+    a.topk = topk;
+    a.route_scale = route_scale;
+    a.idx = idx;
+    a.w = w;
+    a.status = g.st;
+    HIPCHK(gate_route_launch(a, st), "route launch");
+    return enqueue_moe(experts, n_experts, idx, w, topk, shared, sfmt, sinter,
+                       hidden, inter, x, out, limit, st);
+}
+
 /* Checks of the host-routed decode entry points: the topk descriptors and
  * weights picked by the host routing ids, and the shared expert's format. */
-int routed_checks(const char *what, const float *out, const float *x, const DSV4ExpertW *experts,
+static int routed_checks(const char *what, const float *out, const float *x, const DSV4ExpertW *experts,
                   int n_experts, const int *idx, const float *w, int topk,
                   const DSV4ExpertW *shared, int hidden, int inter, DSV4ExpertW *routed,
                   float *wv, int *sfmt, int *sinter)
@@ -926,7 +1035,7 @@ static_assert(sizeof(ExpLoc) == 24, "experts.idx record");
 constexpr int EXP_TENSORS = 6;                 /* w1, w1 scales, w2, w2 scales, w3, w3 scales */
 
 /* The *.safetensors files of dir in strcmp order: shard i of the index. */
-int list_shards(const char *dir, std::vector<std::string> &out)
+static int list_shards(const char *dir, std::vector<std::string> &out)
 {
     DIR *d = opendir(dir);
     if (!d) return fail("load_experts: cannot open directory %s", dir);
@@ -944,7 +1053,7 @@ int list_shards(const char *dir, std::vector<std::string> &out)
 }
 
 /* The layer's records: n_experts x 6, in the packer's tensor order. */
-int read_expert_index(const char *index_dir, int layer, std::vector<ExpLoc> &loc, int *n_experts)
+static int read_expert_index(const char *index_dir, int layer, std::vector<ExpLoc> &loc, int *n_experts)
 {
     const std::string path = std::string(index_dir) + "/experts.idx";
     FILE *f = fopen(path.c_str(), "rb");
@@ -971,10 +1080,10 @@ int read_expert_index(const char *index_dir, int layer, std::vector<ExpLoc> &loc
 }
 
 /* Device arenas handed out by dsv4_hip_load_experts. */
-std::map<uintptr_t, size_t> g_expert_arenas;
+static std::map<uintptr_t, size_t> g_expert_arenas;
 
 /* Shared checks of the FP8 GEMM entry points; returns the weight format. */
-int gemm_checks(const void *C, const void *A, int M, const DSV4QMat *W, const char *what, int *fmt)
+static int gemm_checks(const void *C, const void *A, int M, const DSV4QMat *W, const char *what, int *fmt)
 {
     if (!C || !A || !W || !W->w || !W->s) return fail("%s: NULL pointer", what);
     *fmt = qmat_fmt(W);
@@ -989,7 +1098,7 @@ int gemm_checks(const void *C, const void *A, int M, const DSV4QMat *W, const ch
 }
 
 /* Sa holds one fp32 per (token, 128-wide K block), block-major [K/128][M]. */
-int enqueue_gemm(void *C, int out_bf16, const uint8_t *Aq, const float *Sa, int M,
+static int enqueue_gemm(void *C, int out_bf16, const uint8_t *Aq, const float *Sa, int M,
                  const DSV4QMat *W, int fmt, hipStream_t st)
 {
     GemmArgs ga;
@@ -1035,7 +1144,7 @@ int dsv4_hip_gemm_fp8q_dev(void *C, int out_bf16, const uint8_t *Aq, const float
 }
 
 /* The hardware-scaled GEMM: W must carry E8M0 128 x 128 block scales. */
-int enqueue_gemm_mx(void *C, int out_bf16, const uint8_t *Aq, const uint8_t *As, int M,
+static int enqueue_gemm_mx(void *C, int out_bf16, const uint8_t *Aq, const uint8_t *As, int M,
                     const DSV4QMat *W, hipStream_t st)
 {
     GemmArgs ga;
@@ -1211,9 +1320,9 @@ int dsv4_hip_gemm_mxfp8q_dev(void *C, int out_bf16, const uint8_t *Aq, const uin
 /* 16-row tiles when buckets are small (batched decode: few tokens per expert,
  * weight streaming dominates and occupancy matters), 128-row tiles otherwise
  * (prefill: weights are reused across a tile's rows). */
-int grouped_tt(long pairs) { return pairs <= 4096 ? 1 : 8; }
+static int grouped_tt(long pairs) { return pairs <= 4096 ? 1 : 8; }
 
-int enqueue_moe_grouped(float *out, const float *x, int n, const DSV4ExpertW *table,
+static int enqueue_moe_grouped(float *out, const float *x, int n, const DSV4ExpertW *table,
                         int n_experts, const int *idx, const float *w, int topk,
                         const DSV4ExpertW *shared, int sfmt, int sinter, int hidden,
                         int inter, float limit, hipStream_t st)
@@ -1298,7 +1407,7 @@ int enqueue_moe_grouped(float *out, const float *x, int n, const DSV4ExpertW *ta
  * xs), the w1 and w3 GEMMs into fp32 gate and up, SwiGLU with mid's 1x128
  * quantization in one pass (mq, ms block-major), and the w2 GEMM into ys;
  * ys == NULL stops after mid. */
-int enqueue_shared_fp8q(float *ys, uint8_t *mq, float *ms, const float *x, int n, const DSV4ExpertW *sh,
+static int enqueue_shared_fp8q(float *ys, uint8_t *mq, float *ms, const float *x, int n, const DSV4ExpertW *sh,
                         int sfmt, int sinter, int hidden, float limit, uint8_t *xq, float *xs, float *gate,
                         float *up, hipStream_t st)
 {
@@ -1316,7 +1425,7 @@ int enqueue_shared_fp8q(float *ys, uint8_t *mq, float *ms, const float *x, int n
  * GEMM with the 1x128 activation quantization (w1 and w3, SwiGLU and mid's
  * quantization in one pass, w2; src/80_prefill/dsv4_prefill_moe.c:40-58 over
  * dsv4_prefill_proj.c:17-27), an FP4 one on the exact fp16 path. */
-int enqueue_moe_grouped_mx(float *out, const float *x, int n, const DSV4ExpertW *table,
+static int enqueue_moe_grouped_mx(float *out, const float *x, int n, const DSV4ExpertW *table,
                            int n_experts, const int *idx, const float *w, int topk,
                            const DSV4ExpertW *shared, int sfmt, int sinter, int hidden, int inter,
                            float limit, hipStream_t st)
@@ -1425,7 +1534,7 @@ int enqueue_moe_grouped_mx(float *out, const float *x, int n, const DSV4ExpertW 
 }
 
 /* Checks shared by both grouped entry points; returns the shared format. */
-int grouped_checks(int n, int topk, int n_experts, int hidden, int inter,
+static int grouped_checks(int n, int topk, int n_experts, int hidden, int inter,
                    const DSV4ExpertW *shared, int *sfmt, int *sinter, const char *what)
 {
     if (n < 1) return fail("%s: n %d < 1", what, n);

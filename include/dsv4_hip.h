@@ -181,6 +181,46 @@ int  dsv4_hip_moe_decode_routed_noalloc_dev(float *out, const float *x,
                                             const DSV4ExpertW *shared, int hidden, int inter,
                                             float limit, void *stream);
 
+/* ------------------------------------------- router on the device (f2) ----
+ * dsv4_route (src/10_compute/dsv4_ops.c:117-157, declared at
+ * src/10_compute/dsv4_kernels.h:23) for n tokens, as the prefill loop calls
+ * it (src/80_prefill/dsv4_prefill_moe.c:22-29): scores [n][n_experts] are
+ * the gate outputs; orig[e] = sqrt(softplus(scores[e])) (softplus(x) = x
+ * for x > 20); the ids are the topk largest orig + bias (bias may be NULL),
+ * descending, ties to the lower id, or tid2eid[token_ids[t]] when tid2eid
+ * ([n_vocab][topk] int64) is given; w[k] = orig[id_k] / sum (double) *
+ * route_scale. The bias steers the selection only. All arrays are device
+ * arrays: idx, w [n][topk], orig [n][n_experts] (may be NULL; the
+ * reference's scores array is not overwritten). n_experts <= 1024, topk <=
+ * 16. Numerics: softplus and sqrt in fp64, rounded once, so orig is the
+ * correctly rounded value; glibc's log1pf is not, and the reference's orig
+ * differs by one unit in the last place on about 1% of scores in [-104, 20]
+ * (ids agree unless two biased scores are that close). A token id outside
+ * [0, n_vocab) or a table id outside [0, n_experts) raises status bit 0 and
+ * makes the token's weights NaN. */
+int  dsv4_hip_route_dev(int *idx, float *w, float *orig, const float *scores, int n,
+                        const float *bias, const int64_t *tid2eid, int n_vocab,
+                        const int *token_ids, int n_experts, int topk, float route_scale,
+                        void *stream);
+
+/* The decode step's MoE block on the device: dsv4_layer_moe
+ * (src/70_decode/dsv4_layer.c:49-116) with no host round trip. scores =
+ * gate . x (dsv4_mmq at src/70_decode/dsv4_layer.c:52; `gate` is a HOST
+ * descriptor with device pointers, [n_experts x hidden], any dsv4_hip_mmq
+ * format, BF16 in the released checkpoints), the router as
+ * dsv4_hip_route_dev with token id `token_id`, then the routed experts and
+ * the shared expert as dsv4_hip_moe_decode_dev (same table, geometry and
+ * limits). idx_out / w_out (device, topk entries each, may be NULL) receive
+ * the routing. Every launch goes on `stream` and no host value depends on
+ * the device, so the call may be captured in a HIP graph once an eager call
+ * of the same n_experts has run (that call sizes the router's workspace). */
+int  dsv4_hip_moe_layer_dev(float *out, const float *x, const DSV4QMat *gate,
+                            const float *bias, const int64_t *tid2eid, int n_vocab,
+                            int token_id, float route_scale,
+                            const DSV4ExpertW *experts, int n_experts, int topk,
+                            const DSV4ExpertW *shared, int hidden, int inter, float limit,
+                            int *idx_out, float *w_out, void *stream);
+
 /* ------------------------------------- grouped MoE (a13-a15, a18) ---------
  * For n tokens (batched decode or a prefill block):
  *   out[t] = sum_{k in 0..topk-1, in k order} w[t][k] * expert_{idx[t][k]}(x[t])

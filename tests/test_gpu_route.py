@@ -1,0 +1,304 @@
+# SPDX-License-Identifier: Apache-2.0
+"""GPU parity of the device router (dsv4_hip_route_dev) and of the decode
+step's MoE block on the device (dsv4_hip_moe_layer_dev: gate matvec, router,
+routed experts and shared expert with no host round trip).
+
+The router's fixture comes from the reference's own dsv4_route compiled from
+its sources (src/10_compute/dsv4_ops.c:117-157); the edge cases run through
+the oracle's restatement, which that fixture pins. Tolerances: ids exact
+unless the two biased scores involved lie within 4 units in the last place
+(the device's softplus is correctly rounded, glibc's log1pf is not, so orig
+may differ by one unit); orig within one unit; weights within 1e-6 relative;
+the MoE block's output within 1e-4 relative L2 of the oracle's pipeline."""
+import zlib
+
+import numpy as np
+import pytest
+import torch
+
+import pyoracle as P
+from conftest import bits, golden
+from test_gpu_decode import DEV, bf16_x, check_close, dev_f32
+from test_gpu_decode_one import _host_slot_expert
+
+pytestmark = pytest.mark.gpu
+
+
+def _ulps(a, b):
+    """|a - b| in units in the last place of fp32 (same-sign finite values)."""
+    ia = np.ascontiguousarray(a, np.float32).view(np.int32).astype(np.int64)
+    ib = np.ascontiguousarray(b, np.float32).view(np.int32).astype(np.int64)
+    return np.abs(ia - ib)
+
+
+def _assert_ids(got, want, biased, what):
+    """ids equal, or every differing pick a near tie of the oracle's biased
+    scores (the pick the device made scores within 4 ulps of the oracle's)."""
+    got, want = np.asarray(got), np.asarray(want)
+    for t in range(got.shape[0]):
+        if np.array_equal(got[t], want[t]):
+            continue
+        for k in np.nonzero(got[t] != want[t])[0]:
+            g, w = biased[t][got[t][k]], biased[t][want[t][k]]
+            assert abs(float(g) - float(w)) <= 4 * np.spacing(np.float32(abs(w))), \
+                f"{what}: token {t} slot {k}: id {got[t][k]} vs {want[t][k]} ({g} vs {w})"
+
+
+def _assert_w(got, want, what):
+    got, want = np.asarray(got, np.float64), np.asarray(want, np.float64)
+    both_nan = np.isnan(got) & np.isnan(want)
+    assert np.array_equal(np.isnan(got), np.isnan(want)), f"{what}: NaN pattern"
+    err = np.abs(got - want)[~both_nan]
+    ref = np.abs(want)[~both_nan]
+    assert np.all(err <= 1e-6 * np.maximum(ref, 1e-30)), f"{what}: max rel {np.max(err / np.maximum(ref, 1e-30)):.3e}"
+
+
+def _route_gpu(lib, scores, topk, scale, bias=None, tid2eid=None, tokens=None, n_vocab=0):
+    n, ne = scores.shape
+    ds = dev_f32(scores)
+    di = torch.full((n * topk,), -7, dtype=torch.int32, device=DEV)
+    dw = torch.empty(n * topk, dtype=torch.float32, device=DEV)
+    do = torch.empty(n * ne, dtype=torch.float32, device=DEV)
+    db = dev_f32(bias) if bias is not None else None
+    dt = torch.from_numpy(np.ascontiguousarray(tid2eid, np.int64).reshape(-1)).to(DEV) \
+        if tid2eid is not None else None
+    dk = torch.from_numpy(np.ascontiguousarray(tokens, np.int32)).to(DEV) if tokens is not None else None
+    lib.route_dev(di.data_ptr(), dw.data_ptr(), do.data_ptr(), ds.data_ptr(), n, ne, topk, scale,
+                  bias_ptr=db.data_ptr() if db is not None else None,
+                  tid2eid_ptr=dt.data_ptr() if dt is not None else None, n_vocab=n_vocab,
+                  token_ids_ptr=dk.data_ptr() if dk is not None else None)
+    torch.cuda.synchronize()
+    return (di.cpu().numpy().reshape(n, topk), dw.cpu().numpy().reshape(n, topk),
+            do.cpu().numpy().reshape(n, ne))
+
+
+def test_route_golden_fixture(lib, oracle):
+    """64 tokens x 256 experts from the compiled reference: biased selection,
+    plain selection and hash routing; orig within one ulp of the oracle's."""
+    g = golden("route")
+    ntok, ne, topk = (int(v) for v in g["dims"])
+    scale = float(g["scale"][0])
+    sc, bias = g["scores"], g["bias"]
+    lib.status()
+    orig_o = np.stack([oracle.route(sc[t], topk, scale)[2] for t in range(ntok)])
+    i, w, o = _route_gpu(lib, sc, topk, scale, bias=bias)
+    assert np.all(_ulps(o, orig_o) <= 1), "orig beyond one ulp"
+    _assert_ids(i, g["idx_b"], orig_o + bias, "biased")
+    _assert_w(w, g["w_b"], "biased")
+    i, w, _ = _route_gpu(lib, sc, topk, scale)
+    _assert_ids(i, g["idx_n"], orig_o, "plain")
+    _assert_w(w, g["w_n"], "plain")
+    i, w, _ = _route_gpu(lib, sc[:16], topk, scale, tid2eid=g["tid2eid"], tokens=np.arange(16),
+                         n_vocab=16)
+    assert np.array_equal(i, g["idx_h"])
+    _assert_w(w, g["w_h"], "hash")
+    assert lib.status() == 0
+
+
+def _edge_cases():
+    rng = np.random.default_rng(zlib.crc32(b"route-edges"))
+    cases = []
+    ne = 256
+    cases.append(("all equal", np.full((2, ne), 0.37, np.float32), None, 6, 1.0))
+    s = rng.standard_normal((4, ne)).astype(np.float32)
+    s[0, 0] = np.nan                                # first untaken is NaN: kept
+    s[1, [0, 1, 2]] = np.nan                        # three leading NaNs
+    s[2, rng.integers(1, ne, 9)] = np.nan           # NaNs inside: never picked
+    s[3, :] = np.nan                                # all NaN
+    cases.append(("NaN", s, None, 6, 1.0))
+    s = rng.standard_normal((3, ne)).astype(np.float32)
+    s[0, [3, 50, 200]] = np.inf
+    s[1, :40] = -np.inf
+    s[2, ::3] = 25.0                                # above softplus's threshold, tied
+    s[2, 1::7] = 19.999998
+    cases.append(("inf and threshold", s, None, 8, 2.5))
+    s = np.repeat(rng.standard_normal((1, 32)).astype(np.float32), 8, axis=0).reshape(1, ne)
+    s = np.concatenate([s, np.round(rng.standard_normal((3, ne)) * 2, 1).astype(np.float32)])
+    b = np.round(rng.standard_normal(ne) * 0.5, 1).astype(np.float32)
+    b[::5] = -np.inf
+    cases.append(("ties with bias", s, b, 6, 1.5))
+    cases.append(("1024 experts top 16", (rng.standard_normal((3, 1024)) * 4).astype(np.float32),
+                  (rng.standard_normal(1024) * 0.1).astype(np.float32), 16, 2.5))
+    cases.append(("topk == n_experts", rng.standard_normal((2, 16)).astype(np.float32), None, 16, 1.0))
+    cases.append(("300 experts", rng.standard_normal((5, 300)).astype(np.float32),
+                  (rng.standard_normal(300) * 0.3).astype(np.float32), 8, 1.0))
+    cases.append(("one expert", rng.standard_normal((2, 1)).astype(np.float32), None, 1, 3.0))
+    s = np.full((1, ne), -200.0, np.float32)         # orig 0 everywhere: weights 0
+    cases.append(("zero sum", s, None, 6, 1.0))
+    return cases
+
+
+@pytest.mark.parametrize("case", _edge_cases(), ids=lambda c: c[0])
+def test_route_edges(lib, oracle, case):
+    """NaN (first untaken kept, others skipped), infinities, the softplus
+    threshold, exact ties with and without a bias (-inf included), 1 to 1024
+    experts, topk up to 16 and topk == n_experts, a zero weight sum: ids and
+    weights as the oracle's loop gives them."""
+    name, sc, bias, topk, scale = case
+    lib.status()
+    i, w, o = _route_gpu(lib, sc, topk, scale, bias=bias)
+    want = [oracle.route(sc[t], topk, scale, bias=bias) for t in range(sc.shape[0])]
+    wi = np.stack([r[0] for r in want])
+    ww = np.stack([r[1] for r in want])
+    wo = np.stack([r[2] for r in want])
+    fin = np.isfinite(wo)
+    assert np.array_equal(np.isnan(o), np.isnan(wo))
+    assert np.all(_ulps(o[fin], wo[fin]) <= 1)
+    biased = wo + (bias if bias is not None else 0)
+    _assert_ids(i, wi, biased, name)
+    _assert_w(w, ww, name)
+    assert lib.status() == 0
+
+
+def test_route_bad_ids_raise_status(lib, oracle):
+    """A token id outside the hash table, or a table entry outside the experts:
+    status bit 0, NaN weights, the ids written as they are (-1 for the token)."""
+    rng = np.random.default_rng(5)
+    sc = rng.standard_normal((3, 64)).astype(np.float32)
+    t2e = np.stack([rng.choice(64, 4, replace=False) for _ in range(8)]).astype(np.int64)
+    t2e[5, 2] = 64
+    lib.status()
+    i, w, _ = _route_gpu(lib, sc, 4, 1.0, tid2eid=t2e, tokens=np.array([1, 8, 5]), n_vocab=8)
+    assert lib.status() & 1
+    assert np.array_equal(i[0], t2e[1]) and np.all(np.isfinite(w[0]))
+    assert np.array_equal(i[1], [-1] * 4) and np.all(np.isnan(w[1]))
+    assert np.array_equal(i[2], t2e[5]) and np.all(np.isnan(w[2]))
+    assert lib.status() == 0
+
+
+def test_route_rejects_bad_arguments(lib):
+    """Sizes the kernel does not take are refused before any launch."""
+    d = torch.zeros(4096, dtype=torch.float32, device=DEV)
+    p = d.data_ptr()
+    for ne, topk in ((1025, 6), (256, 17), (8, 9), (0, 1)):
+        with pytest.raises(Exception):
+            lib.route_dev(p, p, None, p, 1, ne, topk, 1.0)
+    with pytest.raises(Exception):          # hash routing without token ids
+        lib.route_dev(p, p, None, p, 1, 64, 4, 1.0, tid2eid_ptr=p, n_vocab=4)
+    lib.route_dev(p, p, None, p, 0, 64, 4, 1.0)       # n == 0: nothing to do
+    torch.cuda.synchronize()
+
+
+class _Layer:
+    """One decode MoE block at the released shape: BF16 gate [256 x 4096], a
+    bias, 256 FP4 experts [2048 x 4096] in one device arena, the FP8 shared
+    expert, top-6."""
+
+    def __init__(self, pkg, lib, seed):
+        import bench
+        self.hidden, self.inter, self.ne, self.topk, self.scale = 4096, 2048, 256, 6, 2.5
+        rng = np.random.default_rng(seed)
+        self.arena = bench.ExpertArena(torch, pkg, lib, self.ne, seed=seed)
+        self.shared, self.skeep = bench.make_shared_fp8(torch, pkg, lib, seed + 1)
+        g32 = (rng.standard_normal((self.ne, self.hidden)) * 0.02).astype(np.float32)
+        self.W16 = (g32.view(np.uint32) >> 16).astype(np.uint16)   # bf16 by truncation
+        self.dW = torch.from_numpy(self.W16.view(np.int16).reshape(-1).copy()).to(DEV)
+        self.gate = pkg.qmat(pkg.DSV4_WBF16, self.dW.data_ptr(), None, self.ne, self.hidden, 0, 0)
+        self.bias = (rng.standard_normal(self.ne) * 0.05).astype(np.float32)
+        self.dbias = dev_f32(self.bias)
+        self.t2e = np.stack([rng.choice(self.ne, self.topk, replace=False)
+                             for _ in range(32)]).astype(np.int64)
+        self.dt2e = torch.from_numpy(self.t2e.reshape(-1)).to(DEV)
+        I, H = self.inter, self.hidden
+        self.hshared = P.HostExpert(*[P.HostMat(P.DSV4_WFP8_F32S, self.skeep[2 * i].cpu().numpy(),
+                                                self.skeep[2 * i + 1].cpu().numpy(), r, c, 128, 128)
+                                      for i, (r, c) in enumerate(((I, H), (I, H), (H, I)))])
+        self._host = {}
+
+    def run(self, lib, x, out, idx, w, hash_tok=None, stream=None):
+        lib.moe_layer_dev(out.data_ptr(), x.data_ptr(), self.gate, self.arena.table.data_ptr(),
+                          self.ne, self.topk, self.scale, self.shared, self.hidden, self.inter, 10.0,
+                          bias_ptr=None if hash_tok is not None else self.dbias.data_ptr(),
+                          tid2eid_ptr=self.dt2e.data_ptr() if hash_tok is not None else None,
+                          n_vocab=len(self.t2e), token_id=hash_tok or 0,
+                          idx_ptr=idx.data_ptr(), w_ptr=w.data_ptr(), stream=stream)
+
+    def expert(self, e):
+        if e not in self._host:
+            self._host[e] = _host_slot_expert(self.arena.host_copy(torch, e))
+        return self._host[e]
+
+    def want(self, oracle, xh, idx, w):
+        acc = np.stack([oracle.expert_forward(self.expert(int(e)), xh, 10.0) for e in idx])
+        return (oracle.moe_combine(acc, w) + oracle.expert_forward(self.hshared, xh, 10.0)).astype(np.float32)
+
+
+@pytest.mark.parametrize("hash_tok", [None, 17])
+def test_moe_layer_matches_oracle_pipeline(lib, pkg, oracle, hash_tok):
+    """The device block against the reference's sequence run by the oracle:
+    gate scores (bf16_n, fp64 sums) within one ulp, the router's picks and
+    weights as dsv4_route gives them on the oracle's scores, and the block's
+    output within 1e-4 relative L2 of the oracle's experts combined in k order
+    plus the shared expert. Biased routing and hash routing (token 17)."""
+    L = _Layer(pkg, lib, zlib.crc32(b"layer") & 0xFFFF)
+    lib.status()
+    for seed in (3, 4):
+        xh = bf16_x(seed, L.hidden)
+        x = dev_f32(xh)
+        out = torch.empty(L.hidden, dtype=torch.float32, device=DEV)
+        di = torch.empty(L.topk, dtype=torch.int32, device=DEV)
+        dw = torch.empty(L.topk, dtype=torch.float32, device=DEV)
+        L.run(lib, x, out, di, dw, hash_tok)
+        sc = torch.empty(L.ne, dtype=torch.float32, device=DEV)
+        lib.mmq_n_dev(sc.data_ptr(), x.data_ptr(), L.gate, 1)
+        torch.cuda.synchronize()
+        assert lib.status() == 0
+        sc_o = oracle.bf16_n(L.W16, xh, L.ne, L.hidden)
+        assert np.all(_ulps(sc.cpu().numpy(), sc_o) <= 1), "gate scores beyond one ulp"
+        bias = None if hash_tok is not None else L.bias
+        wi, ww, wo = oracle.route(sc_o, L.topk, L.scale, bias=bias,
+                                  tid2eid=L.t2e if hash_tok is not None else None,
+                                  token_id=hash_tok or 0)
+        gi, gw = di.cpu().numpy(), dw.cpu().numpy()
+        _assert_ids(gi[None], wi[None], (wo + (bias if bias is not None else 0))[None], "layer")
+        _assert_w(gw, ww, "layer")
+        check_close(out.cpu().numpy(), L.want(oracle, xh, wi, ww), 1e-4)
+
+
+def test_moe_layer_graph_replays(lib, pkg, oracle):
+    """The whole block captured once in a HIP graph and replayed for four
+    tokens (new x copied in between, synchronised): output, ids and weights
+    of every replay bit for bit the eager call's, status clean."""
+    L = _Layer(pkg, lib, 0x6A7E)
+    xs = [bf16_x(70 + i, L.hidden) for i in range(4)]
+    out = torch.empty(L.hidden, dtype=torch.float32, device=DEV)
+    di = torch.empty(L.topk, dtype=torch.int32, device=DEV)
+    dw = torch.empty(L.topk, dtype=torch.float32, device=DEV)
+    x = dev_f32(xs[0])
+    st = torch.cuda.Stream()
+    want = []
+    lib.status()
+    for xh in xs:
+        x.copy_(torch.from_numpy(xh))
+        torch.cuda.synchronize()
+        with torch.cuda.stream(st):
+            L.run(lib, x, out, di, dw, stream=st.cuda_stream)
+        torch.cuda.synchronize()
+        want.append((bits(out.cpu().numpy()), di.cpu().numpy().copy(), bits(dw.cpu().numpy())))
+    assert lib.status() == 0
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=st):
+        L.run(lib, x, out, di, dw, stream=st.cuda_stream)
+    torch.cuda.synchronize()
+    for rep in range(3):
+        for i, xh in enumerate(xs):
+            x.copy_(torch.from_numpy(xh))
+            torch.cuda.synchronize()
+            graph.replay()
+            torch.cuda.synchronize()
+            assert np.array_equal(bits(out.cpu().numpy()), want[i][0]), f"replay {rep} token {i}"
+            assert np.array_equal(di.cpu().numpy(), want[i][1])
+            assert np.array_equal(bits(dw.cpu().numpy()), want[i][2])
+    assert lib.status() == 0
+    check_close(out.cpu().numpy(), L.want(oracle, xs[-1], want[-1][1], want[-1][2].view(np.float32)), 1e-4)
+
+
+def test_moe_layer_rejects_bad_gate(lib, pkg):
+    """A gate whose shape is not [n_experts x hidden] is refused on the host,
+    before anything is launched."""
+    d = torch.zeros(1 << 20, dtype=torch.float32, device=DEV)
+    p = d.data_ptr()
+    gate = pkg.qmat(pkg.DSV4_WBF16, p, None, 128, 4096, 0, 0)
+    with pytest.raises(Exception, match="gate"):
+        lib.moe_layer_dev(p, p, gate, p, 256, 6, 1.0, None, 4096, 2048, 10.0)
+    torch.cuda.synchronize()
