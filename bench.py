@@ -644,6 +644,77 @@ def bench_cfg3(args, torch, pkg, lib, stream, sp, K, W):
 
 # ------------------------------------------------------------------ main ----
 
+def bench_layer(torch, pkg, lib, arena, xs, K, W, graph_calls=16):
+    """The decode step's MoE block with the router on the device
+    (dsv4_hip_moe_layer_dev: BF16 gate 256 x 4096 matvec, sqrt-softplus
+    top-6 with a bias, the six routed experts): per-token time enqueued
+    eagerly, and replayed from a HIP graph of `graph_calls` consecutive tokens
+    captured on a side stream. Each token is its own x, so each picks its own
+    experts from the 3.4 GB arena. Then the same block with the FP8 shared
+    expert, which runs beside the gate and the router, next to the routed
+    experts plus the shared expert with the routing already known
+    (dsv4_hip_moe_decode_dev)."""
+    dev = "cuda:0"
+    tmp = torch.empty(N_EXPERTS * HIDDEN, dtype=torch.float32, device=dev)
+    lib.synth_normal_dev(tmp.data_ptr(), tmp.numel(), 0x6A7E, 0.02)
+    gw = tmp.bfloat16()
+    gate = pkg.qmat(pkg.DSV4_WBF16, gw.data_ptr(), None, N_EXPERTS, HIDDEN, 0, 0)
+    bias = torch.empty(N_EXPERTS, dtype=torch.float32, device=dev)
+    lib.synth_normal_dev(bias.data_ptr(), N_EXPERTS, 0x6A7F, 0.05)
+    shared, keep = make_shared_fp8(torch, pkg, lib, 0x6A80)
+    out = torch.empty(HIDDEN, dtype=torch.float32, device=dev)
+    di = torch.empty(TOPK, dtype=torch.int32, device=dev)
+    dw = torch.empty(TOPK, dtype=torch.float32, device=dev)
+    st = torch.cuda.Stream()
+    n_x = xs.numel() // HIDDEN
+    idx_h, w_h = routing(n_x, seed=0x6A81)
+    didx = torch.from_numpy(idx_h).to(dev)
+    dwts = torch.from_numpy(w_h).to(dev)
+
+    def call(i, s=None, sh=None):
+        lib.moe_layer_dev(out.data_ptr(), xs.data_ptr() + 4 * HIDDEN * (i % n_x), gate,
+                          arena.table.data_ptr(), N_EXPERTS, TOPK, 2.5, sh, HIDDEN, INTER, 10.0,
+                          bias_ptr=bias.data_ptr(), idx_ptr=di.data_ptr(), w_ptr=dw.data_ptr(),
+                          stream=s)
+
+    def known(i, s=None):
+        j = i % n_x
+        lib.moe_decode_dev(out.data_ptr(), xs.data_ptr() + 4 * HIDDEN * j, arena.table.data_ptr(),
+                           N_EXPERTS, didx.data_ptr() + 4 * TOPK * j, dwts.data_ptr() + 4 * TOPK * j,
+                           TOPK, shared, HIDDEN, INTER, 10.0, s)
+
+    torch.cuda.synchronize()
+    ss = st.cuda_stream
+    with torch.cuda.stream(st):
+        for i in range(W):
+            call(i, ss)
+            call(i, ss, shared)
+            known(i, ss)
+        torch.cuda.synchronize()
+        t_eager = time_events(torch, st, lambda i: call(W + i, ss), K)
+        t_shared = time_events(torch, st, lambda i: call(W + i, ss, shared), K)
+        t_known = time_events(torch, st, lambda i: known(W + i, ss), K)
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph, stream=st):
+            for i in range(graph_calls):
+                call(W + K + i, ss)
+        torch.cuda.synchronize()
+        reps = max(1, K // graph_calls)
+        graph.replay()
+        torch.cuda.synchronize()
+        t_graph = time_events(torch, st, lambda i: graph.replay(), reps) / graph_calls
+    assert lib.status() == 0
+    b = TOPK * EXPERT_BYTES + N_EXPERTS * HIDDEN * 2 + 8192 + 16384
+    return {"entry": "dsv4_hip_moe_layer_dev (gate matvec + router + routed experts, no host "
+                     "round trip)",
+            "bytes_per_token": b,
+            "eager_us": round(t_eager * 1e6, 3), "graph_us": round(t_graph * 1e6, 3),
+            "graph_calls": graph_calls,
+            "eager_GBs": round(b / t_eager / 1e9, 1), "graph_GBs": round(b / t_graph / 1e9, 1),
+            "with_shared_us": round(t_shared * 1e6, 3),
+            "known_routing_with_shared_us": round(t_known * 1e6, 3)}
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -745,6 +816,7 @@ def main():
         t_launch = time_events(torch, stream, lambda i: step(W + K + i), K)
         t_launch_dev = time_events(torch, stream, lambda i: step_dev(W + K + i), K)
         assert lib.status() == 0
+        layer = bench_layer(torch, pkg, lib, arena, xs, K, W)
         bytes_step = TOPK * EXPERT_BYTES + 8192 + 16384
         value = bytes_step / t_step / 1e9
         achieved = bytes_step / t_launch / 1e9
@@ -783,6 +855,7 @@ def main():
                               "ms_per_step": round(t_step_dev * 1e3, 5),
                               "value": round(bytes_step / t_step_dev / 1e9, 2),
                               "launch_us": round(t_launch_dev * 1e6, 3)},
+            "moe_layer": layer,
             "cpu_baseline": cpu,
             "wall_s": round(wall, 4),
         }

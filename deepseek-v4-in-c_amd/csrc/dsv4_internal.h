@@ -297,11 +297,19 @@ struct RouteArgs {
 };
 hipError_t moe_route_launch(const RouteArgs &a, hipStream_t st);
 
-/* dsv4_route for n tokens, one workgroup each: scores [n][scores_ld] fp32
+/* dsv4_route for n tokens, one wavefront each: scores [n][scores_ld] fp32
  * (the gate matvec's output) -> idx, w [n][topk], orig [n][n_experts] (may
  * be NULL). bias [n_experts] may be NULL. With tid2eid ([n_vocab][topk]
  * int64) the ids are tid2eid[token], token = token_ids[t] (device) or
- * token_id when token_ids is NULL (n == 1). */
+ * token_id when token_ids is NULL (n == 1).
+ * With gate_w set (n == 1) the launch also computes the scores: gate_w is
+ * the BF16 gate [n_experts][cols] (cols % 8 == 0, cols <= 4096, 16-byte
+ * aligned rows), x the token (fp32, 16-byte aligned); ws_orig / ws_biased
+ * hold n_experts floats each and counter GATE_ROUTE_GROUPS + 1 words, each
+ * on its own 128-byte line (GATE_ROUTE_COUNTER_BYTES), zero before the
+ * launch and zero after it; scores_out (may be NULL) receives the scores. */
+constexpr int GATE_ROUTE_GROUPS = 8;
+constexpr int GATE_ROUTE_COUNTER_BYTES = (GATE_ROUTE_GROUPS + 1) * 128;
 constexpr int GATE_ROUTE_MAX_EXPERTS = 1024;
 constexpr int GATE_ROUTE_MAX_TOPK = 16;
 struct GateRouteArgs {
@@ -319,6 +327,11 @@ struct GateRouteArgs {
     float *w;
     float *orig;
     unsigned *status;
+    const uint16_t *gate_w;
+    const float *x;
+    int cols;
+    float *ws_orig, *ws_biased, *scores_out;
+    unsigned *counter;
 };
 hipError_t gate_route_launch(const GateRouteArgs &a, hipStream_t st);
 

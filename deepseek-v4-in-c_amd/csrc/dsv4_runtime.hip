@@ -85,6 +85,7 @@ struct State {
     unsigned *status = nullptr;          /* status words: [0] _dev calls, [HOST_WORD] host calls */
     unsigned *st = nullptr;              /* the word the call being enqueued raises */
     unsigned *pub = nullptr;             /* one-launch decode: count, done, leave (own lines) */
+    unsigned *rt_count = nullptr;        /* fused gate + router: arrival counters (zero between launches) */
     std::map<uintptr_t, Region> regions; /* host start -> resident copy   */
     DevBuf x, y, mid, table, small, ys, gemm_ws, moe_ws, x16, msplit, route;
 };
@@ -534,6 +535,10 @@ int dsv4_hip_init(int device)
     if (hipMemset(g.status, 0, 256) != hipSuccess) return fail("status clear failed");
     if (hipMalloc((void **)&g.pub, ONE_PUB_BYTES) != hipSuccess) return fail("counter alloc failed");
     if (hipMemset(g.pub, 0, ONE_PUB_BYTES) != hipSuccess) return fail("counter clear failed");
+    if (hipMalloc((void **)&g.rt_count, GATE_ROUTE_COUNTER_BYTES) != hipSuccess)
+        return fail("counter alloc failed");
+    if (hipMemset(g.rt_count, 0, GATE_ROUTE_COUNTER_BYTES) != hipSuccess)
+        return fail("counter clear failed");
     g.st = g.status;
     /* this device's copy of the allocation-free entry point's scratch: its
      * address, once, with the device current; the hand-off words start at
@@ -569,6 +574,8 @@ void dsv4_hip_shutdown(void)
     g.status = nullptr;
     if (g.pub) (void)hipFree(g.pub);
     g.pub = nullptr;
+    if (g.rt_count) (void)hipFree(g.rt_count);
+    g.rt_count = nullptr;
     if (g.stream) (void)hipStreamDestroy(g.stream);
     if (g.side) (void)hipStreamDestroy(g.side);
     if (g.side2) (void)hipStreamDestroy(g.side2);
@@ -902,13 +909,24 @@ int dsv4_hip_moe_layer_dev(float *out, const float *x, const DSV4QMat *gate,
         return -1;
     const hipStream_t st = (hipStream_t)stream;
     const size_t sb = ((size_t)n_experts * 4 + 255) & ~(size_t)255;
-    HIPCHK(g.route.need(sb + 2 * 256), "router workspace");
+    HIPCHK(g.route.need(3 * sb + 2 * 256), "router workspace");
     float *scores = (float *)g.route.p;
-    int *idx = idx_out ? idx_out : (int *)((uint8_t *)g.route.p + sb);
-    float *w = w_out ? w_out : (float *)((uint8_t *)g.route.p + sb + 256);
-    if (enqueue_mmq(*gate, gfmt, x, scores, 1, st)) return -1;
+    int *idx = idx_out ? idx_out : (int *)((uint8_t *)g.route.p + 3 * sb);
+    float *w = w_out ? w_out : (float *)((uint8_t *)g.route.p + 3 * sb + 256);
+    /* a BF16 gate of up to 4096 columns runs fused with the router (one
+     * launch); any other gate runs through dsv4_mmq's kernels first */
+    const bool fused = gfmt == FMT_BF16 && hidden <= 4096;
+    if (!fused && enqueue_mmq(*gate, gfmt, x, scores, 1, st)) return -1;
     GateRouteArgs a;
     memset(&a, 0, sizeof a);
+    if (fused) {
+        a.gate_w = (const uint16_t *)gate->w;
+        a.x = x;
+        a.cols = hidden;
+        a.ws_orig = (float *)((uint8_t *)g.route.p + sb);
+        a.ws_biased = (float *)((uint8_t *)g.route.p + 2 * sb);
+        a.counter = g.rt_count;
+    }
     a.scores = scores;
     a.scores_ld = n_experts;
     a.n = 1;
@@ -923,6 +941,8 @@ int dsv4_hip_moe_layer_dev(float *out, const float *x, const DSV4QMat *gate,
     a.w = w;
     a.status = g.st;
     HIPCHK(gate_route_launch(a, st), "route launch");
+    /* everything on the caller's stream: a fork of the shared expert onto a
+     * second stream cost about 10 us per event wait, more than it hid */
     return enqueue_moe(experts, n_experts, idx, w, topk, shared, sfmt, sinter,
                        hidden, inter, x, out, limit, st);
 }

@@ -184,16 +184,26 @@ class _Layer:
     bias, 256 FP4 experts [2048 x 4096] in one device arena, the FP8 shared
     expert, top-6."""
 
-    def __init__(self, pkg, lib, seed):
+    def __init__(self, pkg, lib, seed, gate_fmt="bf16"):
         import bench
         self.hidden, self.inter, self.ne, self.topk, self.scale = 4096, 2048, 256, 6, 2.5
         rng = np.random.default_rng(seed)
         self.arena = bench.ExpertArena(torch, pkg, lib, self.ne, seed=seed)
         self.shared, self.skeep = bench.make_shared_fp8(torch, pkg, lib, seed + 1)
         g32 = (rng.standard_normal((self.ne, self.hidden)) * 0.02).astype(np.float32)
-        self.W16 = (g32.view(np.uint32) >> 16).astype(np.uint16)   # bf16 by truncation
-        self.dW = torch.from_numpy(self.W16.view(np.int16).reshape(-1).copy()).to(DEV)
-        self.gate = pkg.qmat(pkg.DSV4_WBF16, self.dW.data_ptr(), None, self.ne, self.hidden, 0, 0)
+        if gate_fmt == "bf16":
+            W16 = (g32.view(np.uint32) >> 16).astype(np.uint16)   # bf16 by truncation
+            self.gkeep = [torch.from_numpy(W16.view(np.int16).reshape(-1).copy()).to(DEV)]
+            self.gate = pkg.qmat(pkg.DSV4_WBF16, self.gkeep[0].data_ptr(), None, self.ne,
+                                 self.hidden, 0, 0)
+            self.hgate = P.HostMat(P.DSV4_WBF16, W16, None, self.ne, self.hidden, 0, 0)
+        else:
+            W, S = P.Oracle().quant_fp8_blk128(g32)
+            self.gkeep = [torch.from_numpy(np.ascontiguousarray(W, np.uint8).reshape(-1)).to(DEV),
+                          dev_f32(S)]
+            self.gate = pkg.qmat(pkg.DSV4_WFP8_F32S, self.gkeep[0].data_ptr(),
+                                 self.gkeep[1].data_ptr(), self.ne, self.hidden, 128, 128)
+            self.hgate = P.HostMat(P.DSV4_WFP8_F32S, W, S, self.ne, self.hidden, 128, 128)
         self.bias = (rng.standard_normal(self.ne) * 0.05).astype(np.float32)
         self.dbias = dev_f32(self.bias)
         self.t2e = np.stack([rng.choice(self.ne, self.topk, replace=False)
@@ -223,14 +233,16 @@ class _Layer:
         return (oracle.moe_combine(acc, w) + oracle.expert_forward(self.hshared, xh, 10.0)).astype(np.float32)
 
 
-@pytest.mark.parametrize("hash_tok", [None, 17])
-def test_moe_layer_matches_oracle_pipeline(lib, pkg, oracle, hash_tok):
+@pytest.mark.parametrize("hash_tok,gate_fmt", [(None, "bf16"), (17, "bf16"), (None, "fp8")])
+def test_moe_layer_matches_oracle_pipeline(lib, pkg, oracle, hash_tok, gate_fmt):
     """The device block against the reference's sequence run by the oracle:
-    gate scores (bf16_n, fp64 sums) within one ulp, the router's picks and
-    weights as dsv4_route gives them on the oracle's scores, and the block's
-    output within 1e-4 relative L2 of the oracle's experts combined in k order
-    plus the shared expert. Biased routing and hash routing (token 17)."""
-    L = _Layer(pkg, lib, zlib.crc32(b"layer") & 0xFFFF)
+    gate scores (dsv4_mmq: bf16_n with fp64 sums, or the FP8 matvec) within one
+    ulp, resp. 1e-4 relative L2, the router's picks and weights as dsv4_route
+    gives them on the oracle's scores, and the block's output within 1e-4
+    relative L2 of the oracle's experts combined in k order plus the shared
+    expert. Biased routing and hash routing (token 17); the BF16 gate runs
+    fused with the router, the FP8 gate through the matvec kernels first."""
+    L = _Layer(pkg, lib, (zlib.crc32(b"layer") & 0xFFFF) + len(gate_fmt), gate_fmt)
     lib.status()
     for seed in (3, 4):
         xh = bf16_x(seed, L.hidden)
@@ -243,16 +255,22 @@ def test_moe_layer_matches_oracle_pipeline(lib, pkg, oracle, hash_tok):
         lib.mmq_n_dev(sc.data_ptr(), x.data_ptr(), L.gate, 1)
         torch.cuda.synchronize()
         assert lib.status() == 0
-        sc_o = oracle.bf16_n(L.W16, xh, L.ne, L.hidden)
-        assert np.all(_ulps(sc.cpu().numpy(), sc_o) <= 1), "gate scores beyond one ulp"
+        sc_o = oracle.mmq_n(L.hgate, xh)
+        if gate_fmt == "bf16":
+            assert np.all(_ulps(sc.cpu().numpy(), sc_o) <= 1), "gate scores beyond one ulp"
+        else:
+            check_close(sc.cpu().numpy(), sc_o, 1e-4)
+        # the router on the device's own scores (a matvec's fp32 rounding can
+        # move a score by an ulp or two; the router's parity is pinned on
+        # identical scores)
         bias = None if hash_tok is not None else L.bias
-        wi, ww, wo = oracle.route(sc_o, L.topk, L.scale, bias=bias,
+        wi, ww, wo = oracle.route(sc.cpu().numpy(), L.topk, L.scale, bias=bias,
                                   tid2eid=L.t2e if hash_tok is not None else None,
                                   token_id=hash_tok or 0)
         gi, gw = di.cpu().numpy(), dw.cpu().numpy()
         _assert_ids(gi[None], wi[None], (wo + (bias if bias is not None else 0))[None], "layer")
         _assert_w(gw, ww, "layer")
-        check_close(out.cpu().numpy(), L.want(oracle, xh, wi, ww), 1e-4)
+        check_close(out.cpu().numpy(), L.want(oracle, xh, gi, gw), 1e-4)
 
 
 def test_moe_layer_graph_replays(lib, pkg, oracle):
