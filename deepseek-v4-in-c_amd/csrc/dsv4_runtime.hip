@@ -1044,7 +1044,7 @@ int dsv4_hip_moe_decode_routed_noalloc_dev(float *out, const float *x, const DSV
                        inter, x, out, limit, (hipStream_t)stream, routed, wv, &ws);
 }
 
-/* ------------------------------------------- checkpoint experts (f4) --- */
+/* ------------------------------------------- checkpoint experts --- */
 
 /* experts.idx record (tools/pack_trunk.py writes "<iiqq"). */
 struct ExpLoc {

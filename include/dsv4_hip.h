@@ -94,7 +94,7 @@ int  dsv4_hip_unregister(const void *host);
 /* Device address of the resident copy of host byte `p`, or NULL. */
 void *dsv4_hip_device_ptr(const void *p);
 
-/* ------------------------------------------------- packed matmul (a7-a9) --
+/* ------------------------------------------------- packed matmul ---------
  * y[t*rows + o] = sum_c x[t*cols + c] * W[o, c] for t in 0..nt-1.
  * Replaces the body of dsv4_mmq_n (src/10_compute/dsv4_matmul.h:40,
  * dsv4_matmul.c:44-73): DSV4_WBF16 (no scales; products and sums in fp64
@@ -110,7 +110,7 @@ int  dsv4_hip_mmq(float *y, const float *x, const DSV4QMat *m);
 int  dsv4_hip_mmq_n_dev(float *y, const float *x, const DSV4QMat *m, int nt,
                         void *stream);
 
-/* -------------------------------------------- expert FFN (a10, a11) -------
+/* -------------------------------------------- expert FFN ----------------
  * out = w2 . swiglu(w1 . x, w3 . x) for one token, SwiGLU with the
  * reference's asymmetric clamp (src/10_compute/dsv4_ops.c:61-79; limit <= 0
  * disables it). Replaces dsv4_expert_forward (src/10_compute/dsv4_kernels.h:30-32)
@@ -118,7 +118,7 @@ int  dsv4_hip_mmq_n_dev(float *y, const float *x, const DSV4QMat *m, int nt,
 int  dsv4_hip_expert_forward(float *out, const float *x, const DSV4ExpertW *e,
                              int inter, float limit);
 
-/* ----------------------------------------- decode MoE (a11 + a12) --------
+/* ----------------------------------------- decode MoE ---------------------
  * out = sum_{k in 0..topk-1, in k order} w[k] * expert(ex[k], x)  +  shared(x)
  * for one token; the shared expert (may be NULL) is added unweighted after the
  * routed sum. Replaces the compute of dsv4_layer_moe
@@ -181,7 +181,7 @@ int  dsv4_hip_moe_decode_routed_noalloc_dev(float *out, const float *x,
                                             const DSV4ExpertW *shared, int hidden, int inter,
                                             float limit, void *stream);
 
-/* ------------------------------------------- router on the device (f2) ----
+/* ------------------------------------------- router on the device ---------
  * dsv4_route (src/10_compute/dsv4_ops.c:117-157, declared at
  * src/10_compute/dsv4_kernels.h:23) for n tokens, as the prefill loop calls
  * it (src/80_prefill/dsv4_prefill_moe.c:22-29): scores [n][n_experts] are
@@ -221,7 +221,7 @@ int  dsv4_hip_moe_layer_dev(float *out, const float *x, const DSV4QMat *gate,
                             const DSV4ExpertW *shared, int hidden, int inter, float limit,
                             int *idx_out, float *w_out, void *stream);
 
-/* ------------------------------------- grouped MoE (a13-a15, a18) ---------
+/* ------------------------------------- grouped MoE -------------------------
  * For n tokens (batched decode or a prefill block):
  *   out[t] = sum_{k in 0..topk-1, in k order} w[t][k] * expert_{idx[t][k]}(x[t])
  *            + shared(x[t])            (shared may be NULL; added unweighted)
@@ -275,7 +275,7 @@ int  dsv4_hip_moe_grouped_mx_dev(float *out, const float *x, int n,
                                  const DSV4ExpertW *shared, int hidden, int inter,
                                  float limit, void *stream);
 
-/* ------------------------------------------------ prefill GEMM (a16, a17) --
+/* ------------------------------------------------ prefill GEMM -------------
  * C[m][n] = sum_k A[m][k] * W[n][k] for m < M on CDNA4 FP8 MFMA, replacing the
  * GPU leg of the prefill projection seam, dsv4_prefill_vk_gemm
  * (src/80_prefill/dsv4_prefill_vk.h:37-41; seam src/80_prefill/dsv4_prefill_proj.c:17-27).

@@ -20,7 +20,7 @@ import pyoracle  # noqa: E402
 PKG_DIR = os.path.join(ROOT, "deepseek-v4-in-c_amd")
 GOLDEN = os.path.join(ROOT, "tests", "golden")
 
-# numerical contract: relative L2 against the oracle (BASELINE north star)
+# numerical contract: relative L2 against the oracle
 REL_L2_TOL = 1e-3
 
 
