@@ -1019,6 +1019,112 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) void k
     gateup_px_item<NP>(a, (int)blockIdx.x, lds);
 }
 
+/* Gate/up + SwiGLU of one FP8 expert (E8M0 or fp32 128 x 128 block scales)
+ * in 8-row tiles, for the shared expert and single experts, whose mid needs
+ * no split table: one workgroup per (slot, 8 rows), so a 2048-row expert
+ * spreads over 256 workgroups (32-row groups gave 64, a quarter of the CUs,
+ * and ran at 1.2 TB/s). Waves 0-3 take w1, waves 4-7 w3, each over a quarter
+ * of K in NP chunk pairs (hidden = 1024 NP <= 4096): A rows 0-7 are the tile's rows
+ * at chunk 2m, rows 8-15 the same rows at chunk 2m + 1, as in the FP4 pair
+ * kernels; B is the workgroup's split of x. E8M0 scales go in the MFMA's
+ * scale operand per lane (rows 8-15 take the odd chunk's), fp32 scales
+ * multiply each pair's product (one MFMA from zero) row by row. */
+template <int FMT, int NP>
+__global__ __launch_bounds__(512) void k_gateup_px8(GateUpMxArgs a)
+{
+    extern __shared__ __align__(16) uint8_t lds[];
+    constexpr int NC = 8 * NP;                         /* chunks of hidden */
+    constexpr int UPL = (NC * 16 + 511) / 512;
+    constexpr bool F32S = FMT == FMT_FP8_F32S;
+    const int lane = threadIdx.x & 63;
+    const int wave = wave_in_group();
+    const int mat = wave >> 2, kq = wave & 3;
+    const int tiles = a.inter / 8;
+    const int slot = blockIdx.x / tiles;
+    const int r0 = (blockIdx.x - slot * tiles) * 8;
+    const int r8 = lane & 7, par = (lane >> 3) & 1, g = lane >> 4;
+    const int c0 = kq * 2 * NP;                        /* the wave's first chunk */
+    uint8_t *tab = lds;                                /* NC chunks + zero operand */
+    float *red = (float *)(lds + NC * TAB_CHUNK + TAB_ZERO);   /* [2 mats][4 quarters][16] */
+    float *mid = a.mid + (size_t)slot * a.mid_ld;
+
+    DSV4ExpertW e;
+    unsigned bad = gateup_expert(a, slot, e);
+    if (!bad && (!mx_desc_ok<FMT>(e.w1, a.inter, a.hidden) || !mx_desc_ok<FMT>(e.w3, a.inter, a.hidden)))
+        bad = ST_BAD_DESCRIPTOR;
+    if (bad) {
+        if (threadIdx.x == 0) atomicOr(a.status, bad);
+        if (threadIdx.x < 8) mid[r0 + threadIdx.x] = qnan_f();
+        return;
+    }
+    const DSV4QMat &m = mat ? e.w3 : e.w1;
+    const uint8_t *wrow = (const uint8_t *)m.w + (size_t)(r0 + r8) * a.hidden;
+    const int sc_cols = a.hidden / 128;
+    const size_t srow = (size_t)(r0 / m.blk_r) * sc_cols;
+
+    XUnits<UPL> xu;
+    load_units<UPL, 512>(xu, a.x, 0, 1, 0, NC, (int)threadIdx.x);
+    DSV4_ORDER();
+    /* this lane's chunk scale per pair: E8M0 for the A rows of the lane
+     * (rows 8-15, par = 1: the odd chunk), fp32 for its accumulator rows
+     * (lanes 32-63 hold rows 8-15) */
+    uint32_t sv[NP];
+#pragma unroll
+    for (int i = 0; i < NP; i++) {
+        if constexpr (F32S) sv[i] = gptr((const uint32_t *)m.s)[srow + c0 + 2 * i + (lane >> 5)];
+        else sv[i] = ld_u8(m.s, srow + c0 + 2 * i + par);
+    }
+    DSV4_ORDER();
+    u32x4 q[NP][2];
+#pragma unroll
+    for (int i = 0; i < NP; i++) {
+        const int c = c0 + 2 * i + par;
+        q[i][0] = ld_stream16(wrow + 128 * c + 16 * g);
+        q[i][1] = ld_stream16(wrow + 128 * c + 64 + 16 * g);
+    }
+    DSV4_ORDER();
+    store_units<UPL, 512>(tab, xu, 1, NC, (int)threadIdx.x);
+    __builtin_amdgcn_s_waitcnt(0xC07F);                /* lgkmcnt(0): own LDS writes done */
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+    const BPair bp = bpair_src(tab, c0, tab + NC * TAB_CHUNK, lane);
+    v4f acc = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int i = 0; i < NP; i++) {
+        const u32x4 lo = *(const u32x4 *)(bp.d + i * bp.step);
+        const u32x4 hi = *(const u32x4 *)(bp.d + i * bp.step + 16);
+        const int sb = *(const int *)(bp.s + i * bp.step);
+        v8i b, av;
+        b[0] = (int)lo.x; b[1] = (int)lo.y; b[2] = (int)lo.z; b[3] = (int)lo.w;
+        b[4] = (int)hi.x; b[5] = (int)hi.y; b[6] = (int)hi.z; b[7] = (int)hi.w;
+        av[0] = (int)q[i][0].x; av[1] = (int)q[i][0].y; av[2] = (int)q[i][0].z; av[3] = (int)q[i][0].w;
+        av[4] = (int)q[i][1].x; av[5] = (int)q[i][1].y; av[6] = (int)q[i][1].z; av[7] = (int)q[i][1].w;
+        if constexpr (F32S) {
+            /* accumulator rows 0-7 (lanes 0-31) are the even chunk's, rows
+             * 8-15 (lanes 32-63) the odd chunk's: each lane scales its rows */
+            const v4f zero = {0.0f, 0.0f, 0.0f, 0.0f};
+            const v4f pr = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(av, b, zero, 0, 0, 0, E8M0_ONE, 0, sb);
+            const float sw = __uint_as_float(sv[i]);
+#pragma unroll
+            for (int e2 = 0; e2 < 4; e2++) acc[e2] = fmaf(pr[e2], sw, acc[e2]);
+        } else {
+            acc = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(av, b, acc, 0, 0, 0, (int)sv[i], 0, sb);
+        }
+    }
+    store_pair_partials(acc, red + (mat * 4 + kq) * 16, lane);
+    __syncthreads();
+    if (threadIdx.x < 8) {
+        const int rr = threadIdx.x;
+        float gs = 0.0f, us = 0.0f;
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+            gs += red[(0 * 4 + k) * 16 + rr] + red[(0 * 4 + k) * 16 + 8 + rr];
+            us += red[(1 * 4 + k) * 16 + rr] + red[(1 * 4 + k) * 16 + 8 + rr];
+        }
+        mid[r0 + rr] = dev_swiglu(gs, us, a.limit);
+    }
+}
+
 /* Routed FP4 down projections (inter = 256 NP) with the k-order combine. One
  * workgroup per 16 output rows, two waves (8-row tiles) per routed expert k,
  * each over all of inter, reading slot k's split table. */
@@ -1290,9 +1396,28 @@ hipError_t gateup_px_k(const GateUpMxArgs &a, hipStream_t st)
     return hipGetLastError();
 }
 
+template <int FMT, int NP>
+hipError_t gateup_px8_k(const GateUpMxArgs &a, hipStream_t st)
+{
+    const size_t lds = (size_t)8 * NP * TAB_CHUNK + TAB_ZERO + 2 * 4 * 16 * 4;
+    const dim3 grid((unsigned)(a.nslots * (a.inter / 8)));
+    hipLaunchKernelGGL((k_gateup_px8<FMT, NP>), grid, dim3(512), lds, st, a);
+    return hipGetLastError();
+}
+
 template <int FMT>
 hipError_t gateup_mx_fmt(const GateUpMxArgs &a, hipStream_t st)
 {
+    if constexpr (FMT != FMT_FP4_E8M0) {
+        if (!a.msplit) {                    /* 8-row tiles: hidden = 1024 NP */
+            switch (a.hidden) {
+            case 1024: return gateup_px8_k<FMT, 1>(a, st);
+            case 2048: return gateup_px8_k<FMT, 2>(a, st);
+            case 4096: return gateup_px8_k<FMT, 4>(a, st);
+            default: break;
+            }
+        }
+    }
     if constexpr (FMT == FMT_FP4_E8M0) {
         switch (a.hidden) {                 /* chunk-pair kernel: hidden = 512 NP */
         case 512: return gateup_px_k<1>(a, st);
