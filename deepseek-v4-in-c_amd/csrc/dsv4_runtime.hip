@@ -1385,20 +1385,11 @@ static int enqueue_moe_grouped(float *out, const float *x, int n, const DSV4Expe
     HIPCHK(moe_route_launch(ra, st), "route launch");
     HIPCHK(to_f16_rows_launch(x16, ex, x, n, hidden, st), "x fp16 launch");
 
-    GroupedArgs ga;
-    memset(&ga, 0, sizeof ga);
-    ga.table = table; ga.n_experts = n_experts; ga.grp_off = grp; ga.tile_pre = tp; ga.tile_grp = tg;
-    ga.row_tok = row; ga.nrows = n; ga.B = x16; ga.bexp = ex; ga.K = hidden; ga.N = inter;
-    ga.out = mid; ga.limit = limit; ga.status = g.st;
-    HIPCHK(grouped_launch(FMT_FP4_E8M0, true, tt, ga, max_tiles, st), "routed gate/up launch");
-    ga.row_tok = nullptr; ga.bexp = nullptr;
-    ga.nrows = (int)P; ga.B = mid; ga.K = inter; ga.N = hidden; ga.out = y;
-    HIPCHK(grouped_launch(FMT_FP4_E8M0, false, tt, ga, max_tiles, st), "routed down launch");
-
     float *ys = nullptr;
     if (shared) {
         /* the shared expert needs only x16: it runs on the side stream,
-         * forked after the fp16 convert and joined before the combine */
+         * forked right after the fp16 convert (before the routed launches
+         * are enqueued, so it overlaps them) and joined before the combine */
         HIPCHK(hipEventRecord(g.fork, st), "fork record");
         HIPCHK(hipStreamWaitEvent(g.side, g.fork, 0), "fork wait");
         uint16_t *smid = (uint16_t *)(ws + o_smid);
@@ -1414,6 +1405,17 @@ static int enqueue_moe_grouped(float *out, const float *x, int n, const DSV4Expe
         HIPCHK(grouped_launch(sfmt, false, stt, sa, stiles, g.side), "shared down launch");
         HIPCHK(hipEventRecord(g.join, g.side), "join record");
     }
+
+    GroupedArgs ga;
+    memset(&ga, 0, sizeof ga);
+    ga.table = table; ga.n_experts = n_experts; ga.grp_off = grp; ga.tile_pre = tp; ga.tile_grp = tg;
+    ga.row_tok = row; ga.nrows = n; ga.B = x16; ga.bexp = ex; ga.K = hidden; ga.N = inter;
+    ga.out = mid; ga.limit = limit; ga.status = g.st;
+    HIPCHK(grouped_launch(FMT_FP4_E8M0, true, tt, ga, max_tiles, st), "routed gate/up launch");
+    ga.row_tok = nullptr; ga.bexp = nullptr;
+    ga.nrows = (int)P; ga.B = mid; ga.K = inter; ga.N = hidden; ga.out = y;
+    HIPCHK(grouped_launch(FMT_FP4_E8M0, false, tt, ga, max_tiles, st), "routed down launch");
+
     if (shared) HIPCHK(hipStreamWaitEvent(st, g.join, 0), "join wait");
     CombineArgs ca;
     ca.out = out; ca.Y = y; ca.YS = ys; ca.w = w; ca.pos = pos;
