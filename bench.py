@@ -726,6 +726,9 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-other", action="store_true",
                     help="config 4: skip timing the other precision path (counter runs)")
+    ap.add_argument("--no-others", action="store_true",
+                    help="config 1: do not run configs 0, 2, 3 and 4 as child processes "
+                         "(their lines go into other_configs)")
     ap.add_argument("--exact", action="store_true",
                     help="config 4: time the exact fp16-MFMA grouped path instead of the "
                          "block-scaled one")
@@ -926,7 +929,30 @@ def main():
             "cpu_baseline": cpu,
             "wall_s": round(wall, 4),
         }
+    if args.config == 1 and not args.no_others:
+        res["other_configs"] = other_configs(args)
     print(json.dumps(res), flush=True)
+
+
+def other_configs(args):
+    """Configs 0, 2, 3 and 4, each in a child process of this one (its own
+    data and HIP context, nothing else on the GPU meanwhile), so that the
+    default run times every workload: their JSON lines, without CPU
+    baselines, keyed by config."""
+    out = {}
+    for c, steps in ((0, 200), (2, 50), (3, 100), (4, 30)):
+        cmd = [sys.executable, os.path.abspath(__file__), "--config", str(c), "--no-cpu",
+               "--steps", str(steps), "--warmup", str(min(args.warmup, 5))]
+        log(f"config {c} in a child process")
+        r = subprocess.run(cmd, stdout=subprocess.PIPE, text=True, timeout=600)
+        lines = [ln for ln in r.stdout.splitlines() if ln.startswith("{")]
+        if r.returncode != 0 or not lines:
+            out[str(c)] = {"error": f"exit {r.returncode}"}
+            continue
+        d = json.loads(lines[-1])
+        d.pop("cpu_baseline", None)
+        out[str(c)] = d
+    return out
 
 
 if __name__ == "__main__":
