@@ -320,3 +320,52 @@ def test_moe_layer_rejects_bad_gate(lib, pkg):
     with pytest.raises(Exception, match="gate"):
         lib.moe_layer_dev(p, p, gate, p, 256, 6, 1.0, None, 4096, 2048, 10.0)
     torch.cuda.synchronize()
+
+
+@pytest.mark.parametrize("ne,hidden,topk", [(64, 1024, 8), (300, 2048, 6), (1024, 512, 16), (8, 4096, 8)])
+def test_fused_gate_router_shapes(lib, pkg, oracle, ne, hidden, topk):
+    """The fused gate matvec + router launch at other geometries (1 to 16
+    experts per lane, 1 to 8 row chunks per lane, one to 256 workgroups):
+    the picks and weights of `dsv4_hip_moe_layer_dev` against dsv4_route on
+    the oracle's bf16_n scores (near ties excepted as above), over four
+    tokens in a row so the arrival counters' reset is exercised; small FP4
+    experts behind it."""
+    rng = np.random.default_rng(ne * 7 + hidden)
+    inter = 256
+    descs, host, keep = [], [], []
+    for _ in range(ne):
+        q, hm = [], []
+        for (r, c) in ((inter, hidden), (inter, hidden), (hidden, inter)):
+            W, S = oracle.quant_fp4_mx((rng.standard_normal((r, c)) * 0.02).astype(np.float32))
+            dW, dS = (torch.from_numpy(np.ascontiguousarray(a, np.uint8).reshape(-1)).to(DEV) for a in (W, S))
+            keep += [dW, dS]
+            q.append(pkg.qmat(pkg.DSV4_WFP4, dW.data_ptr(), dS.data_ptr(), r, c, 1, 32))
+            hm.append(P.HostMat(pkg.DSV4_WFP4, W, S, r, c, 1, 32))
+        descs.append(pkg.ExpertW(q[0], q[1], q[2]))
+        host.append(P.HostExpert(hm[0], hm[1], hm[2]))
+    tbl = torch.from_numpy(np.frombuffer(b"".join(bytes(d) for d in descs), np.uint8).copy()).to(DEV)
+    g32 = (rng.standard_normal((ne, hidden)) * 0.05).astype(np.float32)
+    W16 = (g32.view(np.uint32) >> 16).astype(np.uint16)
+    dW16 = torch.from_numpy(W16.view(np.int16).reshape(-1).copy()).to(DEV)
+    gate = pkg.qmat(pkg.DSV4_WBF16, dW16.data_ptr(), None, ne, hidden, 0, 0)
+    bias = (rng.standard_normal(ne) * 0.05).astype(np.float32)
+    dbias = dev_f32(bias)
+    out = torch.empty(hidden, dtype=torch.float32, device=DEV)
+    di = torch.empty(topk, dtype=torch.int32, device=DEV)
+    dw = torch.empty(topk, dtype=torch.float32, device=DEV)
+    lib.status()
+    for tkn in range(4):
+        xh = bf16_x(100 + tkn, hidden)
+        x = dev_f32(xh)
+        lib.moe_layer_dev(out.data_ptr(), x.data_ptr(), gate, tbl.data_ptr(), ne, topk, 1.5, None,
+                          hidden, inter, 10.0, bias_ptr=dbias.data_ptr(), idx_ptr=di.data_ptr(),
+                          w_ptr=dw.data_ptr())
+        torch.cuda.synchronize()
+        assert lib.status() == 0
+        sc_o = oracle.bf16_n(W16, xh, ne, hidden)
+        wi, ww, wo = oracle.route(sc_o, topk, 1.5, bias=bias)
+        gi, gw = di.cpu().numpy(), dw.cpu().numpy()
+        _assert_ids(gi[None], wi[None], (wo + bias)[None], f"token {tkn}")
+        _assert_w(gw, ww, f"token {tkn}")
+        acc = np.stack([oracle.expert_forward(host[int(i)], xh, 10.0) for i in gi])
+        check_close(out.cpu().numpy(), oracle.moe_combine(acc, gw), 1e-4)
