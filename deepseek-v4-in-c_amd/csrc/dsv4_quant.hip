@@ -210,12 +210,31 @@ hipError_t quant_fp8_blk128_launch(uint8_t *W, float *S, const float *w,
 
 /* --------------------------------------------- activation quantizers ---- */
 
+/* e4m3(v / s) with v / s correctly rounded (the oracle's rule), without a
+ * division in almost every case: q0 = v * (1 / s) lies within 3 * 2^-24 of
+ * v / s relative, so the correctly rounded quotient lies between
+ * q0 (1 - 2^-21) and q0 (1 + 2^-21); when both ends convert to the same code
+ * (the convert rounds to nearest even, monotonically, below 464), so does
+ * the quotient. Otherwise -- near a rounding boundary, about 1e-5 of
+ * Gaussian inputs, or |q0| >= 448, NaN, infinities -- the division. */
+__device__ __forceinline__ uint32_t e4m3_quot(float v, float s, float rs)
+{
+    const float q0 = v * rs;
+    if (fabsf(q0) < 448.0f) {
+        const float lo = q0 * (1.0f - 0x1p-21f), hi = q0 * (1.0f + 0x1p-21f);
+        const uint32_t pk = (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(lo, hi, 0, false);
+        if ((pk & 0xFFu) == ((pk >> 8) & 0xFFu)) return pk & 0xFFu;
+    }
+    return hw_e4m3(v / s);
+}
+
 /* 16 lanes per 1x128 group, 8 consecutive elements per lane (one 16-byte
  * bf16 load or two fp32 loads, one 8-byte store); a 256-thread block covers
  * 16 groups. s = amax / 448 (1 if the group is all zero), q = e4m3(v / s)
- * with a correctly rounded division -- the oracle's rule. The scale of token
- * t, block b goes to S[t][b], or to S[b][t] (S_BLK_MAJOR: one block's scales
- * of consecutive tokens are contiguous, as the GEMM reads them). */
+ * with a correctly rounded division -- the oracle's rule (e4m3_quot). The
+ * scale of token t, block b goes to S[t][b], or to S[b][t] (S_BLK_MAJOR: one
+ * block's scales of consecutive tokens are contiguous, as the GEMM reads
+ * them). */
 template <bool S_BLK_MAJOR>
 __device__ __forceinline__ void quant8_1x128(const float (&v)[8], uint8_t *Q, float *S, size_t e, bool live,
                                              int n, int k)
@@ -231,11 +250,12 @@ __device__ __forceinline__ void quant8_1x128(const float (&v)[8], uint8_t *Q, fl
         if (S_BLK_MAJOR) S[(e % (size_t)k) / 128 * (size_t)n + e / (size_t)k] = sc;
         else S[e / 128] = sc;
     }
+    const float rs = 1.0f / sc;
     uint2 out;
-    out.x = hw_e4m3(v[0] / sc) | (hw_e4m3(v[1] / sc) << 8) | (hw_e4m3(v[2] / sc) << 16) |
-            (hw_e4m3(v[3] / sc) << 24);
-    out.y = hw_e4m3(v[4] / sc) | (hw_e4m3(v[5] / sc) << 8) | (hw_e4m3(v[6] / sc) << 16) |
-            (hw_e4m3(v[7] / sc) << 24);
+    out.x = e4m3_quot(v[0], sc, rs) | (e4m3_quot(v[1], sc, rs) << 8) | (e4m3_quot(v[2], sc, rs) << 16) |
+            (e4m3_quot(v[3], sc, rs) << 24);
+    out.y = e4m3_quot(v[4], sc, rs) | (e4m3_quot(v[5], sc, rs) << 8) | (e4m3_quot(v[6], sc, rs) << 16) |
+            (e4m3_quot(v[7], sc, rs) << 24);
     *(uint2 *)(Q + e) = out;
 }
 

@@ -181,6 +181,44 @@ def test_gemm_rejects_bad_geometry(lib, pkg):
     assert rc == -1 and "multiples of 128" in lib.error()
 
 
+def _e4m3_values():
+    v = []
+    for c in range(0x7F):
+        e, m = c >> 3, c & 7
+        v.append((1 + m / 8) * 2.0 ** (e - 7) if e else m / 8 * 2.0 ** -6)
+    return np.array(v)
+
+
+def test_act_quant_1x128_near_rounding_boundaries(lib, pkg, oracle):
+    """Elements placed within four fp32 ulps of an e4m3 rounding boundary (the
+    midpoint of two codes) times the group's scale, at scales from 2^-40 to
+    2^40 and both signs: the quantizer's multiply-by-reciprocal fast path
+    must hand every such element to the division, bit-exact against the
+    oracle's e4m3(v / s)."""
+    rng = np.random.default_rng(23)
+    n, k = 64, 1024
+    vals = _e4m3_values()
+    mids = (vals[:-1] + vals[1:]) / 2
+    a = np.empty((n, k), np.float32)
+    for t in range(n):
+        amax = np.float32(2.0 ** rng.integers(-40, 40) * rng.uniform(0.5, 1.0))
+        s = np.float32(amax / np.float32(448.0))
+        m = rng.choice(mids, k).astype(np.float32)
+        v = (m * s).astype(np.float32).view(np.int32) + rng.integers(-4, 5, k).astype(np.int32)
+        row = v.view(np.float32) * np.where(rng.random(k) < 0.5, -1, 1).astype(np.float32)
+        row[:: 128] = amax                              # every group's maximum is amax
+        a[t] = np.clip(row, -amax, amax)
+    da = dev(a)
+    Q = torch.empty(n * k, dtype=torch.uint8, device=DEV)
+    S = torch.empty(n * (k // 128), dtype=torch.float32, device=DEV)
+    lib.quant_act_fp8_1x128_dev(Q.data_ptr(), S.data_ptr(), da.data_ptr(), n, k)
+    torch.cuda.synchronize()
+    Qo, So = oracle.quant_act_fp8_1x128(a)
+    got_q = Q.cpu().numpy()
+    bad = np.nonzero(got_q != Qo)[0]
+    assert bad.size == 0, f"{bad.size} codes differ, first at {bad[:4]}: {got_q[bad[:4]]} vs {Qo[bad[:4]]}"
+
+
 def test_act_quant_1x128_edge_cases(lib, pkg, oracle):
     """Bit-exact against the oracle on values the fast path must get right:
     magnitudes from e4m3's subnormal range to its maximum, exact
