@@ -322,10 +322,12 @@ def test_moe_layer_rejects_bad_gate(lib, pkg):
     torch.cuda.synchronize()
 
 
-@pytest.mark.parametrize("ne,hidden,topk", [(64, 1024, 8), (300, 2048, 6), (1024, 512, 16), (8, 4096, 8)])
+@pytest.mark.parametrize("ne,hidden,topk", [(64, 1024, 8), (300, 2048, 6), (1024, 512, 16), (8, 4096, 8),
+                                           (16, 8192, 4)])
 def test_fused_gate_router_shapes(lib, pkg, oracle, ne, hidden, topk):
     """The fused gate matvec + router launch at other geometries (1 to 16
-    experts per lane, 1 to 8 row chunks per lane, one to 256 workgroups):
+    experts per lane, 1 to 8 row chunks per lane, 8 to 1024 workgroups), and
+    a gate too wide for it (8192 columns: the BF16 matvec, then the router):
     the picks and weights of `dsv4_hip_moe_layer_dev` against dsv4_route on
     the oracle's bf16_n scores (near ties excepted as above), over four
     tokens in a row so the arrival counters' reset is exercised; small FP4
