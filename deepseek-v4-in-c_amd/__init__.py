@@ -39,7 +39,7 @@ EXPORTS = (
     "dsv4_hip_quant_fp4_mx_dev", "dsv4_hip_quant_act_fp8_1x128_dev",
     "dsv4_hip_quant_act_mxfp8_dev", "dsv4_hip_synth_normal_dev", "dsv4_hip_moe_route_dev",
     "dsv4_hip_moe_grouped_mx_mid_dev", "dsv4_hip_shared_fp8q_mid_dev",
-    "dsv4_hip_route_dev", "dsv4_hip_moe_layer_dev",
+    "dsv4_hip_route_dev", "dsv4_hip_moe_layer_dev", "dsv4_hip_moe_layer_n_dev",
 )
 # the reference-named C mirror (host/dsv4_compute_hip.c)
 MIRROR_EXPORTS = ("dsv4_mmq_n", "dsv4_mmq", "dsv4_expert_forward")
@@ -141,6 +141,10 @@ class Lib:
         L.dsv4_hip_moe_route_dev.argtypes = [_P, _P, _P, _P, _P, _I, _I, _I, _P]
         L.dsv4_hip_route_dev.restype = _I
         L.dsv4_hip_route_dev.argtypes = [_P, _P, _P, _P, _I, _P, _P, _I, _P, _I, _I, _F, _P]
+        L.dsv4_hip_moe_layer_n_dev.restype = _I
+        L.dsv4_hip_moe_layer_n_dev.argtypes = [_P, _P, _I, C.POINTER(QMat), _P, _P, _I, _P, _F,
+                                               _P, _I, _I, C.POINTER(ExpertW), _I, _I, _F, _I,
+                                               _P, _P, _P]
         L.dsv4_hip_moe_layer_dev.restype = _I
         L.dsv4_hip_moe_layer_dev.argtypes = [_P, _P, C.POINTER(QMat), _P, _P, _I, _I, _F,
                                              _P, _I, _I, C.POINTER(ExpertW), _I, _I, _F,
@@ -387,6 +391,19 @@ class Lib:
                                                    topk, sp, hidden, inter, float(limit),
                                                    idx_ptr, w_ptr, stream),
                    "dsv4_hip_moe_layer_dev")
+
+
+    def moe_layer_n_dev(self, out_ptr, x_ptr, n, gate: QMat, table_ptr, n_experts, topk,
+                        route_scale, shared: ExpertW | None, hidden, inter, limit, mx=False,
+                        bias_ptr=None, tid2eid_ptr=None, n_vocab=0, token_ids_ptr=None,
+                        idx_ptr=None, w_ptr=None, stream=None):
+        sp = C.pointer(shared) if shared is not None else None
+        self.check(self.lib.dsv4_hip_moe_layer_n_dev(out_ptr, x_ptr, n, C.byref(gate), bias_ptr,
+                                                     tid2eid_ptr, n_vocab, token_ids_ptr,
+                                                     float(route_scale), table_ptr, n_experts, topk,
+                                                     sp, hidden, inter, float(limit), int(bool(mx)),
+                                                     idx_ptr, w_ptr, stream),
+                   "dsv4_hip_moe_layer_n_dev")
 
 
 class Mirror:

@@ -1604,6 +1604,62 @@ int dsv4_hip_moe_grouped_dev(float *out, const float *x, int n, const DSV4Expert
                                hidden, inter, limit, (hipStream_t)stream);
 }
 
+int dsv4_hip_moe_layer_n_dev(float *out, const float *x, int n, const DSV4QMat *gate,
+                             const float *bias, const int64_t *tid2eid, int n_vocab,
+                             const int *token_ids, float route_scale,
+                             const DSV4ExpertW *experts, int n_experts, int topk,
+                             const DSV4ExpertW *shared, int hidden, int inter, float limit, int mx,
+                             int *idx_out, float *w_out, void *stream)
+{
+    std::lock_guard<std::mutex> lk(g.mu);
+    Range rg("dsv4_hip_moe_layer_n_dev");
+    if (usable()) return -1;
+    dev_call();
+    const char *what = "moe_layer_n_dev";
+    if (n <= 0) return fail("%s: n %d < 1", what, n);
+    if (!out || !x || !experts) return fail("%s: NULL pointer", what);
+    int gfmt, sfmt, sinter;
+    if (check_qmat(gate, "moe_layer_n_dev gate", &gfmt)) return -1;
+    if (!gate->w || (gfmt != FMT_BF16 && !gate->s)) return fail("%s: NULL gate pointer", what);
+    if (gate->rows != n_experts || gate->cols != hidden)
+        return fail("%s: gate is [%d x %d], expected [%d x %d]", what, gate->rows, gate->cols,
+                    n_experts, hidden);
+    if (!aligned16(gate->w)) return fail("%s: gate weights must be 16-byte aligned", what);
+    if (route_checks(what, n_experts, topk, tid2eid, n_vocab)) return -1;
+    if (tid2eid && !token_ids) return fail("%s: hash routing needs token_ids", what);
+    if (grouped_checks(n, topk, n_experts, hidden, inter, shared, &sfmt, &sinter, what)) return -1;
+    if (mx && hidden % 256) return fail("%s: hidden %d is not a multiple of 256", what, hidden);
+    if (!aligned16(x) || !aligned16(out)) return fail("%s: x and out must be 16-byte aligned", what);
+    const hipStream_t st = (hipStream_t)stream;
+    const size_t sb = ((size_t)n * n_experts * 4 + 255) & ~(size_t)255;
+    const size_t rb = ((size_t)n * topk * 4 + 255) & ~(size_t)255;
+    HIPCHK(g.route.need(sb + 2 * rb), "router workspace");
+    float *scores = (float *)g.route.p;
+    int *idx = idx_out ? idx_out : (int *)((uint8_t *)g.route.p + sb);
+    float *w = w_out ? w_out : (float *)((uint8_t *)g.route.p + sb + rb);
+    if (enqueue_mmq(*gate, gfmt, x, scores, n, st)) return -1;
+    GateRouteArgs a;
+    memset(&a, 0, sizeof a);
+    a.scores = scores;
+    a.scores_ld = n_experts;
+    a.n = n;
+    a.bias = bias;
+    a.tid2eid = tid2eid;
+    a.n_vocab = n_vocab;
+    a.token_ids = token_ids;
+    a.n_experts = n_experts;
+    a.topk = topk;
+    a.route_scale = route_scale;
+    a.idx = idx;
+    a.w = w;
+    a.status = g.st;
+    HIPCHK(gate_route_launch(a, st), "route launch");
+    return mx ? enqueue_moe_grouped_mx(out, x, n, experts, n_experts, idx, w, topk, shared, sfmt, sinter,
+                                       hidden, inter, limit, st)
+              : enqueue_moe_grouped(out, x, n, experts, n_experts, idx, w, topk, shared, sfmt, sinter,
+                                    hidden, inter, limit, st);
+}
+
 int dsv4_hip_moe_grouped_mx_dev(float *out, const float *x, int n, const DSV4ExpertW *experts,
                                 int n_experts, const int *idx, const float *w, int topk,
                                 const DSV4ExpertW *shared, int hidden, int inter, float limit,

@@ -275,6 +275,22 @@ int  dsv4_hip_moe_grouped_mx_dev(float *out, const float *x, int n,
                                  const DSV4ExpertW *shared, int hidden, int inter,
                                  float limit, void *stream);
 
+/* The prefill MoE layer (and batched decode) with the router on the device:
+ * dsv4_prefill_moe (src/80_prefill/dsv4_prefill_moe.c:12-60) for n tokens
+ * x [n][hidden] -- the gate outputs (dsv4_hip_mmq_n_dev with `gate`, a HOST
+ * descriptor with device pointers, [n_experts x hidden]), dsv4_route on
+ * every token (dsv4_hip_route_dev; token_ids: device int32 [n], the
+ * vocabulary ids hash routing looks up), then the routed and shared experts
+ * as dsv4_hip_moe_grouped_dev (mx = 0) or dsv4_hip_moe_grouped_mx_dev
+ * (mx = 1) -- with no host round trip. idx_out / w_out: device [n][topk]
+ * receiving the routing, or NULL. The limits of both entry points apply. */
+int  dsv4_hip_moe_layer_n_dev(float *out, const float *x, int n, const DSV4QMat *gate,
+                              const float *bias, const int64_t *tid2eid, int n_vocab,
+                              const int *token_ids, float route_scale,
+                              const DSV4ExpertW *experts, int n_experts, int topk,
+                              const DSV4ExpertW *shared, int hidden, int inter, float limit, int mx,
+                              int *idx_out, float *w_out, void *stream);
+
 /* ------------------------------------------------ prefill GEMM -------------
  * C[m][n] = sum_k A[m][k] * W[n][k] for m < M on CDNA4 FP8 MFMA, replacing the
  * GPU leg of the prefill projection seam, dsv4_prefill_vk_gemm

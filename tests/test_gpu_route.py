@@ -371,3 +371,55 @@ def test_fused_gate_router_shapes(lib, pkg, oracle, ne, hidden, topk):
         _assert_w(gw, ww, f"token {tkn}")
         acc = np.stack([oracle.expert_forward(host[int(i)], xh, 10.0) for i in gi])
         check_close(out.cpu().numpy(), oracle.moe_combine(acc, gw), 1e-4)
+
+
+@pytest.mark.parametrize("n,mx,hashed", [(64, False, False), (300, True, False), (48, False, True)])
+def test_moe_layer_n_matches_router_and_grouped(lib, pkg, oracle, n, mx, hashed):
+    """The many-token MoE layer with the router on the device
+    (dsv4_hip_moe_layer_n_dev, dsv4_prefill_moe's sequence for n tokens):
+    the picks and weights of every token as dsv4_route gives them on the gate
+    scores of dsv4_hip_mmq_n_dev for the same tokens (near ties excepted, as
+    above), and the layer's output bit for bit the grouped entry point's
+    (exact fp16 path, or the block-scaled path when mx) run on those picks.
+    Two tokens also against the oracle's experts (exact path only)."""
+    L = _Layer(pkg, lib, 0x4E00 + n)
+    rng = np.random.default_rng(n)
+    xh = np.stack([bf16_x(200 + t, L.hidden) for t in range(n)]).astype(np.float32)
+    x = dev_f32(xh)
+    toks = rng.integers(0, len(L.t2e), n).astype(np.int32)
+    dtok = torch.from_numpy(toks).to(DEV)
+    out = torch.empty(n * L.hidden, dtype=torch.float32, device=DEV)
+    di = torch.full((n * L.topk,), -1, dtype=torch.int32, device=DEV)
+    dw = torch.empty(n * L.topk, dtype=torch.float32, device=DEV)
+    lib.status()
+    lib.moe_layer_n_dev(out.data_ptr(), x.data_ptr(), n, L.gate, L.arena.table.data_ptr(), L.ne,
+                        L.topk, L.scale, L.shared, L.hidden, L.inter, 10.0, mx=mx,
+                        bias_ptr=None if hashed else L.dbias.data_ptr(),
+                        tid2eid_ptr=L.dt2e.data_ptr() if hashed else None,
+                        n_vocab=len(L.t2e) if hashed else 0,
+                        token_ids_ptr=dtok.data_ptr() if hashed else None,
+                        idx_ptr=di.data_ptr(), w_ptr=dw.data_ptr())
+    sc = torch.empty(n * L.ne, dtype=torch.float32, device=DEV)
+    lib.mmq_n_dev(sc.data_ptr(), x.data_ptr(), L.gate, n)
+    ref = torch.empty_like(out)
+    grouped = lib.moe_grouped_mx_dev if mx else lib.moe_grouped_dev
+    grouped(ref.data_ptr(), x.data_ptr(), n, L.arena.table.data_ptr(), L.ne, di.data_ptr(),
+            dw.data_ptr(), L.topk, L.shared, L.hidden, L.inter, 10.0)
+    torch.cuda.synchronize()
+    assert lib.status() == 0
+    scores = sc.cpu().numpy().reshape(n, L.ne)
+    gi = di.cpu().numpy().reshape(n, L.topk)
+    gw = dw.cpu().numpy().reshape(n, L.topk)
+    bias = None if hashed else L.bias
+    for t in range(n):
+        wi, ww, wo = oracle.route(scores[t], L.topk, L.scale, bias=bias,
+                                  tid2eid=L.t2e if hashed else None, token_id=int(toks[t]))
+        _assert_ids(gi[t][None], wi[None], (wo + (bias if bias is not None else 0))[None], f"token {t}")
+        _assert_w(gw[t], ww, f"token {t}")
+    got = out.cpu().numpy()
+    assert np.all(np.isfinite(got))
+    assert np.array_equal(bits(got), bits(ref.cpu().numpy())), "layer output differs from the grouped entry"
+    if not mx:
+        go = got.reshape(n, L.hidden)
+        for t in (0, n - 1):
+            check_close(go[t], L.want(oracle, xh[t], gi[t], gw[t]), 1e-3)
