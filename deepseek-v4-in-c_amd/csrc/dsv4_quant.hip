@@ -228,6 +228,13 @@ __device__ __forceinline__ uint32_t e4m3_quot(float v, float s, float rs)
     return hw_e4m3(v / s);
 }
 
+/* v of the lane DPP control CTRL names (every lane of the row active) */
+template <int CTRL>
+__device__ __forceinline__ float dpp_f(float v)
+{
+    return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), CTRL, 0xF, 0xF, false));
+}
+
 /* e4m3_quot of eight elements, the bracketing test done with packed
  * converts: lo = v * RN(rs (1 - 2^-21)) and hi = v * RN(rs (1 + 2^-21))
  * still enclose v / s (the three roundings add at most 3 * 2^-24 relative to
@@ -281,13 +288,22 @@ __device__ __forceinline__ void quant8_1x128(const float (&v)[8], uint8_t *Q, fl
     float m = 0.0f;
 #pragma unroll
     for (int i = 0; i < 8; i++) m = fmaxf(m, fabsf(v[i]));
-#pragma unroll
-    for (int off = 8; off > 0; off >>= 1) m = fmaxf(m, __shfl_xor(m, off));
+    /* maximum over the 16 lanes of the group (one DPP row): quad swaps,
+     * then the half-row and row mirrors, every step a VALU operation */
+    m = fmaxf(m, dpp_f<DPP_QUAD_1032>(m));
+    m = fmaxf(m, dpp_f<DPP_QUAD_2301>(m));
+    m = fmaxf(m, dpp_f<DPP_ROW_HALF_MIRROR>(m));
+    m = fmaxf(m, dpp_f<DPP_ROW_MIRROR>(m));
     const float sc = m > 0.0f ? m / 448.0f : 1.0f;
     if (!live) return;
     if ((threadIdx.x & 15) == 0) {
-        if (S_BLK_MAJOR) S[(e % (size_t)k) / 128 * (size_t)n + e / (size_t)k] = sc;
-        else S[e / 128] = sc;
+        /* group gi = e / 128 of token gi / (k / 128): a 32-bit division (a
+         * 64-bit one by a runtime divisor is a long instruction sequence
+         * that every lane of the wave runs) */
+        const uint32_t gi = (uint32_t)(e >> 7), kb = (uint32_t)k >> 7;
+        const uint32_t t = gi / kb;
+        if (S_BLK_MAJOR) S[(size_t)(gi - t * kb) * (size_t)n + t] = sc;
+        else S[gi] = sc;
     }
     const float rs = 1.0f / sc;
     *(uint2 *)(Q + e) = e4m3_quot8(v, sc, rs);
@@ -355,6 +371,7 @@ __global__ __launch_bounds__(256) void k_swiglu_quant_fp8_1x128(uint8_t *Q, floa
 hipError_t swiglu_quant_fp8_launch(uint8_t *Q, float *S, const float *gate, const float *up, int n, int k,
                                    float limit, hipStream_t st)
 {
+    if (k % 128 || ((size_t)n * k >> 39)) return hipErrorInvalidValue;   /* 32-bit group indices */
     const size_t lanes = (size_t)n * k / 8;
     hipLaunchKernelGGL(k_swiglu_quant_fp8_1x128, dim3((unsigned)((lanes + 255) / 256)), dim3(256), 0, st,
                        Q, S, gate, up, n, k, limit);
@@ -365,6 +382,7 @@ hipError_t quant_act_fp8_1x128_launch(uint8_t *Q, float *S, const void *a,
                                       int n, int k, bool bf16_in, bool s_blk_major,
                                       hipStream_t st)
 {
+    if (k % 128 || ((size_t)n * k >> 39)) return hipErrorInvalidValue;   /* 32-bit group indices */
     const size_t units = ((size_t)n * k / 8 + 255) / 256;
     const dim3 grid((unsigned)((units + QA_U_1X128 - 1) / QA_U_1X128)), block(256);
     if (bf16_in && s_blk_major)
@@ -385,10 +403,14 @@ __device__ __forceinline__ void quant4_mx(const float (&v)[4], long g, int sub, 
     float amax = 0.0f;
 #pragma unroll
     for (int i = 0; i < 4; i++) amax = fabsf(v[i]) > amax ? fabsf(v[i]) : amax;
-    /* group maximum over the eight lanes (NaN never wins a > compare) */
-#pragma unroll
-    for (int d = 1; d < 8; d <<= 1) {
-        const float o = __shfl_xor(amax, d, 8);
+    /* group maximum over the eight lanes (NaN never wins a > compare): quad
+     * swaps and the half-row mirror, DPP operations */
+    {
+        float o = dpp_f<DPP_QUAD_1032>(amax);
+        amax = o > amax ? o : amax;
+        o = dpp_f<DPP_QUAD_2301>(amax);
+        amax = o > amax ? o : amax;
+        o = dpp_f<DPP_ROW_HALF_MIRROR>(amax);
         amax = o > amax ? o : amax;
     }
     if (!live) return;
