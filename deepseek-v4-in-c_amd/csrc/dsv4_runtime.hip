@@ -81,7 +81,7 @@ struct State {
     hipStream_t stream = nullptr;
     hipStream_t side = nullptr;          /* concurrent work of one call (shared expert) */
     hipStream_t side2 = nullptr;         /* concurrent work of one call (thin routed tiles) */
-    hipEvent_t fork = nullptr, join = nullptr, fork2 = nullptr, join2 = nullptr;
+    hipEvent_t fork = nullptr, join = nullptr, fork2 = nullptr, join2 = nullptr, xq = nullptr;
     unsigned *status = nullptr;          /* status words: [0] _dev calls, [HOST_WORD] host calls */
     unsigned *st = nullptr;              /* the word the call being enqueued raises */
     unsigned *pub = nullptr;             /* one-launch decode: count, done, leave (own lines) */
@@ -529,7 +529,8 @@ int dsv4_hip_init(int device)
     if (hipEventCreateWithFlags(&g.fork, hipEventDisableTiming) != hipSuccess ||
         hipEventCreateWithFlags(&g.join, hipEventDisableTiming) != hipSuccess ||
         hipEventCreateWithFlags(&g.fork2, hipEventDisableTiming) != hipSuccess ||
-        hipEventCreateWithFlags(&g.join2, hipEventDisableTiming) != hipSuccess)
+        hipEventCreateWithFlags(&g.join2, hipEventDisableTiming) != hipSuccess ||
+        hipEventCreateWithFlags(&g.xq, hipEventDisableTiming) != hipSuccess)
         return fail("event creation failed");
     if (hipMalloc((void **)&g.status, 256) != hipSuccess) return fail("status alloc failed");
     if (hipMemset(g.status, 0, 256) != hipSuccess) return fail("status clear failed");
@@ -583,8 +584,9 @@ void dsv4_hip_shutdown(void)
     if (g.join) (void)hipEventDestroy(g.join);
     if (g.fork2) (void)hipEventDestroy(g.fork2);
     if (g.join2) (void)hipEventDestroy(g.join2);
+    if (g.xq) (void)hipEventDestroy(g.xq);
     g.stream = g.side = g.side2 = nullptr;
-    g.fork = g.join = g.fork2 = g.join2 = nullptr;
+    g.fork = g.join = g.fork2 = g.join2 = g.xq = nullptr;
     g.ready = 0;
     g.dead = 0;
     g.device = -1;
@@ -1491,6 +1493,14 @@ static int enqueue_moe_grouped_mx(float *out, const float *x, int n, const DSV4E
     uint8_t *x8 = ws + o_x8, *xs = ws + o_xs, *mid = ws + o_mid, *ms = ws + o_ms;
     float *y = (float *)(ws + o_y);
 
+    /* x to MXFP8 on the side stream, beside the routing permutation on this
+     * one (neither reads the other's output); the shared expert follows it
+     * there */
+    HIPCHK(hipEventRecord(g.fork, st), "fork record");
+    HIPCHK(hipStreamWaitEvent(g.side, g.fork, 0), "fork wait");
+    HIPCHK(quant_act_mxfp8_launch(x8, xs, x, n, hidden, g.side), "x MXFP8 launch");
+    HIPCHK(hipEventRecord(g.xq, g.side), "quant record");
+
     RouteArgs ra;
     ra.idx = idx; ra.npairs = (int)P; ra.topk = topk; ra.n_experts = n_experts;
     ra.tile_rows = trows; ra.grp_off = grp; ra.tile_pre = tp; ra.tile_grp = tg; ra.pos = pos;
@@ -1501,8 +1511,6 @@ static int enqueue_moe_grouped_mx(float *out, const float *x, int n, const DSV4E
 
     float *ys = nullptr;
     if (sh_fp8) {
-        HIPCHK(hipEventRecord(g.fork, st), "fork record");
-        HIPCHK(hipStreamWaitEvent(g.side, g.fork, 0), "fork wait");
         ys = (float *)(ws + o_ys);
         if (enqueue_shared_fp8q(ys, ws + o_smq, (float *)(ws + o_sms), x, n, shared, sfmt, sinter, hidden, limit,
                                 ws + o_sxq, (float *)(ws + o_sxs), (float *)(ws + o_sg), (float *)(ws + o_su),
@@ -1511,8 +1519,6 @@ static int enqueue_moe_grouped_mx(float *out, const float *x, int n, const DSV4E
         HIPCHK(hipEventRecord(g.join, g.side), "join record");
     } else if (shared) {
         /* an FP4 shared expert on the side stream: its own fp16 copy of x */
-        HIPCHK(hipEventRecord(g.fork, st), "fork record");
-        HIPCHK(hipStreamWaitEvent(g.side, g.fork, 0), "fork wait");
         uint16_t *x16 = (uint16_t *)(ws + o_x16), *smid = (uint16_t *)(ws + o_smid);
         int *ex = (int *)(ws + o_ex);
         ys = (float *)(ws + o_ys);
@@ -1529,7 +1535,7 @@ static int enqueue_moe_grouped_mx(float *out, const float *x, int n, const DSV4E
         HIPCHK(hipEventRecord(g.join, g.side), "join record");
     }
 
-    HIPCHK(quant_act_mxfp8_launch(x8, xs, x, n, hidden, st), "x MXFP8 launch");
+    HIPCHK(hipStreamWaitEvent(st, g.xq, 0), "quant wait");
     GroupedMxArgs ga;
     memset(&ga, 0, sizeof ga);
     ga.table = table; ga.n_experts = n_experts; ga.grp_off = grp; ga.tile_pre = tp; ga.tile_grp = tg;
