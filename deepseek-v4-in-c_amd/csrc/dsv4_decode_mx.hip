@@ -62,6 +62,12 @@ constexpr int NPART = 4;                          /* e4m3 parts per activation *
 constexpr int TAB_DATA = 4 * NPART * 32;          /* operand bytes of one chunk */
 constexpr int TAB_CHUNK = TAB_DATA + 4 * NPART * 4; /* + one scale dword per (block, part) */
 constexpr int TAB_ZERO = 64;                      /* zero operand + unit scale */
+/* A mid table (the split of a routed slot's mid, the down projection's B
+ * operand): per chunk of 128 the same operand bytes as TAB_DATA, then an E8M0
+ * scale dword per (32-element block, 16-element half, part), so that the
+ * writer of 16 consecutive mid rows splits them alone. */
+constexpr int MTAB_DATA = TAB_DATA;
+constexpr int MTAB_CHUNK = MTAB_DATA + 4 * 2 * NPART * 4;
 constexpr int E8M0_ONE = 127;
 constexpr int KSLICES = 4;                        /* waves per tile along K */
 
@@ -114,7 +120,8 @@ __device__ __forceinline__ void leave(const OnePub &p)
     if (old != in_grp - 1) return;
     const unsigned told = __hip_atomic_fetch_add(top, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     if (told != groups - 1) return;
-    __hip_atomic_store(p.count, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    for (unsigned g = 0; g <= ONE_LEAVE_GROUPS; g++)
+        __hip_atomic_store(p.count + g * ONE_PUB_LINE_WORDS, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     __hip_atomic_store(p.done, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     for (unsigned g = 0; g < ONE_LEAVE_GROUPS; g++)
         __hip_atomic_store(p.leave + g * ONE_PUB_LINE_WORDS, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -208,6 +215,43 @@ __device__ __forceinline__ void split8(float (&v)[8], uint32_t (&code)[NPART][2]
         }
     }
 }
+
+/* The same for a half block: 16 consecutive values, eight in each lane of a
+ * lane pair (lanes 2 i, 2 i + 1), one E8M0 scale per part for the 16. */
+__device__ __forceinline__ void split8_half(float (&v)[8], uint32_t (&code)[NPART][2], int (&E)[NPART])
+{
+#pragma unroll
+    for (int p = 0; p < NPART; p++) {
+        float m = fabsf(v[0]);
+#pragma unroll
+        for (int i = 1; i < 8; i++) m = fmaxf(m, fabsf(v[i]));
+        m = fmaxf(m, dpp_f<DPP_QUAD_1032>(m));
+        E[p] = part_e8m0(m);
+        const int e = E[p] - E8M0_ONE;
+        float s[8];
+#pragma unroll
+        for (int i = 0; i < 8; i++) s[i] = ldexpf(v[i], -e);
+        code[p][0] = e4m3_pk4(s[0], s[1], s[2], s[3]);
+        code[p][1] = e4m3_pk4(s[4], s[5], s[6], s[7]);
+        if (p + 1 < NPART) {
+#pragma unroll
+            for (int d = 0; d < 2; d++) {
+                const f32x2 lo = __builtin_amdgcn_cvt_pk_f32_fp8((int)code[p][d], false);
+                const f32x2 hi = __builtin_amdgcn_cvt_pk_f32_fp8((int)code[p][d], true);
+                v[4 * d + 0] -= ldexpf(lo.x, e);
+                v[4 * d + 1] -= ldexpf(lo.y, e);
+                v[4 * d + 2] -= ldexpf(hi.x, e);
+                v[4 * d + 3] -= ldexpf(hi.y, e);
+            }
+        }
+    }
+}
+
+/* Byte offsets, inside a chunk of a mid table, of part p's 16 codes of the
+ * half block that starts at element k0 of the chunk (k0 % 16 == 0), and of
+ * its scale dword. */
+__device__ __forceinline__ int mtab_code_off(int k0, int p) { return (((k0 & 63) >> 4) * NPART + p) * 32 + (k0 >> 6) * 16; }
+__device__ __forceinline__ int mtab_scale_off(int k0, int p) { return MTAB_DATA + ((k0 >> 4) * NPART + p) * 4; }
 
 /* Split table of one wave's chunks for its tokens (LDS, wave-private).
  * For token t and chunk j (of the wave's ncw) the TAB_CHUNK bytes at
@@ -453,6 +497,58 @@ __device__ __forceinline__ void sum_parts(v4f &acc)
     }
 }
 
+/* B operand of chunk pair m from a mid table (chunk index relative to `tab`):
+ * column c = 8 par + 2 p + hf carries part p of half hf of every 32-element
+ * block of chunk c0 + 2 m + par. Lane l (column l % 16, lane group g = l / 16)
+ * holds k in [16 g, +16) and [64 + 16 g, +16), which lie in half g % 2 of
+ * blocks g / 2 and 2 + g / 2: its bytes are the table's when hf == g % 2 and
+ * the zero operand's otherwise. Its scale is the column's scale of block g. */
+struct BMid {
+    const uint8_t *d, *s;
+    int dstep, sstep;
+};
+
+__device__ __forceinline__ BMid bmid_src(const uint8_t *tab, int c0, const uint8_t *zero, int lane)
+{
+    const int col = lane & 15, g = lane >> 4;
+    const int par = col >> 3, p = (col >> 1) & 3, hf = col & 1;
+    const uint8_t *cb = tab + (size_t)(c0 + par) * MTAB_CHUNK;
+    BMid b;
+    const bool live = hf == (g & 1);
+    b.d = live ? cb + (g * NPART + p) * 32 : zero;
+    b.dstep = live ? 2 * MTAB_CHUNK : 0;
+    b.s = cb + MTAB_DATA + ((g * 2 + hf) * NPART + p) * 4;
+    b.sstep = 2 * MTAB_CHUNK;
+    return b;
+}
+
+/* Column sums over the eight columns of each chunk of a mid-table pair
+ * accumulator ((c0 + c1) + (c2 + c3)) + ((c4 + c5) + (c6 + c7)), written as 8
+ * even-chunk and 8 odd-chunk row partials to dst[0..7], dst[8..15]. */
+__device__ __forceinline__ void sum_cols8(v4f &acc)
+{
+#pragma unroll
+    for (int e = 0; e < 4; e++) {
+        acc[e] = acc[e] + dpp_f<DPP_QUAD_1032>(acc[e]);
+        acc[e] = acc[e] + dpp_f<DPP_QUAD_2301>(acc[e]);
+        acc[e] = acc[e] + dpp_f<DPP_ROW_HALF_MIRROR>(acc[e]);
+    }
+}
+
+__device__ __forceinline__ void store_mid_partials(v4f acc, float *dst, int lane)
+{
+    sum_cols8(acc);
+    const int q = lane >> 4, col = lane & 15;
+    if (col == 0 && q < 2) {
+#pragma unroll
+        for (int e = 0; e < 4; e++) dst[4 * q + e] = acc[e];
+    }
+    if (col == 8 && q >= 2) {
+#pragma unroll
+        for (int e = 0; e < 4; e++) dst[8 + 4 * (q - 2) + e] = acc[e];
+    }
+}
+
 /* The expert of gate/up slot `slot`: by value from the kernel arguments (host
  * routing), the direct descriptor, or table[idx[slot]]; a routing id out of
  * range is reported. */
@@ -594,9 +690,9 @@ __device__ __forceinline__ void gateup_mx_body(const GateUpMxArgs &a)
         if (threadIdx.x == 0) atomicOr(a.status, bad);
         if (threadIdx.x < 32) mid[j0 + threadIdx.x] = qnan_f();
         /* NaN block scales (E8M0 255) make the down projection of this slot NaN */
-        if (a.msplit && threadIdx.x < NPART)
-            *(int *)(a.msplit + (size_t)slot * a.msplit_ld + (size_t)(j0 >> 7) * TAB_CHUNK +
-                     TAB_DATA + (((j0 >> 5) & 3) * NPART + threadIdx.x) * 4) = 255;
+        if (a.msplit && threadIdx.x < 2 * NPART)
+            *(int *)(a.msplit + (size_t)slot * a.msplit_ld + (size_t)(j0 >> 7) * MTAB_CHUNK +
+                     mtab_scale_off((j0 & 127) + 16 * (threadIdx.x / NPART), threadIdx.x % NPART)) = 255;
         return;
     }
     const int row_bytes = FP4 ? a.hidden / 2 : a.hidden;
@@ -651,22 +747,21 @@ __device__ __forceinline__ void gateup_mx_body(const GateUpMxArgs &a)
     }
     if (!a.msplit) return;
 
-    /* split of the 32-element block j0 / 32 of mid, in the down projection's
-     * table layout (chunk j0 / 128, block (j0 / 32) % 4) */
-    uint8_t *cb = a.msplit + (size_t)slot * a.msplit_ld + (size_t)(j0 >> 7) * TAB_CHUNK;
-    const int b4 = (j0 >> 5) & 3;
-    const int kk = 32 * b4 + (lane & 31);
-    uint8_t *dst = cb + ((kk & 63) >> 4) * NPART * 32 + (kk >> 6) * 16 + (kk & 15);
+    /* split of the two 16-element halves of block j0 / 32 of mid, each with
+     * its own scales, in the down projection's table layout (chunk j0 / 128) */
+    uint8_t *cb = a.msplit + (size_t)slot * a.msplit_ld + (size_t)(j0 >> 7) * MTAB_CHUNK;
+    const int kk = (j0 & 127) + (lane & 31);
+    uint8_t *dst = cb + mtab_code_off(kk & ~15, 0) + (kk & 15);
 #pragma unroll
     for (int p = 0; p < NPART; p++) {
         float m = fabsf(v);
 #pragma unroll
-        for (int o = 1; o < 32; o <<= 1) m = fmaxf(m, __shfl_xor(m, o));
+        for (int o = 1; o < 16; o <<= 1) m = fmaxf(m, __shfl_xor(m, o));
         const int E = part_e8m0(m);
         const int ex = E - E8M0_ONE;
         const uint32_t q = (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(ldexpf(v, -ex), 0.0f, 0, false) & 0xFFu;
         if (lane < 32) dst[p * 32] = (uint8_t)q;
-        if (lane == 0) *(int *)(cb + TAB_DATA + (b4 * NPART + p) * 4) = E;
+        if (lane < 32 && (lane & 15) == 0) *(int *)(cb + mtab_scale_off(kk, p)) = E;
         v -= ldexpf(__builtin_amdgcn_cvt_pk_f32_fp8((int)q, false)[0], ex);
     }
 }
@@ -714,20 +809,23 @@ __global__ __launch_bounds__(1024) void k_down_mx(DownMxArgs a)
     if (!bad && !mx_desc_ok<FMT_FP4_E8M0>(m, a.hidden, a.inter)) bad = ST_BAD_DESCRIPTOR;
     float mine[4] = {qnan_f(), qnan_f(), qnan_f(), qnan_f()};
     if (!bad) {
-        /* B: columns 0..3 are the four parts of slot k's mid */
+        /* B: column c = 2 p + hf < 8 is part p of half hf of slot k's mid
+         * (data in the lanes whose k range lies in half hf, see bmid_src) */
         const uint8_t *tb = a.msplit + (size_t)k * a.msplit_ld;
         const uint8_t *zero = (const uint8_t *)g_zero_operand;
-        const bool live = col < NPART;
-        const uint8_t *bd = live ? tb + (g * NPART + col) * 32 : zero;
-        const uint8_t *bsc = live ? tb + TAB_DATA + (g * NPART + col) * 4 : zero + 32;
-        const int step = live ? TAB_CHUNK : 0;
+        const int p = (col >> 1) & 3, hf = col & 1;
+        const bool live = col < 8 && hf == (g & 1);
+        const uint8_t *bd = live ? tb + (g * NPART + p) * 32 : zero;
+        const int dstep = live ? MTAB_CHUNK : 0;
+        const uint8_t *bsc = col < 8 ? tb + MTAB_DATA + ((g * 2 + hf) * NPART + p) * 4 : zero + 32;
+        const int sstep = col < 8 ? MTAB_CHUNK : 0;
         v8i bv[CPW];
         int bsv[CPW];
 #pragma unroll
         for (int j = 0; j < CPW; j++) {
             /* slots past the wave's chunks read the zero operand (adds zero) */
-            const uint8_t *pd = j < ncw ? bd + (size_t)(cb0 + j) * step : zero;
-            const uint8_t *ps = j < ncw ? bsc + (size_t)(cb0 + j) * step : zero + 32;
+            const uint8_t *pd = j < ncw ? bd + (size_t)(cb0 + j) * dstep : zero;
+            const uint8_t *ps = j < ncw ? bsc + (size_t)(cb0 + j) * sstep : zero + 32;
             const u32x4 lo = *gptr((const u32x4 *)pd);
             const u32x4 hi = *gptr((const u32x4 *)(pd + 16));
             bv[j][0] = (int)lo.x; bv[j][1] = (int)lo.y; bv[j][2] = (int)lo.z; bv[j][3] = (int)lo.w;
@@ -746,7 +844,7 @@ __global__ __launch_bounds__(1024) void k_down_mx(DownMxArgs a)
         v4f acc = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
         for (int j = 0; j < CPW; j++) acc = mfma_a<true>(w[j], bv[j], acc, (int)sc.v[j], bsv[j]);
-        sum_parts(acc);
+        sum_cols8(acc);
 #pragma unroll
         for (int e = 0; e < 4; e++) mine[e] = acc[e];
     } else if (threadIdx.x == 64 * wave && half == 0) {
@@ -927,9 +1025,9 @@ __device__ __forceinline__ void gateup_px_item(const GateUpMxArgs &a, int item, 
         if (threadIdx.x == 0) atomicOr(a.status, bad);
         if (threadIdx.x < 32) mid[j0 + threadIdx.x] = qnan_f();
         /* NaN block scales (E8M0 255) make the down projection of this slot NaN */
-        if (a.msplit && threadIdx.x < NPART)
-            st_dev32(a.msplit + (size_t)slot * a.msplit_ld + (size_t)(j0 >> 7) * TAB_CHUNK + TAB_DATA +
-                     (((j0 >> 5) & 3) * NPART + threadIdx.x) * 4, 255u);
+        if (a.msplit && threadIdx.x < 2 * NPART)
+            st_dev32(a.msplit + (size_t)slot * a.msplit_ld + (size_t)(j0 >> 7) * MTAB_CHUNK +
+                     mtab_scale_off((j0 & 127) + 16 * (threadIdx.x / NPART), threadIdx.x % NPART), 255u);
     } else {
         const int row_bytes = a.hidden / 2, sc_cols = a.hidden / 32;
         XUnits<UPL> xu;
@@ -982,29 +1080,27 @@ __device__ __forceinline__ void gateup_px_item(const GateUpMxArgs &a, int item, 
                 mid[j0 + lane] = v;
                 vl[lane] = v;
             }
-            /* the 32-element block j0 / 32 of mid in four lanes of eight (one
-             * DPP quad), split like the activations, into the down
-             * projection's table (chunk j0 / 128, block (j0 / 32) % 4) */
+            /* the two halves of block j0 / 32 of mid, each in a lane pair of
+             * eight values, split with their own scales into the down
+             * projection's table (chunk j0 / 128) */
             if (a.msplit && lane < 4) {
                 float v8[8];
 #pragma unroll
                 for (int i = 0; i < 8; i++) v8[i] = vl[8 * lane + i];
                 uint32_t code[NPART][2];
                 int E[NPART];
-                split8(v8, code, E);
-                uint8_t *cb = a.msplit + (size_t)slot * a.msplit_ld + (size_t)(j0 >> 7) * TAB_CHUNK;
-                const int b4 = (j0 >> 5) & 3;
-                const int kk = 32 * b4 + 8 * lane;
-                const int h = (kk & 63) >> 4, half = kk >> 6;
+                split8_half(v8, code, E);
+                uint8_t *cb = a.msplit + (size_t)slot * a.msplit_ld + (size_t)(j0 >> 7) * MTAB_CHUNK;
+                const int k0 = (j0 & 127) + 16 * (lane >> 1);
 #pragma unroll
                 for (int p = 0; p < NPART; p++) {
-                    uint8_t *d = cb + (h * NPART + p) * 32 + half * 16 + (kk & 15);
+                    uint8_t *d = cb + mtab_code_off(k0, p) + 8 * (lane & 1);
                     st_dev32(d, code[p][0]);
                     st_dev32(d + 4, code[p][1]);
                 }
-                if (lane == 0) {
+                if ((lane & 1) == 0) {
 #pragma unroll
-                    for (int p = 0; p < NPART; p++) st_dev32(cb + TAB_DATA + (b4 * NPART + p) * 4, (uint32_t)E[p]);
+                    for (int p = 0; p < NPART; p++) st_dev32(cb + mtab_scale_off(k0, p), (uint32_t)E[p]);
                 }
             }
         }
@@ -1147,17 +1243,16 @@ __global__ __launch_bounds__(1024) void k_down_px(DownMxArgs a)
 #pragma unroll
     for (int i = 0; i < 16; i++) part[i] = qnan_f();
     if (!bad) {
-        const BPair bp = bpair_src(a.msplit + (size_t)k * a.msplit_ld, 0,
-                                   (const uint8_t *)g_zero_operand, lane);
+        const BMid bp = bmid_src(a.msplit + (size_t)k * a.msplit_ld, 0, (const uint8_t *)g_zero_operand, lane);
         v8i bv[NP];
         int bs[NP];
 #pragma unroll
         for (int mm = 0; mm < NP; mm++) {
-            const u32x4 lo = *gptr((const u32x4 *)(bp.d + (size_t)mm * bp.step));
-            const u32x4 hi = *gptr((const u32x4 *)(bp.d + (size_t)mm * bp.step + 16));
+            const u32x4 lo = *gptr((const u32x4 *)(bp.d + (size_t)mm * bp.dstep));
+            const u32x4 hi = *gptr((const u32x4 *)(bp.d + (size_t)mm * bp.dstep + 16));
             bv[mm][0] = (int)lo.x; bv[mm][1] = (int)lo.y; bv[mm][2] = (int)lo.z; bv[mm][3] = (int)lo.w;
             bv[mm][4] = (int)hi.x; bv[mm][5] = (int)hi.y; bv[mm][6] = (int)hi.z; bv[mm][7] = (int)hi.w;
-            bs[mm] = *gptr((const int *)(bp.s + (size_t)mm * bp.step));
+            bs[mm] = *gptr((const int *)(bp.s + (size_t)mm * bp.sstep));
         }
         DSV4_ORDER();
         APairs<NP> w;
@@ -1176,7 +1271,7 @@ __global__ __launch_bounds__(1024) void k_down_px(DownMxArgs a)
             default: acc = mfma_f4_sel<3>(w.q[mm], bv[mm], acc, w.s[mm >> 2], bs[mm]); break;
             }
         }
-        store_pair_partials(acc, &ylds[k][t][0], lane);
+        store_mid_partials(acc, &ylds[k][t][0], lane);
     } else {
         if (lane == 0 && t == 0) atomicOr(a.status, bad);
         if (lane < 16) ylds[k][t][lane] = qnan_f();
@@ -1202,7 +1297,7 @@ typedef __attribute__((address_space(3))) void lds_void_t;
  * whole 1 KiB DMA rounds and a zero operand. */
 constexpr int ONE_YL_BYTES = MX_ROUTED_MAX * 2 * 16 * 4;
 constexpr int ONE_HEAD_BYTES = ONE_YL_BYTES + 64;
-__host__ __device__ constexpr int one_tab_rounds(int inter) { return (inter / 128 * TAB_CHUNK + 1023) / 1024; }
+__host__ __device__ constexpr int one_tab_rounds(int inter) { return (inter / 128 * MTAB_CHUNK + 1023) / 1024; }
 __host__ __device__ constexpr int one_slot_lds(int inter) { return one_tab_rounds(inter) * 1024 + TAB_ZERO; }
 
 /* s_waitcnt lgkmcnt(0) + s_barrier: a workgroup barrier that leaves the
@@ -1277,13 +1372,13 @@ __device__ __forceinline__ void down_one_group(const MoeOneArgs &A, int grp, uin
                                                          1024 * r + 16 * lane, 0, 0, CPOL_SC1);
             __builtin_amdgcn_s_waitcnt(0x0F70);        /* vmcnt(0): the copy (and the weights) landed */
             asm volatile("" ::: "memory");
-            const BPair bp = bpair_src(tab, 0, tab + ROUNDS * 1024, lane);
+            const BMid bp = bmid_src(tab, 0, tab + ROUNDS * 1024, lane);
             v4f acc0 = {0.0f, 0.0f, 0.0f, 0.0f}, acc1 = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
             for (int mm = 0; mm < NP; mm++) {
-                const u32x4 lo = *(const u32x4 *)(bp.d + mm * bp.step);
-                const u32x4 hi = *(const u32x4 *)(bp.d + mm * bp.step + 16);
-                const int sb = *(const int *)(bp.s + mm * bp.step);
+                const u32x4 lo = *(const u32x4 *)(bp.d + mm * bp.dstep);
+                const u32x4 hi = *(const u32x4 *)(bp.d + mm * bp.dstep + 16);
+                const int sb = *(const int *)(bp.s + mm * bp.sstep);
                 v8i b;
                 b[0] = (int)lo.x; b[1] = (int)lo.y; b[2] = (int)lo.z; b[3] = (int)lo.w;
                 b[4] = (int)hi.x; b[5] = (int)hi.y; b[6] = (int)hi.z; b[7] = (int)hi.w;
@@ -1298,8 +1393,8 @@ __device__ __forceinline__ void down_one_group(const MoeOneArgs &A, int grp, uin
                          acc1 = mfma_f4_sel<3>(w1.q[mm], b, acc1, w1.s[mm >> 2], sb); break;
                 }
             }
-            store_pair_partials(acc0, &yl[k][0][0], lane);
-            store_pair_partials(acc1, &yl[k][1][0], lane);
+            store_mid_partials(acc0, &yl[k][0][0], lane);
+            store_mid_partials(acc1, &yl[k][1][0], lane);
         } else {
             if (lane == 0) atomicOr(a.status, bad);
             if (lane < 32) yl[k][lane >> 4][lane & 15] = qnan_f();
@@ -1332,6 +1427,309 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) void k
         gateup_px_item<NPG>(a.gu, (int)blockIdx.x, lds, &a.pub);
     else
         down_one_group<NPD>(a, (int)blockIdx.x - a.gu_blocks, lds);
+}
+
+/* ------------------------------------- balanced one-launch decode MoE --- */
+
+/* One workgroup per CU, every workgroup resident at once, each doing an equal
+ * share of both phases:
+ *   - waves 0-11 compute BAL_HB half blocks of gate/up (16 mid rows of one
+ *     routed slot each, grid-size apart, so consecutive 32 KB pieces of a
+ *     matrix stream to consecutive workgroups): wave u the 8-row tile
+ *     (u / 2) % 2 of half block u / 4 for matrix u % 2 (w1, w3), over both
+ *     halves of K, in the MFMA sequence of gateup_px_item (the same bits);
+ *   - then waves 0-11 load down unit u (routed slot u / 2, 8-row tile u % 2 of
+ *     the workgroup's 16 down rows) into registers: the down bytes queue
+ *     behind every CU's gate/up bytes;
+ *   - waves 12-15 split the workgroup's half blocks of mid (split8_half: the
+ *     bytes and scales gateup_px_item writes) into mid_copies replicas of the
+ *     slots' mid tables in HBM, then one add per workgroup on grouped
+ *     counters; the add that completes the count raises the done flag;
+ *   - one wave polls the flag, waves 12-15 copy every slot's table from
+ *     replica blockIdx % mid_copies into LDS, waves 0-11 run the MFMA
+ *     sequence of down_one_group for their unit, and the first 16 lanes
+ *     combine in k order.
+ * The workgroups wait on each other, so the host launches this form only when
+ * the whole grid fits on the device at once (one workgroup per CU); the wait
+ * is bounded (spin_max polls) as in k_moe_one. */
+constexpr int BAL_WAVES = 16;
+constexpr int BAL_GU_WAVES = 12;
+constexpr int BAL_HB = BAL_GU_WAVES / 4;          /* half blocks (16 mid rows) per workgroup */
+constexpr int BAL_POLL_WAVE = BAL_GU_WAVES + 1;
+constexpr int BAL_HB_DW = 4 * NPART + NPART;      /* table dwords of one half block */
+
+struct BalLds {
+    int tab, red, stage, yl, flag, total;
+};
+
+/* x's split table, later every slot's mid tables (tab); the gate/up partials
+ * (red); the writer waves' staging of the table dwords (stage); the down
+ * partials (yl); the ready word (flag). */
+__host__ __device__ constexpr BalLds bal_lds(int hidden, int inter, int topk)
+{
+    BalLds l{};
+    const int xt = (hidden / 128) * TAB_CHUNK + TAB_ZERO;
+    const int mt = (topk * (inter / 128) * MTAB_CHUNK + 1023) / 1024 * 1024 + TAB_ZERO;   /* whole copy rounds */
+    l.tab = 0;
+    l.red = xt > mt ? xt : mt;
+    l.stage = l.red + 2 * BAL_HB * 2 * 2 * 16 * 4;
+    l.yl = l.stage + (BAL_WAVES - BAL_GU_WAVES) * 64 * 4;
+    l.flag = l.yl + MX_ROUTED_MAX * 2 * 16 * 4;
+    l.total = l.flag + 16;
+    return l;
+}
+
+template <int NPH, int NPD>
+__global__ __launch_bounds__(1024) void k_moe_bal(MoeOneArgs A)
+{
+    extern __shared__ __align__(16) uint8_t lds[];
+    const GateUpMxArgs &a = A.gu;
+    const DownMxArgs &d = A.dn;
+    constexpr int NC = 4 * NPH;                      /* chunks of hidden */
+    constexpr int NCD = 2 * NPD;                     /* chunks of inter  */
+    constexpr int GU_THR = BAL_GU_WAVES * 64;
+    constexpr int XUPL = (NC * 16 + GU_THR - 1) / GU_THR;
+    const int lane = threadIdx.x & 63;
+    const int wave = wave_in_group();
+    const int topk = d.topk;
+    const BalLds L = bal_lds(512 * NPH, 256 * NPD, topk);
+    uint8_t *tab = lds + L.tab;
+    float *red = (float *)(lds + L.red);             /* [tile 2 j + th][K half][mat][16] */
+    float(*yl)[2][16] = (float(*)[2][16])(lds + L.yl);
+    int *ready_ok = (int *)(lds + L.flag);
+    const int tiles_per_slot = a.inter / 8;
+    const int n_hb = topk * tiles_per_slot / 2;
+    const int G = (int)gridDim.x;
+    const int r0d = (int)blockIdx.x * 16;            /* first down row */
+    const int tab_bytes = topk * NCD * MTAB_CHUNK;
+
+    /* ---- gate/up: x, then the tile's scales and weights ---- */
+    const int j = wave >> 2, th = (wave >> 1) & 1, mat = wave & 1;
+    const int hb = j * G + (int)blockIdx.x;
+    const bool live = wave < BAL_GU_WAVES && hb < n_hb;
+    unsigned gbad = 0;
+    APairs<NPH> gw[2];
+    if (wave < BAL_GU_WAVES) {
+        /* A wave without a valid tile still issues its loads, from inside x
+         * (4 hidden bytes: eight FP4 rows of hidden / 2 bytes, and their
+         * scale bytes with every row in scale row 0), so that no branch
+         * merges before the x split and its wait counts only the x loads. */
+        const int ti = 2 * hb + th;
+        const int gslot = live ? ti / tiles_per_slot : 0;
+        const int gr0 = live ? (ti - gslot * tiles_per_slot) * 8 : 0;
+        const int row_bytes = a.hidden / 2, sc_cols = a.hidden / 32;
+        const uint8_t *wb = (const uint8_t *)a.x, *sb = (const uint8_t *)a.x;
+        int blk_r = 8, row = lane & 7, trow0 = 0, row_max = 7;
+        if (live) {
+            DSV4ExpertW e;
+            gbad = gateup_expert(a, gslot, e);
+            if (!gbad && (!mx_desc_ok<FMT_FP4_E8M0>(e.w1, a.inter, a.hidden) ||
+                          !mx_desc_ok<FMT_FP4_E8M0>(e.w3, a.inter, a.hidden)))
+                gbad = ST_BAD_DESCRIPTOR;
+            if (!gbad) {
+                const DSV4QMat &m = mat ? e.w3 : e.w1;
+                wb = (const uint8_t *)m.w;
+                sb = (const uint8_t *)m.s;
+                blk_r = m.blk_r;
+                row = gr0 + (lane & 7);
+                trow0 = gr0;
+                row_max = a.inter - 1;
+            }
+        }
+        XUnits<XUPL> xu;
+        load_units<XUPL, GU_THR>(xu, a.x, 0, 1, 0, NC, (int)threadIdx.x);
+        DSV4_ORDER();
+#pragma unroll
+        for (int h = 0; h < 2; h++)
+            ld_pairs_scales<NPH>(gw[h], sb, sc_cols, blk_r, row, trow0, row_max, h * 2 * NPH, lane);
+        DSV4_ORDER();
+#pragma unroll
+        for (int h = 0; h < 2; h++) ld_pairs_w<NPH>(gw[h], wb + (size_t)row * row_bytes, h * 2 * NPH, lane);
+        DSV4_ORDER();
+        store_units<XUPL, GU_THR>(tab, xu, 1, NC, (int)threadIdx.x);
+        ld_pairs_scales_finish<NPH>(gw[0], lane);
+        ld_pairs_scales_finish<NPH>(gw[1], lane);
+    }
+    lds_barrier();                                   /* B1: x's table */
+
+    /* ---- gate/up MFMAs: K half h over chunk pairs [h NPH, (h + 1) NPH) ---- */
+    if (live) {
+        float *rt = red + (size_t)(2 * j + th) * 2 * 2 * 16;
+        if (!gbad) {
+#pragma unroll
+            for (int h = 0; h < 2; h++) {
+                const BPair bp = bpair_src(tab, h * 2 * NPH, tab + NC * TAB_CHUNK, lane);
+                v4f acc = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+                for (int m = 0; m < NPH; m++) {
+                    const u32x4 lo = *(const u32x4 *)(bp.d + m * bp.step);
+                    const u32x4 hi = *(const u32x4 *)(bp.d + m * bp.step + 16);
+                    const int sbv = *(const int *)(bp.s + m * bp.step);
+                    v8i b;
+                    b[0] = (int)lo.x; b[1] = (int)lo.y; b[2] = (int)lo.z; b[3] = (int)lo.w;
+                    b[4] = (int)hi.x; b[5] = (int)hi.y; b[6] = (int)hi.z; b[7] = (int)hi.w;
+                    switch (m & 3) {
+                    case 0: acc = mfma_f4_sel<0>(gw[h].q[m], b, acc, gw[h].s[m >> 2], sbv); break;
+                    case 1: acc = mfma_f4_sel<1>(gw[h].q[m], b, acc, gw[h].s[m >> 2], sbv); break;
+                    case 2: acc = mfma_f4_sel<2>(gw[h].q[m], b, acc, gw[h].s[m >> 2], sbv); break;
+                    default: acc = mfma_f4_sel<3>(gw[h].q[m], b, acc, gw[h].s[m >> 2], sbv); break;
+                    }
+                }
+                store_pair_partials(acc, rt + (h * 2 + mat) * 16, lane);
+            }
+        } else {
+            if (lane == 0 && mat == 0) atomicOr(a.status, gbad);
+            if (lane < 16) {
+                rt[(0 * 2 + mat) * 16 + lane] = qnan_f();
+                rt[(1 * 2 + mat) * 16 + lane] = qnan_f();
+            }
+        }
+    }
+    lds_barrier();                                   /* B2: the tiles' partials */
+
+    /* ---- waves 0-11: the down unit's weights; waves 12-15: the mid tables ---- */
+    const int uk = wave >> 1, ut = wave & 1;         /* down unit: slot, 8-row tile */
+    const bool dlive = wave < BAL_GU_WAVES && uk < topk;
+    unsigned dbad = 0;
+    APairs<NPD> dw;
+    if (dlive) {
+        DSV4QMat m;
+        dbad = down_expert(d, uk, m);
+        if (!dbad && !mx_desc_ok<FMT_FP4_E8M0>(m, d.hidden, d.inter)) dbad = ST_BAD_DESCRIPTOR;
+        if (!dbad) {
+            const int rt = r0d + 8 * ut;
+            const int row = min(rt + (lane & 7), d.hidden - 1);
+            ld_pairs_scales<NPD>(dw, (const uint8_t *)m.s, d.inter / 32, m.blk_r, row, rt, d.hidden - 1, 0, lane);
+            DSV4_ORDER();
+            ld_pairs_w<NPD>(dw, (const uint8_t *)m.w + (size_t)row * (d.inter / 2), 0, lane);
+            DSV4_ORDER();
+        }
+    }
+    if (wave >= BAL_GU_WAVES) {
+        /* Lanes 2 i and 2 i + 1 (i < BAL_HB) form half block i's 16 mid
+         * values, eight each, and split them; its BAL_HB_DW table dwords go
+         * through the wave's staging so that lane 20 i + dw stores dword dw
+         * (codes of part dw / 4, bytes 4 (dw % 4) .., then the part scales),
+         * one store instruction per replica. */
+        uint32_t *stg = (uint32_t *)(lds + L.stage) + (wave - BAL_GU_WAVES) * 64;
+        const int i = lane >> 1, hl = lane & 1;
+        if (lane < 2 * BAL_HB) {
+            float v[8];
+#pragma unroll
+            for (int r = 0; r < 8; r++) {
+                const int rr = 8 * hl + r;           /* row of the half block */
+                const float *p0 = red + (size_t)(2 * i + (rr >> 3)) * 2 * 2 * 16;
+                const int q = rr & 7;
+                const float gs = ((p0[q] + p0[8 + q]) + p0[32 + q]) + p0[40 + q];
+                const float us = ((p0[16 + q] + p0[24 + q]) + p0[48 + q]) + p0[56 + q];
+                v[r] = dev_swiglu(gs, us, a.limit);
+            }
+            uint32_t code[NPART][2];
+            int E[NPART];
+            split8_half(v, code, E);
+#pragma unroll
+            for (int pp = 0; pp < NPART; pp++) {
+                stg[BAL_HB_DW * i + 4 * pp + 2 * hl] = code[pp][0];
+                stg[BAL_HB_DW * i + 4 * pp + 2 * hl + 1] = code[pp][1];
+                if (!hl) stg[BAL_HB_DW * i + 4 * NPART + pp] = (uint32_t)E[pp];
+            }
+        }
+        __builtin_amdgcn_s_waitcnt(0xC07F);          /* lgkmcnt(0): the wave's staging is written */
+        asm volatile("" ::: "memory");
+        const int hi = lane / BAL_HB_DW, dwi = lane - hi * BAL_HB_DW;
+        const int hbl = hi * G + (int)blockIdx.x;
+        if (hi < BAL_HB && hbl < n_hb) {
+            const int k = (hbl % (a.inter / 16)) * 16;                 /* row of the slot's mid */
+            const int s2 = hbl / (a.inter / 16);
+            const int k0 = k & 127;
+            const int off = (s2 * NCD + (k >> 7)) * MTAB_CHUNK +
+                            (dwi < 4 * NPART ? mtab_code_off(k0, dwi >> 2) + 4 * (dwi & 3)
+                                             : mtab_scale_off(k0, dwi - 4 * NPART));
+            const uint32_t val = stg[lane];
+            for (int c = wave - BAL_GU_WAVES; c < A.mid_copies; c += BAL_WAVES - BAL_GU_WAVES)
+                st_dev32(A.midc + (size_t)c * A.copy_ld + off, val);
+        }
+        /* the replicas acknowledged before the barrier below */
+        __builtin_amdgcn_s_waitcnt(0x0F70);
+        asm volatile("" ::: "memory");
+    }
+    lds_barrier();                                   /* B2b: the workgroup's tables are out */
+    if (wave == BAL_GU_WAVES && lane == 0) {
+        /* the add that completes the count raises the flag */
+        const OnePub &p = A.pub;
+        const unsigned grp = blockIdx.x % ONE_LEAVE_GROUPS;
+        const unsigned in_grp = (p.items - grp + ONE_LEAVE_GROUPS - 1) / ONE_LEAVE_GROUPS;
+        const unsigned groups = p.items < ONE_LEAVE_GROUPS ? p.items : ONE_LEAVE_GROUPS;
+        unsigned *top = p.count + ONE_LEAVE_GROUPS * ONE_PUB_LINE_WORDS;
+        if (__hip_atomic_fetch_add(p.count + grp * ONE_PUB_LINE_WORDS, 1u, __ATOMIC_RELAXED,
+                                   __HIP_MEMORY_SCOPE_AGENT) == in_grp - 1 &&
+            __hip_atomic_fetch_add(top, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == groups - 1)
+            __hip_atomic_store(p.done, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    if (wave == BAL_POLL_WAVE) {
+        const bool ok = wait_done(A.pub, A.spin_max);
+        if (lane == 0) *ready_ok = ok ? 1 : 0;
+    }
+    lds_barrier();                                   /* B3: every slot's table is out (or the wait gave up) */
+    const bool ready = *ready_ok != 0;
+
+    /* ---- every slot's table into LDS (over x's), 1 KiB per instruction ---- */
+    if (wave >= BAL_GU_WAVES) {
+        if (ready) {
+            const __amdgpu_buffer_rsrc_t rt =
+                dev_rsrc(A.midc + (size_t)(blockIdx.x % A.mid_copies) * A.copy_ld, (uint32_t)tab_bytes);
+            for (int r = wave - BAL_GU_WAVES; r * 1024 < tab_bytes; r += BAL_WAVES - BAL_GU_WAVES)
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(rt, (lds_void_t *)(tab + 1024 * r), 16,
+                                                         1024 * r + 16 * lane, 0, 0, CPOL_SC1);
+        }
+        if (wave == BAL_GU_WAVES && lane < TAB_ZERO / 4)   /* zero operand, unit scale (past the copies) */
+            ((uint32_t *)(tab + (tab_bytes + 1023) / 1024 * 1024))[lane] = lane == 8 ? E8M0_ONE : 0u;
+        __builtin_amdgcn_s_waitcnt(0x0F70);          /* the copies landed */
+        asm volatile("" ::: "memory");
+    }
+    lds_barrier();                                   /* B4: the tables */
+
+    /* ---- down MFMAs: wave u = unit (slot u / 2, tile u % 2) ---- */
+    if (dlive) {
+        unsigned bad = dbad;
+        if (!bad && !ready) bad = ST_SYNC_TIMEOUT;
+        if (!bad) {
+            ld_pairs_scales_finish<NPD>(dw, lane);
+            const BMid bp = bmid_src(tab + (size_t)uk * NCD * MTAB_CHUNK, 0,
+                                     tab + (tab_bytes + 1023) / 1024 * 1024, lane);
+            v4f acc = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+            for (int mm = 0; mm < NPD; mm++) {
+                const u32x4 lo = *(const u32x4 *)(bp.d + mm * bp.dstep);
+                const u32x4 hi = *(const u32x4 *)(bp.d + mm * bp.dstep + 16);
+                const int sbv = *(const int *)(bp.s + mm * bp.sstep);
+                v8i bv;
+                bv[0] = (int)lo.x; bv[1] = (int)lo.y; bv[2] = (int)lo.z; bv[3] = (int)lo.w;
+                bv[4] = (int)hi.x; bv[5] = (int)hi.y; bv[6] = (int)hi.z; bv[7] = (int)hi.w;
+                switch (mm & 3) {
+                case 0: acc = mfma_f4_sel<0>(dw.q[mm], bv, acc, dw.s[mm >> 2], sbv); break;
+                case 1: acc = mfma_f4_sel<1>(dw.q[mm], bv, acc, dw.s[mm >> 2], sbv); break;
+                case 2: acc = mfma_f4_sel<2>(dw.q[mm], bv, acc, dw.s[mm >> 2], sbv); break;
+                default: acc = mfma_f4_sel<3>(dw.q[mm], bv, acc, dw.s[mm >> 2], sbv); break;
+                }
+            }
+            store_mid_partials(acc, &yl[uk][ut][0], lane);
+        } else {
+            if (lane == 0 && (ut == 0 || bad == ST_SYNC_TIMEOUT)) atomicOr(a.status, bad);
+            if (lane < 16) yl[uk][ut][lane] = qnan_f();
+        }
+    }
+    __syncthreads();                                 /* B5: every slot's partial rows */
+    if (threadIdx.x == 0) leave(A.pub);              /* the add and the poll were this workgroup's last */
+    if (threadIdx.x >= 16 || r0d + (int)threadIdx.x >= d.hidden) return;
+    const int t = threadIdx.x >> 3, rr = threadIdx.x & 7;
+    float o = 0.0f;
+    for (int kk = 0; kk < topk; kk++) {
+        const float y = yl[kk][t][rr] + yl[kk][t][8 + rr];
+        o = __fadd_rn(o, __fmul_rn(route_weight(d, kk), y));
+    }
+    if (d.shared) o = __fadd_rn(o, d.shared[r0d + threadIdx.x]);
+    d.out[r0d + threadIdx.x] = o;
 }
 
 /* ------------------------------------------------------------ launches --- */
@@ -1457,7 +1855,7 @@ int gateup_mx_ncw(int fmt, int cols)
     return fmt == FMT_FP4_E8M0 || ncw <= 8 ? ncw : 0;
 }
 
-size_t mx_split_bytes(int inter) { return (size_t)(inter / 128) * TAB_CHUNK; }
+size_t mx_split_bytes(int inter) { return (size_t)(inter / 128) * MTAB_CHUNK; }
 
 hipError_t gemv_mx_launch(int fmt, GemvMxArgs a, hipStream_t st)
 {
@@ -1546,12 +1944,81 @@ static hipError_t moe_one_d(const MoeOneArgs &a, hipStream_t st)
     }
 }
 
-hipError_t moe_one_launch(MoeOneArgs a, hipStream_t st)
+/* Whether the balanced form takes this geometry: every gate/up half block in
+ * one round of BAL_HB per workgroup, a down scale row of whole 16-byte pieces
+ * (inter >= 512), one gate/up wave per down unit (topk <= 6), the LDS of one
+ * workgroup. */
+static bool bal_geometry_ok(int hidden, int inter, int topk)
+{
+    const long half_blocks = (long)topk * inter / 16, groups = hidden / 16;
+    return inter >= 512 && half_blocks <= (long)BAL_HB * groups && 2 * topk <= BAL_GU_WAVES &&
+           bal_lds(hidden, inter, topk).total <= 160 * 1024;
+}
+
+/* Launch k_moe_bal when the whole grid is resident at once (one workgroup of
+ * 1024 threads per CU); hipErrorNotSupported otherwise, and the caller takes
+ * k_moe_one. The occupancy check and the LDS attribute are set up once per
+ * instantiation (not inside a stream capture of a later call). */
+template <int NPH, int NPD>
+static hipError_t moe_bal_k(const MoeOneArgs &a, hipStream_t st)
+{
+    static int fits = -1;
+    const size_t lds = (size_t)bal_lds(512 * NPH, 256 * NPD, a.dn.topk).total;
+    const unsigned grid = (unsigned)(a.dn.hidden / 16);
+    if (fits < 0) {
+        int dev = 0, cus = 0, per_cu = 0;
+        hipError_t e = hipGetDevice(&dev);
+        if (e == hipSuccess) e = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
+        if (e == hipSuccess)
+            e = hipFuncSetAttribute((const void *)k_moe_bal<NPH, NPD>,
+                                    hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
+        if (e == hipSuccess)
+            e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, (const void *)k_moe_bal<NPH, NPD>,
+                                                             BAL_WAVES * 64, 160 * 1024);
+        /* the largest grid of this instantiation is hidden / 16 = 32 NPH; a
+         * device that cannot hold it (or a failed query) keeps k_moe_one */
+        fits = e == hipSuccess && (long)per_cu * cus >= 32L * NPH ? 1 : 0;
+        if (e != hipSuccess) (void)hipGetLastError();
+    }
+    if (!fits) return hipErrorNotSupported;
+    hipLaunchKernelGGL((k_moe_bal<NPH, NPD>), dim3(grid), dim3(BAL_WAVES * 64), lds, st, a);
+    return hipGetLastError();
+}
+
+template <int NPH>
+static hipError_t moe_bal_d(const MoeOneArgs &a, hipStream_t st)
+{
+    switch (a.dn.inter) {
+    case 512: return moe_bal_k<NPH, 2>(a, st);
+    case 1024: return moe_bal_k<NPH, 4>(a, st);
+    default: return moe_bal_k<NPH, 8>(a, st);
+    }
+}
+
+static hipError_t moe_bal_launch(MoeOneArgs a, hipStream_t st)
+{
+    if (!a.midc || a.mid_copies < 1 || a.copy_ld < (size_t)a.dn.topk * mx_split_bytes(a.dn.inter))
+        return hipErrorNotSupported;
+    a.pub.items = (unsigned)(a.dn.hidden / 16);
+    a.pub.total = a.pub.items;
+    switch (a.gu.hidden) {
+    case 512: return moe_bal_d<1>(a, st);
+    case 1024: return moe_bal_d<2>(a, st);
+    case 2048: return moe_bal_d<4>(a, st);
+    default: return moe_bal_d<8>(a, st);
+    }
+}
+
+hipError_t moe_one_launch(MoeOneArgs a, hipStream_t st, bool balanced)
 {
     if (!moe_one_ok(a.gu.hidden, a.gu.inter, a.gu.nslots) || a.dn.hidden != a.gu.hidden ||
         a.dn.inter != a.gu.inter || a.dn.topk != a.gu.nslots || !a.gu.msplit || !a.pub.count ||
         !a.pub.done || !a.pub.leave)
         return hipErrorInvalidValue;
+    if (balanced && bal_geometry_ok(a.gu.hidden, a.gu.inter, a.gu.nslots)) {
+        const hipError_t e = moe_bal_launch(a, st);
+        if (e != hipErrorNotSupported) return e;
+    }
     a.gu_blocks = a.gu.nslots * (a.gu.inter / 32);
     a.pub.items = (unsigned)a.gu_blocks;
     a.pub.total = (unsigned)(a.gu_blocks + a.dn.hidden / 16);

@@ -217,26 +217,41 @@ hipError_t down_mx_launch(DownMxArgs a, hipStream_t st);
  * counter (after the group counters), and the last top add sets every word
  * back to 0, so each launch finds them zero (a HIP graph can replay the
  * launch). Every word is on its own 128-byte line, zero before the first
- * launch: count, done, the group counters, the top counter. */
+ * launch: count (ONE_LEAVE_GROUPS group counters and a top counter when every
+ * workgroup publishes, as in the balanced form; the first word alone
+ * otherwise), done, the leave group counters, the leave top counter. */
 struct OnePub {
     unsigned *count, *done, *leave;
     unsigned items, total;
 };
 constexpr int ONE_PUB_LINE_WORDS = 32;    /* one 128-byte line per word */
 constexpr int ONE_LEAVE_GROUPS = 8;
+constexpr int ONE_COUNT_LINES = ONE_LEAVE_GROUPS + 1;
 struct MoeOneArgs {
     GateUpMxArgs gu;
     DownMxArgs dn;
     OnePub pub;
     int gu_blocks;
     unsigned spin_max;
+    /* the balanced form's hand-off of mid: mid_copies replicas of every routed
+     * slot's mid table (topk x mx_split_bytes(inter) bytes each), copy_ld bytes
+     * apart from midc; every workgroup writes its rows to all of them and reads
+     * replica blockIdx % mid_copies, so no few memory channels serve every
+     * CU's reads */
+    uint8_t *midc;
+    int mid_copies;
+    size_t copy_ld;
 };
+/* most replicas of mid the balanced form writes */
+constexpr int BAL_MAX_COPIES = 32;
 /* whether one launch takes this geometry */
 bool moe_one_ok(int hidden, int inter, int topk);
-hipError_t moe_one_launch(MoeOneArgs a, hipStream_t st);
-/* the publication words of the one-launch form: count, done, the group
- * leave counters and the top counter, a 128-byte line each */
-constexpr size_t ONE_PUB_BYTES = (size_t)(2 + ONE_LEAVE_GROUPS + 1) * ONE_PUB_LINE_WORDS * 4;
+/* balanced: the balanced form (k_moe_bal) when it takes the geometry and the
+ * device holds its whole grid at once, else the grid-ordered form (k_moe_one) */
+hipError_t moe_one_launch(MoeOneArgs a, hipStream_t st, bool balanced);
+/* the publication words of the one-launch forms: the count lines, done, the
+ * group leave counters and the top counter, a 128-byte line each */
+constexpr size_t ONE_PUB_BYTES = (size_t)(ONE_COUNT_LINES + 1 + ONE_LEAVE_GROUPS + 1) * ONE_PUB_LINE_WORDS * 4;
 /* bytes of one slot's split table for a K of `inter` */
 size_t mx_split_bytes(int inter);
 

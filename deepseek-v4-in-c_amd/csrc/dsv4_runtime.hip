@@ -96,11 +96,11 @@ constexpr int HOST_WORD = 32;            /* the host calls' word, on its own 128
  * for callers that cannot allocate: the one-launch hand-off words (zero
  * between launches), the mid rows, the mid split tables and the shared
  * expert's output of one decode MoE call with topk <= 8, inter <= 2048 and
- * hidden <= 4096 (165,376 bytes at those maxima). Each GPU holds its own
+ * hidden <= 4096 (166,400 bytes at those maxima). Each GPU holds its own
  * copy until the process ends. Host code uses only the device address that
  * hipGetSymbolAddress returns for it (scratch_ptr, filled at init), never
  * this name. */
-constexpr size_t SCRATCH_BYTES = 165376;
+constexpr size_t SCRATCH_BYTES = 166400;
 __device__ __align__(256) uint8_t scratch[SCRATCH_BYTES];
 constexpr int MAX_DEVICES = 64;
 void *scratch_ptr_of[MAX_DEVICES];       /* device address of `scratch` per device */
@@ -352,12 +352,17 @@ int enqueue_expert(const DSV4ExpertW &e, int fmt, int inter, int hidden,
  * launches). */
 struct MoeWs {
     float *mid;
-    uint8_t *msplit;
+    uint8_t *msplit;          /* split tables, or the balanced form's replicas of mid */
+    size_t msplit_bytes;
     float *ys;
     unsigned *pub;
 };
 
 size_t moe_mid_ld(int inter) { return (size_t)((inter + 3) & ~3); }
+
+/* bytes of one replica of the routed slots' mid tables in the balanced decode
+ * form, 256-byte aligned */
+size_t moe_copy_bytes(int topk, int inter) { return ((size_t)topk * mx_split_bytes(inter) + 255) & ~(size_t)255; }
 
 /* Enqueue the decode MoE from device tables. */
 /* Routed slots come from table[idx[k]] with weights w[k] (device arrays), or,
@@ -385,9 +390,14 @@ int enqueue_moe(const DSV4ExpertW *table, int n_experts, const int *idx,
         HIPCHK(g.mid.need(((size_t)topk * mid_ld + (shared_dev ? moe_mid_ld(shared_inter) : 0)) * 4),
                "mid alloc");
         if (shared_dev) HIPCHK(g.ys.need((size_t)hidden * 4), "shared output alloc");
-        if (mx) HIPCHK(g.msplit.need((size_t)topk * sl), "mid split alloc");
+        /* the split tables of the grid-ordered and two-launch forms, or the
+         * balanced form's replicas of mid */
+        if (mx)
+            HIPCHK(g.msplit.need(std::max((size_t)topk * sl, BAL_MAX_COPIES * moe_copy_bytes(topk, inter))),
+                   "mid split alloc");
         m.mid = (float *)g.mid.p;
         m.msplit = (uint8_t *)g.msplit.p;
+        m.msplit_bytes = g.msplit.cap;
         m.ys = (float *)g.ys.p;
         m.pub = g.pub;
     }
@@ -443,23 +453,29 @@ int enqueue_moe(const DSV4ExpertW *table, int n_experts, const int *idx,
                 da.wv[k] = wv[k];
             }
         }
-        /* one launch: the down workgroups' weight stream overlaps gate/up
-         * and there is no second launch ramp; DSV4_HIP_DECODE_LAUNCHES=2
-         * keeps the two-launch form (same bits) */
+        /* one launch: the down weight stream overlaps gate/up and there is
+         * no second launch ramp. DSV4_HIP_DECODE_LAUNCHES selects the form
+         * (same bits in all three): 0 the balanced one-launch form where it
+         * applies, unset or 1 the grid-ordered one-launch form, 2 two
+         * launches */
         const char *nl = getenv("DSV4_HIP_DECODE_LAUNCHES");
-        if (!(nl && atoi(nl) == 2) && moe_one_ok(hidden, inter, topk)) {
+        const int form = nl ? atoi(nl) : 1;
+        if (form != 2 && moe_one_ok(hidden, inter, topk)) {
             MoeOneArgs oa;
             memset(&oa, 0, sizeof oa);
             oa.gu = ga;
             oa.dn = da;
             oa.pub.count = m.pub;
-            oa.pub.done = m.pub + ONE_PUB_LINE_WORDS;
-            oa.pub.leave = m.pub + 2 * ONE_PUB_LINE_WORDS;
+            oa.pub.done = m.pub + ONE_COUNT_LINES * ONE_PUB_LINE_WORDS;
+            oa.pub.leave = m.pub + (ONE_COUNT_LINES + 1) * ONE_PUB_LINE_WORDS;
+            oa.midc = m.msplit;
+            oa.copy_ld = moe_copy_bytes(topk, inter);
+            oa.mid_copies = (int)std::min<size_t>(BAL_MAX_COPIES, m.msplit_bytes / moe_copy_bytes(topk, inter));
             /* DSV4_HIP_DECODE_SPIN: most polls of a down workgroup's wait
              * (default 2^20); 0 gives up without polling */
             const char *sp = getenv("DSV4_HIP_DECODE_SPIN");
             oa.spin_max = sp ? (unsigned)strtoul(sp, nullptr, 10) : 1u << 20;
-            HIPCHK(moe_one_launch(oa, st), "one-launch decode MoE");
+            HIPCHK(moe_one_launch(oa, st, form == 0), "one-launch decode MoE");
             return 0;
         }
         HIPCHK(gateup_mx_launch(FMT_FP4_E8M0, ga, st), "routed gate/up launch");
@@ -1041,6 +1057,7 @@ int dsv4_hip_moe_decode_routed_noalloc_dev(float *out, const float *x, const DSV
     ws.pub = (unsigned *)base;
     ws.mid = (float *)(base + o_mid);
     ws.msplit = base + o_split;
+    ws.msplit_bytes = o_ys - o_split;
     ws.ys = (float *)(base + o_ys);
     return enqueue_moe(nullptr, n_experts, nullptr, nullptr, topk, shared, sfmt, sinter, hidden,
                        inter, x, out, limit, (hipStream_t)stream, routed, wv, &ws);

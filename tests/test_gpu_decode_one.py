@@ -71,43 +71,51 @@ class _Setup:
         return y
 
 
+# DSV4_HIP_DECODE_LAUNCHES: "0" the balanced one-launch form (the default where
+# it takes the geometry), "1" the grid-ordered one-launch form, "2" two launches.
+FORMS = ("0", "1", "2")
+
+
 @pytest.mark.parametrize("inter,hidden,topk", [(2048, 4096, 6), (256, 1024, 8), (512, 2048, 3),
-                                               (1024, 512, 1)])
+                                               (1024, 512, 1), (1024, 2048, 8), (2048, 2048, 2)])
 def test_one_launch_matches_two_launch(lib, pkg, oracle, monkeypatch, inter, hidden, topk):
-    """Twelve calls enqueued back to back on the one-launch form, each with its
-    own routing and token, then the same twelve on the two-launch form: bit for
-    bit equal, status clear, and the first and last against the oracle."""
+    """Twelve calls enqueued back to back on each one-launch form, each with
+    its own routing and token, then the same twelve on the two-launch form:
+    bit for bit equal, status clear, and the first and last against the
+    oracle. (1024, 2048, 8) has more gate/up tiles than the balanced form
+    takes in one round, so its default is the grid-ordered form."""
     s = _Setup(pkg, oracle, zlib.crc32(b"one") + inter + topk, inter, hidden, topk, topk + 4)
     calls = [s.draw(100 + i) for i in range(12)]
     lib.status()
-    monkeypatch.delenv(ENV, raising=False)
-    one = [s.run(lib, *c) for c in calls]
-    torch.cuda.synchronize()
-    assert lib.status() == 0
-    monkeypatch.setenv(ENV, "2")
-    two = [s.run(lib, *c) for c in calls]
-    torch.cuda.synchronize()
-    assert lib.status() == 0
-    for i, ((o1, _), (o2, _)) in enumerate(zip(one, two)):
-        assert np.array_equal(bits(o1.cpu().numpy()), bits(o2.cpu().numpy())), f"call {i}"
+    outs = {}
+    for form in FORMS:
+        monkeypatch.setenv(ENV, form)
+        res = [s.run(lib, *c) for c in calls]
+        torch.cuda.synchronize()
+        assert lib.status() == 0, f"form {form}"
+        outs[form] = [o.cpu().numpy() for o, _ in res]
+    for form in ("0", "1"):
+        for i in range(len(calls)):
+            assert np.array_equal(bits(outs[form][i]), bits(outs["2"][i])), f"form {form} call {i}"
     for i in (0, len(calls) - 1):
-        assert check_close(one[i][0].cpu().numpy(), s.want(oracle, *calls[i])) < 1e-4
+        assert check_close(outs["0"][i], s.want(oracle, *calls[i])) < 1e-4
 
 
 def test_one_launch_with_shared_expert(lib, pkg, oracle, monkeypatch):
-    """An FP8 shared expert (fp32 128x128 scales) added in the combine: both
-    forms agree bit for bit and match the oracle."""
+    """An FP8 shared expert (fp32 128x128 scales) added in the combine: every
+    form agrees bit for bit and matches the oracle."""
     s = _Setup(pkg, oracle, zlib.crc32(b"one-shared"), 2048, 4096, 6, 10, shared=True)
     c = s.draw(7)
-    monkeypatch.delenv(ENV, raising=False)
-    o1, _ = s.run(lib, *c)
-    monkeypatch.setenv(ENV, "2")
-    o2, _ = s.run(lib, *c)
-    torch.cuda.synchronize()
+    outs = {}
+    for form in FORMS:
+        monkeypatch.setenv(ENV, form)
+        o, _ = s.run(lib, *c)
+        torch.cuda.synchronize()
+        outs[form] = o.cpu().numpy()
     assert lib.status() == 0
-    g = o1.cpu().numpy()
-    assert np.array_equal(bits(g), bits(o2.cpu().numpy()))
-    assert check_close(g, s.want(oracle, *c)) < 1e-4
+    for form in ("0", "1"):
+        assert np.array_equal(bits(outs[form]), bits(outs["2"])), f"form {form}"
+    assert check_close(outs["0"], s.want(oracle, *c)) < 1e-4
 
 
 def test_one_launch_bad_id_then_good(lib, pkg, oracle, monkeypatch):
@@ -137,7 +145,7 @@ def test_one_launch_host_routed(lib, pkg, oracle, monkeypatch):
     arr = (pkg.ExpertW * s.n_exp)(*s.descs)
     calls = [s.draw(40 + i) for i in range(4)]
     outs = {}
-    for mode in ("1", "2"):
+    for mode in FORMS:
         monkeypatch.setenv(ENV, mode)
         res = []
         for idx, w, xh in calls:
@@ -149,13 +157,15 @@ def test_one_launch_host_routed(lib, pkg, oracle, monkeypatch):
         torch.cuda.synchronize()
         outs[mode] = [bits(o.cpu().numpy()) for o, _ in res]
     assert lib.status() == 0
-    for i in range(len(calls)):
-        assert np.array_equal(outs["1"][i], outs["2"][i]), f"call {i}"
-    assert check_close(res[0][0].cpu().numpy(), s.want(oracle, *calls[0])) < 1e-4
+    for form in ("0", "1"):
+        for i in range(len(calls)):
+            assert np.array_equal(outs[form][i], outs["2"][i]), f"form {form} call {i}"
+    assert check_close(outs["0"][0].view(np.float32), s.want(oracle, *calls[0])) < 1e-4
 
 
-def test_one_launch_wait_timeout_then_recovers(lib, pkg, oracle, monkeypatch):
-    """The down workgroups' wait forced to give up from the host
+@pytest.mark.parametrize("form", ["0", "1"])
+def test_one_launch_wait_timeout_then_recovers(lib, pkg, oracle, monkeypatch, form):
+    """The down phase's wait forced to give up from the host
     (DSV4_HIP_DECODE_SPIN=0: every down workgroup gives up without polling,
     and every kernel still exits normally): status bit 3, and every output
     row NaN. The hand-off words are reset by the launch's last workgroup
@@ -167,7 +177,7 @@ def test_one_launch_wait_timeout_then_recovers(lib, pkg, oracle, monkeypatch):
     ref, _ = s.run(lib, idx, w, xh)
     torch.cuda.synchronize()
     want = bits(ref.cpu().numpy())
-    monkeypatch.delenv(ENV, raising=False)
+    monkeypatch.setenv(ENV, form)
     assert lib.status() == 0
     monkeypatch.setenv("DSV4_HIP_DECODE_SPIN", "0")
     o, _ = s.run(lib, idx, w, xh)
@@ -294,7 +304,7 @@ def test_one_launch_soak(lib, pkg, oracle, monkeypatch):
     lib.synth_normal_dev(xs.data_ptr(), xs.numel(), 0x50A7, 1.0, True)
     outs = {}
     lib.status()
-    for mode in ("1", "2"):
+    for mode in FORMS:
         monkeypatch.setenv(ENV, mode)
         o = torch.empty((n_calls, hidden), dtype=torch.float32, device=DEV)
         for i in range(n_calls):
@@ -302,10 +312,11 @@ def test_one_launch_soak(lib, pkg, oracle, monkeypatch):
                                n_exp, didx.data_ptr() + 4 * topk * i, dw.data_ptr() + 4 * topk * i, topk,
                                shared, hidden, inter, 10.0)
         torch.cuda.synchronize()
-        assert lib.status() == 0, f"status after the {'one' if mode == '1' else 'two'}-launch form"
+        assert lib.status() == 0, f"status after form {mode}"
         outs[mode] = bits(o.cpu().numpy())
-    same = (outs["1"] == outs["2"]).all(1)
-    assert same.all(), f"first mismatch at call {int(np.argmin(same))} of {n_calls}"
+    for form in ("0", "1"):
+        same = (outs[form] == outs["2"]).all(1)
+        assert same.all(), f"form {form}: first mismatch at call {int(np.argmin(same))} of {n_calls}"
     hsh = P.HostExpert(*[P.HostMat(P.DSV4_WFP8_F32S, keep[2 * i].cpu().numpy(), keep[2 * i + 1].cpu().numpy(),
                                    r, c, 128, 128)
                          for i, (r, c) in enumerate(((inter, hidden), (inter, hidden), (hidden, inter)))])
