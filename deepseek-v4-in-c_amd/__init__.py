@@ -40,6 +40,7 @@ EXPORTS = (
     "dsv4_hip_quant_act_mxfp8_dev", "dsv4_hip_synth_normal_dev", "dsv4_hip_moe_route_dev",
     "dsv4_hip_moe_grouped_mx_mid_dev", "dsv4_hip_shared_fp8q_mid_dev",
     "dsv4_hip_route_dev", "dsv4_hip_moe_layer_dev", "dsv4_hip_moe_layer_n_dev",
+    "dsv4_hip_alloc_count",
 )
 # the reference-named C mirror (host/dsv4_compute_hip.c)
 MIRROR_EXPORTS = ("dsv4_mmq_n", "dsv4_mmq", "dsv4_expert_forward")
@@ -89,6 +90,7 @@ class Lib:
         L.dsv4_hip_init.restype = _I; L.dsv4_hip_init.argtypes = [_I]
         L.dsv4_hip_shutdown.restype = None; L.dsv4_hip_shutdown.argtypes = []
         L.dsv4_hip_last_error.restype = C.c_char_p; L.dsv4_hip_last_error.argtypes = []
+        L.dsv4_hip_alloc_count.restype = C.c_ulonglong; L.dsv4_hip_alloc_count.argtypes = []
         L.dsv4_hip_register.restype = _I; L.dsv4_hip_register.argtypes = [_P, C.c_size_t]
         L.dsv4_hip_unregister.restype = _I; L.dsv4_hip_unregister.argtypes = [_P]
         L.dsv4_hip_device_ptr.restype = _P; L.dsv4_hip_device_ptr.argtypes = [_P]
@@ -156,6 +158,10 @@ class Lib:
         L.dsv4_hip_shared_fp8q_mid_dev.argtypes = [_P, _P, _P, _I, _P, _I, _F, _P]
 
     # ------------------------------------------------------------ basics
+    def alloc_count(self) -> int:
+        """hipMalloc calls the library has made since it was loaded."""
+        return int(self.lib.dsv4_hip_alloc_count())
+
     def error(self) -> str:
         return (self.lib.dsv4_hip_last_error() or b"").decode()
 

@@ -23,6 +23,7 @@
  * vector and y are read/written once per call.
  */
 #include "dsv4_internal.h"
+#include "dsv4_bf16.h"
 
 namespace dsv4 {
 
@@ -124,78 +125,45 @@ static hipError_t launch_fmt(const GemvArgs &a, hipStream_t st)
 
 /* ------------------------------------------------------------- BF16 --- */
 
-/* Replaces bf16_n (src/10_compute/dsv4_matmul.c:88-113), which widens every
- * weight and activation to double and accumulates in double before one final
- * rounding to float. Same arithmetic here: bf16 -> fp32 is exact (the stored
- * halfword is the top of the float), fp32 -> fp64 is exact, products and
- * sums are fp64 FMAs, and only the row's total is rounded to fp32. The sum
- * order differs from the reference's 16-lane tree, which can move the final
- * rounding by one fp32 ulp at most in rare ties of the double sum.
- *
- * Lane `lane` owns the eight weights at row byte offset 16 lane + 1024 j
- * (columns 8 lane + 512 j ...), like the packed kernels above; a wave owns
- * ROWS rows (ROWS x KCH = 16 chunks of 16 bytes in flight per lane) and
- * holds them in registers across the call's tokens. The wave's 64 lane sums
- * of a row meet in a fixed xor-butterfly (deterministic). fp64 FMA runs at
- * the fp32 vector rate on gfx950, so one token stays HBM-bound. */
-__device__ __forceinline__ double wave_sum_f64(double v)
+/* One wave per ROWS rows: the rows go to LDS once, then every token's dot
+ * products. ROWS x (1 KiB KCH + 64) bytes of LDS (64: a bank offset between
+ * rows). */
+constexpr int BF16_PAD = 64;
+template <int KCH, int ROWS>
+__global__ __launch_bounds__(64) void k_gemv_bf16(GemvBf16Args a)
 {
-#pragma unroll
-    for (int m = 32; m >= 1; m >>= 1) v += __shfl_xor(v, m, 64);
-    return v;
+    extern __shared__ __align__(16) uint8_t lds[];
+    const int lane = threadIdx.x;
+    const int r0 = blockIdx.x * ROWS;
+    constexpr int STRIDE = KCH * 1024 + BF16_PAD;
+    bf16_rows_to_lds<KCH>(lds, STRIDE, a.W, r0, ROWS, a.rows - r0, 2 * a.cols, lane);
+    __builtin_amdgcn_s_waitcnt(0x0F70);              /* vmcnt(0): the rows landed */
+    asm volatile("" ::: "memory");
+    const int r = lane >> 4;
+    if (r >= ROWS) return;
+    const uint16_t *wl = (const uint16_t *)(lds + r * STRIDE);
+    for (int t = 0; t < a.nt; t++) {
+        const double acc = bf16_row_dot(wl, a.x + (size_t)t * a.x_ld, a.cols, lane);
+        if ((lane & 15) == 0 && r0 + r < a.rows) a.y[(size_t)t * a.y_ld + r0 + r] = (float)acc;
+    }
 }
 
 template <int KCH, int ROWS>
-__global__ __launch_bounds__(256) void k_gemv_bf16(GemvBf16Args a)
-{
-    const int lane = threadIdx.x & 63;
-    const int r0 = wave_id() * ROWS;
-    if (r0 >= a.rows) return;
-    const int row_bytes = 2 * a.cols;
-    u32x4 w[ROWS][KCH];
-#pragma unroll
-    for (int r = 0; r < ROWS; r++) {
-        const int row = r0 + r < a.rows ? r0 + r : a.rows - 1;
-        load_w_row<KCH, false>(w[r], (const uint8_t *)a.W + (size_t)row * row_bytes, lane, row_bytes);
-    }
-    for (int t = 0; t < a.nt; t++) {
-        const float *xt = a.x + (size_t)t * a.x_ld;
-        float xs[KCH][8];
-#pragma unroll
-        for (int j = 0; j < KCH; j++) {
-            const int c = 8 * lane + 512 * j;
-            const float *p = xt + (c < a.cols ? c : 0);
-            const f32x4 lo = *(const f32x4 *)p, hi = *(const f32x4 *)(p + 4);
-            xs[j][0] = lo.x; xs[j][1] = lo.y; xs[j][2] = lo.z; xs[j][3] = lo.w;
-            xs[j][4] = hi.x; xs[j][5] = hi.y; xs[j][6] = hi.z; xs[j][7] = hi.w;
-        }
-        double keep = 0.0;
-#pragma unroll
-        for (int r = 0; r < ROWS; r++) {
-            double acc = 0.0;
-#pragma unroll
-            for (int j = 0; j < KCH; j++) {
-                if (8 * lane + 512 * j >= a.cols) continue;
-#pragma unroll
-                for (int d = 0; d < 4; d++) {
-                    const uint32_t v = w[r][j][d];
-                    acc = fma((double)__uint_as_float(v << 16), (double)xs[j][2 * d], acc);
-                    acc = fma((double)__uint_as_float(v & 0xFFFF0000u), (double)xs[j][2 * d + 1], acc);
-                }
-            }
-            const double s = wave_sum_f64(acc);
-            if (lane == r) keep = s;
-        }
-        if (lane < ROWS && r0 + lane < a.rows) a.y[(size_t)t * a.y_ld + r0 + lane] = (float)keep;
-    }
-}
-
-template <int KCH>
 static hipError_t launch_bf16_k(const GemvBf16Args &a, hipStream_t st)
 {
-    constexpr int ROWS = KCH >= 16 ? 1 : 16 / KCH;
-    const int waves = (a.rows + ROWS - 1) / ROWS;
-    hipLaunchKernelGGL((k_gemv_bf16<KCH, ROWS>), dim3((unsigned)((waves + 3) / 4)), dim3(256), 0, st, a);
+    constexpr size_t lds = (size_t)ROWS * (KCH * 1024 + BF16_PAD);
+    if constexpr (lds > 64 * 1024) {
+        /* set once (not inside a stream capture of a later call) */
+        static bool set = false;
+        if (!set) {
+            const hipError_t e = hipFuncSetAttribute((const void *)k_gemv_bf16<KCH, ROWS>,
+                                                     hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+            if (e != hipSuccess) return e;
+            set = true;
+        }
+    }
+    hipLaunchKernelGGL((k_gemv_bf16<KCH, ROWS>), dim3((unsigned)((a.rows + ROWS - 1) / ROWS)), dim3(64), lds,
+                       st, a);
     return hipGetLastError();
 }
 
@@ -203,11 +171,11 @@ hipError_t gemv_bf16_launch(const GemvBf16Args &a, hipStream_t st)
 {
     if (a.rows <= 0 || a.cols <= 0 || a.cols % 8 || a.nt <= 0) return hipErrorInvalidValue;
     switch ((2 * a.cols + 1023) / 1024) {
-    case 1: return launch_bf16_k<1>(a, st);
-    case 2: return launch_bf16_k<2>(a, st);
-    case 3: case 4: return launch_bf16_k<4>(a, st);
-    case 5: case 6: case 7: case 8: return launch_bf16_k<8>(a, st);
-    case 9: case 10: case 11: case 12: case 13: case 14: case 15: case 16: return launch_bf16_k<16>(a, st);
+    case 1: return launch_bf16_k<1, 4>(a, st);
+    case 2: return launch_bf16_k<2, 4>(a, st);
+    case 3: case 4: return launch_bf16_k<4, 4>(a, st);
+    case 5: case 6: case 7: case 8: return launch_bf16_k<8, 4>(a, st);
+    case 9: case 10: case 11: case 12: case 13: case 14: case 15: case 16: return launch_bf16_k<16, 4>(a, st);
     default: return hipErrorInvalidValue;
     }
 }

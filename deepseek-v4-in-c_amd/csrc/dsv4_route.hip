@@ -23,12 +23,9 @@
  * complemented id below) over DPP lane moves, with no LDS and no barrier;
  * the first-untaken minimum is taken only when the token has a NaN.
  *
- * softplus and sqrt are evaluated in fp64 and rounded once to fp32:
- * (float)log1p((double)(float)exp(x)) is the correctly rounded log1pf of the
- * correctly rounded expf. glibc's log1pf is not correctly rounded, so orig
- * may differ from the reference's by one unit in the last place on about 1%
- * of inputs in [-104, 20] (sqrt agrees on all of them); the ids agree unless
- * two biased scores lie within that unit of each other.
+ * orig is the reference's bits: sqrtf, log1pf and expf restated from the
+ * host library's algorithms (dsv4_route_math.h; identical to the host's libm
+ * on every fp32 input of [-104, 20]), so the picks are the reference's ids.
  *
  * A hash-routed id outside [0, n_experts), or a token id outside [0, n_vocab)
  * (whose ids are then -1), raises ST_BAD_EXPERT_ID; every weight of that
@@ -36,9 +33,10 @@
  * range check catches them too.
  *
  * The fused gate + router (k_gate_route_bf16): one wavefront per gate row
- * computes the row's fp64 dot product (bf16 weights and fp32 x widened
- * exactly, fp64 FMAs, one rounding, as bf16_n at
- * src/10_compute/dsv4_matmul.c:88-113), its orig and biased score, stores
+ * computes the row's fp64 dot product in bf16_n's order (16 serial FMA
+ * chains and the reference's combine, src/10_compute/dsv4_matmul.c:88-113,
+ * dsv4_dec_common.h:45-61; the bits of dsv4_mmq on the host), its orig and
+ * biased score, stores
  * them device-scope (written through its XCD's L2); once the workgroup's
  * stores are acknowledged it adds one to a counter (one wave per
  * workgroup, so the rows spread over as many CUs as there are rows). The workgroup whose add
@@ -51,6 +49,8 @@
  * once, by n_experts waves.
  */
 #include "dsv4_internal.h"
+#include "dsv4_bf16.h"
+#include "dsv4_route_math.h"
 
 namespace dsv4 {
 
@@ -109,33 +109,8 @@ __device__ __forceinline__ uint32_t wave_min_u32(uint32_t v)
     return (uint32_t)__builtin_amdgcn_readlane((int)v, 63);
 }
 
-/* fp64 sum over the wave in a fixed order; the total is in lane 63. */
-template <int CTRL, int ROWMASK = 0xF>
-__device__ __forceinline__ double dpp_f64(double v)
-{
-    const uint64_t u = (uint64_t)__double_as_longlong(v);
-    const uint32_t lo = (uint32_t)u, hi = (uint32_t)(u >> 32);
-    const uint64_t r = ((uint64_t)dpp_u32<CTRL, ROWMASK>(0u, hi) << 32) | dpp_u32<CTRL, ROWMASK>(0u, lo);
-    return __longlong_as_double((long long)r);
-}
-
-__device__ __forceinline__ double wave_sum_f64_l63(double v)
-{
-    v += dpp_f64<DPP_QUAD_1032>(v);
-    v += dpp_f64<DPP_QUAD_2301>(v);
-    v += dpp_f64<DPP_ROW_HALF_MIRROR>(v);
-    v += dpp_f64<DPP_ROW_MIRROR>(v);
-    v += dpp_f64<DPP_ROW_BCAST15, 0xA>(v);
-    v += dpp_f64<DPP_ROW_BCAST31, 0xC>(v);
-    return v;
-}
-
-/* sqrt(softplus(x)), softplus's threshold at 20 as torch's */
-__device__ __forceinline__ float route_orig(float x)
-{
-    const float sp = x > 20.0f ? x : (float)log1p((double)(float)exp((double)x));
-    return (float)sqrt((double)sp);
-}
+/* sqrt(softplus(x)) bit for bit as the reference's host libm computes it */
+__device__ __forceinline__ float route_orig(float x) { return dsv4_route::route_orig(x); }
 
 /* Order-preserving key of a non-NaN score (-0 as +0) over the complemented
  * expert id: the larger key is the reference's preferred pick. */
@@ -289,32 +264,20 @@ __device__ __forceinline__ float ld_dev(__amdgpu_buffer_rsrc_t r, int byte_off)
  * gate row r; the last wave to finish routes the token. KCH 16-byte chunks
  * of the row per lane (row bytes <= 1024 KCH). */
 template <int KCH, int NJ>
-__global__ __launch_bounds__(256) void k_gate_route_bf16(GateRouteArgs a)
+__global__ __launch_bounds__(64) void k_gate_route_bf16(GateRouteArgs a)
 {
     __shared__ unsigned s_old;
+    __shared__ __align__(16) uint8_t wrow[KCH * 1024];
     const int r = wave_id();
     const int ne = a.n_experts;
     const int lane = threadIdx.x & 63;
     if (r < ne) {
-        const int row_bytes = 2 * a.cols;
-        u32x4 wv[KCH];
-        load_w_row<KCH, false>(wv, (const uint8_t *)a.gate_w + (size_t)r * row_bytes, lane, row_bytes);
-        double acc = 0.0;
-#pragma unroll
-        for (int j = 0; j < KCH; j++) {
-            const int c = 8 * lane + 512 * j;
-            if (c >= a.cols) continue;
-            const f32x4 lo = ld_f4(a.x + c), hi = ld_f4(a.x + c + 4);
-            const float xs[8] = {lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
-#pragma unroll
-            for (int d = 0; d < 4; d++) {
-                const uint32_t v = wv[j][d];
-                acc = fma((double)__uint_as_float(v << 16), (double)xs[2 * d], acc);
-                acc = fma((double)__uint_as_float(v & 0xFFFF0000u), (double)xs[2 * d + 1], acc);
-            }
-        }
-        acc = wave_sum_f64_l63(acc);
-        if (lane == 63) {
+        /* the row into LDS, then bf16_n's 16 FMA chains in lanes 0-15 */
+        bf16_rows_to_lds<KCH>(wrow, 0, a.gate_w, r, 1, 1, 2 * a.cols, lane);
+        __builtin_amdgcn_s_waitcnt(0x0F70);         /* vmcnt(0): the row landed */
+        asm volatile("" ::: "memory");
+        const double acc = bf16_row_dot((const uint16_t *)wrow, a.x, a.cols, lane);
+        if (lane == 0) {
             const float s = (float)acc;
             const float o = route_orig(s);
             st_dev(a.ws_orig + r, o);

@@ -22,6 +22,7 @@
  * machine without the GPU backend). Every entry point is one roctx range
  * named after it, visible in rocprofv3 --marker-trace.
  */
+#include <atomic>
 #include <map>
 #include <mutex>
 #include <string>
@@ -52,6 +53,15 @@ struct Region {
     void *dev;
 };
 
+/* Every device allocation of the library goes through dev_malloc, which
+ * counts the attempts (dsv4_hip_alloc_count). */
+std::atomic<unsigned long long> g_alloc_calls{0};
+hipError_t dev_malloc(void **p, size_t bytes)
+{
+    g_alloc_calls.fetch_add(1, std::memory_order_relaxed);
+    return hipMalloc(p, bytes);
+}
+
 /* A device buffer that only grows. */
 struct DevBuf {
     void *p = nullptr;
@@ -61,7 +71,7 @@ struct DevBuf {
         if (bytes <= cap) return hipSuccess;
         if (p) { (void)hipFree(p); p = nullptr; cap = 0; }
         const size_t want = bytes < 4096 ? 4096 : bytes;
-        hipError_t e = hipMalloc(&p, want);
+        hipError_t e = dev_malloc(&p, want);
         if (e == hipSuccess) cap = want;
         return e;
     }
@@ -96,11 +106,12 @@ constexpr int HOST_WORD = 32;            /* the host calls' word, on its own 128
  * for callers that cannot allocate: the one-launch hand-off words (zero
  * between launches), the mid rows, the mid split tables and the shared
  * expert's output of one decode MoE call with topk <= 8, inter <= 2048 and
- * hidden <= 4096 (166,400 bytes at those maxima). Each GPU holds its own
+ * hidden <= 4096 (174,592 bytes at those maxima: 2,560 + 9 x 2048 x 4 +
+ * 8 x 16 x 640 + 4096 x 4). Each GPU holds its own
  * copy until the process ends. Host code uses only the device address that
  * hipGetSymbolAddress returns for it (scratch_ptr, filled at init), never
  * this name. */
-constexpr size_t SCRATCH_BYTES = 166400;
+constexpr size_t SCRATCH_BYTES = 174592;
 __device__ __align__(256) uint8_t scratch[SCRATCH_BYTES];
 constexpr int MAX_DEVICES = 64;
 void *scratch_ptr_of[MAX_DEVICES];       /* device address of `scratch` per device */
@@ -548,20 +559,21 @@ int dsv4_hip_init(int device)
         hipEventCreateWithFlags(&g.join2, hipEventDisableTiming) != hipSuccess ||
         hipEventCreateWithFlags(&g.xq, hipEventDisableTiming) != hipSuccess)
         return fail("event creation failed");
-    if (hipMalloc((void **)&g.status, 256) != hipSuccess) return fail("status alloc failed");
+    if (dev_malloc((void **)&g.status, 256) != hipSuccess) return fail("status alloc failed");
     if (hipMemset(g.status, 0, 256) != hipSuccess) return fail("status clear failed");
-    if (hipMalloc((void **)&g.pub, ONE_PUB_BYTES) != hipSuccess) return fail("counter alloc failed");
+    if (dev_malloc((void **)&g.pub, ONE_PUB_BYTES) != hipSuccess) return fail("counter alloc failed");
     if (hipMemset(g.pub, 0, ONE_PUB_BYTES) != hipSuccess) return fail("counter clear failed");
-    if (hipMalloc((void **)&g.rt_count, GATE_ROUTE_COUNTER_BYTES) != hipSuccess)
+    if (dev_malloc((void **)&g.rt_count, GATE_ROUTE_COUNTER_BYTES) != hipSuccess)
         return fail("counter alloc failed");
     if (hipMemset(g.rt_count, 0, GATE_ROUTE_COUNTER_BYTES) != hipSuccess)
         return fail("counter clear failed");
     g.st = g.status;
     /* this device's copy of the allocation-free entry point's scratch: its
-     * address, once, with the device current; the hand-off words start at
-     * zero and every launch leaves them so */
+     * address, looked up with the device current on every init, and its
+     * hand-off words cleared (every launch leaves them at zero; an init after
+     * a call that ended on a timeout starts from zero again) */
     if (device >= MAX_DEVICES) return fail("device %d beyond %d", device, MAX_DEVICES);
-    if (!scratch_ptr_of[device]) {
+    {
         void *p = nullptr;
         const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
         if (e != hipSuccess || !p)
@@ -610,6 +622,8 @@ void dsv4_hip_shutdown(void)
 
 const char *dsv4_hip_last_error(void) { return g_err.c_str(); }
 
+unsigned long long dsv4_hip_alloc_count(void) { return g_alloc_calls.load(std::memory_order_relaxed); }
+
 int dsv4_hip_register(const void *host, size_t bytes)
 {
     std::lock_guard<std::mutex> lk(g.mu);
@@ -625,7 +639,7 @@ int dsv4_hip_register(const void *host, size_t bytes)
             return fail("register: range overlaps a registered one");
     }
     void *dev = nullptr;
-    hipError_t e = hipMalloc(&dev, bytes);
+    hipError_t e = dev_malloc(&dev, bytes);
     if (e != hipSuccess) return fail("register: hipMalloc(%zu) failed", bytes);
     e = hipMemcpy(dev, host, bytes, hipMemcpyHostToDevice);
     if (e != hipSuccess) {
@@ -1253,7 +1267,7 @@ void *dsv4_hip_load_experts(const char *model_dir, const char *index_dir, int la
         }
     }
     uint8_t *arena = nullptr, *stage = nullptr;
-    if (hipMalloc((void **)&arena, slot * (size_t)ne) != hipSuccess ||
+    if (dev_malloc((void **)&arena, slot * (size_t)ne) != hipSuccess ||
         hipHostMalloc((void **)&stage, slot, hipHostMallocDefault) != hipSuccess) {
         if (arena) (void)hipFree(arena);
         close_all();

@@ -169,7 +169,7 @@ int  dsv4_hip_moe_decode_routed_dev(float *out, const float *x,
  * (code under HIP graph capture, tight serving loops, harnesses that forbid
  * allocation). Same arguments, kernels and results bit for bit; every
  * intermediate (mid rows, mid split tables, the shared expert's output, the
- * one-launch hand-off words) lives in a file-scope device array of 165,376
+ * one-launch hand-off words) lives in a file-scope device array of 174,592
  * bytes that each GPU holds until the process ends, mapped by
  * dsv4_hip_init. It calls no allocating routine. Limits: topk <= 8, inter
  * <= 2048, hidden <= 4096 (multiples of 128), shared inter <= 2048; larger

@@ -82,6 +82,12 @@ int dsv4_hip_shared_fp8q_mid_dev(uint8_t *mid, float *mid_s, const float *x, int
 int dsv4_hip_synth_normal_dev(float *out, size_t n, uint64_t seed, float sigma,
                               int round_bf16, void *stream);
 
+/* Number of device allocations (hipMalloc calls) the library has made since
+ * it was loaded: workspaces, status words, registered copies, expert arenas.
+ * A diagnostic for callers that must not allocate: it stays unchanged
+ * across calls of dsv4_hip_moe_decode_routed_noalloc_dev. */
+unsigned long long dsv4_hip_alloc_count(void);
+
 #ifdef __cplusplus
 }
 #endif

@@ -2,9 +2,9 @@
 """The allocation-free decode MoE entry point
 (dsv4_hip_moe_decode_routed_noalloc_dev) against the entry point it is a
 variant of (dsv4_hip_moe_decode_routed_dev): bit-identical outputs on two
-calls in a row, the second with a smaller input; the device's free memory
-unchanged across its calls; a call beyond the scratch limits returns -1
-with the reason."""
+calls in a row, the second with a smaller input; no allocation by the
+library and the device's free memory unchanged across its calls; a call
+beyond the scratch limits returns -1 with the reason."""
 import ctypes as C
 
 import numpy as np
@@ -47,19 +47,33 @@ class _Case:
 
 
 def test_noalloc_matches_allocating_entry(lib, pkg, oracle):
-    big = _Case(pkg, oracle, 701, 2048, 4096, 6, 8, True)
+    """After a fresh dsv4_hip_init (empty workspaces, scratch address looked
+    up again): the allocation-free calls first, at the scratch's maxima
+    (topk 8, inter 2048, hidden 4096, shared expert) and then a smaller
+    call, with no hipMalloc of the library (its allocation counter) and no
+    change of the device's free memory; then the allocating entry point on the
+    same inputs, which does allocate its workspaces (the counter's positive
+    control), and bit-identical outputs."""
+    big = _Case(pkg, oracle, 701, 2048, 4096, 8, 8, True)
     small = _Case(pkg, oracle, 702, 512, 1024, 3, 5, False)
-    for c in (big, small):
-        c.reference(lib)
     torch.cuda.synchronize()
-    assert lib.status() == 0
+    lib.shutdown()
+    assert lib.init(0) == 0, lib.error()
+    lib.status()
+    n0 = lib.alloc_count()
     free0 = torch.cuda.mem_get_info()[0]
     for c in (big, small):
         assert c.noalloc_rc(lib) == 0, lib.error()
     torch.cuda.synchronize()
     free1 = torch.cuda.mem_get_info()[0]
-    assert lib.status() == 0
+    assert lib.alloc_count() == n0, "the allocation-free entry point allocated"
     assert free1 == free0, f"free device memory changed by {free0 - free1} bytes"
+    assert lib.status() == 0
+    for c in (big, small):
+        c.reference(lib)
+    torch.cuda.synchronize()
+    assert lib.alloc_count() > n0, "the allocating entry point did not count its workspaces"
+    assert lib.status() == 0
     for c in (big, small):
         got = c.out.cpu().numpy()
         assert np.isfinite(got).all()
