@@ -398,7 +398,9 @@ def bench_grouped(args, torch, pkg, lib, stream, sp, K, W, cfg):
     torch.cuda.synchronize()
 
     # config 4 runs the routed experts on the block-scaled MFMA (FP4 weights x
-    # MXFP8 tokens); config 2 (and config 4 with --exact) the exact fp16 path
+    # MXFP8 tokens and mid: within 1e-3 relative L2 of the reference fed the
+    # same quantized tokens and mid, a few 1e-2 from the unquantized one, both
+    # reported); config 2 (and config 4 with --exact) the exact fp16 path
     mx = cfg == 4 and not args.exact
 
     def call(fn, i):
@@ -435,14 +437,28 @@ def bench_grouped(args, torch, pkg, lib, stream, sp, K, W, cfg):
     t_launch = time_events(torch, stream, lambda i: step(W + i), K)
     other = None
     if cfg == 4 and not args.no_other:
-        # the other precision path of the same call, timed the same way
+        # the other precision path of the same call, timed the same way, and
+        # the block-scaled path's error against the exact one on one step
         for i in range(W):
             step_other(i)
         t_other = time_events(torch, stream, lambda i: step_other(W + i), K)
+        call(lib.moe_grouped_dev, W)
+        exact_out = out.clone()
+        call(lib.moe_grouped_mx_dev, W)
+        torch.cuda.synchronize()
+        e = (out.double() - exact_out.double()).norm() / exact_out.double().norm()
+        rel = float(e)
         other = {"entry": "dsv4_hip_moe_grouped_dev" if mx else "dsv4_hip_moe_grouped_mx_dev",
                  "path": "exact: fp16 MFMA on exactly decoded weights" if mx
-                 else "block-scaled MFMA, MXFP8 tokens",
-                 "launch_us": round(t_other * 1e6, 3)}
+                 else "block-scaled MFMA, MXFP8 tokens and mid",
+                 "launch_us": round(t_other * 1e6, 3),
+                 "tflops": round(flops_step / t_other / 1e12, 2),
+                 "mx_rel_l2_vs_exact": float(f"{rel:.3e}"),
+                 "mx_error_note": "the block-scaled path rounds tokens and mid to MXFP8 (e4m3, "
+                                  "E8M0 per 32): rel L2 <= 1e-3 per token against the reference "
+                                  "fed the same quantized tokens and mid (tests/test_gpu_moe_mx.py); "
+                                  "mx_rel_l2_vs_exact against the unquantized computation, beyond "
+                                  "1e-3; the exact path is within 1e-3 of the unquantized reference"}
     assert lib.status() == 0
     bytes_avg = float(np.mean([step_bytes((W + i) % nsets) for i in range(K)]))
     d_avg = (bytes_avg - SHARED_BYTES - n * HIDDEN * 6) / EXPERT_BYTES
@@ -611,6 +627,24 @@ def bench_cfg3(args, torch, pkg, lib, stream, sp, K, W):
                   "gemm_launch_us": round(t_gemm_mx * 1e6, 3),
                   "gemm_tflops": round(flops / t_gemm_mx / 1e12, 2),
                   "gemm_frac": round(flops / t_gemm_mx / 1e12 / FP8_PEAK_TFLOPS, 4)}
+    # the drop-in seam: dsv4_mmq_n's own form (fp32 x and y, no quantization
+    # of x beyond the exact power-of-two row scaling and fp16 rounding) on the
+    # same weight, as the prefill projections call it (src/80_prefill/
+    # dsv4_prefill_proj.c:21-24); the dense fp16-MFMA GEMM plus its x converter
+    y32 = torch.empty(M * N, dtype=torch.float32, device=dev)
+
+    def seam(i):
+        lib.mmq_n_dev(y32.data_ptr(), af.data_ptr(), desc, M, sp)
+
+    for i in range(W):
+        seam(i)
+    t_seam = time_events(torch, stream, seam, K)
+    seam_rec = {"entry": "dsv4_hip_mmq_n_dev (fp32 x [2048x4096], fp32 y)",
+                "path": "x rows scaled by a power of two and rounded to fp16, weights decoded "
+                        "exactly to fp16 in LDS, fp16 MFMA, fp32 accumulation",
+                "ms_per_call": round(t_seam * 1e3, 5),
+                "tflops": round(flops / t_seam / 1e12, 2),
+                "frac_of_fp16_peak": round(flops / t_seam / 1e12 / FP16_PEAK_TFLOPS, 4)}
     cpu = None
     if not args.no_cpu:
         # the reference's fp8_n, nt > 1 body (src/10_compute/dsv4_matmul_fp8.c:
@@ -637,6 +671,7 @@ def bench_cfg3(args, torch, pkg, lib, stream, sp, K, W):
                      "flops_per_launch": flops, "launch_us": round(t_gemm * 1e6, 3)},
         "step_includes": "activation quantization kernel + GEMM kernel",
         "checkpoint_format": checkpoint,
+        "drop_in_seam": seam_rec,
         "cpu_baseline": cpu,
         "wall_s": round(wall, 4),
     }
@@ -730,8 +765,8 @@ def main():
                     help="config 1: do not run configs 0, 2, 3 and 4 as child processes "
                          "(their lines go into other_configs)")
     ap.add_argument("--exact", action="store_true",
-                    help="config 4: time the exact fp16-MFMA grouped path instead of the "
-                         "block-scaled one")
+                    help="config 4: time the exact fp16-MFMA grouped path as the value instead "
+                         "of the block-scaled one")
     ap.add_argument("--cpu-worker", metavar="SPEC",
                     help="internal: run one CPU-baseline measurement described by SPEC and exit")
     ap.add_argument("--copy-calib", action="store_true",
@@ -937,21 +972,22 @@ def main():
 def other_configs(args):
     """Configs 0, 2, 3 and 4, each in a child process of this one (its own
     data and HIP context, nothing else on the GPU meanwhile), so that the
-    default run times every workload: their JSON lines, without CPU
-    baselines, keyed by config."""
+    default run times every workload: their JSON lines keyed by config, each
+    with its CPU baseline (a shorter sample than config 1's) unless --no-cpu."""
     out = {}
     for c, steps in ((0, 200), (2, 50), (3, 100), (4, 30)):
-        cmd = [sys.executable, os.path.abspath(__file__), "--config", str(c), "--no-cpu",
+        cmd = [sys.executable, os.path.abspath(__file__), "--config", str(c),
                "--steps", str(steps), "--warmup", str(min(args.warmup, 5))]
+        cmd += ["--no-cpu"] if args.no_cpu else ["--cpu-seconds", str(min(args.cpu_seconds, 4.0))]
+        if args.cpu_threads:
+            cmd += ["--cpu-threads", str(args.cpu_threads)]
         log(f"config {c} in a child process")
         r = subprocess.run(cmd, stdout=subprocess.PIPE, text=True, timeout=600)
         lines = [ln for ln in r.stdout.splitlines() if ln.startswith("{")]
         if r.returncode != 0 or not lines:
             out[str(c)] = {"error": f"exit {r.returncode}"}
             continue
-        d = json.loads(lines[-1])
-        d.pop("cpu_baseline", None)
-        out[str(c)] = d
+        out[str(c)] = json.loads(lines[-1])
     return out
 
 

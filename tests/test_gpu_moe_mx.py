@@ -183,8 +183,13 @@ def check_mx(oracle, hexperts, hshared, x, idx, w, got, mid, ms, pos, tokens, li
     for j, t in enumerate(tokens):
         e = rel_l2(got[t], outs[j])
         assert e <= REL_L2_TOL, f"token {t}: rel L2 {e:.3e} (max abs {max_abs(got[t], outs[j]):.3e})"
-    # the MXFP8 rounding of tokens and mid against the unrounded reference
-    assert rel_l2(got[tokens], np.stack(exact)) < 0.1
+    # The MXFP8 rounding of tokens and mid against the unrounded reference:
+    # e4m3 keeps 4 significant bits, so each rounded value is off by up to
+    # 2^-5 relative and the outputs by about 4-5e-2 relative L2 (the config-4
+    # run reports the same figure at full size); model-sized weights only.
+    if strict:
+        e = rel_l2(got[tokens], np.stack(exact))
+        assert e <= 6e-2, f"rel L2 {e:.3e} against the unquantized reference"
 
 
 def run_mx(lib, experts, shared, x, idx, w, hidden, inter, limit=10.0):
