@@ -959,7 +959,7 @@ def main():
             "roofline": {"bound": "hbm", "achieved": round(bytes_step / t_launch / 1e9, 2),
                          "peak": HBM_PEAK_GBS, "unit": "GB/s",
                          "frac": round(bytes_step / t_launch / 1e9 / HBM_PEAK_GBS, 4),
-                         "traffic": traffic_for(0), "kernel": "k_gemv_mx<FP8_F32S,8,1>",
+                         "traffic": traffic_for(0), "kernel": "k_gemv_px8<FP8_F32S,4,4,2>",
                          "bytes_per_launch": bytes_step, "launch_us": round(t_launch * 1e6, 3)},
             "cpu_baseline": cpu,
             "wall_s": round(wall, 4),

@@ -22,23 +22,31 @@ namespace dsv4 {
  * row r. */
 __device__ __forceinline__ double bf16_of(uint16_t h) { return (double)__uint_as_float((uint32_t)h << 16); }
 
-/* chain c over `steps` steps: weights from the row in LDS, activations from x */
-__device__ __forceinline__ double bf16_chain(const uint16_t *wl, const float *x, int steps, int c)
+/* chain c over `steps` steps: weights and activations from LDS, the next
+ * eight steps' reads issued before this eight's FMAs (a dependent fp64 FMA
+ * chain; the reads' latency hides behind it) */
+__device__ __forceinline__ double bf16_chain(const uint16_t *wl, const float *xl, int steps, int c)
 {
     double acc = 0.0;
-    int s = 0;
-    for (; s + 8 <= steps; s += 8) {
-        uint16_t w[8];
-        float xv[8];
+    const int full = steps & ~7;
+    uint16_t w[8];
+    float xv[8];
+    if (full) {
 #pragma unroll
-        for (int i = 0; i < 8; i++) {
-            w[i] = wl[16 * (s + i) + c];
-            xv[i] = x[16 * (s + i) + c];
-        }
+        for (int i = 0; i < 8; i++) { w[i] = wl[16 * i + c]; xv[i] = xl[16 * i + c]; }
+    }
+    for (int s = 0; s < full; s += 8) {
+        uint16_t wn[8];
+        float xn[8];
+        const int sn = s + 8 < full ? s + 8 : s;        /* the last round re-reads its own */
+#pragma unroll
+        for (int i = 0; i < 8; i++) { wn[i] = wl[16 * (sn + i) + c]; xn[i] = xl[16 * (sn + i) + c]; }
 #pragma unroll
         for (int i = 0; i < 8; i++) acc = fma(bf16_of(w[i]), (double)xv[i], acc);
+#pragma unroll
+        for (int i = 0; i < 8; i++) { w[i] = wn[i]; xv[i] = xn[i]; }
     }
-    for (; s < steps; s++) acc = fma(bf16_of(wl[16 * s + c]), (double)x[16 * s + c], acc);
+    for (int s = full; s < steps; s++) acc = fma(bf16_of(wl[16 * s + c]), (double)xl[16 * s + c], acc);
     return acc;
 }
 
@@ -53,14 +61,15 @@ __device__ __forceinline__ double bf16_combine16(double v)
     return v;
 }
 
-/* The whole dot product of one row for lane group (row) lane / 16: returns the
- * fp64 acc in lane 16 (lane / 16), the trailing columns included. */
-__device__ __forceinline__ double bf16_row_dot(const uint16_t *wl, const float *x, int cols, int lane)
+/* The whole dot product of one row (wl) with x (xl, fp32), both in LDS, for
+ * lane group (row) lane / 16: returns the fp64 acc in lane 16 (lane / 16),
+ * the trailing columns included. */
+__device__ __forceinline__ double bf16_row_dot(const uint16_t *wl, const float *xl, int cols, int lane)
 {
     const int c = lane & 15, steps = cols / 16;
-    double acc = bf16_combine16(bf16_chain(wl, x, steps, c));
+    double acc = bf16_combine16(bf16_chain(wl, xl, steps, c));
     if (c == 0)
-        for (int e = 16 * steps; e < cols; e++) acc = fma(bf16_of(wl[e]), (double)x[e], acc);
+        for (int e = 16 * steps; e < cols; e++) acc = fma(bf16_of(wl[e]), (double)xl[e], acc);
     return acc;
 }
 
@@ -82,6 +91,17 @@ __device__ __forceinline__ void bf16_rows_to_lds(uint8_t *lds, int stride, const
             __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (bf_lds_t *)(lds + r * stride + 1024 * k), 16,
                                                      1024 * k + 16 * lane, 0, 0, 0);
     }
+}
+
+/* x (cols fp32 values) into LDS at xl, 1 KiB per instruction, bytes past
+ * cols read as zero; xl_bytes = bf16_x_lds_bytes(cols). The caller waits. */
+__host__ __device__ constexpr int bf16_x_lds_bytes(int cols) { return (cols * 4 + 1023) / 1024 * 1024; }
+
+__device__ __forceinline__ void bf16_x_to_lds(uint8_t *xl, const float *x, int cols, int lane)
+{
+    const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc((void *)x, (short)0, cols * 4, 0x00020000);
+    for (int k = 0; k < bf16_x_lds_bytes(cols) / 1024; k++)
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (bf_lds_t *)(xl + 1024 * k), 16, 1024 * k + 16 * lane, 0, 0, 0);
 }
 
 } // namespace dsv4

@@ -1115,30 +1115,97 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) void k
     gateup_px_item<NP>(a, (int)blockIdx.x, lds);
 }
 
+/* One wave's share of an 8-row FP8 tile in chunk pairs: rows r0 .. r0 + 7 of
+ * a matrix (row pitch row_bytes, scale grid sc_cols wide, blk_r rows high)
+ * over chunk pairs starting at chunk c0. A rows 0-7 are the tile's rows at
+ * chunk 2 i, rows 8-15 the same rows at chunk 2 i + 1, as in the FP4 pair
+ * kernels; B is the workgroup's split of x. E8M0 scales go in the MFMA's
+ * scale operand per lane (rows 8-15 take the odd chunk's), fp32 scales
+ * multiply each pair's product (one MFMA from zero) row by row. */
+template <int FMT, int NP>
+struct Px8Tile {
+    uint32_t sv[NP];                                   /* E8M0 byte or fp32 bits */
+    u32x4 q[NP][2];
+};
+
+/* Issue the tile's scale loads, then its weight loads (they complete in issue
+ * order, behind whatever the wave issued before). */
+template <int FMT, int NP>
+__device__ __forceinline__ void px8_load(Px8Tile<FMT, NP> &t, const uint8_t *W, const void *S, int row_bytes,
+                                         int sc_cols, int blk_r, int r0, int c0, int lane)
+{
+    constexpr bool F32S = FMT == FMT_FP8_F32S;
+    const int r8 = lane & 7, par = (lane >> 3) & 1, g = lane >> 4;
+    const uint8_t *wrow = W + (size_t)(r0 + r8) * row_bytes;
+    const size_t srow = (size_t)(r0 / blk_r) * sc_cols;
+    /* this lane's chunk scale per pair: E8M0 for the A rows of the lane
+     * (rows 8-15, par = 1: the odd chunk), fp32 for its accumulator rows
+     * (lanes 32-63 hold rows 8-15) */
+#pragma unroll
+    for (int i = 0; i < NP; i++) {
+        if constexpr (F32S) t.sv[i] = gptr((const uint32_t *)S)[srow + c0 + 2 * i + (lane >> 5)];
+        else t.sv[i] = ld_u8(S, srow + c0 + 2 * i + par);
+    }
+    DSV4_ORDER();
+#pragma unroll
+    for (int i = 0; i < NP; i++) {
+        const int c = c0 + 2 * i + par;
+        t.q[i][0] = ld_stream16(wrow + 128 * c + 16 * g);
+        t.q[i][1] = ld_stream16(wrow + 128 * c + 64 + 16 * g);
+    }
+}
+
+/* The tile's pair accumulator against x's split table (tab: chunk-major,
+ * zero operand after nc chunks). */
+template <int FMT, int NP>
+__device__ __forceinline__ v4f px8_mma(const Px8Tile<FMT, NP> &t, const uint8_t *tab, int nc, int c0, int lane)
+{
+    constexpr bool F32S = FMT == FMT_FP8_F32S;
+    const BPair bp = bpair_src(tab, c0, tab + (size_t)nc * TAB_CHUNK, lane);
+    v4f acc = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int i = 0; i < NP; i++) {
+        const u32x4 lo = *(const u32x4 *)(bp.d + i * bp.step);
+        const u32x4 hi = *(const u32x4 *)(bp.d + i * bp.step + 16);
+        const int sb = *(const int *)(bp.s + i * bp.step);
+        v8i b, av;
+        b[0] = (int)lo.x; b[1] = (int)lo.y; b[2] = (int)lo.z; b[3] = (int)lo.w;
+        b[4] = (int)hi.x; b[5] = (int)hi.y; b[6] = (int)hi.z; b[7] = (int)hi.w;
+        av[0] = (int)t.q[i][0].x; av[1] = (int)t.q[i][0].y; av[2] = (int)t.q[i][0].z; av[3] = (int)t.q[i][0].w;
+        av[4] = (int)t.q[i][1].x; av[5] = (int)t.q[i][1].y; av[6] = (int)t.q[i][1].z; av[7] = (int)t.q[i][1].w;
+        if constexpr (F32S) {
+            /* accumulator rows 0-7 (lanes 0-31) are the even chunk's, rows
+             * 8-15 (lanes 32-63) the odd chunk's: each lane scales its rows */
+            const v4f zero = {0.0f, 0.0f, 0.0f, 0.0f};
+            const v4f pr = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(av, b, zero, 0, 0, 0, E8M0_ONE, 0, sb);
+            const float sw = __uint_as_float(t.sv[i]);
+#pragma unroll
+            for (int e2 = 0; e2 < 4; e2++) acc[e2] = fmaf(pr[e2], sw, acc[e2]);
+        } else {
+            acc = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(av, b, acc, 0, 0, 0, (int)t.sv[i], 0, sb);
+        }
+    }
+    return acc;
+}
+
 /* Gate/up + SwiGLU of one FP8 expert (E8M0 or fp32 128 x 128 block scales)
  * in 8-row tiles, for the shared expert and single experts, whose mid needs
  * no split table: one workgroup per (slot, 8 rows), so a 2048-row expert
  * spreads over 256 workgroups (32-row groups gave 64, a quarter of the CUs,
  * and ran at 1.2 TB/s). Waves 0-3 take w1, waves 4-7 w3, each over a quarter
- * of K in NP chunk pairs (hidden = 1024 NP <= 4096): A rows 0-7 are the tile's rows
- * at chunk 2m, rows 8-15 the same rows at chunk 2m + 1, as in the FP4 pair
- * kernels; B is the workgroup's split of x. E8M0 scales go in the MFMA's
- * scale operand per lane (rows 8-15 take the odd chunk's), fp32 scales
- * multiply each pair's product (one MFMA from zero) row by row. */
+ * of K in NP chunk pairs (hidden = 1024 NP <= 4096). */
 template <int FMT, int NP>
 __global__ __launch_bounds__(512) void k_gateup_px8(GateUpMxArgs a)
 {
     extern __shared__ __align__(16) uint8_t lds[];
     constexpr int NC = 8 * NP;                         /* chunks of hidden */
     constexpr int UPL = (NC * 16 + 511) / 512;
-    constexpr bool F32S = FMT == FMT_FP8_F32S;
     const int lane = threadIdx.x & 63;
     const int wave = wave_in_group();
     const int mat = wave >> 2, kq = wave & 3;
     const int tiles = a.inter / 8;
     const int slot = blockIdx.x / tiles;
     const int r0 = (blockIdx.x - slot * tiles) * 8;
-    const int r8 = lane & 7, par = (lane >> 3) & 1, g = lane >> 4;
     const int c0 = kq * 2 * NP;                        /* the wave's first chunk */
     uint8_t *tab = lds;                                /* NC chunks + zero operand */
     float *red = (float *)(lds + NC * TAB_CHUNK + TAB_ZERO);   /* [2 mats][4 quarters][16] */
@@ -1154,59 +1221,18 @@ __global__ __launch_bounds__(512) void k_gateup_px8(GateUpMxArgs a)
         return;
     }
     const DSV4QMat &m = mat ? e.w3 : e.w1;
-    const uint8_t *wrow = (const uint8_t *)m.w + (size_t)(r0 + r8) * a.hidden;
-    const int sc_cols = a.hidden / 128;
-    const size_t srow = (size_t)(r0 / m.blk_r) * sc_cols;
 
     XUnits<UPL> xu;
     load_units<UPL, 512>(xu, a.x, 0, 1, 0, NC, (int)threadIdx.x);
     DSV4_ORDER();
-    /* this lane's chunk scale per pair: E8M0 for the A rows of the lane
-     * (rows 8-15, par = 1: the odd chunk), fp32 for its accumulator rows
-     * (lanes 32-63 hold rows 8-15) */
-    uint32_t sv[NP];
-#pragma unroll
-    for (int i = 0; i < NP; i++) {
-        if constexpr (F32S) sv[i] = gptr((const uint32_t *)m.s)[srow + c0 + 2 * i + (lane >> 5)];
-        else sv[i] = ld_u8(m.s, srow + c0 + 2 * i + par);
-    }
-    DSV4_ORDER();
-    u32x4 q[NP][2];
-#pragma unroll
-    for (int i = 0; i < NP; i++) {
-        const int c = c0 + 2 * i + par;
-        q[i][0] = ld_stream16(wrow + 128 * c + 16 * g);
-        q[i][1] = ld_stream16(wrow + 128 * c + 64 + 16 * g);
-    }
+    Px8Tile<FMT, NP> t;
+    px8_load<FMT, NP>(t, (const uint8_t *)m.w, m.s, a.hidden, a.hidden / 128, m.blk_r, r0, c0, lane);
     DSV4_ORDER();
     store_units<UPL, 512>(tab, xu, 1, NC, (int)threadIdx.x);
     __builtin_amdgcn_s_waitcnt(0xC07F);                /* lgkmcnt(0): own LDS writes done */
     __builtin_amdgcn_s_barrier();
     asm volatile("" ::: "memory");
-    const BPair bp = bpair_src(tab, c0, tab + NC * TAB_CHUNK, lane);
-    v4f acc = {0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-    for (int i = 0; i < NP; i++) {
-        const u32x4 lo = *(const u32x4 *)(bp.d + i * bp.step);
-        const u32x4 hi = *(const u32x4 *)(bp.d + i * bp.step + 16);
-        const int sb = *(const int *)(bp.s + i * bp.step);
-        v8i b, av;
-        b[0] = (int)lo.x; b[1] = (int)lo.y; b[2] = (int)lo.z; b[3] = (int)lo.w;
-        b[4] = (int)hi.x; b[5] = (int)hi.y; b[6] = (int)hi.z; b[7] = (int)hi.w;
-        av[0] = (int)q[i][0].x; av[1] = (int)q[i][0].y; av[2] = (int)q[i][0].z; av[3] = (int)q[i][0].w;
-        av[4] = (int)q[i][1].x; av[5] = (int)q[i][1].y; av[6] = (int)q[i][1].z; av[7] = (int)q[i][1].w;
-        if constexpr (F32S) {
-            /* accumulator rows 0-7 (lanes 0-31) are the even chunk's, rows
-             * 8-15 (lanes 32-63) the odd chunk's: each lane scales its rows */
-            const v4f zero = {0.0f, 0.0f, 0.0f, 0.0f};
-            const v4f pr = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(av, b, zero, 0, 0, 0, E8M0_ONE, 0, sb);
-            const float sw = __uint_as_float(sv[i]);
-#pragma unroll
-            for (int e2 = 0; e2 < 4; e2++) acc[e2] = fmaf(pr[e2], sw, acc[e2]);
-        } else {
-            acc = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(av, b, acc, 0, 0, 0, (int)sv[i], 0, sb);
-        }
-    }
+    const v4f acc = px8_mma<FMT, NP>(t, tab, NC, c0, lane);
     store_pair_partials(acc, red + (mat * 4 + kq) * 16, lane);
     __syncthreads();
     if (threadIdx.x < 8) {
@@ -1218,6 +1244,46 @@ __global__ __launch_bounds__(512) void k_gateup_px8(GateUpMxArgs a)
             us += red[(1 * 4 + k) * 16 + rr] + red[(1 * 4 + k) * 16 + 8 + rr];
         }
         mid[r0 + rr] = dev_swiglu(gs, us, a.limit);
+    }
+}
+
+/* One-token FP8 matvec in the same 8-row chunk-pair tiles: one workgroup per
+ * TILES 8-row tiles, KQ waves per tile each over NP chunk pairs (cols =
+ * 256 KQ NP), every workgroup splitting x once into LDS. */
+template <int FMT, int NP, int KQ, int TILES>
+__global__ __launch_bounds__(64 * KQ * TILES) void k_gemv_px8(GemvMxArgs a)
+{
+    extern __shared__ __align__(16) uint8_t lds[];
+    constexpr int NC = 2 * KQ * NP;
+    constexpr int NTHR = 64 * KQ * TILES;
+    constexpr int UPL = (NC * 16 + NTHR - 1) / NTHR;
+    const int lane = threadIdx.x & 63;
+    const int wave = wave_in_group();
+    const int h = wave / KQ, kq = wave % KQ;
+    const int r0 = blockIdx.x * 8 * TILES + 8 * h;
+    const int c0 = kq * 2 * NP;
+    uint8_t *tab = lds;
+    float *red = (float *)(lds + NC * TAB_CHUNK + TAB_ZERO);   /* [TILES][KQ][16] */
+
+    XUnits<UPL> xu;
+    load_units<UPL, NTHR>(xu, a.x, 0, 1, 0, NC, (int)threadIdx.x);
+    DSV4_ORDER();
+    Px8Tile<FMT, NP> t;
+    px8_load<FMT, NP>(t, a.W, a.S, a.row_bytes, a.sc_cols, a.blk_r, r0, c0, lane);
+    DSV4_ORDER();
+    store_units<UPL, NTHR>(tab, xu, 1, NC, (int)threadIdx.x);
+    __builtin_amdgcn_s_waitcnt(0xC07F);
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+    const v4f acc = px8_mma<FMT, NP>(t, tab, NC, c0, lane);
+    store_pair_partials(acc, red + (h * KQ + kq) * 16, lane);
+    __syncthreads();
+    if (threadIdx.x < 8 * TILES) {
+        const int hh = threadIdx.x >> 3, rr = threadIdx.x & 7;
+        float s = 0.0f;
+#pragma unroll
+        for (int k = 0; k < KQ; k++) s += red[(hh * KQ + k) * 16 + rr] + red[(hh * KQ + k) * 16 + 8 + rr];
+        a.y[blockIdx.x * 8 * TILES + threadIdx.x] = s;
     }
 }
 
@@ -1857,10 +1923,42 @@ int gateup_mx_ncw(int fmt, int cols)
 
 size_t mx_split_bytes(int inter) { return (size_t)(inter / 128) * MTAB_CHUNK; }
 
+template <int FMT, int NP, int KQ, int TILES>
+hipError_t gemv_px8_k(const GemvMxArgs &a, hipStream_t st)
+{
+    const size_t lds = (size_t)2 * KQ * NP * TAB_CHUNK + TAB_ZERO + TILES * KQ * 16 * 4;
+    hipLaunchKernelGGL((k_gemv_px8<FMT, NP, KQ, TILES>), dim3((unsigned)(a.rows / (8 * TILES))),
+                       dim3(64 * KQ * TILES), lds, st, a);
+    return hipGetLastError();
+}
+
+/* One token, FP8, rows in whole 16-row groups, scale blocks whole 8-row
+ * tiles, 1024 / 2048 / 4096 columns: the 8-row chunk-pair matvec, two tiles
+ * x four quarters of K per workgroup (measured on 4096 x 4096: 5.2 us,
+ * against 5.4-5.7 for one tile per workgroup, eight waves per tile or two
+ * quarters). */
+template <int FMT>
+hipError_t gemv_px8_fmt(const GemvMxArgs &a, hipStream_t st)
+{
+    switch (a.cols) {
+    case 1024: return gemv_px8_k<FMT, 1, 4, 2>(a, st);
+    case 2048: return gemv_px8_k<FMT, 2, 4, 2>(a, st);
+    default: return gemv_px8_k<FMT, 4, 4, 2>(a, st);
+    }
+}
+
+static bool gemv_px8_ok(int fmt, const GemvMxArgs &a)
+{
+    return (fmt == FMT_FP8_E8M0 || fmt == FMT_FP8_F32S) && a.nt == 1 && a.rows % 16 == 0 &&
+           a.blk_r % 8 == 0 && a.row_bytes == a.cols && (a.cols == 1024 || a.cols == 2048 || a.cols == 4096);
+}
+
 hipError_t gemv_mx_launch(int fmt, GemvMxArgs a, hipStream_t st)
 {
     a.ncw = gemv_mx_ncw(fmt, a.cols);
     if (!a.ncw || a.nt <= 0) return hipErrorInvalidValue;
+    if (gemv_px8_ok(fmt, a))
+        return fmt == FMT_FP8_E8M0 ? gemv_px8_fmt<FMT_FP8_E8M0>(a, st) : gemv_px8_fmt<FMT_FP8_F32S>(a, st);
     switch (fmt) {
     case FMT_FP8_E8M0: return gemv_mx_fmt<FMT_FP8_E8M0>(a, st);
     case FMT_FP8_F32S: return gemv_mx_fmt<FMT_FP8_F32S>(a, st);

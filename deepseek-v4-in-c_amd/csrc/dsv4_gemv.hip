@@ -125,10 +125,14 @@ static hipError_t launch_fmt(const GemvArgs &a, hipStream_t st)
 
 /* ------------------------------------------------------------- BF16 --- */
 
-/* One wave per ROWS rows: the rows go to LDS once, then every token's dot
- * products. ROWS x (1 KiB KCH + 64) bytes of LDS (64: a bank offset between
- * rows). */
+/* One wave per ROWS rows: the rows go to LDS once, then for every token its
+ * x goes to LDS and the rows' dot products run from there. ROWS x (1 KiB KCH
+ * + 64) bytes of rows (64: a bank offset between rows), then up to 2 KiB
+ * KCH of x. */
 constexpr int BF16_PAD = 64;
+template <int KCH, int ROWS>
+__host__ __device__ constexpr size_t bf16_gemv_lds() { return (size_t)ROWS * (KCH * 1024 + BF16_PAD) + 2048 * KCH; }
+
 template <int KCH, int ROWS>
 __global__ __launch_bounds__(64) void k_gemv_bf16(GemvBf16Args a)
 {
@@ -136,22 +140,24 @@ __global__ __launch_bounds__(64) void k_gemv_bf16(GemvBf16Args a)
     const int lane = threadIdx.x;
     const int r0 = blockIdx.x * ROWS;
     constexpr int STRIDE = KCH * 1024 + BF16_PAD;
+    uint8_t *xl = lds + ROWS * STRIDE;
     bf16_rows_to_lds<KCH>(lds, STRIDE, a.W, r0, ROWS, a.rows - r0, 2 * a.cols, lane);
-    __builtin_amdgcn_s_waitcnt(0x0F70);              /* vmcnt(0): the rows landed */
-    asm volatile("" ::: "memory");
     const int r = lane >> 4;
-    if (r >= ROWS) return;
-    const uint16_t *wl = (const uint16_t *)(lds + r * STRIDE);
+    const uint16_t *wl = (const uint16_t *)(lds + (r < ROWS ? r : 0) * STRIDE);
     for (int t = 0; t < a.nt; t++) {
-        const double acc = bf16_row_dot(wl, a.x + (size_t)t * a.x_ld, a.cols, lane);
-        if ((lane & 15) == 0 && r0 + r < a.rows) a.y[(size_t)t * a.y_ld + r0 + r] = (float)acc;
+        /* a single wave: its reads of the previous token's x are done */
+        bf16_x_to_lds(xl, a.x + (size_t)t * a.x_ld, a.cols, lane);
+        __builtin_amdgcn_s_waitcnt(0x0F70);          /* vmcnt(0): rows and x landed */
+        asm volatile("" ::: "memory");
+        const double acc = bf16_row_dot(wl, (const float *)xl, a.cols, lane);
+        if (r < ROWS && (lane & 15) == 0 && r0 + r < a.rows) a.y[(size_t)t * a.y_ld + r0 + r] = (float)acc;
     }
 }
 
 template <int KCH, int ROWS>
 static hipError_t launch_bf16_k(const GemvBf16Args &a, hipStream_t st)
 {
-    constexpr size_t lds = (size_t)ROWS * (KCH * 1024 + BF16_PAD);
+    constexpr size_t lds = bf16_gemv_lds<KCH, ROWS>();
     if constexpr (lds > 64 * 1024) {
         /* set once (not inside a stream capture of a later call) */
         static bool set = false;

@@ -268,15 +268,17 @@ __global__ __launch_bounds__(64) void k_gate_route_bf16(GateRouteArgs a)
 {
     __shared__ unsigned s_old;
     __shared__ __align__(16) uint8_t wrow[KCH * 1024];
+    __shared__ __align__(16) uint8_t xl[KCH * 2048];
     const int r = wave_id();
     const int ne = a.n_experts;
     const int lane = threadIdx.x & 63;
     if (r < ne) {
-        /* the row into LDS, then bf16_n's 16 FMA chains in lanes 0-15 */
+        /* the row and x into LDS, then bf16_n's 16 FMA chains in lanes 0-15 */
         bf16_rows_to_lds<KCH>(wrow, 0, a.gate_w, r, 1, 1, 2 * a.cols, lane);
-        __builtin_amdgcn_s_waitcnt(0x0F70);         /* vmcnt(0): the row landed */
+        bf16_x_to_lds(xl, a.x, a.cols, lane);
+        __builtin_amdgcn_s_waitcnt(0x0F70);         /* vmcnt(0): row and x landed */
         asm volatile("" ::: "memory");
-        const double acc = bf16_row_dot((const uint16_t *)wrow, a.x, a.cols, lane);
+        const double acc = bf16_row_dot((const uint16_t *)wrow, (const float *)xl, a.cols, lane);
         if (lane == 0) {
             const float s = (float)acc;
             const float o = route_orig(s);

@@ -188,7 +188,8 @@ def _rand_fp8(rng, n):
 
 @pytest.mark.parametrize("rows,cols,nt,blk_r", [
     (4096, 4096, 1, 128), (1024, 4096, 2, 128), (37, 384, 3, 128), (130, 256, 1, 128),
-    (2048, 2048, 1, 128), (100, 1024, 1, 1), (9, 3072, 1, 128)])
+    (2048, 2048, 1, 128), (100, 1024, 1, 1), (9, 3072, 1, 128),
+    (1024, 1024, 1, 16), (64, 4096, 1, 8), (48, 2048, 1, 24)])
 def test_fp8_e8m0_gemv(lib, pkg, oracle, rows, cols, nt, blk_r):
     rng = np.random.default_rng(rows * 7 + cols)
     W = _rand_fp8(rng, rows * cols)
