@@ -153,6 +153,134 @@ def make_shared_fp8(torch, pkg, lib, seed):
     return pkg.ExpertW(q[0], q[1], q[2]), keep
 
 
+class DecodeLayer:
+    """The matrices of one decode layer at DeepSeek-V4-Flash shapes
+    (src/00_base/dsv4_weights.h:44-112), run on the device in the order
+    src/70_decode/dsv4_layer_attn.c:21-106 and dsv4_layer.c:52-116 call
+    dsv4_mmq: wq_a, wq_b, wkv, the compressor's wkv and wgate (BF16, ratio-4
+    layer), the indexer's wq_b and weights_proj (BF16), the eight wo_a group
+    slices of one [8192 x 4096] arena (dsv4_wo_a_group), wo_b [4096 x 8192],
+    then the MoE block (dsv4_hip_moe_layer_dev: BF16 gate 256 x 4096, the
+    router with a bias, six of the 256 FP4 experts, the FP8 shared expert).
+    FP8 matrices carry E8M0 128 x 128 scales as the checkpoint's do. The
+    steps between the matrices (norms, RoPE, the compressor's pooling, the
+    indexer's scores, sparse attention) are not on the matmul path and are
+    left out: a matrix takes the previous one's output where the layer
+    feeds it one (qr into wq_b and the indexer's wq_b; the attention output,
+    here q itself, 64 heads x 512, into wo_a; the group outputs into wo_b;
+    wo_b's output into the MoE block), else x."""
+
+    FP8 = (("wq_a", 1024, 4096, "x"), ("wq_b", 32768, 1024, "qr"), ("wkv", 512, 4096, "x"),
+           ("idx_wq_b", 8192, 1024, "qr"))
+    BF16 = (("comp_wkv", 1024, 4096), ("comp_wgate", 1024, 4096), ("idx_wproj", 64, 4096),
+            ("gate", N_EXPERTS, HIDDEN))
+
+    def __init__(self, torch, pkg, lib, arena, seed):
+        dev = "cuda:0"
+        self.arena = arena
+        self.keep = {}
+        self.desc = {}
+        tmp = torch.empty(8192 * 4096, dtype=torch.float32, device=dev)
+
+        def fp8(name, r, c, sd):
+            W = torch.empty(r * c, dtype=torch.uint8, device=dev)
+            S32 = torch.empty((r // 128) * (c // 128), dtype=torch.float32, device=dev)
+            lib.synth_normal_dev(tmp.data_ptr(), r * c, sd, 0.02)
+            lib.quant_fp8_blk128_dev(W.data_ptr(), S32.data_ptr(), tmp.data_ptr(), r, c)
+            S = torch.clamp(torch.ceil(torch.log2(S32)) + 127, 0, 254).to(torch.uint8)
+            self.keep[name] = (W, S)
+            return pkg.qmat(pkg.DSV4_WFP8, W.data_ptr(), S.data_ptr(), r, c, 128, 128)
+
+        for i, (name, r, c, _) in enumerate(self.FP8):
+            self.desc[name] = fp8(name, r, c, seed * 97 + i)
+        self.desc["wo_a"] = fp8("wo_a", 8192, 4096, seed * 97 + 10)
+        self.desc["wo_b"] = fp8("wo_b", 4096, 8192, seed * 97 + 11)
+        for i, (name, r, c) in enumerate(self.BF16):
+            lib.synth_normal_dev(tmp.data_ptr(), r * c, seed * 97 + 20 + i, 0.02)
+            W = tmp[:r * c].bfloat16()
+            self.keep[name] = (W, None)
+            self.desc[name] = pkg.qmat(pkg.DSV4_WBF16, W.data_ptr(), None, r, c, 0, 0)
+        W, S = self.keep["wo_a"]
+        self.slices = [pkg.qmat(pkg.DSV4_WFP8, W.data_ptr() + g * 1024 * 4096, S.data_ptr() + g * 8 * 32,
+                                1024, 4096, 128, 128) for g in range(8)]
+        self.bias = torch.empty(N_EXPERTS, dtype=torch.float32, device=dev)
+        lib.synth_normal_dev(self.bias.data_ptr(), N_EXPERTS, seed * 97 + 30, 0.05)
+        self.shared, self.skeep = make_shared_fp8(torch, pkg, lib, seed * 97 + 31)
+        f = lambda n: torch.empty(n, dtype=torch.float32, device=dev)
+        self.out = {"qr": f(1024), "q": f(32768), "kv": f(512), "comp_kv": f(1024), "comp_sc": f(1024),
+                    "idx_q": f(8192), "idx_w": f(64), "ogrp": f(8192), "attn": f(HIDDEN), "moe": f(HIDDEN)}
+        self.idx = torch.empty(TOPK, dtype=torch.int32, device=dev)
+        self.w = torch.empty(TOPK, dtype=torch.float32, device=dev)
+        torch.cuda.synchronize()
+        del tmp
+
+    # bytes one token reads: every matrix once, the six routed experts
+    def bytes_per_token(self):
+        b = sum(r * c + (r // 128) * (c // 128) for _, r, c, _ in self.FP8)
+        b += 2 * (8192 * 4096 + 32 * 32 * 2)
+        b += sum(2 * r * c for _, r, c in self.BF16)
+        return b + TOPK * EXPERT_BYTES + SHARED_BYTES
+
+    def run(self, lib, x_ptr, sp):
+        """Enqueue the layer's matrices for the token at x_ptr on stream sp."""
+        o = self.out
+        mm = lambda y, x, name: lib.mmq_n_dev(o[y].data_ptr(), x, self.desc[name], 1, sp)
+        mm("qr", x_ptr, "wq_a")
+        mm("q", o["qr"].data_ptr(), "wq_b")
+        mm("kv", x_ptr, "wkv")
+        mm("comp_kv", x_ptr, "comp_wkv")
+        mm("comp_sc", x_ptr, "comp_wgate")
+        mm("idx_q", o["qr"].data_ptr(), "idx_wq_b")
+        mm("idx_w", x_ptr, "idx_wproj")
+        for g in range(8):
+            lib.mmq_n_dev(o["ogrp"].data_ptr() + 4 * 1024 * g, o["q"].data_ptr() + 4 * 4096 * g,
+                          self.slices[g], 1, sp)
+        mm("attn", o["ogrp"].data_ptr(), "wo_b")
+        lib.moe_layer_dev(o["moe"].data_ptr(), o["attn"].data_ptr(), self.desc["gate"],
+                          self.arena.table.data_ptr(), N_EXPERTS, TOPK, 2.5, self.shared, HIDDEN, INTER,
+                          10.0, bias_ptr=self.bias.data_ptr(), idx_ptr=self.idx.data_ptr(),
+                          w_ptr=self.w.data_ptr(), stream=sp)
+
+
+def bench_decode_layer(torch, pkg, lib, arena, xs, n_layers=4, graph_calls=16, reps=8):
+    """One decode layer's whole matrix chain per token (DecodeLayer), replayed
+    from a HIP graph of graph_calls tokens that cycle through n_layers layers
+    with their own weights (so the attention matrices, 129 MB a layer, do not
+    stay in the 256 MB memory-side cache between a layer's tokens), each
+    token its own x and so its own experts."""
+    layers = [DecodeLayer(torch, pkg, lib, arena, 0xDEC0 + i) for i in range(n_layers)]
+    n_x = xs.numel() // HIDDEN
+    st = torch.cuda.Stream()
+    ss = st.cuda_stream
+
+    def token(i):
+        layers[i % n_layers].run(lib, xs.data_ptr() + 4 * HIDDEN * (i % n_x), ss)
+
+    torch.cuda.synchronize()
+    with torch.cuda.stream(st):
+        for i in range(2 * n_layers):
+            token(i)
+        torch.cuda.synchronize()
+        assert lib.status() == 0
+        eager = time_events(torch, st, token, graph_calls)
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g, stream=st):
+            for i in range(graph_calls):
+                token(i)
+        torch.cuda.synchronize()
+        g.replay()                                   # replays go to the current stream, st
+        torch.cuda.synchronize()
+        per_tok = time_events(torch, st, lambda i: g.replay(), reps) / graph_calls
+    assert lib.status() == 0
+    nb = layers[0].bytes_per_token()
+    return {"entry": "one decode layer's matrices: 8 FP8 projections incl. 8 wo_a slices and wo_b, "
+                     "4 BF16 matrices, then dsv4_hip_moe_layer_dev with the FP8 shared expert",
+            "bytes_per_token": nb, "layers_cycled": n_layers,
+            "eager_us": round(eager * 1e6, 3), "graph_us": round(per_tok * 1e6, 3),
+            "graph_GBs": round(nb / per_tok / 1e9, 1),
+            "graph_hbm_frac": round(nb / per_tok / 1e9 / HBM_PEAK_GBS, 4)}
+
+
 def time_events(torch, stream, fn, n):
     """Average duration of one fn() call over n calls enqueued back to back on
     `stream` (the stream the kernels are launched on), from one pair of HIP
@@ -855,6 +983,7 @@ def main():
         t_launch_dev = time_events(torch, stream, lambda i: step_dev(W + K + i), K)
         assert lib.status() == 0
         layer = bench_layer(torch, pkg, lib, arena, xs, K, W)
+        dlayer = bench_decode_layer(torch, pkg, lib, arena, xs)
         bytes_step = TOPK * EXPERT_BYTES + 8192 + 16384
         value = bytes_step / t_step / 1e9
         achieved = bytes_step / t_launch / 1e9
@@ -894,6 +1023,7 @@ def main():
                               "value": round(bytes_step / t_step_dev / 1e9, 2),
                               "launch_us": round(t_launch_dev * 1e6, 3)},
             "moe_layer": layer,
+            "decode_layer": dlayer,
             "cpu_baseline": cpu,
             "wall_s": round(wall, 4),
         }
