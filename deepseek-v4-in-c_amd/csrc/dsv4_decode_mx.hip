@@ -1933,17 +1933,21 @@ hipError_t gemv_px8_k(const GemvMxArgs &a, hipStream_t st)
 }
 
 /* One token, FP8, rows in whole 16-row groups, scale blocks whole 8-row
- * tiles, 1024 / 2048 / 4096 columns: the 8-row chunk-pair matvec, two tiles
- * x four quarters of K per workgroup (measured on 4096 x 4096: 5.2 us,
- * against 5.4-5.7 for one tile per workgroup, eight waves per tile or two
- * quarters). */
+ * tiles, 1024 / 2048 / 4096 columns: the 8-row chunk-pair matvec. Waves per
+ * tile (KQ) and tiles per workgroup by shape, as measured (us per call,
+ * weights cold): 4096 x 4096 two tiles x four quarters 5.2 (one tile x eight
+ * 5.4); 1024 x 4096 one tile x eight 3.5 (two x four 4.6); 4096 x 2048 one
+ * tile x four 3.6; 8192 x 1024 one tile x two 3.6; 32768 x 1024 two tiles x
+ * two 8.5. */
 template <int FMT>
 hipError_t gemv_px8_fmt(const GemvMxArgs &a, hipStream_t st)
 {
     switch (a.cols) {
-    case 1024: return gemv_px8_k<FMT, 1, 4, 2>(a, st);
-    case 2048: return gemv_px8_k<FMT, 2, 4, 2>(a, st);
-    default: return gemv_px8_k<FMT, 4, 4, 2>(a, st);
+    case 1024:
+        return a.rows >= 16384 ? gemv_px8_k<FMT, 2, 2, 2>(a, st) : gemv_px8_k<FMT, 2, 2, 1>(a, st);
+    case 2048: return gemv_px8_k<FMT, 2, 4, 1>(a, st);
+    default:
+        return a.rows >= 4096 ? gemv_px8_k<FMT, 4, 4, 2>(a, st) : gemv_px8_k<FMT, 2, 8, 1>(a, st);
     }
 }
 
