@@ -1938,7 +1938,8 @@ hipError_t gemv_px8_k(const GemvMxArgs &a, hipStream_t st)
  * weights cold): 4096 x 4096 two tiles x four quarters 5.2 (one tile x eight
  * 5.4); 1024 x 4096 one tile x eight 3.5 (two x four 4.6); 4096 x 2048 one
  * tile x four 3.6; 8192 x 1024 one tile x two 3.6; 32768 x 1024 two tiles x
- * two 8.5. */
+ * two 8.5; 4096 x 8192 two tiles x eight 8.4 (two x four 8.9, the 16-chunk
+ * GEMV 11.7); 1024 x 8192 one tile x eight 5.3. */
 template <int FMT>
 hipError_t gemv_px8_fmt(const GemvMxArgs &a, hipStream_t st)
 {
@@ -1946,6 +1947,8 @@ hipError_t gemv_px8_fmt(const GemvMxArgs &a, hipStream_t st)
     case 1024:
         return a.rows >= 16384 ? gemv_px8_k<FMT, 2, 2, 2>(a, st) : gemv_px8_k<FMT, 2, 2, 1>(a, st);
     case 2048: return gemv_px8_k<FMT, 2, 4, 1>(a, st);
+    case 8192:
+        return a.rows >= 4096 ? gemv_px8_k<FMT, 4, 8, 2>(a, st) : gemv_px8_k<FMT, 4, 8, 1>(a, st);
     default:
         return a.rows >= 4096 ? gemv_px8_k<FMT, 4, 4, 2>(a, st) : gemv_px8_k<FMT, 2, 8, 1>(a, st);
     }
@@ -1954,7 +1957,8 @@ hipError_t gemv_px8_fmt(const GemvMxArgs &a, hipStream_t st)
 static bool gemv_px8_ok(int fmt, const GemvMxArgs &a)
 {
     return (fmt == FMT_FP8_E8M0 || fmt == FMT_FP8_F32S) && a.nt == 1 && a.rows % 16 == 0 &&
-           a.blk_r % 8 == 0 && a.row_bytes == a.cols && (a.cols == 1024 || a.cols == 2048 || a.cols == 4096);
+           a.blk_r % 8 == 0 && a.row_bytes == a.cols &&
+           (a.cols == 1024 || a.cols == 2048 || a.cols == 4096 || a.cols == 8192);
 }
 
 hipError_t gemv_mx_launch(int fmt, GemvMxArgs a, hipStream_t st)
