@@ -117,10 +117,11 @@ def test_bf16_gemv_special_values(lib, pkg, oracle, rows, cols, nt):
 
 # ------------------------------------------------------- wide FP8 rows ----
 
-@pytest.mark.parametrize("rows,nt", [(4096, 1), (512, 3), (512, 40)])
+@pytest.mark.parametrize("rows,nt", [(4096, 1), (1024, 1), (512, 3), (512, 40)])
 def test_fp8_e8m0_8192_wide_rows(lib, pkg, oracle, rows, nt):
-    """wo_b: FP8 [4096 x 8192] with E8M0 128x128 scales; nt = 1 and 3 take
-    the block-scaled MFMA GEMV with 16 chunks per wave, 40 the fp16 seam."""
+    """wo_b: FP8 [4096 x 8192] with E8M0 128x128 scales; nt = 1 takes the
+    chunk-pair matvec (two or one 8-row tiles per workgroup), nt = 3 the
+    block-scaled MFMA GEMV with 16 chunks per wave, 40 the fp16 seam."""
     cols = 8192
     rng = np.random.default_rng(rows + nt)
     W = e4m3_codes(rng, rows * cols)
