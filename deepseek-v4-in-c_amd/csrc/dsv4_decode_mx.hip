@@ -78,10 +78,11 @@ __device__ uint32_t g_zero_operand[16] = {0, 0, 0, 0, 0, 0, 0, 0, E8M0_ONE, 0, 0
 /* Publication of mid's split tables between the workgroups of one launch,
  * without fences: a writer's stores are device-scope (written through the
  * XCD's L2) and acknowledged (vmcnt) before it adds one to the call's item
- * counter; the writer whose add completes the call stores the call's epoch
- * to a done flag on another cache line. Readers poll only the flag, then read
- * the tables with device-scope loads, which bypass their CU's L1 and their
- * XCD's L2, so a line cached by the previous call is never used. */
+ * counter; the writer whose add completes the call sets a done flag on
+ * another cache line. Readers poll only the flag, then read the tables with
+ * device-scope loads, which bypass their CU's L1 and their XCD's L2, so a
+ * line cached by the previous call is never used. The last workgroup to
+ * leave sets every word back to zero (leave below). */
 __device__ __forceinline__ void st_dev32(void *p, uint32_t v)
 {
     __hip_atomic_store((uint32_t *)p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
