@@ -159,7 +159,9 @@ class DecodeLayer:
     src/70_decode/dsv4_layer_attn.c:21-106 and dsv4_layer.c:52-116 call
     dsv4_mmq: wq_a, wq_b, wkv, the compressor's wkv and wgate (BF16, ratio-4
     layer), the indexer's wq_b and weights_proj (BF16), the eight wo_a group
-    slices of one [8192 x 4096] arena (dsv4_wo_a_group), wo_b [4096 x 8192],
+    slices of one [8192 x 4096] arena (dsv4_wo_a_group) as one multi-job call
+    (dsv4_hip_mmq_multi_dev, as dsv4_prefill_oproj hands them to
+    dsv4_prefill_pm_multi), wo_b [4096 x 8192],
     then the MoE block (dsv4_hip_moe_layer_dev: BF16 gate 256 x 4096, the
     router with a bias, six of the 256 FP4 experts, the FP8 shared expert).
     FP8 matrices carry E8M0 128 x 128 scales as the checkpoint's do. The
@@ -232,9 +234,8 @@ class DecodeLayer:
         mm("comp_sc", x_ptr, "comp_wgate")
         mm("idx_q", o["qr"].data_ptr(), "idx_wq_b")
         mm("idx_w", x_ptr, "idx_wproj")
-        for g in range(8):
-            lib.mmq_n_dev(o["ogrp"].data_ptr() + 4 * 1024 * g, o["q"].data_ptr() + 4 * 4096 * g,
-                          self.slices[g], 1, sp)
+        lib.mmq_multi_dev([(self.slices[g], o["q"].data_ptr() + 4 * 4096 * g, o["ogrp"].data_ptr() + 4 * 1024 * g, 1)
+                           for g in range(8)], sp)
         mm("attn", o["ogrp"].data_ptr(), "wo_b")
         lib.moe_layer_dev(o["moe"].data_ptr(), o["attn"].data_ptr(), self.desc["gate"],
                           self.arena.table.data_ptr(), N_EXPERTS, TOPK, 2.5, self.shared, HIDDEN, INTER,

@@ -40,7 +40,7 @@ EXPORTS = (
     "dsv4_hip_quant_act_mxfp8_dev", "dsv4_hip_synth_normal_dev", "dsv4_hip_moe_route_dev",
     "dsv4_hip_moe_grouped_mx_mid_dev", "dsv4_hip_shared_fp8q_mid_dev",
     "dsv4_hip_route_dev", "dsv4_hip_moe_layer_dev", "dsv4_hip_moe_layer_n_dev",
-    "dsv4_hip_alloc_count",
+    "dsv4_hip_alloc_count", "dsv4_hip_mmq_multi_dev",
 )
 # the reference-named C mirror (host/dsv4_compute_hip.c)
 MIRROR_EXPORTS = ("dsv4_mmq_n", "dsv4_mmq", "dsv4_expert_forward")
@@ -51,6 +51,11 @@ class QMat(C.Structure):
     _fields_ = [("w", C.c_void_p), ("s", C.c_void_p), ("wdt", C.c_int),
                 ("rows", C.c_int), ("cols", C.c_int),
                 ("blk_r", C.c_int), ("blk_c", C.c_int)]
+
+
+class HipJob(C.Structure):
+    """DSV4HipJob: DSV4PMJob's fields (src/80_prefill/dsv4_prefill_int.h:21-28)."""
+    _fields_ = [("m", C.POINTER(QMat)), ("x", C.c_void_p), ("y", C.c_void_p), ("n", C.c_int)]
 
 
 class ExpertW(C.Structure):
@@ -99,6 +104,8 @@ class Lib:
         L.dsv4_hip_mmq.restype = _I; L.dsv4_hip_mmq.argtypes = [_P, _P, C.POINTER(QMat)]
         L.dsv4_hip_mmq_n_dev.restype = _I
         L.dsv4_hip_mmq_n_dev.argtypes = [_P, _P, C.POINTER(QMat), _I, _P]
+        L.dsv4_hip_mmq_multi_dev.restype = _I
+        L.dsv4_hip_mmq_multi_dev.argtypes = [C.POINTER(HipJob), _I, _P]
         L.dsv4_hip_expert_forward.restype = _I
         L.dsv4_hip_expert_forward.argtypes = [_P, _P, C.POINTER(ExpertW), _I, _F]
         L.dsv4_hip_moe_decode.restype = _I
@@ -254,6 +261,16 @@ class Lib:
     def mmq_n_dev(self, y_ptr, x_ptr, desc: QMat, nt, stream=None):
         self.check(self.lib.dsv4_hip_mmq_n_dev(y_ptr, x_ptr, C.byref(desc), nt, stream),
                    "dsv4_hip_mmq_n_dev")
+
+    def mmq_multi_dev_rc(self, jobs, stream=None) -> int:
+        """jobs: (QMat, x_ptr, y_ptr, n) tuples; returns the C return code. The
+        descriptors must stay alive until the call returns."""
+        descs = [d for d, _, _, _ in jobs]
+        arr = (HipJob * max(1, len(jobs)))(*[HipJob(C.pointer(d), x, y, n) for d, (_, x, y, n) in zip(descs, jobs)])
+        return self.lib.dsv4_hip_mmq_multi_dev(arr, len(jobs), stream)
+
+    def mmq_multi_dev(self, jobs, stream=None):
+        self.check(self.mmq_multi_dev_rc(jobs, stream), "dsv4_hip_mmq_multi_dev")
 
     def moe_decode_dev(self, out_ptr, x_ptr, table_ptr, n_experts, idx_ptr, w_ptr, topk,
                        shared: ExpertW | None, hidden, inter, limit, stream=None):

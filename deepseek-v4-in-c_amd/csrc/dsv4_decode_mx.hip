@@ -50,6 +50,7 @@
 #include "dsv4_internal.h"
 
 #include <algorithm>
+#include <cstring>
 
 namespace dsv4 {
 
@@ -1250,9 +1251,10 @@ __global__ __launch_bounds__(512) void k_gateup_px8(GateUpMxArgs a)
 
 /* One-token FP8 matvec in the same 8-row chunk-pair tiles: one workgroup per
  * TILES 8-row tiles, KQ waves per tile each over NP chunk pairs (cols =
- * 256 KQ NP), every workgroup splitting x once into LDS. */
+ * 256 KQ NP), every workgroup splitting x once into LDS. blk: the
+ * workgroup's tile group within the matrix. */
 template <int FMT, int NP, int KQ, int TILES>
-__global__ __launch_bounds__(64 * KQ * TILES) void k_gemv_px8(GemvMxArgs a)
+__device__ __forceinline__ void gemv_px8_body(const GemvMxArgs &a, int blk)
 {
     extern __shared__ __align__(16) uint8_t lds[];
     constexpr int NC = 2 * KQ * NP;
@@ -1261,7 +1263,7 @@ __global__ __launch_bounds__(64 * KQ * TILES) void k_gemv_px8(GemvMxArgs a)
     const int lane = threadIdx.x & 63;
     const int wave = wave_in_group();
     const int h = wave / KQ, kq = wave % KQ;
-    const int r0 = blockIdx.x * 8 * TILES + 8 * h;
+    const int r0 = blk * 8 * TILES + 8 * h;
     const int c0 = kq * 2 * NP;
     uint8_t *tab = lds;
     float *red = (float *)(lds + NC * TAB_CHUNK + TAB_ZERO);   /* [TILES][KQ][16] */
@@ -1284,8 +1286,30 @@ __global__ __launch_bounds__(64 * KQ * TILES) void k_gemv_px8(GemvMxArgs a)
         float s = 0.0f;
 #pragma unroll
         for (int k = 0; k < KQ; k++) s += red[(hh * KQ + k) * 16 + rr] + red[(hh * KQ + k) * 16 + 8 + rr];
-        a.y[blockIdx.x * 8 * TILES + threadIdx.x] = s;
+        a.y[blk * 8 * TILES + threadIdx.x] = s;
     }
+}
+
+template <int FMT, int NP, int KQ, int TILES>
+__global__ __launch_bounds__(64 * KQ * TILES) void k_gemv_px8(GemvMxArgs a)
+{
+    gemv_px8_body<FMT, NP, KQ, TILES>(a, (int)blockIdx.x);
+}
+
+/* Several one-token matvecs of one geometry class in one launch (the jobs of
+ * a multi-job projection): job j owns workgroups first[j] .. first[j + 1] - 1. */
+struct Px8Jobs {
+    GemvMxArgs job[PX8_MAX_JOBS];
+    int first[PX8_MAX_JOBS + 1];
+    int nj;
+};
+
+template <int FMT, int NP, int KQ, int TILES>
+__global__ __launch_bounds__(64 * KQ * TILES) void k_gemv_px8_multi(Px8Jobs m)
+{
+    int j = 0;
+    while (j + 1 < m.nj && (int)blockIdx.x >= m.first[j + 1]) j++;
+    gemv_px8_body<FMT, NP, KQ, TILES>(m.job[j], (int)blockIdx.x - m.first[j]);
 }
 
 /* Routed FP4 down projections (inter = 256 NP) with the k-order combine. One
@@ -1925,41 +1949,71 @@ int gateup_mx_ncw(int fmt, int cols)
 size_t mx_split_bytes(int inter) { return (size_t)(inter / 128) * MTAB_CHUNK; }
 
 template <int FMT, int NP, int KQ, int TILES>
-hipError_t gemv_px8_k(const GemvMxArgs &a, hipStream_t st)
+hipError_t gemv_px8_k(const GemvMxArgs *jobs, int nj, hipStream_t st)
 {
     const size_t lds = (size_t)2 * KQ * NP * TAB_CHUNK + TAB_ZERO + TILES * KQ * 16 * 4;
-    hipLaunchKernelGGL((k_gemv_px8<FMT, NP, KQ, TILES>), dim3((unsigned)(a.rows / (8 * TILES))),
-                       dim3(64 * KQ * TILES), lds, st, a);
+    if (nj == 1) {
+        hipLaunchKernelGGL((k_gemv_px8<FMT, NP, KQ, TILES>), dim3((unsigned)(jobs[0].rows / (8 * TILES))),
+                           dim3(64 * KQ * TILES), lds, st, jobs[0]);
+        return hipGetLastError();
+    }
+    Px8Jobs m;
+    memset(&m, 0, sizeof m);
+    m.nj = nj;
+    for (int j = 0; j < nj; j++) {
+        m.job[j] = jobs[j];
+        m.first[j + 1] = m.first[j] + jobs[j].rows / (8 * TILES);
+    }
+    hipLaunchKernelGGL((k_gemv_px8_multi<FMT, NP, KQ, TILES>), dim3((unsigned)m.first[nj]), dim3(64 * KQ * TILES),
+                       lds, st, m);
     return hipGetLastError();
 }
 
 /* One token, FP8, rows in whole 16-row groups, scale blocks whole 8-row
- * tiles, 1024 / 2048 / 4096 columns: the 8-row chunk-pair matvec. Waves per
- * tile (KQ) and tiles per workgroup by shape, as measured (us per call,
- * weights cold): 4096 x 4096 two tiles x four quarters 5.2 (one tile x eight
- * 5.4); 1024 x 4096 one tile x eight 3.5 (two x four 4.6); 4096 x 2048 one
- * tile x four 3.6; 8192 x 1024 one tile x two 3.6; 32768 x 1024 two tiles x
- * two 8.5; 4096 x 8192 two tiles x eight 8.4 (two x four 8.9, the 16-chunk
- * GEMV 11.7); 1024 x 8192 one tile x eight 5.3. */
+ * tiles, 1024 / 2048 / 4096 / 8192 columns: the 8-row chunk-pair matvec.
+ * Waves per tile (KQ) and tiles per workgroup by the matrix's shape (the
+ * jobs of one launch share it, so each job's bits are its single call's),
+ * as measured (us per call, weights cold): 4096 x 4096
+ * two tiles x four quarters 5.2 (one tile x eight 5.4); 1024 x 4096 one tile
+ * x eight 3.5 (two x four 4.6); 4096 x 2048 one tile x four 3.6; 8192 x 1024
+ * one tile x two 3.6; 32768 x 1024 two tiles x two 8.5; 4096 x 8192 two
+ * tiles x eight 8.4 (two x four 8.9, the 16-chunk GEMV 11.7); 1024 x 8192
+ * one tile x eight 5.3. */
 template <int FMT>
-hipError_t gemv_px8_fmt(const GemvMxArgs &a, hipStream_t st)
+hipError_t gemv_px8_fmt(const GemvMxArgs *jobs, int nj, hipStream_t st)
 {
-    switch (a.cols) {
+    const int rows = jobs[0].rows;
+    switch (jobs[0].cols) {
     case 1024:
-        return a.rows >= 16384 ? gemv_px8_k<FMT, 2, 2, 2>(a, st) : gemv_px8_k<FMT, 2, 2, 1>(a, st);
-    case 2048: return gemv_px8_k<FMT, 2, 4, 1>(a, st);
+        return rows >= 16384 ? gemv_px8_k<FMT, 2, 2, 2>(jobs, nj, st) : gemv_px8_k<FMT, 2, 2, 1>(jobs, nj, st);
+    case 2048: return gemv_px8_k<FMT, 2, 4, 1>(jobs, nj, st);
     case 8192:
-        return a.rows >= 4096 ? gemv_px8_k<FMT, 4, 8, 2>(a, st) : gemv_px8_k<FMT, 4, 8, 1>(a, st);
+        return rows >= 4096 ? gemv_px8_k<FMT, 4, 8, 2>(jobs, nj, st) : gemv_px8_k<FMT, 4, 8, 1>(jobs, nj, st);
     default:
-        return a.rows >= 4096 ? gemv_px8_k<FMT, 4, 4, 2>(a, st) : gemv_px8_k<FMT, 2, 8, 1>(a, st);
+        return rows >= 4096 ? gemv_px8_k<FMT, 4, 4, 2>(jobs, nj, st) : gemv_px8_k<FMT, 2, 8, 1>(jobs, nj, st);
     }
 }
 
-static bool gemv_px8_ok(int fmt, const GemvMxArgs &a)
+bool gemv_px8_ok(int fmt, const GemvMxArgs &a)
 {
     return (fmt == FMT_FP8_E8M0 || fmt == FMT_FP8_F32S) && a.nt == 1 && a.rows % 16 == 0 &&
            a.blk_r % 8 == 0 && a.row_bytes == a.cols &&
            (a.cols == 1024 || a.cols == 2048 || a.cols == 4096 || a.cols == 8192);
+}
+
+int gemv_px8_class(const GemvMxArgs &a)
+{
+    const bool big = a.cols == 1024 ? a.rows >= 16384 : a.cols == 2048 ? false : a.rows >= 4096;
+    return a.cols * 2 + (big ? 1 : 0);
+}
+
+hipError_t gemv_px8_multi_launch(int fmt, const GemvMxArgs *jobs, int nj, hipStream_t st)
+{
+    if (nj < 1 || nj > PX8_MAX_JOBS) return hipErrorInvalidValue;
+    for (int j = 0; j < nj; j++)
+        if (!gemv_px8_ok(fmt, jobs[j]) || gemv_px8_class(jobs[j]) != gemv_px8_class(jobs[0]))
+            return hipErrorInvalidValue;
+    return fmt == FMT_FP8_E8M0 ? gemv_px8_fmt<FMT_FP8_E8M0>(jobs, nj, st) : gemv_px8_fmt<FMT_FP8_F32S>(jobs, nj, st);
 }
 
 hipError_t gemv_mx_launch(int fmt, GemvMxArgs a, hipStream_t st)
@@ -1967,7 +2021,7 @@ hipError_t gemv_mx_launch(int fmt, GemvMxArgs a, hipStream_t st)
     a.ncw = gemv_mx_ncw(fmt, a.cols);
     if (!a.ncw || a.nt <= 0) return hipErrorInvalidValue;
     if (gemv_px8_ok(fmt, a))
-        return fmt == FMT_FP8_E8M0 ? gemv_px8_fmt<FMT_FP8_E8M0>(a, st) : gemv_px8_fmt<FMT_FP8_F32S>(a, st);
+        return fmt == FMT_FP8_E8M0 ? gemv_px8_fmt<FMT_FP8_E8M0>(&a, 1, st) : gemv_px8_fmt<FMT_FP8_F32S>(&a, 1, st);
     switch (fmt) {
     case FMT_FP8_E8M0: return gemv_mx_fmt<FMT_FP8_E8M0>(a, st);
     case FMT_FP8_F32S: return gemv_mx_fmt<FMT_FP8_F32S>(a, st);

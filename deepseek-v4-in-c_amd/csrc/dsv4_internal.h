@@ -153,6 +153,13 @@ int gemv_mx_ncw(int fmt, int cols);
 /* the same for the gate/up kernels (FP8 hidden at most 4096) */
 int gateup_mx_ncw(int fmt, int cols);
 hipError_t gemv_mx_launch(int fmt, GemvMxArgs a, hipStream_t st);
+/* whether a one-token FP8 matvec takes the chunk-pair kernel, which can run
+ * up to PX8_MAX_JOBS such matvecs of the same format and width in one launch */
+constexpr int PX8_MAX_JOBS = 16;
+bool gemv_px8_ok(int fmt, const GemvMxArgs &a);
+/* the launch shape class of such a matvec: one launch takes one class */
+int gemv_px8_class(const GemvMxArgs &a);
+hipError_t gemv_px8_multi_launch(int fmt, const GemvMxArgs *jobs, int nj, hipStream_t st);
 
 /* Routed experts whose descriptors travel by value in the kernel arguments
  * (routing known on the host): at most this many slots. */

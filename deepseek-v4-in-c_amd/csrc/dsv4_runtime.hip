@@ -753,6 +753,57 @@ int dsv4_hip_mmq_n_dev(float *y, const float *x, const DSV4QMat *m, int nt,
     return enqueue_mmq(*m, fmt, x, y, nt, (hipStream_t)stream);
 }
 
+int dsv4_hip_mmq_multi_dev(const DSV4HipJob *jobs, int njobs, void *stream)
+{
+    std::lock_guard<std::mutex> lk(g.mu);
+    Range rg("dsv4_hip_mmq_multi_dev");
+    if (usable()) return -1;
+    if (njobs < 0 || (njobs > 0 && !jobs)) return fail("mmq_multi_dev: %d jobs at %p", njobs, (const void *)jobs);
+    std::vector<int> fmts((size_t)njobs, 0);
+    for (int j = 0; j < njobs; j++) {
+        const DSV4HipJob &jb = jobs[j];
+        if (jb.n < 0) return fail("mmq_multi_dev: job %d has n = %d", j, jb.n);
+        if (jb.n == 0) continue;
+        if (check_qmat(jb.m, "mmq_multi_dev", &fmts[j])) return -1;
+        if (!jb.x || !jb.y || !jb.m->w || (fmts[j] != FMT_BF16 && !jb.m->s))
+            return fail("mmq_multi_dev: job %d has a NULL pointer", j);
+        if (!aligned16(jb.x) || !aligned16(jb.m->w))
+            return fail("mmq_multi_dev: job %d: x and W must be 16-byte aligned", j);
+    }
+    dev_call();
+    const hipStream_t st = (hipStream_t)stream;
+    /* one-token FP8 jobs that take the chunk-pair matvec, by format and launch
+     * shape class, at most PX8_MAX_JOBS a launch; everything else one call
+     * each */
+    std::vector<GemvMxArgs> batch;
+    std::vector<int> taken((size_t)njobs, 0);
+    for (int j = 0; j < njobs; j++) {
+        if (jobs[j].n == 0 || taken[j]) continue;
+        const DSV4QMat &m = *jobs[j].m;
+        /* the scale grid's width is only defined for the packed formats */
+        const bool fp8 = fmts[j] == FMT_FP8_E8M0 || fmts[j] == FMT_FP8_F32S;
+        const GemvMxArgs aj = fp8 ? gemv_mx_args(m, jobs[j].x, jobs[j].y, 1) : GemvMxArgs{};
+        const bool pair = fp8 && jobs[j].n == 1 && mx_gemv_ok(m, fmts[j], jobs[j].x) && gemv_px8_ok(fmts[j], aj);
+        if (!pair) {
+            if (enqueue_mmq(m, fmts[j], jobs[j].x, jobs[j].y, jobs[j].n, st)) return -1;
+            taken[j] = 1;
+            continue;
+        }
+        batch.clear();
+        for (int k = j; k < njobs && (int)batch.size() < PX8_MAX_JOBS; k++) {
+            if (taken[k] || jobs[k].n != 1 || fmts[k] != fmts[j]) continue;   /* fmts[j] is FP8 */
+            GemvMxArgs ak = gemv_mx_args(*jobs[k].m, jobs[k].x, jobs[k].y, 1);
+            if (!mx_gemv_ok(*jobs[k].m, fmts[k], jobs[k].x) || !gemv_px8_ok(fmts[k], ak) ||
+                gemv_px8_class(ak) != gemv_px8_class(aj))
+                continue;
+            batch.push_back(ak);
+            taken[k] = 1;
+        }
+        HIPCHK(gemv_px8_multi_launch(fmts[j], batch.data(), (int)batch.size(), st), "multi-job matvec launch");
+    }
+    return 0;
+}
+
 int dsv4_hip_expert_forward(float *out, const float *x, const DSV4ExpertW *e,
                             int inter, float limit)
 {

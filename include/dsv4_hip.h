@@ -110,6 +110,24 @@ int  dsv4_hip_mmq(float *y, const float *x, const DSV4QMat *m);
 int  dsv4_hip_mmq_n_dev(float *y, const float *x, const DSV4QMat *m, int nt,
                         void *stream);
 
+/* One job of the batched-matmul seam: DSV4PMJob's fields
+ * (src/80_prefill/dsv4_prefill_int.h:21-28), device pointers. */
+typedef struct {
+    const DSV4QMat *m;
+    const float    *x;
+    float          *y;
+    int             n;
+} DSV4HipJob;
+
+/* dsv4_prefill_pm_multi (src/80_prefill/dsv4_prefill_proj.c:17-27) on the
+ * device: y_j = W_j . x_j over n_j tokens for every job (n_j = 0: nothing),
+ * the same bits as one dsv4_hip_mmq_n_dev per job. One-token FP8 jobs of one
+ * format and width share one launch (the grouped output projection's eight
+ * wo_a slices); other jobs run one after another on `stream`. Every job is
+ * checked before anything is enqueued: -1 with the reason and nothing
+ * enqueued when one is refused. */
+int  dsv4_hip_mmq_multi_dev(const DSV4HipJob *jobs, int njobs, void *stream);
+
 /* -------------------------------------------- expert FFN ----------------
  * out = w2 . swiglu(w1 . x, w3 . x) for one token, SwiGLU with the
  * reference's asymmetric clamp (src/10_compute/dsv4_ops.c:61-79; limit <= 0

@@ -135,3 +135,50 @@ def test_bf16_head_full_vocabulary(lib, pkg, oracle):
     assert lib.status() == 0
     W16 = W.view(torch.int16).cpu().numpy().view(np.uint16)
     check_bf16(y.cpu().numpy(), oracle.bf16_n(W16, xh, rows, cols))
+
+
+def test_multi_job_seam_matches_single_calls(lib, pkg, oracle):
+    """dsv4_hip_mmq_multi_dev (dsv4_prefill_pm_multi's jobs on the device):
+    the eight wo_a slices of one [8192 x 4096] E8M0 arena in one launch, next
+    to a 4096-row job, a BF16 job, a three-token FP8 job and an empty one --
+    every output bit for bit its single dsv4_hip_mmq_n_dev call's, the
+    slices within 1e-3 of the oracle; a refused job (n < 0) returns -1 and
+    writes nothing."""
+    import bench
+    arena = bench.ExpertArena(torch, pkg, lib, 8, seed=0x3A7E)
+    L = bench.DecodeLayer(torch, pkg, lib, arena, 0x3ADE)
+    hm = _host_mats(L)
+    g = torch.Generator(device=DEV).manual_seed(77)
+    o = torch.randn(32768, generator=g, device=DEV).bfloat16().float()
+    x = torch.randn(4096 * 3, generator=g, device=DEV).bfloat16().float()
+    outs = [torch.full((1024,), float("nan"), device=DEV) for _ in range(8)]
+    y_b = torch.full((4096,), float("nan"), device=DEV)
+    y_bf = torch.full((1024,), float("nan"), device=DEV)
+    y_3 = torch.full((3 * 1024,), float("nan"), device=DEV)
+    jobs = [(L.slices[gi], o.data_ptr() + 4 * 4096 * gi, outs[gi].data_ptr(), 1) for gi in range(8)]
+    shared_w2 = L.shared.w2                                            # FP8 [4096 x 2048], fp32 scales
+    x2 = torch.randn(2048, generator=g, device=DEV)
+    jobs += [(shared_w2, x2.data_ptr(), y_b.data_ptr(), 1),
+             (L.desc["comp_wkv"], x.data_ptr(), y_bf.data_ptr(), 1),
+             (L.desc["wq_a"], x.data_ptr(), y_3.data_ptr(), 3),
+             (L.desc["wkv"], x.data_ptr(), y_b.data_ptr(), 0)]
+    lib.status()
+    lib.mmq_multi_dev(jobs)
+    torch.cuda.synchronize()
+    assert lib.status() == 0
+    got = [t.cpu().numpy().copy() for t in outs + [y_b, y_bf, y_3]]
+    for (d, xp, yp, n), want_t in zip(jobs[:-1], got):
+        single = torch.full((want_t.size,), float("nan"), device=DEV)
+        lib.mmq_n_dev(single.data_ptr(), xp, d, n)
+        torch.cuda.synchronize()
+        assert np.array_equal(bits(single.cpu().numpy()), bits(want_t))
+    oh = o.cpu().numpy()
+    for gi in range(8):
+        check_close(got[gi], oracle.mmq_n(hm["slices"][gi], np.ascontiguousarray(oh[gi * 4096:(gi + 1) * 4096])))
+    # a refused job: nothing enqueued
+    sentinel = torch.full((1024,), 7.0, device=DEV)
+    rc = lib.mmq_multi_dev_rc([(L.slices[0], o.data_ptr(), sentinel.data_ptr(), 1),
+                               (L.slices[1], o.data_ptr(), sentinel.data_ptr(), -1)])
+    torch.cuda.synchronize()
+    assert rc == -1 and "n = -1" in lib.error()
+    assert torch.all(sentinel == 7.0)
