@@ -600,7 +600,8 @@ hipError_t gemm_fp8_launch(const GemmArgs &a, bool w_f32s, bool out_bf16, hipStr
 
 hipError_t gemm_mx_launch(const GemmArgs &a, bool out_bf16, hipStream_t st)
 {
-    if (a.K % GK || a.N % 128 || a.M <= 0 || a.sa_tok != a.K / GK || a.sa_kb != 1)
+    const bool tok_major = a.sa_tok == a.K / GK && a.sa_kb == 1, blk_major = a.sa_tok == 1 && a.sa_kb == a.M;
+    if (a.K % GK || a.N % 128 || a.M <= 0 || !(tok_major || blk_major))
         return hipErrorInvalidValue;
     if ((size_t)a.M * a.K > 0xFFFFFFFFull || (size_t)a.N * a.K > 0xFFFFFFFFull)
         return hipErrorInvalidValue;

@@ -277,8 +277,11 @@ struct GemmArgs {
     int sa_tok, sa_kb;
 };
 hipError_t gemm_fp8_launch(const GemmArgs &a, bool w_f32s, bool out_bf16, hipStream_t st);
-/* The same with E8M0 weight bytes and MXFP8 token scales: Sa holds E8M0 bytes
- * [M][K / 32] (sa_tok = K / 128 dwords per token, sa_kb = 1). */
+/* The same with E8M0 weight bytes and MXFP8 token scales: Sa holds a dword
+ * of four E8M0 bytes per token and 128-wide K block, token-major [M][K / 32]
+ * bytes (sa_tok = K / 128, sa_kb = 1) or block-major (sa_tok = 1, sa_kb = M:
+ * a K block's tokens in one contiguous run, which the workgroup's scale loads
+ * read as whole lines). */
 hipError_t gemm_mx_launch(const GemmArgs &a, bool out_bf16, hipStream_t st);
 
 /* ---------------------------------------------- dequant / quantizers --- */
@@ -296,8 +299,11 @@ hipError_t quant_act_fp8_1x128_launch(uint8_t *Q, float *S, const void *a,
  * SwiGLU(gate, up) over [n][k] fp32 rows (k % 128 == 0). */
 hipError_t swiglu_quant_fp8_launch(uint8_t *Q, float *S, const float *gate, const float *up, int n, int k,
                                    float limit, hipStream_t st);
+/* S token-major [n][k / 32], or block-major [k / 128][n] dwords (the four
+ * scale bytes of a token's 128-wide K block, k % 128 == 0) when s_blk_major */
 hipError_t quant_act_mxfp8_launch(uint8_t *Q, uint8_t *S, const void *a,
-                                  int n, int k, hipStream_t st, bool bf16_in = false);
+                                  int n, int k, hipStream_t st, bool bf16_in = false,
+                                  bool s_blk_major = false);
 hipError_t synth_normal_launch(float *out, size_t n, uint64_t seed, float sigma,
                                int round_bf16, hipStream_t st);
 

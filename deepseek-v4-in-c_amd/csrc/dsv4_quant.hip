@@ -398,7 +398,7 @@ hipError_t quant_act_fp8_1x128_launch(uint8_t *Q, float *S, const void *a,
 
 /* one unit: the group g's four elements v of lane sub (of eight) */
 __device__ __forceinline__ void quant4_mx(const float (&v)[4], long g, int sub, bool live, uint8_t *Q,
-                                          uint8_t *S)
+                                          uint8_t *S, long s_at)
 {
     float amax = 0.0f;
 #pragma unroll
@@ -416,7 +416,7 @@ __device__ __forceinline__ void quant4_mx(const float (&v)[4], long g, int sub, 
     if (!live) return;
     const uint32_t sb = mxfp8_scale_byte(amax);
     const int e = (int)sb - 127;
-    if (sub == 0) S[g] = (uint8_t)sb;
+    if (sub == 0) S[s_at] = (uint8_t)sb;
     /* the hardware convert is the exact rounding below 464 (and NaN is
      * mapped explicitly); an infinity takes the software rounding */
     float x[4];
@@ -438,8 +438,11 @@ __device__ __forceinline__ void quant4_mx(const float (&v)[4], long g, int sub, 
 }
 
 /* eight lanes per 1x32 group (four elements each), so a wave reads one
- * contiguous run of eight groups; fp32 or bf16 (widened exactly) input */
-template <bool BF16_IN>
+ * contiguous run of eight groups; fp32 or bf16 (widened exactly) input.
+ * Scale byte of token m, 32-group j: S[m (k / 32) + j] token-major, or
+ * S[4 (kb n + m) + j % 4] with kb = j / 4 block-major (one dword per token
+ * and 128-wide K block, the K block's tokens contiguous). */
+template <bool BF16_IN, bool BLK>
 __global__ __launch_bounds__(256) void k_quant_act_mxfp8(uint8_t *Q, uint8_t *S,
                                                         const void *a, int n, int k)
 {
@@ -466,18 +469,32 @@ __global__ __launch_bounds__(256) void k_quant_act_mxfp8(uint8_t *Q, uint8_t *S,
         if (!live[u]) v[u][0] = v[u][1] = v[u][2] = v[u][3] = 0.0f;
     }
 #pragma unroll
-    for (int u = 0; u < QA_U_MX; u++) quant4_mx(v[u], g[u], (int)(threadIdx.x & 7), live[u], Q, S);
+    for (int u = 0; u < QA_U_MX; u++) {
+        long at = g[u];
+        if constexpr (BLK) {
+            const long gpt = k / 32, m = g[u] / gpt, j = g[u] - m * gpt;
+            at = 4 * ((j >> 2) * (long)n + m) + (j & 3);
+        }
+        quant4_mx(v[u], g[u], (int)(threadIdx.x & 7), live[u], Q, S, at);
+    }
 }
 
 hipError_t quant_act_mxfp8_launch(uint8_t *Q, uint8_t *S, const void *a,
-                                  int n, int k, hipStream_t st, bool bf16_in)
+                                  int n, int k, hipStream_t st, bool bf16_in, bool s_blk_major)
 {
+    if (s_blk_major && k % 128) return hipErrorInvalidValue;
     const long units = ((long)n * (k / 32) * 8 + 255) / 256;
     const dim3 grid((unsigned)((units + QA_U_MX - 1) / QA_U_MX)), block(256);
-    if (bf16_in)
-        hipLaunchKernelGGL(k_quant_act_mxfp8<true>, grid, block, 0, st, Q, S, a, n, k);
-    else
-        hipLaunchKernelGGL(k_quant_act_mxfp8<false>, grid, block, 0, st, Q, S, a, n, k);
+    if (s_blk_major) {
+        if (bf16_in)
+            hipLaunchKernelGGL((k_quant_act_mxfp8<true, true>), grid, block, 0, st, Q, S, a, n, k);
+        else
+            hipLaunchKernelGGL((k_quant_act_mxfp8<false, true>), grid, block, 0, st, Q, S, a, n, k);
+    } else if (bf16_in) {
+        hipLaunchKernelGGL((k_quant_act_mxfp8<true, false>), grid, block, 0, st, Q, S, a, n, k);
+    } else {
+        hipLaunchKernelGGL((k_quant_act_mxfp8<false, false>), grid, block, 0, st, Q, S, a, n, k);
+    }
     return hipGetLastError();
 }
 

@@ -1247,15 +1247,17 @@ int dsv4_hip_gemm_fp8q_dev(void *C, int out_bf16, const uint8_t *Aq, const float
     return enqueue_gemm(C, out_bf16, Aq, Sa, M, W, fmt, (hipStream_t)stream);
 }
 
-/* The hardware-scaled GEMM: W must carry E8M0 128 x 128 block scales. */
+/* The hardware-scaled GEMM: W must carry E8M0 128 x 128 block scales. As
+ * token-major [M][K / 32] bytes, or block-major (s_blk_major: one dword per
+ * token and 128-wide K block, [K / 128][M] dwords). */
 static int enqueue_gemm_mx(void *C, int out_bf16, const uint8_t *Aq, const uint8_t *As, int M,
-                    const DSV4QMat *W, hipStream_t st)
+                    const DSV4QMat *W, bool s_blk_major, hipStream_t st)
 {
     GemmArgs ga;
     ga.Aq = Aq; ga.Sa = (const float *)As; ga.W = (const uint8_t *)W->w; ga.Sw = W->s; ga.C = C;
     ga.M = M; ga.N = W->rows; ga.K = W->cols; ga.ldc = W->rows;
-    ga.sa_tok = W->cols / 128;
-    ga.sa_kb = 1;
+    ga.sa_tok = s_blk_major ? 1 : W->cols / 128;
+    ga.sa_kb = s_blk_major ? M : 1;
     HIPCHK(gemm_mx_launch(ga, out_bf16 != 0, st), "gemm launch");
     return 0;
 }
@@ -1401,8 +1403,8 @@ int dsv4_hip_gemm_mxfp8_dev(void *C, int out_bf16, const void *A, int a_bf16, in
     uint8_t *Aq = (uint8_t *)g.gemm_ws.p;
     uint8_t *As = Aq + qbytes;
     hipStream_t st = (hipStream_t)stream;
-    HIPCHK(quant_act_mxfp8_launch(Aq, As, A, M, K, st, a_bf16 != 0), "activation quant launch");
-    return enqueue_gemm_mx(C, out_bf16, Aq, As, M, W, st);
+    HIPCHK(quant_act_mxfp8_launch(Aq, As, A, M, K, st, a_bf16 != 0, true), "activation quant launch");
+    return enqueue_gemm_mx(C, out_bf16, Aq, As, M, W, true, st);
 }
 
 int dsv4_hip_gemm_mxfp8q_dev(void *C, int out_bf16, const uint8_t *Aq, const uint8_t *As,
@@ -1416,7 +1418,7 @@ int dsv4_hip_gemm_mxfp8q_dev(void *C, int out_bf16, const uint8_t *Aq, const uin
     if (gemm_checks(C, Aq, M, W, "gemm_mxfp8q_dev", &fmt)) return -1;
     if (fmt != FMT_FP8_E8M0) return fail("gemm_mxfp8q_dev: W must carry E8M0 block scales (DSV4_WFP8)");
     if (!As) return fail("gemm_mxfp8q_dev: NULL scales");
-    return enqueue_gemm_mx(C, out_bf16, Aq, As, M, W, (hipStream_t)stream);
+    return enqueue_gemm_mx(C, out_bf16, Aq, As, M, W, false, (hipStream_t)stream);
 }
 
 /* ------------------------------------------------------ grouped MoE --- */
