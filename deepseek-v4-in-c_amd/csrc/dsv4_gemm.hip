@@ -382,7 +382,11 @@ __device__ __forceinline__ void stage_frag(uint8_t *lds, const v4f &acc, int tok
 
 /* Output staging: the workgroup's 128 x 256 tile sits in LDS as rows of GN
  * elements, 16-byte chunk c of row r stored at chunk c ^ (r % 32), and is
- * copied to C in whole 16-byte pieces of contiguous rows. */
+ * copied to C in whole 16-byte pieces of contiguous rows. The stores are
+ * non-temporal (streaming, no L2 allocation): every workgroup of a one-round
+ * grid writes its tile at the same moment, after the last K block (measured
+ * at 2048 x 4096 x 4096, bf16 out, alternating builds on one device: 40.3 ->
+ * 39.8 us). */
 template <bool OUT_BF16>
 __device__ __forceinline__ void write_tile(const GemmArgs &a, const uint8_t *lds, int m0, int n0)
 {
@@ -394,7 +398,7 @@ __device__ __forceinline__ void write_tile(const GemmArgs &a, const uint8_t *lds
         const int m = m0 + r;
         if (m >= a.M || c >= live) continue;
         const u32x4 v = *(const u32x4 *)(lds + r * (GN * EB) + 16 * (c ^ (r & 31)));
-        *(u32x4 *)((uint8_t *)a.C + ((size_t)m * a.ldc + n0) * EB + 16 * c) = v;
+        __builtin_nontemporal_store(v, (u32x4 *)((uint8_t *)a.C + ((size_t)m * a.ldc + n0) * EB + 16 * c));
     }
 }
 
