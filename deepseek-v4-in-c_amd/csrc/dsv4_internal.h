@@ -321,8 +321,17 @@ struct RouteArgs {
     int *pos;                 /* [npairs] row of each pair (-1: bad id)   */
     int *row_tok;             /* [npairs] token of each row               */
     int *row_k;               /* [npairs] k of each row, or NULL          */
+    int *chist;               /* [chunks of 1024 pairs][n_experts] counts, or
+                                 NULL: every placing workgroup counts every pair */
     unsigned *status;
 };
+/* from this many chunks of 1024 pairs on (and with chist set), a counting
+ * launch per chunk precedes the placing launch */
+constexpr int ROUTE_PRECOUNT_CHUNKS = 4;
+inline size_t route_chist_bytes(long npairs, int n_experts)
+{
+    return (size_t)((npairs + 1023) / 1024) * (size_t)n_experts * 4;
+}
 hipError_t moe_route_launch(const RouteArgs &a, hipStream_t st);
 
 /* dsv4_route for n tokens, one wavefront each: scores [n][scores_ld] fp32

@@ -212,12 +212,34 @@ __device__ __forceinline__ int route_leader_count(int e, int E, uint64_t below)
     return ((unsigned)e < (unsigned)E && __popcll(peers & below) == n - 1) ? n : 0;
 }
 
-/* Stable counting sort of the pairs by expert, in one launch of up to
- * ROUTE_MAX_BLOCKS workgroups. Pairs go in chunks of 1024; workgroup b places
- * chunks [b * cpb, (b + 1) * cpb). Every workgroup counts every pair (the
- * bucket sizes, and how many of each expert precede its first chunk), so no
- * workgroup waits for another; workgroup 0 also writes grp_off, tile_pre and
- * tile_grp and reports bad ids. */
+/* Pass one of the two-launch form: workgroup c counts chunk c's pairs per
+ * expert into chist[c][E] (and reports bad ids). */
+__global__ __launch_bounds__(1024) void k_moe_route_count(RouteArgs a)
+{
+    __shared__ int hist[MAX_ROUTE_EXPERTS];
+    const int tid = threadIdx.x, E = a.n_experts, c = blockIdx.x;
+    const int lane = tid & 63;
+    const uint64_t below = lane ? (~0ull >> (64 - lane)) : 0ull;
+    const int p = c * 1024 + tid;
+    const int e = p < a.npairs ? a.idx[p] : -1;
+    hist[tid] = 0;
+    __syncthreads();
+    const int n = route_leader_count(e, E, below);
+    if (n) atomicAdd(&hist[e], n);
+    else if ((unsigned)e >= (unsigned)E && p < a.npairs) atomicOr(a.status, ST_BAD_EXPERT_ID);
+    __syncthreads();
+    if (tid < E) a.chist[(size_t)c * E + tid] = hist[tid];
+}
+
+/* Stable counting sort of the pairs by expert. Pairs go in chunks of 1024;
+ * workgroup b places chunks [b * cpb, (b + 1) * cpb). It needs the bucket
+ * sizes and how many pairs of each expert precede its first chunk: with
+ * PRECOUNT it sums them from the per-chunk counts k_moe_route_count wrote
+ * (two launches); without, every workgroup counts every pair itself (one
+ * launch, no workgroup waits for another: the form for a few chunks).
+ * Workgroup 0 also writes grp_off, tile_pre and tile_grp; bad ids are
+ * reported by workgroup 0 (one launch) or by the counting pass. */
+template <bool PRECOUNT>
 __global__ __launch_bounds__(1024) void k_moe_route(RouteArgs a, int cpb)
 {
     __shared__ int hist[MAX_ROUTE_EXPERTS], before[MAX_ROUTE_EXPERTS];
@@ -238,6 +260,25 @@ __global__ __launch_bounds__(1024) void k_moe_route(RouteArgs a, int cpb)
     int ev[ROUTE_BATCH];
     const int lane = tid & 63, wv = tid >> 6;
     const uint64_t below = lane ? (~0ull >> (64 - lane)) : 0ull;
+    if constexpr (PRECOUNT) {
+        /* expert tid's count in every chunk: sixteen loads in flight per
+         * round, summed in chunk order (integers: any order gives the same) */
+        if (tid < E) {
+            int tot = 0, bef = 0;
+            for (int c0 = 0; c0 < nch; c0 += 16) {
+                int v[16];
+#pragma unroll
+                for (int i = 0; i < 16; i++) v[i] = c0 + i < nch ? a.chist[(size_t)(c0 + i) * E + tid] : 0;
+#pragma unroll
+                for (int i = 0; i < 16; i++) {
+                    tot += v[i];
+                    if (c0 + i < c_lo) bef += v[i];
+                }
+            }
+            hist[tid] = tot;
+            before[tid] = bef;
+        }
+    } else
     for (int c0 = 0; c0 < nch; c0 += ROUTE_BATCH) {
         route_load(ev, a, c0, nch, tid);
 #pragma unroll
@@ -330,7 +371,7 @@ __global__ __launch_bounds__(1024) void k_moe_route(RouteArgs a, int cpb)
             __syncthreads();
         }
     }
-    if (bad && blockIdx.x == 0) atomicOr(a.status, bad);
+    if (!PRECOUNT && bad && blockIdx.x == 0) atomicOr(a.status, bad);
 }
 
 /* One workgroup per row: the row's largest finite magnitude (a fixed-order
@@ -1219,7 +1260,12 @@ hipError_t moe_route_launch(const RouteArgs &a, hipStream_t st)
     const int nch = (a.npairs + 1023) / 1024;
     const int cpb = nch > ROUTE_MAX_BLOCKS ? (nch + ROUTE_MAX_BLOCKS - 1) / ROUTE_MAX_BLOCKS : 1;
     const int blocks = nch > 0 ? (nch + cpb - 1) / cpb : 1;
-    hipLaunchKernelGGL(k_moe_route, dim3(blocks), dim3(1024), 0, st, a, cpb);
+    if (a.chist && nch >= ROUTE_PRECOUNT_CHUNKS) {
+        hipLaunchKernelGGL(k_moe_route_count, dim3(nch), dim3(1024), 0, st, a);
+        hipLaunchKernelGGL(k_moe_route<true>, dim3(blocks), dim3(1024), 0, st, a, cpb);
+    } else {
+        hipLaunchKernelGGL(k_moe_route<false>, dim3(blocks), dim3(1024), 0, st, a, cpb);
+    }
     return hipGetLastError();
 }
 

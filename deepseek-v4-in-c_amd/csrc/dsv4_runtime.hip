@@ -1447,6 +1447,7 @@ static int enqueue_moe_grouped(float *out, const float *x, int n, const DSV4Expe
     const size_t o_grp = take((size_t)(n_experts + 1) * 4), o_tp = take((size_t)(n_experts + 1) * 4);
     const size_t o_tg = take((size_t)max_tiles * 4);
     const size_t o_pos = take((size_t)P * 4), o_row = take((size_t)P * 4);
+    const size_t o_ch = take(route_chist_bytes(P, n_experts));
     const size_t o_x16 = take((size_t)n * hidden * 2), o_mid = take((size_t)P * inter * 2);
     const size_t o_y = take((size_t)P * hidden * 4), o_ex = take((size_t)n * 4);
     size_t o_smid = 0, o_ys = 0;
@@ -1467,6 +1468,7 @@ static int enqueue_moe_grouped(float *out, const float *x, int n, const DSV4Expe
     ra.tile_rows = trows; ra.grp_off = grp; ra.tile_pre = tp; ra.tile_grp = tg; ra.pos = pos;
     ra.row_tok = row;
     ra.row_k = nullptr;
+    ra.chist = (int *)(ws + o_ch);
     ra.status = g.st;
     HIPCHK(moe_route_launch(ra, st), "route launch");
     HIPCHK(to_f16_rows_launch(x16, ex, x, n, hidden, st), "x fp16 launch");
@@ -1550,6 +1552,7 @@ static int enqueue_moe_grouped_mx(float *out, const float *x, int n, const DSV4E
     const size_t o_grp = take((size_t)(n_experts + 1) * 4), o_tp = take((size_t)(n_experts + 1) * 4);
     const size_t o_tg = take((size_t)max_tiles * 4);
     const size_t o_pos = take((size_t)P * 4), o_row = take((size_t)P * 4);
+    const size_t o_ch = take(route_chist_bytes(P, n_experts));
     const size_t o_x8 = take((size_t)n * hidden), o_xs = take((size_t)n * hidden / 32);
     const size_t o_mid = take((size_t)P * inter), o_ms = take((size_t)P * inter / 32);
     const size_t o_y = take((size_t)P * hidden * 4);
@@ -1590,6 +1593,7 @@ static int enqueue_moe_grouped_mx(float *out, const float *x, int n, const DSV4E
     ra.tile_rows = trows; ra.grp_off = grp; ra.tile_pre = tp; ra.tile_grp = tg; ra.pos = pos;
     ra.row_tok = row;
     ra.row_k = nullptr;
+    ra.chist = (int *)(ws + o_ch);
     ra.status = g.st;
     HIPCHK(moe_route_launch(ra, st), "route launch");
 
@@ -1798,6 +1802,7 @@ int dsv4_hip_moe_grouped_mx_mid_dev(uint8_t *mid, uint8_t *mid_s, int *row_tok, 
     auto take = [&](size_t b) { const size_t o = off; off += (b + 255) & ~(size_t)255; return o; };
     const size_t o_grp = take((size_t)(n_experts + 1) * 4), o_tp = take((size_t)(n_experts + 1) * 4);
     const size_t o_tg = take((size_t)max_tiles * 4), o_pos = take((size_t)P * 4);
+    const size_t o_ch = take(route_chist_bytes(P, n_experts));
     const size_t o_x8 = take((size_t)n * hidden), o_xs = take((size_t)n * hidden / 32);
     HIPCHK(g.moe_ws.need(off), "grouped MoE workspace");
     uint8_t *ws = (uint8_t *)g.moe_ws.p;
@@ -1805,6 +1810,7 @@ int dsv4_hip_moe_grouped_mx_mid_dev(uint8_t *mid, uint8_t *mid_s, int *row_tok, 
     ra.idx = idx; ra.npairs = (int)P; ra.topk = topk; ra.n_experts = n_experts; ra.tile_rows = trows;
     ra.grp_off = (int *)(ws + o_grp); ra.tile_pre = (int *)(ws + o_tp); ra.tile_grp = (int *)(ws + o_tg);
     ra.pos = (int *)(ws + o_pos); ra.row_tok = row_tok; ra.row_k = row_k; ra.status = g.st;
+    ra.chist = (int *)(ws + o_ch);
     HIPCHK(moe_route_launch(ra, st), "route launch");
     HIPCHK(quant_act_mxfp8_launch(ws + o_x8, ws + o_xs, x, n, hidden, st), "x MXFP8 launch");
     GroupedMxArgs ga;
@@ -1904,13 +1910,15 @@ int dsv4_hip_moe_route_dev(int *ex_off, int *ex_tok, int *ex_k, int *pos, const 
     const int trows = 16;
     const long max_tiles = (P + trows - 1) / trows + n_experts;
     const size_t o_tp = 0, o_tg = (((size_t)n_experts + 1) * 4 + 255) & ~(size_t)255;
-    HIPCHK(g.small.need(o_tg + (size_t)max_tiles * 4), "route workspace");
+    const size_t o_ch = (o_tg + (size_t)max_tiles * 4 + 255) & ~(size_t)255;
+    HIPCHK(g.small.need(o_ch + route_chist_bytes(P, n_experts)), "route workspace");
     RouteArgs ra;
     ra.idx = idx; ra.npairs = (int)P; ra.topk = topk; ra.n_experts = n_experts;
     ra.tile_rows = trows; ra.grp_off = ex_off;
     ra.tile_pre = (int *)((uint8_t *)g.small.p + o_tp);
     ra.tile_grp = (int *)((uint8_t *)g.small.p + o_tg);
     ra.pos = pos; ra.row_tok = ex_tok; ra.row_k = ex_k; ra.status = g.st;
+    ra.chist = (int *)((uint8_t *)g.small.p + o_ch);
     HIPCHK(moe_route_launch(ra, (hipStream_t)stream), "route launch");
     return 0;
 }

@@ -396,6 +396,35 @@ def test_route_matches_union_prepare(lib, oracle, n, topk, ne, zipf):
     assert np.array_equal(w_k[pp], pairs % topk)
 
 
+def test_route_bad_id_counting_pass(lib, oracle):
+    """A bad id among 6,000 pairs (six chunks of 1024, the two-launch form):
+    status bit 0, its pos -1, and every good pair placed as union_prepare
+    places the ids with the bad one left out."""
+    rng = np.random.default_rng(6000)
+    n, topk, ne = 1000, 6, 64
+    idx = np.stack([rng.choice(ne, topk, replace=False) for _ in range(n)]).astype(np.int32)
+    idx[777, 3] = ne + 5
+    P_ = n * topk
+    di = torch.from_numpy(idx.reshape(-1)).to(DEV)
+    off = torch.full((ne + 1,), -7, dtype=torch.int32, device=DEV)
+    tok, kk, pos = (torch.full((P_,), -7, dtype=torch.int32, device=DEV) for _ in range(3))
+    lib.status()
+    lib.moe_route_dev(off.data_ptr(), tok.data_ptr(), kk.data_ptr(), pos.data_ptr(), di.data_ptr(),
+                      n, topk, ne)
+    torch.cuda.synchronize()
+    assert lib.status() & 1
+    pp = pos.cpu().numpy()
+    assert pp[777 * topk + 3] == -1
+    flat = idx.reshape(-1)
+    good = np.flatnonzero(flat < ne)
+    order = good[np.argsort(flat[good], kind="stable")]
+    o = off.cpu().numpy()
+    assert np.array_equal(np.diff(o), np.bincount(flat[good], minlength=ne))
+    got_tok, got_k = tok.cpu().numpy()[:len(order)], kk.cpu().numpy()[:len(order)]
+    assert np.array_equal(got_tok, order // topk) and np.array_equal(got_k, order % topk)
+    assert np.array_equal(pp[order], np.arange(len(order)))
+
+
 def test_route_bad_id(lib):
     idx = np.array([[0, 1], [2, 9], [1, 0]], np.int32)
     di = torch.from_numpy(idx.reshape(-1)).to(DEV)
