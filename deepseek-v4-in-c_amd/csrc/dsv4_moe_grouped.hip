@@ -295,19 +295,33 @@ __global__ __launch_bounds__(1024) void k_moe_route(RouteArgs a, int cpb)
         }
     }
     __syncthreads();
-    /* inclusive scans of the bucket sizes and tile counts (Hillis-Steele,
-     * one expert per thread; E <= 1024) */
+    /* inclusive scans of the bucket sizes and tile counts, one expert per
+     * thread (E <= 1024): within each wave by shuffles, then the totals of
+     * the lower waves added (two barriers) */
     const int cnt = tid < E ? hist[tid] : 0;
     const int tls = (cnt + a.tile_rows - 1) / a.tile_rows;
-    scan_r[tid] = cnt;
-    scan_t[tid] = tls;
-    __syncthreads();
-    for (int d = 1; d < MAX_ROUTE_EXPERTS; d <<= 1) {
-        const int xr = tid >= d ? scan_r[tid - d] : 0;
-        const int xt = tid >= d ? scan_t[tid - d] : 0;
+    {
+        __shared__ int wsum[2][16];
+        int ir = cnt, it = tls;
+#pragma unroll
+        for (int d = 1; d < 64; d <<= 1) {
+            const int xr = __shfl_up(ir, d, 64), xt = __shfl_up(it, d, 64);
+            if (lane >= d) {
+                ir += xr;
+                it += xt;
+            }
+        }
+        if (lane == 63) {
+            wsum[0][wv] = ir;
+            wsum[1][wv] = it;
+        }
         __syncthreads();
-        scan_r[tid] += xr;
-        scan_t[tid] += xt;
+        for (int w = 0; w < wv; w++) {
+            ir += wsum[0][w];
+            it += wsum[1][w];
+        }
+        scan_r[tid] = ir;
+        scan_t[tid] = it;
         __syncthreads();
     }
     /* each tile's bucket: the first expert whose inclusive tile prefix

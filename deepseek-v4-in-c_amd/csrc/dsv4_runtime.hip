@@ -1470,16 +1470,19 @@ static int enqueue_moe_grouped(float *out, const float *x, int n, const DSV4Expe
     ra.row_k = nullptr;
     ra.chist = (int *)(ws + o_ch);
     ra.status = g.st;
+    /* x to fp16 on the side stream, beside the routing permutation on this
+     * one (neither reads the other's output); the shared expert, which needs
+     * only x16, follows it there, overlaps the routed launches and is joined
+     * before the combine */
+    HIPCHK(hipEventRecord(g.fork, st), "fork record");
+    HIPCHK(hipStreamWaitEvent(g.side, g.fork, 0), "fork wait");
+    HIPCHK(to_f16_rows_launch(x16, ex, x, n, hidden, g.side), "x fp16 launch");
+    HIPCHK(hipEventRecord(g.xq, g.side), "convert record");
     HIPCHK(moe_route_launch(ra, st), "route launch");
-    HIPCHK(to_f16_rows_launch(x16, ex, x, n, hidden, st), "x fp16 launch");
+    HIPCHK(hipStreamWaitEvent(st, g.xq, 0), "convert wait");
 
     float *ys = nullptr;
     if (shared) {
-        /* the shared expert needs only x16: it runs on the side stream,
-         * forked right after the fp16 convert (before the routed launches
-         * are enqueued, so it overlaps them) and joined before the combine */
-        HIPCHK(hipEventRecord(g.fork, st), "fork record");
-        HIPCHK(hipStreamWaitEvent(g.side, g.fork, 0), "fork wait");
         uint16_t *smid = (uint16_t *)(ws + o_smid);
         ys = (float *)(ws + o_ys);
         const int stt = n <= 64 ? 1 : 4;     /* enough workgroups for a small batch */
