@@ -297,6 +297,32 @@ def test_grouped_bucket_shapes(lib, pkg, oracle, n, topk, ne, zipf, hidden, inte
     assert e <= REL_L2_TOL, f"rel L2 {e:.3e} (max abs {max_abs(got[tokens], want):.3e})"
 
 
+def test_grouped_tile_fill_levels(lib, pkg, oracle):
+    """Buckets of 4, 5, 1, 16, 17 (a full 16-token tile and a one-token
+    tile), 3, 0 and 2 tokens: every token checked against the oracle, and two
+    calls bit-identical."""
+    counts = [4, 5, 1, 16, 17, 3, 0, 2]
+    ne, hidden, inter = len(counts), 512, 256
+    gen = torch.Generator().manual_seed(4516)
+    dgen = torch.Generator(device=DEV).manual_seed(4516)
+    rng = np.random.default_rng(4516)
+    ids = np.concatenate([np.full(c, e, np.int32) for e, c in enumerate(counts)])
+    rng.shuffle(ids)
+    n = len(ids)
+    idx = ids.reshape(n, 1)
+    w = np.ones((n, 1), np.float32)
+    experts = [DevExpert(lib, pkg, "fp4", inter, hidden, dgen) for _ in range(ne)]
+    x = bf16_rows(gen, n, hidden)
+    lib.status()
+    got = run_dev(lib, experts, None, x, idx, w, hidden, inter)
+    again = run_dev(lib, experts, None, x, idx, w, hidden, inter)
+    assert lib.status() == 0
+    assert np.array_equal(bits(got), bits(again))
+    want = oracle_tokens(oracle, experts, None, x, idx, w, list(range(n)))
+    e = rel_l2(got, want)
+    assert e <= REL_L2_TOL, f"rel L2 {e:.3e} (max abs {max_abs(got, want):.3e})"
+
+
 def test_grouped_bad_id_real_width(lib, pkg, oracle):
     """A routing id out of range at hidden 512 (whole 256-wide K stages):
     status bit 0, that token NaN, the others exact."""
