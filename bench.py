@@ -769,8 +769,9 @@ def bench_cfg3(args, torch, pkg, lib, stream, sp, K, W):
         seam(i)
     t_seam = time_events(torch, stream, seam, K)
     seam_rec = {"entry": "dsv4_hip_mmq_n_dev (fp32 x [2048x4096], fp32 y)",
-                "path": "x rows scaled by a power of two and rounded to fp16, weights decoded "
-                        "exactly to fp16 in LDS, fp16 MFMA, fp32 accumulation",
+                "path": "x rows scaled by a power of two and rounded to fp16 (k_to_f16_rows), then "
+                        "k_gemm_seam: 128x256 tiles, e4m3 weights decoded exactly to fp16 in "
+                        "registers, fp16 MFMA, fp32 block-scale promotion",
                 "ms_per_call": round(t_seam * 1e3, 5),
                 "tflops": round(flops / t_seam / 1e12, 2),
                 "frac_of_fp16_peak": round(flops / t_seam / 1e12 / FP16_PEAK_TFLOPS, 4)}

@@ -612,4 +612,174 @@ hipError_t gemm_mx_launch(const GemmArgs &a, bool out_bf16, hipStream_t st)
     return out_bf16 ? launch_gemm_mx<true>(a, st) : launch_gemm_mx<false>(a, st);
 }
 
+/* ------------------------------------------------- seam dense GEMM --- */
+
+/* The drop-in seam's dense form for FP8 weights (dsv4_mmq_n with many
+ * tokens: src/10_compute/dsv4_matmul_fp8.c:102-155 with nt > 31):
+ *   C[m][n] = 2^-ex[m] sum_kb s_w[n / 128][kb] sum_{k in block kb} X[m][k] W[n][k]
+ * X fp16 rows scaled by 2^ex[m] (k_to_f16_rows), W e4m3 decoded exactly to
+ * fp16 in registers (v_cvt_scalef32_pk_f16_fp8 with scale 1), the block's
+ * partial from four v_mfma_f32_16x16x32_f16 steps started from zero, then
+ * multiplied by the fp32 (or E8M0) block scale into the fp32 accumulator.
+ * The steps' reduction order and the promotion order over blocks are those of
+ * the grouped kernel's dense form (kmap / bchunk for FP8), so both give the
+ * same bits. Tile and tile order as the FP8 GEMM (128 tokens x 256 features,
+ * wave (wm, wn) 64 x 64); a K block stages 256 W rows x 128 B and 128 token
+ * rows x 256 B (64 KiB) by direct loads into a two-stage ring. */
+namespace {
+
+constexpr int H_XB = GK * 2;                  /* fp16 token bytes per row per block */
+constexpr int H_ST_X = GN * GK;               /* after 256 W rows of 128 B          */
+constexpr int H_STAGE = H_ST_X + GM * H_XB;   /* 64 KiB                             */
+constexpr int H_LDS = 2 * H_STAGE;            /* the fp32 output tile reuses it      */
+static_assert(H_LDS >= GM * GN * 4 && H_LDS <= 160 * 1024, "seam GEMM LDS");
+
+typedef _Float16 h8v __attribute__((ext_vector_type(8)));
+
+/* physical 16-byte slot of logical chunk c in staged token row r (16 slots) */
+__device__ __forceinline__ int swx(int r, int c) { return c ^ (r & 15); }
+
+/* eight e4m3 (dwords 2 hi, 2 hi + 1 of a 16-byte chunk) to eight fp16, exact */
+__device__ __forceinline__ h8v w_f16(const u32x4 &w, int hi)
+{
+    const uint32_t d0 = hi ? w.z : w.x, d1 = hi ? w.w : w.y;
+    u32x4 v;
+    v.x = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(d0, 1.0f, false));
+    v.y = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(d0, 1.0f, true));
+    v.z = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(d1, 1.0f, false));
+    v.w = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(d1, 1.0f, true));
+    return __builtin_bit_cast(h8v, v);
+}
+
+} // namespace
+
+template <bool WF32S>
+__global__ __launch_bounds__(512) void k_gemm_seam(SeamGemmArgs s)
+{
+    extern __shared__ __align__(16) uint8_t lds[];
+    const int lane = threadIdx.x & 63;
+    const int wave = wave_in_group();
+    const int wm = wave & 1, wn = wave >> 1, rr = lane & 15, gq = lane >> 4;
+    int m0, n0;
+    tile_of(m0, n0);
+    GemmArgs g;                                /* the FP8 GEMM's view: scales, epilogue */
+    g.Aq = nullptr; g.Sa = nullptr; g.W = s.W; g.Sw = s.Sw; g.C = s.C;
+    g.M = s.M; g.N = s.N; g.K = s.K; g.ldc = s.N; g.sa_tok = 0; g.sa_kb = 0;
+    const int nkb = s.K / GK;
+    const int nb = min((n0 + 64 * wn) / 128, s.N / 128 - 1);
+    const __amdgpu_buffer_rsrc_t rw = buf_rsrc(s.W, (uint32_t)s.N * (uint32_t)s.K);
+    const __amdgpu_buffer_rsrc_t rx = buf_rsrc(s.X, (uint32_t)s.M * (uint32_t)s.K * 2u);
+    /* direct loads: W instruction j (4 wave .. + 3) fills W rows 8j .. 8j+7,
+     * X instruction j token rows 4j .. 4j+3, lane l landing in physical slot
+     * l % 8 (W) or l % 16 (X) of its row */
+    uint32_t wo[4], xo[4];
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const int j = 4 * wave + i;
+        const int rw8 = 8 * j + (lane >> 3), rx4 = 4 * j + (lane >> 4);
+        wo[i] = (uint32_t)min(n0 + rw8, s.N - 1) * (uint32_t)s.K + 16u * (uint32_t)swz(rw8, lane & 7);
+        xo[i] = (uint32_t)min(m0 + rx4, s.M - 1) * (uint32_t)s.K * 2u + 16u * (uint32_t)swx(rx4, lane & 15);
+    }
+    auto issue = [&](int kb, uint8_t *buf) {
+#pragma unroll
+        for (int i = 0; i < 4; i++) dma16(rw, wo[i], (uint32_t)kb * GK, buf + 1024 * (4 * wave + i));
+#pragma unroll
+        for (int i = 0; i < 4; i++) dma16(rx, xo[i], (uint32_t)kb * H_XB, buf + H_ST_X + 1024 * (4 * wave + i));
+    };
+
+    v4f acc[4][4];
+#pragma unroll
+    for (int f = 0; f < 4; f++)
+#pragma unroll
+        for (int t = 0; t < 4; t++) acc[f][t] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+
+    issue(0, lds);
+    for (int kb = 0; kb < nkb; kb++) {
+        /* this wave's loads of block kb have landed; after the barrier every
+         * wave's have, and no wave still reads the other stage, which the
+         * loads of block kb + 1 refill */
+        __builtin_amdgcn_s_waitcnt(waitcnt(0, true));
+        __builtin_amdgcn_s_barrier();
+        asm volatile("" ::: "memory");
+        if (kb + 1 < nkb) issue(kb + 1, lds + ((kb + 1) & 1) * H_STAGE);
+        const uint8_t *buf = lds + (kb & 1) * H_STAGE;
+        const float sw = weight_scale<WF32S>(g, nb, kb);
+        v4f p[4][4];
+        u32x4 w16[4];
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            h8v b[4];
+#pragma unroll
+            for (int t = 0; t < 4; t++) {
+                const int r = 64 * wm + 16 * t + rr;
+                b[t] = *(const h8v *)(buf + H_ST_X + r * H_XB + 16 * swx(r, 8 * (j >> 1) + 2 * gq + (j & 1)));
+            }
+#pragma unroll
+            for (int f = 0; f < 4; f++) {
+                if ((j & 1) == 0) {
+                    const int r = 64 * wn + 16 * f + rr;
+                    w16[f] = *(const u32x4 *)(buf + r * GK + 16 * swz(r, 4 * (j >> 1) + gq));
+                }
+                const h8v av = w_f16(w16[f], j & 1);
+#pragma unroll
+                for (int t = 0; t < 4; t++)
+                    p[f][t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, b[t], j == 0 ? v4f{0.0f, 0.0f, 0.0f, 0.0f}
+                                                                                  : p[f][t], 0, 0, 0);
+            }
+        }
+#pragma unroll
+        for (int f = 0; f < 4; f++)
+#pragma unroll
+            for (int t = 0; t < 4; t++)
+#pragma unroll
+                for (int e = 0; e < 4; e++) acc[f][t][e] = fmaf(p[f][t][e], sw, acc[f][t][e]);
+    }
+    __builtin_amdgcn_s_waitcnt(waitcnt(0, true));
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+#pragma unroll
+    for (int t = 0; t < 4; t++) {
+        const int tok = m0 + 64 * wm + 16 * t + rr;
+        const int ex = tok < s.M ? s.ex[tok] : 0;
+#pragma unroll
+        for (int f = 0; f < 4; f++)
+#pragma unroll
+            for (int e = 0; e < 4; e++) acc[f][t][e] = ex ? ldexpf(acc[f][t][e], -ex) : acc[f][t][e];
+    }
+#pragma unroll
+    for (int f = 0; f < 4; f++)
+#pragma unroll
+        for (int t = 0; t < 4; t++)
+            stage_frag<false>(lds, acc[f][t], 64 * wm + 16 * t + rr, 64 * wn + 16 * f + 4 * gq);
+    __syncthreads();
+    write_tile<false>(g, lds, m0, n0);
+}
+
+template <bool WS>
+static hipError_t launch_gemm_seam(const SeamGemmArgs &s, hipStream_t st)
+{
+    static bool attr_done = false;
+    if (!attr_done) {
+        const hipError_t e = hipFuncSetAttribute((const void *)k_gemm_seam<WS>,
+                                                 hipFuncAttributeMaxDynamicSharedMemorySize, H_LDS);
+        if (e != hipSuccess) return e;
+        attr_done = true;
+    }
+    const dim3 grid((unsigned)((s.N + GN - 1) / GN), (unsigned)((s.M + GM - 1) / GM)), block(512);
+    hipLaunchKernelGGL((k_gemm_seam<WS>), grid, block, H_LDS, st, s);
+    return hipGetLastError();
+}
+
+bool gemm_seam_ok(int M, int N, int K)
+{
+    return M > 0 && N > 0 && K > 0 && K % GK == 0 && N % 128 == 0 &&
+           (size_t)N * K <= 0xFFFFFFFFull && (size_t)M * K * 2 <= 0xFFFFFFFFull;
+}
+
+hipError_t gemm_seam_launch(const SeamGemmArgs &s, bool w_f32s, hipStream_t st)
+{
+    if (!gemm_seam_ok(s.M, s.N, s.K) || !s.X || !s.ex || !s.W || !s.Sw || !s.C) return hipErrorInvalidValue;
+    return w_f32s ? launch_gemm_seam<true>(s, st) : launch_gemm_seam<false>(s, st);
+}
+
 } // namespace dsv4

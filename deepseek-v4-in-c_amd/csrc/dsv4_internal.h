@@ -284,6 +284,21 @@ hipError_t gemm_fp8_launch(const GemmArgs &a, bool w_f32s, bool out_bf16, hipStr
  * read as whole lines). */
 hipError_t gemm_mx_launch(const GemmArgs &a, bool out_bf16, hipStream_t st);
 
+/* The seam's dense FP8 form: C fp32 [M][N] = 2^-ex[m] * sum over 128-K blocks
+ * of the block scale (fp32 when w_f32s, else E8M0 bytes, [N/128][K/128])
+ * times the fp16 MFMA partial of X fp16 [M][K] (rows scaled by 2^ex[m]) and
+ * W e4m3 [N][K] decoded exactly. K % 128 == 0, N % 128 == 0. */
+struct SeamGemmArgs {
+    const uint16_t *X;
+    const int *ex;
+    const uint8_t *W;
+    const void *Sw;
+    float *C;
+    int M, N, K;
+};
+bool gemm_seam_ok(int M, int N, int K);
+hipError_t gemm_seam_launch(const SeamGemmArgs &s, bool w_f32s, hipStream_t st);
+
 /* ---------------------------------------------- dequant / quantizers --- */
 hipError_t dequant_launch(int fmt, const DSV4QMat &m, float *out, hipStream_t st);
 hipError_t quant_fp4_mx_launch(uint8_t *W, uint8_t *S, const float *w, int rows,

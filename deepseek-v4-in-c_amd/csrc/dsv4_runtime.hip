@@ -674,10 +674,13 @@ void *dsv4_hip_device_ptr(const void *p)
  * every nt. From MMQ_MFMA_MIN_TOKENS tokens on, packed matrices the grouped
  * kernel takes (rows, cols multiples of 128; FP8 with 128x128 blocks or FP4
  * with 1x32) run as one dense fp16-MFMA GEMM (x row-scaled by a power of two
- * and rounded to fp16, weights decoded exactly, fp32 accumulation); fewer
- * tokens run the block-scaled MFMA GEMV where its geometry fits, else the
- * per-token VALU GEMV. */
+ * and rounded to fp16, weights decoded exactly, fp32 accumulation): FP8 from
+ * MMQ_SEAM_GEMM_MIN_TOKENS tokens on in the GEMM-shaped seam kernel (128 x
+ * 256 tiles), else in the grouped kernel with one group (the same bits);
+ * fewer tokens run the block-scaled MFMA GEMV where its geometry fits, else
+ * the per-token VALU GEMV. */
 constexpr int MMQ_MFMA_MIN_TOKENS = 32;
+constexpr int MMQ_SEAM_GEMM_MIN_TOKENS = 128;
 
 static int enqueue_mmq(const DSV4QMat &d, int fmt, const float *x, float *y, int nt, hipStream_t st)
 {
@@ -696,6 +699,14 @@ static int enqueue_mmq(const DSV4QMat &d, int fmt, const float *x, float *y, int
         uint16_t *x16 = (uint16_t *)g.x16.p;
         int *ex = (int *)((uint8_t *)g.x16.p + xb);
         HIPCHK(to_f16_rows_launch(x16, ex, x, nt, d.cols, st), "x fp16 launch");
+        if (fmt != FMT_FP4_E8M0 && nt >= MMQ_SEAM_GEMM_MIN_TOKENS && aligned16(d.w) &&
+            gemm_seam_ok(nt, d.rows, d.cols)) {
+            SeamGemmArgs sg;
+            sg.X = x16; sg.ex = ex; sg.W = (const uint8_t *)d.w; sg.Sw = d.s; sg.C = y;
+            sg.M = nt; sg.N = d.rows; sg.K = d.cols;
+            HIPCHK(gemm_seam_launch(sg, fmt == FMT_FP8_F32S, st), "seam GEMM launch");
+            return 0;
+        }
         GroupedArgs a;
         memset(&a, 0, sizeof a);
         a.m1 = d; a.nrows = nt; a.B = x16; a.bexp = ex; a.K = d.cols; a.N = d.rows; a.out = y;

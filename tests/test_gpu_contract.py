@@ -182,6 +182,61 @@ def test_mmq_n_token_groups(lib, pkg, oracle, nt, fmt):
     m.drop()
 
 
+# ------------------------------------------------------ seam GEMM (FP8) ----
+
+def _fp8_resident(lib, pkg, oracle, fmt, rng, rows, cols):
+    if fmt == "fp8":
+        W = e4m3_codes(rng, rows * cols)
+        S = rng.integers(112, 121, (rows // 128) * (cols // 128)).astype(np.uint8)
+        m = Resident(lib, pkg, pkg.DSV4_WFP8, W, S, rows, cols, 128, 128)
+        return m, lambda x, nt: oracle.fp8_n(W, S, x, rows, cols, 128, 128, nt)
+    w = (rng.standard_normal((rows, cols)) * 0.02).astype(np.float32)
+    W, S = oracle.quant_fp8_blk128(w)
+    m = Resident(lib, pkg, pkg.DSV4_WFP8_F32S, W, S, rows, cols, 128, 128)
+    return m, lambda x, nt: oracle.fp8f_n(W, S, x, rows, cols, 128, 128, nt)
+
+
+@pytest.mark.parametrize("rows,cols,nt", [
+    (256, 1024, 128),     # one full 128-token tile
+    (384, 512, 200),      # a partial token tile and a 128-row feature tail
+    (1024, 2048, 160),
+])
+@pytest.mark.parametrize("fmt", ["fp8", "fp8f"])
+def test_seam_gemm_shapes(lib, pkg, oracle, rows, cols, nt, fmt):
+    """128 tokens and more on FP8 weights: the GEMM-shaped seam kernel
+    (128 x 256 tiles, fp16 tokens, weights decoded in registers) against the
+    oracle, every token within 1e-3."""
+    rng = np.random.default_rng(rows + cols + nt + len(fmt))
+    m, want_of = _fp8_resident(lib, pkg, oracle, fmt, rng, rows, cols)
+    x = rng.standard_normal(nt * cols).astype(np.float32)
+    got = lib.mmq_n(m.desc, x, nt).reshape(nt, rows)
+    want = want_of(x, nt).reshape(nt, rows)
+    for t in range(nt):
+        e = rel_l2(got[t], want[t])
+        assert e <= REL_L2_TOL, f"token {t}: rel L2 {e:.3e}"
+    m.drop()
+
+
+@pytest.mark.parametrize("fmt", ["fp8", "fp8f"])
+def test_seam_gemm_bits_equal_grouped_form(lib, pkg, oracle, fmt):
+    """The seam kernel (128 tokens) and the grouped kernel's dense form (127
+    tokens) run the same MFMA steps and block promotions: every one of the
+    first 127 tokens' outputs is bit for bit the same in both, including
+    rows beyond fp16 (|x| 1e5) and below its normal range (1e-9)."""
+    rows, cols = 512, 2048
+    rng = np.random.default_rng(128 + len(fmt))
+    m, _ = _fp8_resident(lib, pkg, oracle, fmt, rng, rows, cols)
+    x = rng.standard_normal((128, cols)).astype(np.float32)
+    x[0] *= 1e5
+    x[1] *= 1e-9
+    x[2] = 0.0
+    x = np.ascontiguousarray(x.reshape(-1))
+    big = lib.mmq_n(m.desc, x, 128).reshape(128, rows)
+    small = lib.mmq_n(m.desc, x, 127).reshape(127, rows)
+    assert np.array_equal(bits(big[:127]), bits(small))
+    m.drop()
+
+
 # ------------------------------------------------ 0 means the whole result ----
 
 def test_scale_byte_outside_fp16_range_returns_minus1(lib, pkg, oracle):
@@ -208,12 +263,12 @@ def test_scale_byte_outside_fp16_range_returns_minus1(lib, pkg, oracle):
     m2.drop()
 
 
-@pytest.mark.parametrize("fmt", ["fp8f", "fp4"])
-def test_seam_large_and_tiny_rows(lib, pkg, oracle, fmt):
+@pytest.mark.parametrize("fmt,nt", [("fp8f", 40), ("fp4", 40), ("fp8f", 136)])
+def test_seam_large_and_tiny_rows(lib, pkg, oracle, fmt, nt):
     """The nt >= 32 seam on rows an unscaled fp16 cast would break: |x| up to
     1e5 (beyond fp16), rows scaled by 1e-9 (below fp16's normal range), an
     all-zero row and a row of fp32 subnormals; every row within 1e-3."""
-    rows, cols, nt = 256, 1024, 40
+    rows, cols = 256, 1024
     rng = np.random.default_rng(5)
     w = (rng.standard_normal((rows, cols)) * 0.02).astype(np.float32)
     x = rng.standard_normal((nt, cols)).astype(np.float32)
