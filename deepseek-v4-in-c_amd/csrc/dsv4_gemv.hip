@@ -196,4 +196,66 @@ hipError_t gemv_launch(int fmt, const GemvArgs &a, hipStream_t st)
     }
 }
 
+/* ------------------------------------------------- generic geometry --- */
+
+/* Any block geometry (blk_r >= 1 rows x blk_c >= 1 columns per scale, any
+ * column count, rows of any width): the reference's generic bodies of fp8_n
+ * and fp4_n (src/10_compute/dsv4_matmul_fp8.c:158-176,
+ * src/10_compute/dsv4_matmul_fp4.c:143-162), which only fixtures and rows
+ * wider than the fast kernels' limits reach. One wave per output row: for
+ * each block of blk_c columns the lanes' products are summed (lane order
+ * over the block, then a butterfly), the block sum times its scale is added
+ * to the row's total in block order. */
+template <int FMT>
+__global__ __launch_bounds__(256) void k_gemv_generic(GemvGenArgs a)
+{
+    const int lane = threadIdx.x & 63;
+    const int o = blockIdx.x * 4 + wave_in_group();
+    if (o >= a.rows) return;
+    const int scg = (a.cols + a.blk_c - 1) / a.blk_c;
+    const size_t srow = (size_t)(o / a.blk_r) * (size_t)scg;
+    const size_t rb = FMT == FMT_GEN_FP4 ? (size_t)a.cols / 2 : (size_t)a.cols;
+    const uint8_t *wr = a.W + (size_t)o * rb;
+    for (int t = 0; t < a.nt; t++) {
+        const float *xt = a.x + (size_t)t * a.cols;
+        float total = 0.0f;
+        int bi = 0;
+        for (int c0 = 0; c0 < a.cols; c0 += a.blk_c, bi++) {
+            const int n = min(a.blk_c, a.cols - c0);
+            float d = 0.0f;
+            for (int i = lane; i < n; i += 64) {
+                const int c = c0 + i;
+                float w;
+                if constexpr (FMT == FMT_GEN_FP4) {
+                    const f32x2 p = dev_e2m1x2<0>((uint32_t)wr[c >> 1]);
+                    w = (c & 1) ? p.y : p.x;
+                } else {
+                    w = dev_e4m3x2<false>((uint32_t)wr[c]).x;
+                }
+                d = fmaf(w, xt[c], d);
+            }
+#pragma unroll
+            for (int sh = 32; sh >= 1; sh >>= 1) d += __shfl_xor(d, sh, 64);
+            const float sc = FMT == FMT_GEN_FP8F ? ld_f32(a.S, srow + bi) : dev_e8m0(ld_u8(a.S, srow + bi));
+            total = total + d * sc;
+        }
+        if (lane == 0) a.y[(size_t)t * a.rows + o] = total;
+    }
+}
+
+hipError_t gemv_generic_launch(int fmt, const GemvGenArgs &a, hipStream_t st)
+{
+    if (a.rows <= 0 || a.cols <= 0 || a.blk_r <= 0 || a.blk_c <= 0 || a.nt <= 0 ||
+        (fmt == FMT_GEN_FP4 && a.cols % 2))
+        return hipErrorInvalidValue;
+    const dim3 grid((unsigned)((a.rows + 3) / 4)), block(256);
+    switch (fmt) {
+    case FMT_GEN_FP8: hipLaunchKernelGGL(k_gemv_generic<FMT_GEN_FP8>, grid, block, 0, st, a); break;
+    case FMT_GEN_FP8F: hipLaunchKernelGGL(k_gemv_generic<FMT_GEN_FP8F>, grid, block, 0, st, a); break;
+    case FMT_GEN_FP4: hipLaunchKernelGGL(k_gemv_generic<FMT_GEN_FP4>, grid, block, 0, st, a); break;
+    default: return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
+}
+
 } // namespace dsv4

@@ -19,6 +19,11 @@ enum {
     FMT_FP8_F32S = 1, /* DSV4_WFP8_F32S, blk_c == 128 */
     FMT_FP4_E8M0 = 2, /* DSV4_WFP4, blk_c == 32       */
     FMT_BF16 = 3,     /* DSV4_WBF16, no scales, cols % 8 == 0 */
+    /* any other block geometry (and rows wider than the fast kernels take),
+     * on the generic VALU matvec only */
+    FMT_GEN_FP8 = 4,  /* DSV4_WFP8                    */
+    FMT_GEN_FP8F = 5, /* DSV4_WFP8_F32S               */
+    FMT_GEN_FP4 = 6,  /* DSV4_WFP4, cols even         */
 };
 
 /* Status bits a kernel may raise in the device status word. */
@@ -47,6 +52,16 @@ static inline int qmat_fmt(const DSV4QMat *m)
         return FMT_FP8_F32S;
     if (m->wdt == DSV4_WFP4 && m->blk_c == 32 && (m->cols % 32) == 0)
         return FMT_FP4_E8M0;
+    return -1;
+}
+
+/* The generic-geometry format of a packed matrix, or -1 */
+static inline int qmat_fmt_generic(const DSV4QMat *m)
+{
+    if (!m || m->rows <= 0 || m->cols <= 0 || m->blk_r <= 0 || m->blk_c <= 0) return -1;
+    if (m->wdt == DSV4_WFP8) return FMT_GEN_FP8;
+    if (m->wdt == DSV4_WFP8_F32S) return FMT_GEN_FP8F;
+    if (m->wdt == DSV4_WFP4) return (m->cols % 2) == 0 ? FMT_GEN_FP4 : -1;
     return -1;
 }
 
@@ -85,6 +100,18 @@ struct GemvArgs {
     int x_ld, y_ld;     /* floats between tokens    */
 };
 hipError_t gemv_launch(int fmt, const GemvArgs &a, hipStream_t st);
+
+/* y[t * rows + o] for t < nt, any block geometry (FMT_GEN_*): W rows of cols
+ * e4m3 bytes or cols / 2 e2m1 bytes, scales [ceil(rows / blk_r)][ceil(cols /
+ * blk_c)] (E8M0 bytes, or fp32 for FMT_GEN_FP8F), x [nt][cols]. */
+struct GemvGenArgs {
+    const uint8_t *W;
+    const void *S;
+    const float *x;
+    float *y;
+    int rows, cols, blk_r, blk_c, nt;
+};
+hipError_t gemv_generic_launch(int fmt, const GemvGenArgs &a, hipStream_t st);
 
 /* y[t*y_ld + o] = (float) sum_c (double) bf16(W[o][c]) * (double) x[t*x_ld + c]
  * for t < nt: BF16 weights (row pitch 2 * cols bytes, 16-byte aligned, cols %

@@ -204,26 +204,38 @@ const void *translate(const void *p, size_t bytes)
 bool aligned16(const void *p) { return ((uintptr_t)p & 15u) == 0; }
 
 /* Check a descriptor the GPU path can run and compute its byte sizes. */
-int check_qmat(const DSV4QMat *m, const char *what, int *fmt)
+/* allow_generic (the matvec entry points): a packed matrix of any other
+ * block geometry, or with rows wider than the fast kernels take, gets its
+ * FMT_GEN_* format (the generic matvec) instead of a refusal. */
+int check_qmat(const DSV4QMat *m, const char *what, int *fmt, bool allow_generic = false)
 {
     if (!m) return fail("%s: NULL matrix", what);
     *fmt = qmat_fmt(m);
+    if (*fmt < 0 && allow_generic) *fmt = qmat_fmt_generic(m);
     if (*fmt < 0)
         return fail("%s: unsupported geometry wdt=%d %dx%d blk %dx%d", what,
                     m->wdt, m->rows, m->cols, m->blk_r, m->blk_c);
+    if (*fmt >= FMT_GEN_FP8) return 0;
     /* FP8 up to 8192 columns, FP4 up to 16384, BF16 up to 8192 */
     const int lim = *fmt == FMT_BF16 ? 16384 : 8192;
-    if (qmat_row_bytes(m) > lim)
+    if (qmat_row_bytes(m) > lim) {
+        if (allow_generic && *fmt != FMT_BF16) {
+            *fmt = qmat_fmt_generic(m);
+            return 0;
+        }
         return fail("%s: rows wider than %d bytes are not supported", what, lim);
+    }
     return 0;
 }
 
 /* Host descriptor -> descriptor with resident device pointers (BF16 has no
  * scales). */
-int resident(const DSV4QMat *m, DSV4QMat *out, const char *what)
+int resident(const DSV4QMat *m, DSV4QMat *out, const char *what, bool allow_generic = false,
+             int *fmt_out = nullptr)
 {
     int fmt;
-    if (check_qmat(m, what, &fmt)) return -1;
+    if (check_qmat(m, what, &fmt, allow_generic)) return -1;
+    if (fmt_out) *fmt_out = fmt;
     *out = *m;
     out->w = translate(m->w, qmat_w_bytes(m));
     out->s = fmt == FMT_BF16 ? nullptr : translate(m->s, qmat_s_bytes(m));
@@ -684,6 +696,13 @@ constexpr int MMQ_SEAM_GEMM_MIN_TOKENS = 128;
 
 static int enqueue_mmq(const DSV4QMat &d, int fmt, const float *x, float *y, int nt, hipStream_t st)
 {
+    if (fmt >= FMT_GEN_FP8) {
+        GemvGenArgs ga;
+        ga.W = (const uint8_t *)d.w; ga.S = d.s; ga.x = x; ga.y = y;
+        ga.rows = d.rows; ga.cols = d.cols; ga.blk_r = d.blk_r; ga.blk_c = d.blk_c; ga.nt = nt;
+        HIPCHK(gemv_generic_launch(fmt, ga, st), "generic gemv launch");
+        return 0;
+    }
     if (fmt == FMT_BF16) {
         GemvBf16Args b;
         b.W = (const uint16_t *)d.w; b.x = x; b.y = y;
@@ -732,9 +751,9 @@ int dsv4_hip_mmq_n(float *y, const float *x, const DSV4QMat *m, int nt)
     if (nt <= 0) return 0;
     if (!x || !y) return fail("mmq_n: NULL x or y");
     DSV4QMat d;
-    if (resident(m, &d, "mmq_n")) return -1;
+    int fmt;
+    if (resident(m, &d, "mmq_n", true, &fmt)) return -1;
     host_call();
-    const int fmt = qmat_fmt(m);
     const size_t xb = (size_t)nt * m->cols * 4, yb = (size_t)nt * m->rows * 4;
     HIPCHK(g.x.need(xb), "x staging");
     HIPCHK(g.y.need(yb), "y staging");
@@ -757,7 +776,7 @@ int dsv4_hip_mmq_n_dev(float *y, const float *x, const DSV4QMat *m, int nt,
     if (usable()) return -1;
     if (nt <= 0) return 0;
     int fmt;
-    if (check_qmat(m, "mmq_n_dev", &fmt)) return -1;
+    if (check_qmat(m, "mmq_n_dev", &fmt, true)) return -1;
     if (!x || !y || !m->w || (fmt != FMT_BF16 && !m->s)) return fail("mmq_n_dev: NULL pointer");
     if (!aligned16(x) || !aligned16(m->w)) return fail("mmq_n_dev: x and W must be 16-byte aligned");
     dev_call();
@@ -775,7 +794,7 @@ int dsv4_hip_mmq_multi_dev(const DSV4HipJob *jobs, int njobs, void *stream)
         const DSV4HipJob &jb = jobs[j];
         if (jb.n < 0) return fail("mmq_multi_dev: job %d has n = %d", j, jb.n);
         if (jb.n == 0) continue;
-        if (check_qmat(jb.m, "mmq_multi_dev", &fmts[j])) return -1;
+        if (check_qmat(jb.m, "mmq_multi_dev", &fmts[j], true)) return -1;
         if (!jb.x || !jb.y || !jb.m->w || (fmts[j] != FMT_BF16 && !jb.m->s))
             return fail("mmq_multi_dev: job %d has a NULL pointer", j);
         if (!aligned16(jb.x) || !aligned16(jb.m->w))

@@ -100,8 +100,11 @@ void *dsv4_hip_device_ptr(const void *p);
  * dsv4_matmul.c:44-73): DSV4_WBF16 (no scales; products and sums in fp64
  * with one final rounding, as bf16_n does, src/10_compute/dsv4_matmul.c:
  * 88-113), DSV4_WFP8 (E8M0 128x128 or any blk_r x 128), DSV4_WFP8_F32S and
- * DSV4_WFP4 (E8M0 1x32). Rows up to 8192 bytes (FP8 and BF16 8192 columns,
- * FP4 16384). Other tags and geometries return -1. */
+ * DSV4_WFP4 (E8M0 1x32) on the fast kernels for rows up to 8192 bytes (FP8
+ * 8192 columns, FP4 16384); packed matrices of any other block geometry or
+ * wider rows on a generic matvec (the reference's generic bodies,
+ * dsv4_matmul_fp8.c:158-176, dsv4_matmul_fp4.c:143-162). BF16 rows up to
+ * 8192 columns with cols % 8 == 0; other tags and geometries return -1. */
 int  dsv4_hip_mmq_n(float *y, const float *x, const DSV4QMat *m, int nt);
 
 /* One token: dsv4_mmq (src/10_compute/dsv4_matmul.h:43). */

@@ -144,13 +144,72 @@ def test_fp4_16384_wide_rows(lib, pkg, oracle, nt):
     m.drop()
 
 
-def test_wider_rows_decline(lib, pkg):
-    rows, cols = 16, 8320
-    W = np.zeros(rows * cols, np.uint8)
-    S = np.full((1) * (cols // 128 + 1), 127, np.uint8)
+@pytest.mark.parametrize("nt", [1, 3])
+def test_wider_rows_take_the_generic_matvec(lib, pkg, oracle, nt):
+    """FP8 rows of 8,320 bytes (beyond the fast kernels' 8 KiB) run on the
+    generic matvec, against the oracle."""
+    rows, cols = 48, 8320
+    rng = np.random.default_rng(8320 + nt)
+    W = e4m3_codes(rng, rows * cols)
+    S = rng.integers(112, 121, (rows // 128 + 1) * (cols // 128)).astype(np.uint8)
+    x = rng.standard_normal(nt * cols).astype(np.float32)
     m = Resident(lib, pkg, pkg.DSV4_WFP8, W, S, rows, cols, 128, 128)
-    assert lib.mmq_n_rc(m.desc, np.zeros(cols, np.float32)) == -1
-    assert "8192" in lib.error()
+    check_close(lib.mmq_n(m.desc, x, nt), oracle.fp8_n(W, S, x, rows, cols, 128, 128, nt))
+    m.drop()
+
+
+def test_wider_bf16_rows_decline(lib, pkg):
+    rows, cols = 4, 8200
+    W = np.zeros(rows * cols, np.uint16)
+    d = pkg.qmat(pkg.DSV4_WBF16, W.ctypes.data, None, rows, cols, 0, 0)
+    assert lib.mmq_n_rc(d, np.zeros(cols, np.float32)) == -1
+    assert "16384" in lib.error()
+
+
+@pytest.mark.parametrize("fmt,rows,cols,blk_r,blk_c,nt", [
+    ("fp8", 40, 300, 1, 64, 1),        # per-row scales, ragged last block
+    ("fp8", 37, 1000, 3, 100, 3),      # three-row scale blocks, rows not a multiple
+    ("fp8f", 130, 512, 128, 64, 2),    # fp32 scales, 64-wide blocks
+    ("fp4", 33, 200, 2, 16, 2),        # 16-wide FP4 blocks
+    ("fp4", 20, 4096, 1, 64, 1),       # 64-wide FP4 blocks
+    ("fp4", 9, 34, 4, 30, 4),          # blocks that start on odd columns
+])
+def test_generic_geometry_shapes(lib, pkg, oracle, fmt, rows, cols, blk_r, blk_c, nt):
+    """Block geometries the fast kernels do not take (the reference's generic
+    bodies) through the drop-in, host and device entry points, against the
+    oracle's generic bodies."""
+    rng = np.random.default_rng(rows * 31 + cols + blk_c)
+    nsc = ((rows + blk_r - 1) // blk_r) * ((cols + blk_c - 1) // blk_c)
+    if fmt == "fp4":
+        W = rng.integers(0, 256, rows * cols // 2).astype(np.uint8)
+        S = rng.integers(120, 133, nsc).astype(np.uint8)
+        wdt = pkg.DSV4_WFP4
+        want_of = lambda x: oracle.fp4_n(W, S, x, rows, cols, blk_r, blk_c, nt)
+    elif fmt == "fp8":
+        W = e4m3_codes(rng, rows * cols)
+        S = rng.integers(112, 121, nsc).astype(np.uint8)
+        wdt = pkg.DSV4_WFP8
+        want_of = lambda x: oracle.fp8_n(W, S, x, rows, cols, blk_r, blk_c, nt)
+    else:
+        W = e4m3_codes(rng, rows * cols)
+        S = (rng.random(nsc) * 0.01 + 1e-3).astype(np.float32)
+        wdt = pkg.DSV4_WFP8_F32S
+        want_of = lambda x: oracle.fp8f_n(W, S, x, rows, cols, blk_r, blk_c, nt)
+    x = rng.standard_normal(nt * cols).astype(np.float32)
+    m = Resident(lib, pkg, wdt, W, S, rows, cols, blk_r, blk_c)
+    want = want_of(x)
+    check_close(lib.mmq_n(m.desc, x, nt), want)
+    # the device entry point on device copies
+    dW = torch.from_numpy(W).to(DEV)
+    dS = torch.from_numpy(S.view(np.uint8)).to(DEV)
+    dx = torch.from_numpy(x).to(DEV)
+    dy = torch.full((nt * rows,), float("nan"), device=DEV)
+    dd = pkg.qmat(wdt, dW.data_ptr(), dS.data_ptr(), rows, cols, blk_r, blk_c)
+    lib.mmq_n_dev(dy.data_ptr(), dx.data_ptr(), dd, nt)
+    torch.cuda.synchronize()
+    got = dy.cpu().numpy()
+    check_close(got, want)
+    assert np.array_equal(bits(got), bits(lib.mmq_n(m.desc, x, nt)))
     m.drop()
 
 

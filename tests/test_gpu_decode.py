@@ -158,17 +158,29 @@ def test_golden_reference_outputs(lib, pkg, name):
 
 
 @pytest.mark.parametrize("name", ["fp8_generic", "fp4_generic"])
-def test_unsupported_geometry_declines(lib, pkg, name):
-    """A block width other than 128 (FP8) / 32 (FP4) is the reference's generic
-    path; the GPU declines with -1 and a reason, so the caller keeps its CPU path
-    (src/80_prefill/dsv4_prefill_vk.h:37-41)."""
+def test_generic_geometry_reference_outputs(lib, pkg, name):
+    """A block width other than 128 (FP8) / 32 (FP4) takes the reference's
+    generic body (src/10_compute/dsv4_matmul_fp8.c:158-176,
+    dsv4_matmul_fp4.c:143-162); the GPU's generic matvec reproduces the
+    reference's own outputs for it (tests/golden) within the tolerance."""
     g = golden(name)
     rows, cols, br, bc, nt = (int(v) for v in g["dims"])
     wdt = pkg.DSV4_WFP8 if name.startswith("fp8") else pkg.DSV4_WFP4
     m = Resident(lib, pkg, wdt, g["W"], g["S"], rows, cols, br, bc)
-    assert lib.mmq_n_rc(m.desc, g["x"], nt) == -1
-    assert "unsupported" in lib.error()
+    y = lib.mmq_n(m.desc, g["x"], nt)
     m.drop()
+    check_close(y, g["y"])
+
+
+def test_unsupported_geometry_declines(lib, pkg):
+    """A BF16 matrix whose width is not a multiple of 8 has no GPU form: -1
+    and a reason, so the caller keeps its CPU path
+    (src/80_prefill/dsv4_prefill_vk.h:37-41)."""
+    rows, cols = 4, 12
+    W = np.zeros(rows * cols, np.uint16)
+    d = pkg.qmat(pkg.DSV4_WBF16, W.ctypes.data, None, rows, cols, 0, 0)
+    assert lib.mmq_n_rc(d, np.zeros(cols, np.float32)) == -1
+    assert "unsupported" in lib.error()
 
 
 def test_unregistered_weights_decline(lib, pkg):
