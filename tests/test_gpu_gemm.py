@@ -118,6 +118,40 @@ def test_gemm_config_shape_row_sample(lib, pkg, oracle):
     assert rel_l2(got[rows], want) <= REL_L2_TOL
 
 
+def test_gemm_config_shape_every_row_against_torch_fp32(lib, pkg, oracle):
+    """The same workload, every one of the 2,048 rows: the GEMM's bf16 output
+    against a float32 torch product (TF32 off) of the same e4m3 tokens and
+    weights, dequantized exactly (torch's float8_e4m3fn) with their block
+    scales, rounded to bf16; each row within 1e-3. The tokens are the device
+    quantizer's (dsv4_hip_quant_act_fp8_1x128_dev, whose codes and scales the
+    1x128 tests above hold to the oracle's)."""
+    rng = np.random.default_rng(33)
+    m, n, k = 2048, 4096, 4096
+    A = bf16_round(rng.standard_normal((m, k)).astype(np.float32))
+    W, S = make_weight(oracle, rng, n, k)
+    got = run_gemm(lib, pkg, A, W, S, n, k, True, out_bf16=1, a_bf16=1)
+    dA = dev(A)
+    Q = torch.empty(m * k, dtype=torch.uint8, device=DEV)
+    Sa = torch.empty(m * k // 128, dtype=torch.float32, device=DEV)
+    lib.quant_act_fp8_1x128_dev(Q.data_ptr(), Sa.data_ptr(), dA.data_ptr(), m, k)
+    torch.cuda.synchronize()
+    Af = Q.view(torch.float8_e4m3fn).float().reshape(m, k) * \
+        Sa.reshape(k // 128, m).t().repeat_interleave(128, dim=1)
+    Wf = dev(W).view(torch.float8_e4m3fn).float().reshape(n, k) * \
+        dev(S).reshape(n // 128, k // 128).repeat_interleave(128, dim=0).repeat_interleave(128, dim=1)
+    tf32 = torch.backends.cuda.matmul.allow_tf32
+    torch.backends.cuda.matmul.allow_tf32 = False
+    try:
+        ref = torch.mm(Af, Wf.t().contiguous()).bfloat16().float().cpu().numpy()
+    finally:
+        torch.backends.cuda.matmul.allow_tf32 = tf32
+    assert np.all(np.isfinite(got))
+    num = np.sqrt(np.sum((got.astype(np.float64) - ref) ** 2, axis=1))
+    den = np.sqrt(np.sum(ref.astype(np.float64) ** 2, axis=1))
+    worst = float(np.max(num / den))
+    assert worst <= REL_L2_TOL, f"worst row rel L2 {worst:.3e}"
+
+
 # The prefill attention side's FP8 projections at their real shapes
 # (src/00_base/dsv4_weights.h:68-98; called through src/80_prefill/
 # dsv4_prefill_proj.c:36-75 and dsv4_prefill_attn.c:26-110), with the

@@ -318,3 +318,101 @@ def test_mx_config4_full_workload_sampled(lib, pkg, oracle):
     hshared = P.HostExpert(hm[0], hm[1], hm[2])
     x = xs.view(n, H).cpu().numpy()
     check_mx(oracle, host, hshared, x, idx, w, got, mid, ms, pos, tokens, smid=smid)
+    _torch_all_tokens(lib, arena, keep, xs, idx, w, got, mid, ms, pos, smq, sms, n, H, I, topk, 10.0)
+
+
+def _e8m0(b):
+    return torch.exp2(b.float() - 127.0)
+
+
+def _torch_all_tokens(lib, arena, keep, xs, idx, w, got, mid, ms, pos, smq, sms, n, H, I, topk, limit):
+    """Every token and every (token, k) pair of the config-4 call against
+    float32 torch products on the device (TF32 off), expert by expert:
+      stage 1: SwiGLU(w1 . x, w3 . x) on the device's MXFP8 tokens
+      (dsv4_hip_quant_act_mxfp8_dev), expert weights dequantized exactly
+      (dsv4_hip_dequant_dev); each element of the GPU's mid, divided by its
+      E8M0 block scale, against the reference divided by the same scale: at
+      most 1e-3 of the elements more than half an e4m3 grid step off (a tie
+      straddled by the two fp32 sums), at most 1e-5 more than one step
+      (three in the subnormal range), and those by no more than 1e-4 of
+      their 32-block's largest value beyond the step -- the block-scaled
+      MFMA keeps about 14 bits below a group's largest product, so a small
+      mid value whose gate or up cancels down moves by that much (measured
+      on this workload: 2.6e-4, 2e-6 and 2.3e-5);
+      stage 2: the GPU's own mid through w2, the shared expert's down on its
+      own 1x128 mid, combined in k order; every token within 1e-3."""
+    P_ = n * topk
+    x8 = torch.empty(n * H, dtype=torch.uint8, device=DEV)
+    xs8 = torch.empty(n * H // 32, dtype=torch.uint8, device=DEV)
+    lib.quant_act_mxfp8_dev(x8.data_ptr(), xs8.data_ptr(), xs.data_ptr(), n, H)
+    torch.cuda.synchronize()
+    xq = x8.view(torch.float8_e4m3fn).float().reshape(n, H) * _e8m0(xs8.reshape(n, H // 32)).repeat_interleave(32, 1)
+    mq = torch.from_numpy(np.ascontiguousarray(mid)).to(DEV)
+    msd = torch.from_numpy(np.ascontiguousarray(ms)).to(DEV)
+    mscale = _e8m0(msd.reshape(P_, I // 32)).repeat_interleave(32, 1)
+    mvals = mq.reshape(P_, I).view(torch.float8_e4m3fn).float()           # e4m3 values, unscaled
+    mdeq = mvals * mscale
+    wtmp = torch.empty(H * I, dtype=torch.float32, device=DEV)
+    Y = torch.zeros((P_, H), dtype=torch.float32, device=DEV)
+    flat = idx.reshape(-1)
+    posd = np.asarray(pos)
+    n_far = n_el = n_over = 0
+    worst_steps = worst_rel = 0.0
+    tf32 = torch.backends.cuda.matmul.allow_tf32
+    torch.backends.cuda.matmul.allow_tf32 = False
+    try:
+        for e in np.unique(flat):
+            pairs = np.nonzero(flat == e)[0]
+            rows = torch.from_numpy(posd[pairs]).to(DEV)
+            toks = torch.from_numpy(pairs // topk).to(DEV)
+            d = arena.descs[int(e)]
+            lib.dequant_dev(wtmp.data_ptr(), d.w1)
+            g = torch.mm(xq[toks], wtmp.view(I, H).t())
+            lib.dequant_dev(wtmp.data_ptr(), d.w3)
+            u = torch.mm(xq[toks], wtmp.view(I, H).t())
+            u = torch.clamp(u, -limit, limit)
+            g = torch.clamp(g, max=limit)
+            ref = (g / (1.0 + torch.exp(-g))) * u
+            sc = mscale[rows]
+            v = ref / sc                                                  # in the block's scaled units
+            c = mvals[rows]
+            mag = torch.maximum(v.abs(), c.abs())
+            step = torch.exp2(torch.floor(torch.log2(torch.clamp(mag, min=2.0 ** -6))) - 3.0)
+            diff = (c - v).abs() / step
+            sub = mag < 2.0 ** -6
+            over = torch.where(sub, diff > 3.0, diff > 1.0)
+            bmax = v.abs().reshape(-1, I // 32, 32).amax(dim=2).repeat_interleave(32, 1)
+            absd = (c - v).abs() - step           # beyond one step, in scaled units
+            n_over += int(over.sum())
+            if bool(over.any()):
+                worst_rel = max(worst_rel, float((absd[over] / bmax[over]).max()))
+            n_far += int((diff > 0.5 + 1e-3).sum())
+            n_el += diff.numel()
+            worst_steps = max(worst_steps, float(diff.max()))
+            lib.dequant_dev(wtmp.data_ptr(), d.w2)
+            Y[rows] = torch.mm(mdeq[rows], wtmp.view(H, I).t())
+        # shared expert: e4m3 W2 with fp32 128x128 scales on its own 1x128 mid
+        W2s, S2s = keep[4], keep[5]
+        W2f = W2s.view(torch.float8_e4m3fn).float().reshape(H, I) * \
+            S2s.reshape(H // 128, I // 128).repeat_interleave(128, 0).repeat_interleave(128, 1)
+        smf = smq.view(torch.float8_e4m3fn).float().reshape(n, I) * \
+            sms.reshape(I // 128, n).t().repeat_interleave(128, 1)
+        ys = torch.mm(smf, W2f.t().contiguous())
+    finally:
+        torch.backends.cuda.matmul.allow_tf32 = tf32
+    stats = (f"{n_el} mid elements: {n_far} beyond half a step, {n_over} beyond one (three "
+             f"subnormal), worst {worst_steps:.2f} steps, worst excess {worst_rel:.3e} of the block max")
+    assert n_far <= max(2, 1e-3 * n_el), stats
+    assert n_over <= max(2, 1e-5 * n_el), stats
+    assert worst_rel <= 1e-4, stats
+    wd = torch.from_numpy(w).to(DEV)
+    pd = torch.from_numpy(posd.reshape(n, topk)).to(DEV)
+    out = torch.zeros((n, H), dtype=torch.float32, device=DEV)
+    for k in range(topk):
+        out = out + wd[:, k:k + 1] * Y[pd[:, k]]
+    out = out + ys
+    ref = out.cpu().numpy().astype(np.float64)
+    num = np.sqrt(np.sum((got.astype(np.float64) - ref) ** 2, axis=1))
+    den = np.sqrt(np.sum(ref ** 2, axis=1))
+    bad = np.nonzero(num / den > REL_L2_TOL)[0]
+    assert bad.size == 0, f"{bad.size} tokens beyond 1e-3, worst {float(np.max(num / den)):.3e} (token {int(np.argmax(num / den))})"
