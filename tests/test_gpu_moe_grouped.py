@@ -406,3 +406,56 @@ def test_grouped_config4_full_workload_sampled(lib, pkg, oracle):
         want = oracle.moe_combine(acc, w[t], oracle.expert_forward(hshared, x[j], 10.0))
         e = rel_l2(got[t], want)
         assert e <= REL_L2_TOL, f"token {t}: rel L2 {e:.3e} (max abs {max_abs(got[t], want):.3e})"
+    _torch_all_tokens_exact(lib, arena, keep, xs.view(n, H), idx, w, got, n, H, I, topk, 10.0)
+
+
+def _torch_swiglu(g, u, limit):
+    """src/10_compute/dsv4_ops.c:61-79 in torch (limit > 0)"""
+    u = torch.clamp(u, -limit, limit)
+    g = torch.clamp(g, max=limit)
+    return (g / (1.0 + torch.exp(-g))) * u
+
+
+def _torch_all_tokens_exact(lib, arena, keep, x, idx, w, got, n, H, I, topk, limit):
+    """Every one of the call's tokens against the unquantized computation in
+    float32 torch on the device (TF32 off): each routed expert's weights
+    dequantized exactly (dsv4_hip_dequant_dev), SwiGLU, w2, the FP8 shared
+    expert on fp32 x with its 128 x 128 scales, the k-order combine; every
+    token within 1e-3 (the exact path's contract: only x's and mid's fp16
+    rounding, 2^-11 relative, separate the two)."""
+    flat = idx.reshape(-1)
+    wtmp = torch.empty(H * I, dtype=torch.float32, device=DEV)
+    Y = torch.zeros((n * topk, H), dtype=torch.float32, device=DEV)
+
+    def fp8_mat(W, S, r, c):
+        return W.view(torch.float8_e4m3fn).float().reshape(r, c) * \
+            S.reshape(r // 128, c // 128).repeat_interleave(128, 0).repeat_interleave(128, 1)
+
+    tf32 = torch.backends.cuda.matmul.allow_tf32
+    torch.backends.cuda.matmul.allow_tf32 = False
+    try:
+        for e in np.unique(flat):
+            pairs = torch.from_numpy(np.nonzero(flat == e)[0]).to(DEV)
+            xe = x[pairs // topk]
+            d = arena.descs[int(e)]
+            lib.dequant_dev(wtmp.data_ptr(), d.w1)
+            g = torch.mm(xe, wtmp.view(I, H).t())
+            lib.dequant_dev(wtmp.data_ptr(), d.w3)
+            u = torch.mm(xe, wtmp.view(I, H).t())
+            lib.dequant_dev(wtmp.data_ptr(), d.w2)
+            Y[pairs] = torch.mm(_torch_swiglu(g, u, limit), wtmp.view(H, I).t())
+        sg = torch.mm(x, fp8_mat(keep[0], keep[1], I, H).t().contiguous())
+        su = torch.mm(x, fp8_mat(keep[2], keep[3], I, H).t().contiguous())
+        ys = torch.mm(_torch_swiglu(sg, su, limit), fp8_mat(keep[4], keep[5], H, I).t().contiguous())
+    finally:
+        torch.backends.cuda.matmul.allow_tf32 = tf32
+    wd = torch.from_numpy(w).to(DEV)
+    out = torch.zeros((n, H), dtype=torch.float32, device=DEV)
+    Yk = Y.view(n, topk, H)
+    for k in range(topk):
+        out = out + wd[:, k:k + 1] * Yk[:, k]
+    ref = (out + ys).cpu().numpy().astype(np.float64)
+    num = np.sqrt(np.sum((got.astype(np.float64) - ref) ** 2, axis=1))
+    den = np.sqrt(np.sum(ref ** 2, axis=1))
+    r = num / den
+    assert np.all(r <= REL_L2_TOL), f"{int(np.sum(r > REL_L2_TOL))} tokens beyond 1e-3, worst {float(r.max()):.3e}"
