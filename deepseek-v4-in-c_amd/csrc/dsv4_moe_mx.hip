@@ -116,10 +116,11 @@ constexpr int GX_LDS = GX<256>::LDS > GX<128>::LDS ? GX<256>::LDS : GX<128>::LDS
 constexpr int TH_TOK = 64;
 constexpr int TH_D = 2;                                /* stages in flight             */
 constexpr int TH_G = 2;                                /* stages per scale group       */
+constexpr int TH_SB = 2;                               /* scale groups per weight-scale block */
 constexpr int TH_B = TH_TOK * 128;                     /* token bytes of a half        */
 constexpr int TH_SLOT = 2 * TH_B;                      /* token bytes of a stage       */
 constexpr int TH_LDS = (TH_D + 1) * TH_SLOT + 2 * 1024;   /* token ring + 2 scale groups */
-constexpr int TH_KQ = 256 * 2 * TH_G;                  /* K granule of the thin kernel */
+constexpr int TH_KQ = 256 * TH_G * TH_SB;              /* K granule of the thin kernel */
 
 constexpr uint32_t RSRC_WORD3 = 0x00020000u;      /* raw dword buffer, gfx9 */
 constexpr uint32_t OOB_OFFSET = 0x80000000u;      /* beyond every buffer    */
@@ -339,14 +340,20 @@ __device__ __forceinline__ void mx_tile(const GroupedMxArgs &a, const DSV4QMat &
         s_dst = C::OFF_BS + 256 * (wave - 4);
     }
     const __amdgpu_buffer_rsrc_t rsc = buf_rsrc(sbase, sbytes);
+    /* Stages past the last are issued as out-of-range loads (zeros, no
+     * memory traffic) into a slot nobody reads: every wave and stage keeps
+     * the same count of loads. Re-reading the last stage instead cost an
+     * L2 fetch per repeat, the lines having been evicted by then. */
     auto issue = [&](int stg, uint8_t *buf) {
+        const uint32_t oob = stg > last ? OOB_OFFSET : 0u;
+        stg = min(stg, last);
 #pragma unroll
         for (int i = 0; i < C::NW; i++)
-            bdma16(rw, wofs[i], stg * C::WB, buf + 1024 * (wave * C::NW + i));
+            bdma16(rw, wofs[i] | oob, stg * C::WB, buf + 1024 * (wave * C::NW + i));
 #pragma unroll
         for (int i = 0; i < C::NB; i++)
-            bdma16(rb, bofs[i], stg * C::KS, buf + C::OFF_B + 1024 * (wave * C::NB + i));
-        bdma4(rsc, sofs, stg * 4, buf + s_dst);
+            bdma16(rb, bofs[i] | oob, stg * C::KS, buf + C::OFF_B + 1024 * (wave * C::NB + i));
+        bdma4(rsc, sofs | oob, stg * 4, buf + s_dst);
     };
 
     /* ---- this wave's share: 4 row tiles x NTMAX token groups ---- */
@@ -366,7 +373,7 @@ __device__ __forceinline__ void mx_tile(const GroupedMxArgs &a, const DSV4QMat &
         for (int u = 0; u < C::NTMAX; u++) acc[i][u] = f4v{0.0f, 0.0f, 0.0f, 0.0f};
 
 #pragma unroll
-    for (int s0 = 0; s0 < C::NST - 1; s0++) issue(min(s0, last), lds + s0 * C::STAGE);
+    for (int s0 = 0; s0 < C::NST - 1; s0++) issue(s0, lds + s0 * C::STAGE);
 
     auto run = [&](auto ntc) {
         constexpr int NT = decltype(ntc)::value;
@@ -380,7 +387,7 @@ __device__ __forceinline__ void mx_tile(const GroupedMxArgs &a, const DSV4QMat &
             {
                 int nb = st + C::NST - 1;
                 nb = nb >= C::NST ? nb - C::NST * (nb / C::NST) : nb;
-                issue(min(st + C::NST - 1, last), lds + nb * C::STAGE);
+                issue(st + C::NST - 1, lds + nb * C::STAGE);
             }
             if constexpr (NT > 0) {
                 /* Operands from LDS one token group ahead: the reads of
@@ -460,38 +467,43 @@ __global__ __launch_bounds__(512) void k_grouped_mx(GroupedMxArgs a, int thin_ro
  * a lane-pair exchange (DPP) then forms the MFMA operand of each half, in
  * which lane 16 g + r holds bytes 64 h + 16 g of row r. Half-line loads (16
  * rows x 64 bytes per instruction) made the L2 fetch many lines twice.
- * Scales move once per group of TH_G stages: a row's 16 scale bytes of a
- * group are one 16-byte load (lane (rr, gq) then takes byte gq of dword c for
- * half c of the group), the tokens' scale dwords one 4-byte-per-lane load
- * per wave (wave w stages dword w of every token).
+ * Weight scales move once per block of TH_SB groups of TH_G stages: lane
+ * (rr, gq) loads the 16 scale bytes of group gq of the block for row rr, so
+ * one instruction reads 64 contiguous bytes of each of 16 rows. At a group's
+ * first stage ds_bpermute hands every lane of row rr the dwords of that
+ * group (lane (rr, gq) then takes byte gq of dword c for half c). Loading a
+ * group's 16 bytes per row at every group instead touched each row's scale
+ * line once per group, and the L2, which turns over several times between
+ * two groups, fetched the line again each time (about 0.7 GB of extra reads
+ * for the gate/up weights of 194 experts at K = 4096). The tokens' scale
+ * dwords are one 4-byte-per-lane load per wave and group (wave w stages
+ * dword w of every token).
  * ---------------------------------------------------------------------- */
 template <bool SWIGLU, int NTG>
 __device__ __forceinline__ void thin_tile(const GroupedMxArgs &a, const DSV4QMat &m1, const DSV4QMat &m3,
                                           int r0, int ntok, int f0, uint8_t *lds)
 {
-    constexpr int D = TH_D, G = TH_G, U = 2 * TH_G;
+    constexpr int D = TH_D, G = TH_G, SB = TH_SB, U = G * SB;
     static_assert(U % D == 0 && D <= G, "ring depth");
     static_assert(2 * G == 4, "a scale group is four 128-wide halves: 16 scale bytes per row, one dword per wave");
     constexpr int NBL = (2 * NTG + 3) / 4;           /* 8-token loads per wave and half  */
     constexpr int VMW = 8 + 2 * NBL;                 /* VMEM per wave and stage            */
-    constexpr int VMG = 4 + 1;                       /* + per group: weight and token scales */
-    static_assert((D - 1) * VMW + VMG < 64, "vmcnt range");
+    constexpr int VMG = 1;                           /* + per group: token scales          */
+    constexpr int VMB = 4;                           /* + per block: weight scales         */
+    static_assert((D - 1) * VMW + VMG + VMB < 64, "vmcnt range");
     const int lane = threadIdx.x & 63, wave = wave_in_group();
     const int rr = lane & 15, gq = lane >> 4;
     const int K = a.K, N = a.N;
     const uint32_t rowb = (uint32_t)K / 2, srow = (uint32_t)K / 32;
-    const int nst = K / 256, last = nst - 1, glast = nst / G - 1;
+    const int nst = K / 256, last = nst - 1, glast = nst / G - 1, blast = nst / U - 1;
 
-    const __amdgpu_buffer_rsrc_t rw1 = buf_rsrc(m1.w, (uint32_t)N * rowb);
-    const __amdgpu_buffer_rsrc_t rs1 = buf_rsrc(m1.s, (uint32_t)N * srow);
-    const __amdgpu_buffer_rsrc_t rw3 = buf_rsrc(SWIGLU ? m3.w : m1.w, (uint32_t)N * rowb);
-    const __amdgpu_buffer_rsrc_t rs3 = buf_rsrc(SWIGLU ? m3.s : m1.s, (uint32_t)N * srow);
-    const __amdgpu_buffer_rsrc_t rb = buf_rsrc(a.B, (uint32_t)a.nrows * (uint32_t)K);
-    const __amdgpu_buffer_rsrc_t rbs = buf_rsrc(a.BS, (uint32_t)a.nrows * srow);
+    const uint32_t wbytes = (uint32_t)N * rowb, sbytes = (uint32_t)N * srow;
+    const uint32_t bbytes = (uint32_t)a.nrows * (uint32_t)K, bsbytes = (uint32_t)a.nrows * srow;
+    const void *const w3p = SWIGLU ? m3.w : m1.w, *const s3p = SWIGLU ? m3.s : m1.s;
 
     /* weights: instruction j of tile i, lane 16 g + 2 r' + h reads 16 bytes
      * of row 2 r' + j at byte 64 h + 16 g of the stage's 128; scales: lane
-     * (rr, gq) the 16 scale bytes of row rr */
+     * (rr, gq) the 16 scale bytes of group gq of a block of row rr */
     uint32_t wo[4][2], so[4];
     const bool odd = lane & 1;
 #pragma unroll
@@ -501,7 +513,7 @@ __device__ __forceinline__ void thin_tile(const GroupedMxArgs &a, const DSV4QMat
         for (int j = 0; j < 2; j++)
             wo[i][j] = (uint32_t)(base + 2 * (rr >> 1) + j) * rowb + 64u * (uint32_t)(lane & 1) +
                        16u * (uint32_t)gq;
-        so[i] = (uint32_t)(base + rr) * srow;
+        so[i] = (uint32_t)(base + rr) * srow + 16u * (uint32_t)(gq % SB);   /* lanes gq >= SB repeat */
     }
     /* tokens: load q = NBL w + j of a half stages token rows 8 q .. 8 q + 7 */
     uint32_t bo[NBL];
@@ -525,14 +537,20 @@ __device__ __forceinline__ void thin_tile(const GroupedMxArgs &a, const DSV4QMat
         for (int u = 0; u < NTG; u++) acc[i][u] = f4v{0.0f, 0.0f, 0.0f, 0.0f};
 
     u32x4 aw[D][2][4];                               /* stage s in slot s % D: [instruction][tile] */
-    u32x4 ws[2][4];                                  /* scale group g in slot g % 2    */
+    u32x4 wsb[4];                                    /* the weight-scale block being used */
+    uint32_t ws[4];                                  /* the current group's scale bytes of lane (rr, gq): byte c for half c */
 
     /* The loads of stage t: weights into slot t % D (both halves of a row
      * tile back to back), at the first stage of a group that group's scales,
      * then the tokens of both halves into LDS slot lslot. Stages past the
-     * last repeat it, so every wave and stage issues the same count of
-     * loads. */
-    auto issue = [&](int t, int lslot, u32x4 (&w)[2][4], u32x4 (&wsg)[4], uint8_t *gslot, bool group) {
+     * last are out-of-range loads (zeros, no memory traffic), so every wave
+     * and stage issues the same count of loads without fetching the last
+     * stage's lines again. */
+    auto issue = [&](int t, int lslot, u32x4 (&w)[2][4], uint8_t *gslot, bool group, bool block) {
+        /* past the last stage every buffer is empty: each load is out of range */
+        const uint32_t live = t > last ? 0u : 1u;
+        const __amdgpu_buffer_rsrc_t rw1 = buf_rsrc(m1.w, live * wbytes), rw3 = buf_rsrc(w3p, live * wbytes);
+        const __amdgpu_buffer_rsrc_t rb = buf_rsrc(a.B, live * bbytes);
         const int tc = min(t, last);
         w[0][0] = __builtin_amdgcn_raw_buffer_load_b128(rw1, wo[0][0], tc * 128, 0);
         w[1][0] = __builtin_amdgcn_raw_buffer_load_b128(rw1, wo[0][1], tc * 128, 0);
@@ -542,14 +560,15 @@ __device__ __forceinline__ void thin_tile(const GroupedMxArgs &a, const DSV4QMat
         w[1][2] = __builtin_amdgcn_raw_buffer_load_b128(rw3, wo[2][1], tc * 128, 0);
         w[0][3] = __builtin_amdgcn_raw_buffer_load_b128(rw3, wo[3][0], tc * 128, 0);
         w[1][3] = __builtin_amdgcn_raw_buffer_load_b128(rw3, wo[3][1], tc * 128, 0);
-        if (group) {
-            const int g = min(t / G, glast);
-            wsg[0] = __builtin_amdgcn_raw_buffer_load_b128(rs1, so[0], g * 16, 0);
-            wsg[1] = __builtin_amdgcn_raw_buffer_load_b128(rs1, so[1], g * 16, 0);
-            wsg[2] = __builtin_amdgcn_raw_buffer_load_b128(rs3, so[2], g * 16, 0);
-            wsg[3] = __builtin_amdgcn_raw_buffer_load_b128(rs3, so[3], g * 16, 0);
-            bdma4(rbs, bso, g * 16, gslot + 256 * wave);
+        if (block) {
+            const __amdgpu_buffer_rsrc_t rs1 = buf_rsrc(m1.s, live * sbytes), rs3 = buf_rsrc(s3p, live * sbytes);
+            const int b = min(t / U, blast);
+            wsb[0] = __builtin_amdgcn_raw_buffer_load_b128(rs1, so[0], b * (16 * SB), 0);
+            wsb[1] = __builtin_amdgcn_raw_buffer_load_b128(rs1, so[1], b * (16 * SB), 0);
+            wsb[2] = __builtin_amdgcn_raw_buffer_load_b128(rs3, so[2], b * (16 * SB), 0);
+            wsb[3] = __builtin_amdgcn_raw_buffer_load_b128(rs3, so[3], b * (16 * SB), 0);
         }
+        if (group) bdma4(buf_rsrc(a.BS, live * bsbytes), bso, min(t / G, glast) * 16, gslot + 256 * wave);
         uint8_t *buf = lds + lslot * TH_SLOT;
 #pragma unroll
         for (int h = 0; h < 2; h++)
@@ -560,7 +579,7 @@ __device__ __forceinline__ void thin_tile(const GroupedMxArgs &a, const DSV4QMat
 
 #pragma unroll
     for (int t = 0; t < D; t++) {
-        issue(t, t, aw[t], ws[(t / G) & 1], gs + ((t / G) & 1) * 1024, t % G == 0);
+        issue(t, t, aw[t], gs + ((t / G) & 1) * 1024, t % G == 0, t % U == 0);
         asm volatile("" ::: "memory");
     }
 
@@ -573,10 +592,28 @@ __device__ __forceinline__ void thin_tile(const GroupedMxArgs &a, const DSV4QMat
              * barrier every wave's tokens of stage s are in LDS and no wave
              * still reads the LDS slot of stage s - 1, which stage s + D
              * reuses (likewise the scale group slot two groups back) */
-            wait_vm<(D - 1) * VMW + VMG * (((q % G) + D - 1) / G)>();
+            wait_vm<(D - 1) * VMW + VMG * (((q % G) + D - 1) / G) + VMB * (((q % U) + D - 1) / U)>();
             __builtin_amdgcn_s_barrier();
             asm volatile("" ::: "memory");
             constexpr int p = (q / G) & 1;
+            if constexpr (q % G == 0) {
+                /* the group's scale dwords of row rr, from lane (rr, group);
+                 * of dword c this lane keeps byte gq, packed as byte c */
+                const int src = 4 * (rr + 16 * (q / G));
+                const uint32_t sel_lo = (uint32_t)gq | (uint32_t)(4 + gq) << 8 | 0x0C0C0000u;
+                const uint32_t sel_hi = 0x00000C0Cu | (uint32_t)gq << 16 | (uint32_t)(4 + gq) << 24;
+#pragma unroll
+                for (int i = 0; i < 4; i++) {
+                    uint32_t d[4];
+#pragma unroll
+                    for (int c = 0; c < 4; c++) {
+                        uint32_t w = wsb[i][c];
+                        asm volatile("" : "+v"(w));
+                        d[c] = (uint32_t)__builtin_amdgcn_ds_bpermute(src, (int)w);
+                    }
+                    ws[i] = __builtin_amdgcn_perm(d[1], d[0], sel_lo) | __builtin_amdgcn_perm(d[3], d[2], sel_hi);
+                }
+            }
             /* operands of both halves: an even lane keeps its own dword of
              * instruction 0 (half 0) and takes its odd neighbour's (half 1);
              * an odd lane keeps its own of instruction 1 (half 1) and takes
@@ -606,9 +643,9 @@ __device__ __forceinline__ void thin_tile(const GroupedMxArgs &a, const DSV4QMat
                 int sa[4];
 #pragma unroll
                 for (int i = 0; i < 4; i++) {
-                    uint32_t w = ws[p][i][c];
+                    uint32_t w = ws[i];
                     asm volatile("" : "+v"(w));
-                    sa[i] = scale_byte(w, gq);
+                    sa[i] = (int)((w >> (8 * c)) & 0xFFu);
                 }
                 const uint8_t *gsl = gs + p * 1024 + 256 * c;
 #pragma unroll
@@ -623,7 +660,7 @@ __device__ __forceinline__ void thin_tile(const GroupedMxArgs &a, const DSV4QMat
             asm volatile("" ::: "memory");
             const int nslot = slot == 0 ? D : slot - 1;
             constexpr int qn = q + D;                /* stage s + D within this or the next iteration */
-            issue(s0 + qn, nslot, aw[q % D], ws[(qn / G) & 1], gs + ((qn / G) & 1) * 1024, qn % G == 0);
+            issue(s0 + qn, nslot, aw[q % D], gs + ((qn / G) & 1) * 1024, qn % G == 0, qn % U == 0);
             asm volatile("" ::: "memory");
             slot = slot == D ? 0 : slot + 1;
         });
