@@ -1500,16 +1500,23 @@ static int enqueue_moe_grouped(float *out, const float *x, int n, const DSV4Expe
     ra.row_k = nullptr;
     ra.chist = (int *)(ws + o_ch);
     ra.status = g.st;
-    /* x to fp16 on the side stream, beside the routing permutation on this
-     * one (neither reads the other's output); the shared expert, which needs
-     * only x16, follows it there, overlaps the routed launches and is joined
-     * before the combine */
+    /* A large x goes to fp16 on the side stream, beside the routing
+     * permutation on this one (neither reads the other's output), and this
+     * stream waits for it before the routed launches. A small one converts
+     * here first: the conversion then takes less than that cross-stream wait
+     * (about 10 us between kernels). Either way the shared expert, which
+     * needs only x16, runs on the side stream after it, overlaps the routed
+     * launches and is joined before the combine. */
+    const bool fork_x = (size_t)n * hidden > ((size_t)1 << 22);
+    if (!fork_x) HIPCHK(to_f16_rows_launch(x16, ex, x, n, hidden, st), "x fp16 launch");
     HIPCHK(hipEventRecord(g.fork, st), "fork record");
     HIPCHK(hipStreamWaitEvent(g.side, g.fork, 0), "fork wait");
-    HIPCHK(to_f16_rows_launch(x16, ex, x, n, hidden, g.side), "x fp16 launch");
-    HIPCHK(hipEventRecord(g.xq, g.side), "convert record");
+    if (fork_x) {
+        HIPCHK(to_f16_rows_launch(x16, ex, x, n, hidden, g.side), "x fp16 launch");
+        HIPCHK(hipEventRecord(g.xq, g.side), "convert record");
+    }
     HIPCHK(moe_route_launch(ra, st), "route launch");
-    HIPCHK(hipStreamWaitEvent(st, g.xq, 0), "convert wait");
+    if (fork_x) HIPCHK(hipStreamWaitEvent(st, g.xq, 0), "convert wait");
 
     float *ys = nullptr;
     if (shared) {
