@@ -250,14 +250,16 @@ __global__ __launch_bounds__(1024) void k_moe_route(RouteArgs a, int cpb)
     const int E = a.n_experts;
     const int nch = (a.npairs + 1023) / 1024;
     const int c_lo = blockIdx.x * cpb, c_hi = min(nch, c_lo + cpb);
-    for (int e = tid; e < MAX_ROUTE_EXPERTS; e += 1024) {
-        hist[e] = 0;
-        before[e] = 0;
-        for (int w = 0; w < 16; w++) wcnt[w][e] = 0;
+    int ev[ROUTE_BATCH];
+    /* the first batch of routing ids is in flight while the tables clear */
+    if (!PRECOUNT) route_load(ev, a, 0, nch, tid);
+    if (tid < E) {
+        hist[tid] = 0;
+        before[tid] = 0;
+        for (int w = 0; w < 16; w++) wcnt[w][tid] = 0;
     }
     __syncthreads();
     unsigned bad = 0;
-    int ev[ROUTE_BATCH];
     const int lane = tid & 63, wv = tid >> 6;
     const uint64_t below = lane ? (~0ull >> (64 - lane)) : 0ull;
     if constexpr (PRECOUNT) {
@@ -280,7 +282,7 @@ __global__ __launch_bounds__(1024) void k_moe_route(RouteArgs a, int cpb)
         }
     } else
     for (int c0 = 0; c0 < nch; c0 += ROUTE_BATCH) {
-        route_load(ev, a, c0, nch, tid);
+        if (c0) route_load(ev, a, c0, nch, tid);
 #pragma unroll
         for (int i = 0; i < ROUTE_BATCH; i++) {
             if (c0 + i >= nch) break;                              /* uniform */
@@ -301,27 +303,33 @@ __global__ __launch_bounds__(1024) void k_moe_route(RouteArgs a, int cpb)
     const int cnt = tid < E ? hist[tid] : 0;
     const int tls = (cnt + a.tile_rows - 1) / a.tile_rows;
     {
+        /* only the waves that hold experts scan (E / 64 rounded up) */
         __shared__ int wsum[2][16];
+        const bool live = wv * 64 < E;
         int ir = cnt, it = tls;
+        if (live) {
 #pragma unroll
-        for (int d = 1; d < 64; d <<= 1) {
-            const int xr = __shfl_up(ir, d, 64), xt = __shfl_up(it, d, 64);
-            if (lane >= d) {
-                ir += xr;
-                it += xt;
+            for (int d = 1; d < 64; d <<= 1) {
+                const int xr = __shfl_up(ir, d, 64), xt = __shfl_up(it, d, 64);
+                if (lane >= d) {
+                    ir += xr;
+                    it += xt;
+                }
+            }
+            if (lane == 63) {
+                wsum[0][wv] = ir;
+                wsum[1][wv] = it;
             }
         }
-        if (lane == 63) {
-            wsum[0][wv] = ir;
-            wsum[1][wv] = it;
-        }
         __syncthreads();
-        for (int w = 0; w < wv; w++) {
-            ir += wsum[0][w];
-            it += wsum[1][w];
+        if (live) {
+            for (int w = 0; w < wv; w++) {
+                ir += wsum[0][w];
+                it += wsum[1][w];
+            }
+            scan_r[tid] = ir;
+            scan_t[tid] = it;
         }
-        scan_r[tid] = ir;
-        scan_t[tid] = it;
         __syncthreads();
     }
     /* each tile's bucket: the first expert whose inclusive tile prefix
@@ -351,9 +359,13 @@ __global__ __launch_bounds__(1024) void k_moe_route(RouteArgs a, int cpb)
     /* Rows inside a bucket in pair order (token-major, k-minor), as the
      * reference's counting sort places them: a pair's row is its bucket's
      * start, plus the pairs of the same expert in earlier chunks, plus those
-     * in lower waves of its chunk, plus those in lower lanes of its wave. */
+     * in lower waves of its chunk (each expert's per-wave counts turned into
+     * exclusive prefixes in place), plus those in lower lanes of its wave.
+     * A workgroup that counted every chunk in one batch already holds its
+     * routing ids. */
+    const bool have_ids = !PRECOUNT && c_lo == 0 && c_hi == nch && nch <= ROUTE_BATCH;
     for (int c0 = c_lo; c0 < c_hi; c0 += ROUTE_BATCH) {
-        route_load(ev, a, c0, c_hi, tid);
+        if (!have_ids) route_load(ev, a, c0, c_hi, tid);
 #pragma unroll
         for (int i = 0; i < ROUTE_BATCH; i++) {
             if (c0 + i >= c_hi) break;                             /* uniform */
@@ -364,9 +376,20 @@ __global__ __launch_bounds__(1024) void k_moe_route(RouteArgs a, int cpb)
             const int rank = __popcll(peers & below);
             if (ok && rank == __popcll(peers) - 1) wcnt[wv][e] = (unsigned short)(rank + 1);
             __syncthreads();
+            int tot = 0;
+            if (tid < E) {
+                unsigned short c[16];
+#pragma unroll
+                for (int w = 0; w < 16; w++) c[w] = wcnt[w][tid];
+#pragma unroll
+                for (int w = 0; w < 16; w++) {
+                    wcnt[w][tid] = (unsigned short)tot;
+                    tot += c[w];
+                }
+            }
+            __syncthreads();
             if (ok) {
-                int r = cur[e] + rank;
-                for (int w = 0; w < wv; w++) r += wcnt[w][e];
+                const int r = cur[e] + wcnt[wv][e] + rank;
                 a.pos[p] = r;
                 a.row_tok[r] = p / a.topk;
                 if (a.row_k) a.row_k[r] = p - (p / a.topk) * a.topk;
@@ -375,12 +398,9 @@ __global__ __launch_bounds__(1024) void k_moe_route(RouteArgs a, int cpb)
             }
             __syncthreads();
             if (tid < E) {
-                int s = 0;
-                for (int w = 0; w < 16; w++) {
-                    s += wcnt[w][tid];
-                    wcnt[w][tid] = 0;
-                }
-                cur[tid] += s;
+                cur[tid] += tot;
+#pragma unroll
+                for (int w = 0; w < 16; w++) wcnt[w][tid] = 0;
             }
             __syncthreads();
         }
