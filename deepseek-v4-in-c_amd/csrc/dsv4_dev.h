@@ -265,6 +265,7 @@ __device__ __forceinline__ f32x4 ld_f4(const float *p)
 #define DPP_ROW_MIRROR 0x140
 #define DPP_ROW_BCAST15 0x142
 #define DPP_ROW_BCAST31 0x143
+#define DPP_ROW_ROR8 0x128   /* row_ror:8, lane i of a row of 16 reads lane i ^ 8 */
 
 #define DPP_ADD(v, CTRL, ROWMASK)                                              \
     (v) = (v) + __int_as_float(__builtin_amdgcn_update_dpp(                    \
