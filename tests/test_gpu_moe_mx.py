@@ -215,6 +215,7 @@ def run_mx(lib, experts, shared, x, idx, w, hidden, inter, limit=10.0):
     (7, 2, 40, None, 512, 256, "fp8e8m0"),  # one-row buckets, most experts idle, E8M0 FP8 shared
     (256, 6, 24, 1.1, 2048, 1024, None),    # skewed buckets
     (130, 6, 12, None, 512, 384, "fp4"),    # FP4 shared expert (exact path), ragged token count
+    (40, 4, 6, None, 3072, 1024, None),     # thin tiles over three weight-scale blocks (K = 3072)
 ])
 def test_mx_shapes(lib, pkg, oracle, n, topk, ne, zipf, hidden, inter, with_shared):
     gen = torch.Generator().manual_seed(n + ne)
