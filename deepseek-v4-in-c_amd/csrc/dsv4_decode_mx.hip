@@ -372,27 +372,46 @@ struct AChunk {
     u32x4 q[FP4 ? 1 : 2];
 };
 
-template <bool FP4>
-__device__ __forceinline__ void ld_a(AChunk<FP4> &a, const uint8_t *wrow, int c, int g)
+/* FP4 chunk c of the lane's row (16 rows x 64 bytes per instruction) */
+__device__ __forceinline__ void ld_a(AChunk<true> &a, const uint8_t *wrow, int c, int g)
 {
-    if constexpr (FP4) {
-        a.q[0] = ld_stream16(wrow + 64 * c + 16 * g);
-    } else {
-        a.q[0] = ld_stream16(wrow + 128 * c + 16 * g);
-        a.q[1] = ld_stream16(wrow + 128 * c + 64 + 16 * g);
-    }
+    a.q[0] = ld_stream16(wrow + 64 * c + 16 * g);
+}
+
+/* FP8 chunk c of a 16-row tile as whole 128-byte lines: q[0] from rows 0-7
+ * (wlo: row r0 + lane % 8), q[1] from rows 8-15 (whi), lane r8 + 8 h + 16 g
+ * taking bytes 16 (4 h + g) of its rows' chunk; mfma_a trades halves between
+ * lanes i and i ^ 8 to form the operand of row lane % 16. (Loading the
+ * operand halves directly, bytes 16 g and 64 + 16 g, read 16 half lines per
+ * instruction.) */
+__device__ __forceinline__ void ld_a(AChunk<false> &a, const uint8_t *wlo, const uint8_t *whi, int c,
+                                     int lane)
+{
+    const int piece = 16 * (4 * ((lane >> 3) & 1) + (lane >> 4));
+    a.q[0] = ld_stream16(wlo + 128 * c + piece);
+    a.q[1] = ld_stream16(whi + 128 * c + piece);
 }
 
 template <bool FP4>
 __device__ __forceinline__ v4f mfma_a(const AChunk<FP4> &a, const v8i &b, const v4f &c, int sa, int sb)
 {
     v8i av;
-    av[0] = (int)a.q[0].x; av[1] = (int)a.q[0].y; av[2] = (int)a.q[0].z; av[3] = (int)a.q[0].w;
     if constexpr (FP4) {
+        av[0] = (int)a.q[0].x; av[1] = (int)a.q[0].y; av[2] = (int)a.q[0].z; av[3] = (int)a.q[0].w;
         av[4] = 0; av[5] = 0; av[6] = 0; av[7] = 0;
         return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(av, b, c, 4, 0, 0, sa, 0, sb);
     } else {
-        av[4] = (int)a.q[1].x; av[5] = (int)a.q[1].y; av[6] = (int)a.q[1].z; av[7] = (int)a.q[1].w;
+        /* row r8 + 8 h of lane group g wants bytes 16 g (half 0) and
+         * 64 + 16 g (half 1) of its chunk: rows 0-7 hold half 0 themselves
+         * and take half 1 from lane ^ 8; rows 8-15 the other way round */
+        const bool odd = (threadIdx.x >> 3) & 1;
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+            const int s0 = __builtin_amdgcn_mov_dpp((int)a.q[0][e], DPP_ROW_ROR8, 0xF, 0xF, false);
+            const int s1 = __builtin_amdgcn_mov_dpp((int)a.q[1][e], DPP_ROW_ROR8, 0xF, 0xF, false);
+            av[e] = odd ? s1 : (int)a.q[0][e];
+            av[4 + e] = odd ? (int)a.q[1][e] : s0;
+        }
         return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(av, b, c, 0, 0, 0, sa, 0, sb);
     }
 }
@@ -621,6 +640,8 @@ __global__ __launch_bounds__(256) void k_gemv_mx(GemvMxArgs a)
     const int g = lane >> 4;
     const int row = min(r0 + (lane & 15), a.rows - 1);
     const uint8_t *wrow = a.W + (size_t)row * a.row_bytes;
+    const uint8_t *wlo = a.W + (size_t)min(r0 + (lane & 7), a.rows - 1) * a.row_bytes;
+    const uint8_t *whi = a.W + (size_t)min(r0 + 8 + (lane & 7), a.rows - 1) * a.row_bytes;
     const size_t tab_bytes = (size_t)a.tpg * a.ncw * TAB_CHUNK + TAB_ZERO;
     uint8_t *tab = lds + wave * tab_bytes;
     float *red = (float *)(lds + KSLICES * tab_bytes);     /* [KSLICES][tpg][16] */
@@ -634,7 +655,10 @@ __global__ __launch_bounds__(256) void k_gemv_mx(GemvMxArgs a)
     DSV4_ORDER();
     AChunk<FP4> w[CPW];
 #pragma unroll
-    for (int j = 0; j < CPW; j++) ld_a<FP4>(w[j], wrow, cb0 + (j < ncw ? j : 0), g);
+    for (int j = 0; j < CPW; j++) {
+        if constexpr (FP4) ld_a(w[j], wrow, cb0 + (j < ncw ? j : 0), g);
+        else ld_a(w[j], wlo, whi, cb0 + (j < ncw ? j : 0), lane);
+    }
     DSV4_ORDER();
     store_units<UPL>(tab, xu, ntok, ncw, lane);
     v4f acc = mma_rows<FMT, CPW>(w, sc, lds_bsrc(tab, ntok, ncw, lane), ncw);
@@ -701,6 +725,7 @@ __device__ __forceinline__ void gateup_mx_body(const GateUpMxArgs &a)
     const int sc_cols = FP4 ? a.hidden / 32 : a.hidden / 128;
     const uint8_t *w1r = (const uint8_t *)e.w1.w + (size_t)row * row_bytes;
     const uint8_t *w3r = (const uint8_t *)e.w3.w + (size_t)row * row_bytes;
+    const size_t lo_off = (size_t)(r0 + (lane & 7)) * row_bytes, hi_off = lo_off + (size_t)8 * row_bytes;
 
     XUnits<UPL> xu;
     load_units<UPL>(xu, a.x, 0, 1, cb0, ncw, lane);
@@ -713,8 +738,13 @@ __device__ __forceinline__ void gateup_mx_body(const GateUpMxArgs &a)
 #pragma unroll
     for (int j = 0; j < CPW; j++) {
         const int c = cb0 + (j < ncw ? j : 0);
-        ld_a<FP4>(w1[j], w1r, c, g);
-        ld_a<FP4>(w3[j], w3r, c, g);
+        if constexpr (FP4) {
+            ld_a(w1[j], w1r, c, g);
+            ld_a(w3[j], w3r, c, g);
+        } else {
+            ld_a(w1[j], (const uint8_t *)e.w1.w + lo_off, (const uint8_t *)e.w1.w + hi_off, c, lane);
+            ld_a(w3[j], (const uint8_t *)e.w3.w + lo_off, (const uint8_t *)e.w3.w + hi_off, c, lane);
+        }
     }
     DSV4_ORDER();
     store_units<UPL>(tab, xu, 1, ncw, lane);
@@ -841,7 +871,7 @@ __global__ __launch_bounds__(1024) void k_down_mx(DownMxArgs a)
         AChunk<true> w[CPW];
         const uint8_t *wrow = (const uint8_t *)m.w + (size_t)row * row_bytes;
 #pragma unroll
-        for (int j = 0; j < CPW; j++) ld_a<true>(w[j], wrow, cb0 + (j < ncw ? j : 0), g);
+        for (int j = 0; j < CPW; j++) ld_a(w[j], wrow, cb0 + (j < ncw ? j : 0), g);
         DSV4_ORDER();
         v4f acc = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
