@@ -690,9 +690,12 @@ void *dsv4_hip_device_ptr(const void *p)
  * MMQ_SEAM_GEMM_MIN_TOKENS tokens on in the GEMM-shaped seam kernel (128 x
  * 256 tiles), else in the grouped kernel with one group (the same bits);
  * fewer tokens run the block-scaled MFMA GEMV where its geometry fits, else
- * the per-token VALU GEMV. */
+ * the per-token VALU GEMV. The seam kernel's tiles fill the device only
+ * from about 2048 tokens (4096 x 4096 FP8: 64 us from 128 to 1024 tokens,
+ * 79 us at 2048), the grouped form's 64-token tiles from far fewer (32 us
+ * at 128, 59 us at 1024, 82 us at 1536): the switch sits between. */
 constexpr int MMQ_MFMA_MIN_TOKENS = 32;
-constexpr int MMQ_SEAM_GEMM_MIN_TOKENS = 128;
+constexpr int MMQ_SEAM_GEMM_MIN_TOKENS = 1280;
 
 static int enqueue_mmq(const DSV4QMat &d, int fmt, const float *x, float *y, int nt, hipStream_t st)
 {

@@ -256,13 +256,13 @@ def _fp8_resident(lib, pkg, oracle, fmt, rng, rows, cols):
 
 
 @pytest.mark.parametrize("rows,cols,nt", [
-    (256, 1024, 128),     # one full 128-token tile
-    (384, 512, 200),      # a partial token tile and a 128-row feature tail
-    (1024, 2048, 160),
+    (256, 1024, 1280),    # ten full 128-token tiles
+    (384, 512, 1337),     # a partial token tile and a 128-row feature tail
+    (1024, 2048, 1296),
 ])
 @pytest.mark.parametrize("fmt", ["fp8", "fp8f"])
 def test_seam_gemm_shapes(lib, pkg, oracle, rows, cols, nt, fmt):
-    """128 tokens and more on FP8 weights: the GEMM-shaped seam kernel
+    """1280 tokens and more on FP8 weights: the GEMM-shaped seam kernel
     (128 x 256 tiles, fp16 tokens, weights decoded in registers) against the
     oracle, every token within 1e-3."""
     rng = np.random.default_rng(rows + cols + nt + len(fmt))
@@ -278,21 +278,22 @@ def test_seam_gemm_shapes(lib, pkg, oracle, rows, cols, nt, fmt):
 
 @pytest.mark.parametrize("fmt", ["fp8", "fp8f"])
 def test_seam_gemm_bits_equal_grouped_form(lib, pkg, oracle, fmt):
-    """The seam kernel (128 tokens) and the grouped kernel's dense form (127
-    tokens) run the same MFMA steps and block promotions: every one of the
-    first 127 tokens' outputs is bit for bit the same in both, including
-    rows beyond fp16 (|x| 1e5) and below its normal range (1e-9)."""
-    rows, cols = 512, 2048
+    """The seam kernel (1280 tokens, where the drop-in switches to it) and
+    the grouped kernel's dense form (1279 tokens) run the same MFMA steps and
+    block promotions: every one of the first 1279 tokens' outputs is bit for
+    bit the same in both, including rows beyond fp16 (|x| 1e5) and below its
+    normal range (1e-9)."""
+    rows, cols, nt = 512, 2048, 1280
     rng = np.random.default_rng(128 + len(fmt))
     m, _ = _fp8_resident(lib, pkg, oracle, fmt, rng, rows, cols)
-    x = rng.standard_normal((128, cols)).astype(np.float32)
+    x = rng.standard_normal((nt, cols)).astype(np.float32)
     x[0] *= 1e5
     x[1] *= 1e-9
     x[2] = 0.0
     x = np.ascontiguousarray(x.reshape(-1))
-    big = lib.mmq_n(m.desc, x, 128).reshape(128, rows)
-    small = lib.mmq_n(m.desc, x, 127).reshape(127, rows)
-    assert np.array_equal(bits(big[:127]), bits(small))
+    big = lib.mmq_n(m.desc, x, nt).reshape(nt, rows)
+    small = lib.mmq_n(m.desc, x, nt - 1).reshape(nt - 1, rows)
+    assert np.array_equal(bits(big[:nt - 1]), bits(small))
     m.drop()
 
 
@@ -322,7 +323,7 @@ def test_scale_byte_outside_fp16_range_returns_minus1(lib, pkg, oracle):
     m2.drop()
 
 
-@pytest.mark.parametrize("fmt,nt", [("fp8f", 40), ("fp4", 40), ("fp8f", 136)])
+@pytest.mark.parametrize("fmt,nt", [("fp8f", 40), ("fp4", 40), ("fp8f", 1288)])
 def test_seam_large_and_tiny_rows(lib, pkg, oracle, fmt, nt):
     """The nt >= 32 seam on rows an unscaled fp16 cast would break: |x| up to
     1e5 (beyond fp16), rows scaled by 1e-9 (below fp16's normal range), an
