@@ -623,6 +623,144 @@ __device__ __forceinline__ float qnan_f() { return __uint_as_float(0x7FC00000u);
 
 /* ------------------------------------------------------------- GEMV --- */
 
+/* x split once for every row block: unit u (eight elements; the four units
+ * of a 32-element block in one DPP quad) of token t, chunk c, written where
+ * store_units puts it, in token t's table of all nc chunks. */
+__global__ __launch_bounds__(256) void k_split_x_tab(uint8_t *tab, const float *x, int x_ld, int nt, int nc)
+{
+    const int units = nt * nc * 16;                        /* a multiple of 16: whole quads */
+    const int u0 = (int)blockIdx.x * 256 + (int)threadIdx.x;
+    const bool live = u0 < units;
+    const int u = live ? u0 : 0;
+    const int per = nc * 16;
+    const int t = u / per, rem = u - t * per, c = rem >> 4, q16 = rem & 15, kk = 8 * q16;
+    const float *src = x + (size_t)t * x_ld + (size_t)c * 128 + kk;
+    const f32x4 a = *(const f32x4 *)src, b = *(const f32x4 *)(src + 4);
+    float v[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+    uint32_t code[NPART][2];
+    int E[NPART];
+    split8(v, code, E);
+    if (!live) return;
+    uint8_t *cb = tab + ((size_t)t * nc + c) * TAB_CHUNK;
+    const int h = (kk & 63) >> 4, half = kk >> 6;
+#pragma unroll
+    for (int p = 0; p < NPART; p++)
+        *(uint2 *)(cb + (h * NPART + p) * 32 + half * 16 + (kk & 15)) = make_uint2(code[p][0], code[p][1]);
+    if ((q16 & 3) == 0) {
+#pragma unroll
+        for (int p = 0; p < NPART; p++) *(int *)(cb + TAB_DATA + ((q16 >> 2) * NPART + p) * 4) = E[p];
+    }
+}
+
+/* This wave's part of token group t0's split tables (ntok tokens, chunks
+ * cb0 .. cb0 + ncw - 1) from the table k_split_x_tab wrote, 16 bytes a lane:
+ * the loads, then (copy_tab_store) the LDS writes and the zero operand. */
+template <int NT, int CPW>
+struct TabCopy {
+    static constexpr int PER = (CPW * TAB_CHUNK / 16 + 63) / 64;   /* 16-byte pieces per lane and token */
+    u32x4 q[NT][PER];
+};
+
+template <int NT, int CPW>
+__device__ __forceinline__ void copy_tab_load(TabCopy<NT, CPW> &c, const uint8_t *tab, int nc, int t0, int ntok,
+                                              int cb0, int ncw, int lane)
+{
+    const int pieces = ncw * (TAB_CHUNK / 16);
+#pragma unroll
+    for (int t = 0; t < NT; t++)
+#pragma unroll
+        for (int i = 0; i < TabCopy<NT, CPW>::PER; i++) {
+            const int r = 64 * i + lane;
+            if (t < ntok && r < pieces)
+                c.q[t][i] = *(const u32x4 *)(tab + ((size_t)(t0 + t) * nc + cb0) * TAB_CHUNK + 16 * r);
+        }
+}
+
+template <int NT, int CPW>
+__device__ __forceinline__ void copy_tab_store(uint8_t *lt, const TabCopy<NT, CPW> &c, int ntok, int ncw, int lane)
+{
+    const int pieces = ncw * (TAB_CHUNK / 16);
+#pragma unroll
+    for (int t = 0; t < NT; t++)
+#pragma unroll
+        for (int i = 0; i < TabCopy<NT, CPW>::PER; i++) {
+            const int r = 64 * i + lane;
+            if (t < ntok && r < pieces) *(u32x4 *)(lt + (size_t)t * ncw * TAB_CHUNK + 16 * r) = c.q[t][i];
+        }
+    if (lane < TAB_ZERO / 4)
+        ((uint32_t *)(lt + (size_t)ntok * ncw * TAB_CHUNK))[lane] = lane == 8 ? E8M0_ONE : 0u;
+}
+
+/* The small-batch matvec on x split beforehand (k_split_x_tab): a workgroup
+ * owns 16 rows and token groups blockIdx.y * gpw .. + gpw - 1 of NT tokens;
+ * the rows' weight operands are loaded once and held while it walks its
+ * groups, each group's tables copied one group ahead. Every token's MFMA
+ * steps are those of k_gemv_mx, so its bits are too. (One token group per
+ * workgroup re-read the whole matrix per group: 31 tokens of a 4096 x 4096
+ * FP8 matrix in groups of two streamed 268 MB.) */
+template <int FMT, int CPW, int NT>
+__global__ __launch_bounds__(256) void k_gemv_mx_tab(GemvMxArgs a)
+{
+    extern __shared__ __align__(16) uint8_t lds[];
+    constexpr bool FP4 = FMT == FMT_FP4_E8M0;
+    const int lane = threadIdx.x & 63;
+    const int wave = wave_in_group();
+    const int r0 = blockIdx.x * 16;
+    const int ngroups = (a.nt + NT - 1) / NT;
+    const int g_lo = blockIdx.y * a.gpw, g_hi = min(ngroups, g_lo + a.gpw);
+    const int nc = a.cols / 128;
+    const int c0 = wave * a.ncw;
+    const int ncw = max(0, min(a.ncw, nc - c0));
+    const int cb0 = ncw > 0 ? c0 : 0;                      /* loads stay inside the row */
+    const int g = lane >> 4;
+    const int row = min(r0 + (lane & 15), a.rows - 1);
+    const uint8_t *wrow = a.W + (size_t)row * a.row_bytes;
+    const uint8_t *wlo = a.W + (size_t)min(r0 + (lane & 7), a.rows - 1) * a.row_bytes;
+    const uint8_t *whi = a.W + (size_t)min(r0 + 8 + (lane & 7), a.rows - 1) * a.row_bytes;
+    const size_t tab_bytes = (size_t)NT * a.ncw * TAB_CHUNK + TAB_ZERO;
+    uint8_t *tab = lds + wave * tab_bytes;
+    float *red = (float *)(lds + KSLICES * tab_bytes);     /* [KSLICES][NT][16] */
+    auto group_tokens = [&](int tg) { return min(NT, a.nt - tg * NT); };
+
+    TabCopy<NT, CPW> tc;
+    copy_tab_load<NT, CPW>(tc, a.tab, nc, g_lo * NT, group_tokens(g_lo), cb0, ncw, lane);
+    DSV4_ORDER();
+    AScales<FMT, CPW> sc;
+    ld_ascales<FMT, CPW>(sc, a.S, a.sc_cols, a.blk_r, row, r0, cb0, ncw, g, a.rows - 1);
+    DSV4_ORDER();
+    AChunk<FP4> w[CPW];
+#pragma unroll
+    for (int j = 0; j < CPW; j++) {
+        if constexpr (FP4) ld_a(w[j], wrow, cb0 + (j < ncw ? j : 0), g);
+        else ld_a(w[j], wlo, whi, cb0 + (j < ncw ? j : 0), lane);
+    }
+    DSV4_ORDER();
+    for (int tg = g_lo; tg < g_hi; tg++) {
+        const int t0 = tg * NT, ntok = group_tokens(tg);
+        TabCopy<NT, CPW> tn;
+        if (tg + 1 < g_hi) copy_tab_load<NT, CPW>(tn, a.tab, nc, t0 + NT, group_tokens(tg + 1), cb0, ncw, lane);
+        copy_tab_store<NT, CPW>(tab, tc, ntok, ncw, lane);
+        v4f acc = mma_rows<FMT, CPW>(w, sc, lds_bsrc(tab, ntok, ncw, lane), ncw);
+        sum_parts(acc);
+        const int col = lane & 15;
+        if ((col & 3) == 0 && (col >> 2) < ntok) {
+#pragma unroll
+            for (int e = 0; e < 4; e++) red[(wave * NT + (col >> 2)) * 16 + 4 * g + e] = acc[e];
+        }
+        __syncthreads();
+        const int tid = threadIdx.x;
+        if (tid < ntok * 16) {
+            const int t = tid >> 4, rr = tid & 15;
+            float s = red[t * 16 + rr];
+#pragma unroll
+            for (int k = 1; k < KSLICES; k++) s += red[(k * NT + t) * 16 + rr];
+            if (r0 + rr < a.rows) a.y[(size_t)(t0 + t) * a.y_ld + r0 + rr] = s;
+        }
+        __syncthreads();                                   /* red is rewritten next group */
+        if (tg + 1 < g_hi) tc = tn;
+    }
+}
+
 template <int FMT, int CPW, int NT>
 __global__ __launch_bounds__(256) void k_gemv_mx(GemvMxArgs a)
 {
@@ -1883,10 +2021,21 @@ hipError_t gemv_mx_nt(GemvMxArgs a, hipStream_t st)
     a.tpg = NT;
     const size_t tab = (size_t)NT * a.ncw * TAB_CHUNK + TAB_ZERO;
     const size_t lds = KSLICES * tab + (size_t)KSLICES * NT * 16 * 4;
-    const dim3 grid((unsigned)((a.rows + 15) / 16), (unsigned)((a.nt + NT - 1) / NT));
-    hipLaunchKernelGGL((k_gemv_mx<FMT, CPW, NT>), grid, dim3(256), lds, st, a);
+    const int row_blocks = (a.rows + 15) / 16, ngroups = (a.nt + NT - 1) / NT;
+    if (a.tab) {
+        /* token groups split over enough workgroups to fill the device
+         * (about 512), each walking its share with the weights held */
+        const int parts = max(1, min(ngroups, (512 + row_blocks - 1) / row_blocks));
+        a.gpw = (ngroups + parts - 1) / parts;
+        const dim3 grid((unsigned)row_blocks, (unsigned)((ngroups + a.gpw - 1) / a.gpw));
+        hipLaunchKernelGGL((k_gemv_mx_tab<FMT, CPW, NT>), grid, dim3(256), lds, st, a);
+    } else {
+        const dim3 grid((unsigned)row_blocks, (unsigned)ngroups);
+        hipLaunchKernelGGL((k_gemv_mx<FMT, CPW, NT>), grid, dim3(256), lds, st, a);
+    }
     return hipGetLastError();
 }
+
 
 template <int FMT, int CPW>
 hipError_t gemv_mx_k(GemvMxArgs a, hipStream_t st)
@@ -1976,6 +2125,18 @@ hipError_t gateup_mx_fmt(const GateUpMxArgs &a, hipStream_t st)
 }
 
 } // namespace
+
+size_t gemv_tab_chunk_bytes() { return TAB_CHUNK; }
+
+hipError_t split_x_tab_launch(uint8_t *tab, const float *x, int x_ld, int nt, int cols, hipStream_t st)
+{
+    if (nt <= 0 || cols <= 0 || cols % 128 || (long)nt * (cols / 128) * 16 >= (1L << 31))
+        return hipErrorInvalidValue;
+    const int nc = cols / 128;
+    const int units = nt * nc * 16;
+    hipLaunchKernelGGL(k_split_x_tab, dim3((unsigned)((units + 255) / 256)), dim3(256), 0, st, tab, x, x_ld, nt, nc);
+    return hipGetLastError();
+}
 
 /* chunks per wave for a K of `cols` (at most 8192 FP8 or FP4 columns), 0
  * when the MFMA path does not take it */

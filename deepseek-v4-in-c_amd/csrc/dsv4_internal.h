@@ -174,12 +174,19 @@ struct GemvMxArgs {
     int rows, cols, row_bytes, sc_cols, blk_r;
     int nt, x_ld, y_ld;
     int ncw, tpg;
+    const uint8_t *tab;       /* x already split (split_x_tab_launch), or NULL */
+    int gpw;                  /* token groups per workgroup, with tab */
 };
 /* chunks of 128 columns per wave, 0 when the MFMA path does not take `cols` */
 int gemv_mx_ncw(int fmt, int cols);
 /* the same for the gate/up kernels (FP8 hidden at most 4096) */
 int gateup_mx_ncw(int fmt, int cols);
 hipError_t gemv_mx_launch(int fmt, GemvMxArgs a, hipStream_t st);
+/* nt tokens of x (x_ld floats apart, cols a multiple of 128, nt * cols / 8
+ * below 2^31) split into the small-batch matvec's e4m3 part tables, token t's
+ * chunk c at tab + (t * cols / 128 + c) * gemv_tab_chunk_bytes() */
+size_t gemv_tab_chunk_bytes();
+hipError_t split_x_tab_launch(uint8_t *tab, const float *x, int x_ld, int nt, int cols, hipStream_t st);
 /* whether a one-token FP8 matvec takes the chunk-pair kernel, which can run
  * up to PX8_MAX_JOBS such matvecs of the same format and width in one launch */
 constexpr int PX8_MAX_JOBS = 16;

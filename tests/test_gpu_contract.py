@@ -241,6 +241,48 @@ def test_mmq_n_token_groups(lib, pkg, oracle, nt, fmt):
     m.drop()
 
 
+@pytest.mark.parametrize("fmt,rows,cols,nt", [
+    ("fp8", 200, 1024, 7),      # rows past the last whole 16-row tile; one token group per workgroup
+    ("fp8f", 4096, 2048, 29),   # many row blocks: token groups split over workgroups
+    ("fp4", 72, 8192, 13),      # few row blocks: every token group in each workgroup
+])
+def test_mmq_n_presplit_shapes(lib, pkg, oracle, fmt, rows, cols, nt):
+    """From five tokens the MFMA GEMV splits x once and walks the token
+    groups with the weights held: ragged rows, many and few row blocks,
+    against the oracle, and bit for bit the same per token as the same
+    tokens in calls of two to four tokens, which split x inside the matvec
+    (a token's MFMA steps do not depend on the other tokens)."""
+    rng = np.random.default_rng(rows + cols + nt)
+    w = (rng.standard_normal((rows, cols)) * 0.02).astype(np.float32)
+    x = rng.standard_normal(nt * cols).astype(np.float32)
+    if fmt == "fp4":
+        W, S = oracle.quant_fp4_mx(w)
+        m = Resident(lib, pkg, pkg.DSV4_WFP4, W, S, rows, cols, 1, 32)
+        want = oracle.fp4_n(W, S, x, rows, cols, 1, 32, nt)
+    elif fmt == "fp8":
+        W = e4m3_codes(rng, rows * cols)
+        S = rng.integers(112, 121, ((rows + 127) // 128) * (cols // 128)).astype(np.uint8)
+        m = Resident(lib, pkg, pkg.DSV4_WFP8, W, S, rows, cols, 128, 128)
+        want = oracle.fp8_n(W, S, x, rows, cols, 128, 128, nt)
+    else:
+        W, S = oracle.quant_fp8_blk128(w)
+        m = Resident(lib, pkg, pkg.DSV4_WFP8_F32S, W, S, rows, cols, 128, 128)
+        want = oracle.fp8f_n(W, S, x, rows, cols, 128, 128, nt)
+    got = lib.mmq_n(m.desc, x, nt)
+    check_close(got, want)
+    got = got.reshape(nt, rows)
+    xs = x.reshape(nt, cols)
+    sizes = [4] * (nt // 4) + ([nt % 4] if nt % 4 else [])
+    if sizes[-1] == 1:                                     # one token would take the single-token matvec
+        sizes[-2:] = [3, 2]
+    t0 = 0
+    for n in sizes:
+        part = lib.mmq_n(m.desc, np.ascontiguousarray(xs[t0:t0 + n].reshape(-1)), n).reshape(n, rows)
+        assert np.array_equal(bits(part), bits(got[t0:t0 + n])), f"tokens {t0}..{t0 + n - 1}"
+        t0 += n
+    m.drop()
+
+
 # ------------------------------------------------------ seam GEMM (FP8) ----
 
 def _fp8_resident(lib, pkg, oracle, fmt, rng, rows, cols):
