@@ -358,6 +358,12 @@ hipError_t synth_normal_launch(float *out, size_t n, uint64_t seed, float sigma,
 
 /* ------------------------------------------------------ grouped MoE --- */
 
+/* One token tile of the grouped GEMMs: its bucket (expert), first bucket
+ * row and rows, so a workgroup finds its work in one load. */
+struct TileRec {
+    int grp, r0, ntok, pad;
+};
+
 /* counting sort of the npairs = n * topk routing ids by expert; rows inside
  * a bucket keep pair order (token-major, k-minor) */
 struct RouteArgs {
@@ -366,7 +372,7 @@ struct RouteArgs {
     int tile_rows;            /* rows per tile of the grouped GEMM        */
     int *grp_off;             /* [n_experts + 1] first row of each bucket */
     int *tile_pre;            /* [n_experts + 1] prefix of tiles          */
-    int *tile_grp;            /* [tiles] bucket (expert) of each tile     */
+    TileRec *tile_rec;        /* [tiles] bucket, first row, rows per tile */
     int *pos;                 /* [npairs] row of each pair (-1: bad id)   */
     int *row_tok;             /* [npairs] token of each row               */
     int *row_k;               /* [npairs] k of each row, or NULL          */
@@ -436,7 +442,8 @@ hipError_t to_f16_rows_launch(uint16_t *o, int *ex, const float *x, int rows, in
 struct GroupedArgs {
     const DSV4ExpertW *table;
     int n_experts;
-    const int *grp_off, *tile_pre, *tile_grp;
+    const int *grp_off, *tile_pre;
+    const TileRec *tile_rec;
     const int *row_tok;       /* B row of each output row, NULL = itself  */
     DSV4QMat m1, m3;
     int nrows;                /* rows of B                                */
@@ -460,7 +467,8 @@ hipError_t grouped_launch(int fmt, bool swiglu, int tt, const GroupedArgs &a, lo
 struct GroupedMxArgs {
     const DSV4ExpertW *table;
     int n_experts;
-    const int *grp_off, *tile_pre, *tile_grp;
+    const int *grp_off, *tile_pre;
+    const TileRec *tile_rec;
     const int *row_tok;       /* B row of each bucket row, NULL = itself  */
     const uint8_t *B;         /* e4m3 [nrows][K]                          */
     const uint8_t *BS;        /* E8M0 [nrows][K / 32]                     */

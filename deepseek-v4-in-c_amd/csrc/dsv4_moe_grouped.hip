@@ -17,6 +17,7 @@
  * PIPELINE (one stream, no host round trip)
  *   k_moe_route     counting sort by expert: first row of each expert's
  *                   bucket (grp_off), prefix of its token tiles (tile_pre),
+ *                   each tile's bucket, first row and rows (tile_rec),
  *                   each pair's row (pos) and each row's token (row_tok);
  *                   one launch, each workgroup placing its own chunks of
  *                   1024 pairs after counting all of them.
@@ -25,9 +26,9 @@
  *                   in [2^14, 2^15); the GEMM epilogues undo it exactly.
  *   k_grouped       one wave = one work item: an expert, a slab of output
  *                   features (64 for gate/up with both w1 and w3 rows, 128 for
- *                   down) and a tile of up to 16*TT of its rows. Item ids are
- *                   decoded on the device from tile_pre (binary search), so
- *                   the grid is an upper bound and surplus waves exit.
+ *                   down) and a tile of up to 16*TT of its rows, read from
+ *                   the tile's record; the grid is an upper bound and
+ *                   surplus waves exit.
  *   k_moe_combine   out[t] = sum_k w[t][k] * Y[pos(t, k)] (k order) + shared[t].
  *
  * NUMERICS
@@ -237,7 +238,8 @@ __global__ __launch_bounds__(1024) void k_moe_route_count(RouteArgs a)
  * PRECOUNT it sums them from the per-chunk counts k_moe_route_count wrote
  * (two launches); without, every workgroup counts every pair itself (one
  * launch, no workgroup waits for another: the form for a few chunks).
- * Workgroup 0 also writes grp_off, tile_pre and tile_grp; bad ids are
+ * Workgroup 0 also writes grp_off and tile_pre, every workgroup a share
+ * of the tile records; bad ids are
  * reported by workgroup 0 (one launch) or by the counting pass. */
 template <bool PRECOUNT>
 __global__ __launch_bounds__(1024) void k_moe_route(RouteArgs a, int cpb)
@@ -333,7 +335,8 @@ __global__ __launch_bounds__(1024) void k_moe_route(RouteArgs a, int cpb)
         __syncthreads();
     }
     /* each tile's bucket: the first expert whose inclusive tile prefix
-     * exceeds it, tiles spread over every workgroup's threads */
+     * exceeds it, tiles spread over every workgroup's threads; with the
+     * bucket's first row and the tile's rows */
     for (int t = blockIdx.x * 1024 + tid; t < scan_t[E - 1]; t += gridDim.x * 1024) {
         int lo = 0, hi = E - 1;
         while (lo < hi) {
@@ -341,7 +344,14 @@ __global__ __launch_bounds__(1024) void k_moe_route(RouteArgs a, int cpb)
             if (scan_t[mid] > t) hi = mid;
             else lo = mid + 1;
         }
-        a.tile_grp[t] = lo;
+        const int go = lo > 0 ? scan_r[lo - 1] : 0, tp = lo > 0 ? scan_t[lo - 1] : 0;
+        const int r0 = go + (t - tp) * a.tile_rows;
+        TileRec rec;
+        rec.grp = lo;
+        rec.r0 = r0;
+        rec.ntok = min(a.tile_rows, scan_r[lo] - r0);
+        rec.pad = 0;
+        a.tile_rec[t] = rec;
     }
     if (tid < E) {
         const int o = scan_r[tid] - cnt;
@@ -466,12 +476,12 @@ __global__ __launch_bounds__(256) void k_grouped(GroupedArgs a)
     DSV4QMat m1, m3;
     if (a.table) {
         const int E = a.n_experts;
-        if (tile >= ld_uniform(a.tile_pre, E)) return;
-        const int grp = ld_uniform(a.tile_grp, tile);   /* the bucket owning this tile */
-        const int go = ld_uniform(a.grp_off, grp), ge = ld_uniform(a.grp_off, grp + 1);
-        r0 = go + (tile - ld_uniform(a.tile_pre, grp)) * TROWS;
-        ntok = min(TROWS, ge - r0);
-        const DSV4ExpertW e = ld_uniform(a.table, grp);
+        const int ntiles = ld_uniform(a.tile_pre, E);
+        const TileRec tr = ld_uniform(a.tile_rec, tile);  /* read beside the count: one round trip */
+        if ((tile >= ntiles) | (tr.ntok <= 0)) return;
+        r0 = tr.r0;
+        ntok = tr.ntok;
+        const DSV4ExpertW e = ld_uniform(a.table, tr.grp);
         m1 = SWIGLU ? e.w1 : e.w2;
         m3 = e.w3;
     } else {
@@ -763,12 +773,12 @@ __global__ __launch_bounds__(512) void k_grouped2(GroupedArgs a)
     DSV4QMat m1, m3;
     if (a.table) {
         const int E = a.n_experts;
-        if (tile >= ld_uniform(a.tile_pre, E)) return;            /* whole workgroup */
-        const int lo = ld_uniform(a.tile_grp, tile);     /* the bucket owning this tile */
-        const int go = ld_uniform(a.grp_off, lo), ge = ld_uniform(a.grp_off, lo + 1);
-        r0 = go + (tile - ld_uniform(a.tile_pre, lo)) * C::TOK;
-        ntok = min(C::TOK, ge - r0);
-        const DSV4ExpertW e = ld_uniform(a.table, lo);
+        const int ntiles = ld_uniform(a.tile_pre, E);
+        const TileRec tr = ld_uniform(a.tile_rec, tile);  /* read beside the count: one round trip */
+        if ((tile >= ntiles) | (tr.ntok <= 0)) return;   /* whole workgroup */
+        r0 = tr.r0;
+        ntok = tr.ntok;
+        const DSV4ExpertW e = ld_uniform(a.table, tr.grp);
         m1 = SWIGLU ? e.w1 : e.w2;
         m3 = e.w3;
     } else {
@@ -1062,12 +1072,12 @@ __global__ __launch_bounds__(512) void k_grouped3(GroupedArgs a)
     DSV4QMat m1, m3;
     if (a.table) {
         const int E = a.n_experts;
-        if (tile >= ld_uniform(a.tile_pre, E)) return;            /* whole workgroup */
-        const int lo = ld_uniform(a.tile_grp, tile);
-        const int go = ld_uniform(a.grp_off, lo), ge = ld_uniform(a.grp_off, lo + 1);
-        r0 = go + (tile - ld_uniform(a.tile_pre, lo)) * C::TOK;
-        ntok = min(C::TOK, ge - r0);
-        const DSV4ExpertW e = ld_uniform(a.table, lo);
+        const int ntiles = ld_uniform(a.tile_pre, E);
+        const TileRec tr = ld_uniform(a.tile_rec, tile);  /* read beside the count: one round trip */
+        if ((tile >= ntiles) | (tr.ntok <= 0)) return;   /* whole workgroup */
+        r0 = tr.r0;
+        ntok = tr.ntok;
+        const DSV4ExpertW e = ld_uniform(a.table, tr.grp);
         m1 = SWIGLU ? e.w1 : e.w2;
         m3 = e.w3;
     } else {

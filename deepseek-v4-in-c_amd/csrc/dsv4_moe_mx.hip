@@ -191,12 +191,12 @@ __device__ __forceinline__ bool mx_item(const GroupedMxArgs &a, MxItem &it)
     const int nslab = a.N / FEAT;
     const int tile = blockIdx.x / nslab, slab = blockIdx.x - tile * nslab;
     const int E = a.n_experts;
-    if (tile >= ld_uniform(a.tile_pre, E)) return false;
-    const int grp = ld_uniform(a.tile_grp, tile);
-    const int go = ld_uniform(a.grp_off, grp), ge = ld_uniform(a.grp_off, grp + 1);
-    it.r0 = go + (tile - ld_uniform(a.tile_pre, grp)) * GX_TILE;
-    it.ntok = min(GX_TILE, ge - it.r0);
-    it.grp = grp;
+    const int ntiles = ld_uniform(a.tile_pre, E);
+    const TileRec tr = ld_uniform(a.tile_rec, tile);      /* read beside the count: one round trip */
+    if ((tile >= ntiles) | (tr.ntok <= 0)) return false;
+    it.r0 = tr.r0;
+    it.ntok = tr.ntok;
+    it.grp = tr.grp;
     it.f0 = slab * FEAT;
     return true;
 }

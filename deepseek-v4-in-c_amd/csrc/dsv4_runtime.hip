@@ -1495,7 +1495,7 @@ static int enqueue_moe_grouped(float *out, const float *x, int n, const DSV4Expe
     /* every bucket adds at most one partial tile */
     const long max_tiles = (P + trows - 1) / trows + n_experts;
     const size_t o_grp = take((size_t)(n_experts + 1) * 4), o_tp = take((size_t)(n_experts + 1) * 4);
-    const size_t o_tg = take((size_t)max_tiles * 4);
+    const size_t o_tg = take((size_t)(max_tiles + 4) * sizeof(TileRec));
     const size_t o_pos = take((size_t)P * 4), o_row = take((size_t)P * 4);
     const size_t o_ch = take(route_chist_bytes(P, n_experts));
     const size_t o_x16 = take((size_t)n * hidden * 2), o_mid = take((size_t)P * inter * 2);
@@ -1507,7 +1507,8 @@ static int enqueue_moe_grouped(float *out, const float *x, int n, const DSV4Expe
     }
     HIPCHK(g.moe_ws.need(off), "grouped MoE workspace");
     uint8_t *ws = (uint8_t *)g.moe_ws.p;
-    int *grp = (int *)(ws + o_grp), *tp = (int *)(ws + o_tp), *tg = (int *)(ws + o_tg);
+    int *grp = (int *)(ws + o_grp), *tp = (int *)(ws + o_tp);
+    TileRec *tg = (TileRec *)(ws + o_tg);
     int *pos = (int *)(ws + o_pos), *row = (int *)(ws + o_row);
     uint16_t *x16 = (uint16_t *)(ws + o_x16), *mid = (uint16_t *)(ws + o_mid);
     float *y = (float *)(ws + o_y);
@@ -1515,7 +1516,7 @@ static int enqueue_moe_grouped(float *out, const float *x, int n, const DSV4Expe
 
     RouteArgs ra;
     ra.idx = idx; ra.npairs = (int)P; ra.topk = topk; ra.n_experts = n_experts;
-    ra.tile_rows = trows; ra.grp_off = grp; ra.tile_pre = tp; ra.tile_grp = tg; ra.pos = pos;
+    ra.tile_rows = trows; ra.grp_off = grp; ra.tile_pre = tp; ra.tile_rec = tg; ra.pos = pos;
     ra.row_tok = row;
     ra.row_k = nullptr;
     ra.chist = (int *)(ws + o_ch);
@@ -1556,7 +1557,7 @@ static int enqueue_moe_grouped(float *out, const float *x, int n, const DSV4Expe
 
     GroupedArgs ga;
     memset(&ga, 0, sizeof ga);
-    ga.table = table; ga.n_experts = n_experts; ga.grp_off = grp; ga.tile_pre = tp; ga.tile_grp = tg;
+    ga.table = table; ga.n_experts = n_experts; ga.grp_off = grp; ga.tile_pre = tp; ga.tile_rec = tg;
     ga.row_tok = row; ga.nrows = n; ga.B = x16; ga.bexp = ex; ga.K = hidden; ga.N = inter;
     ga.out = mid; ga.limit = limit; ga.status = g.st;
     HIPCHK(grouped_launch(FMT_FP4_E8M0, true, tt, ga, max_tiles, st), "routed gate/up launch");
@@ -1610,7 +1611,7 @@ static int enqueue_moe_grouped_mx(float *out, const float *x, int n, const DSV4E
     auto take = [&](size_t b) { const size_t o = off; off += (b + 255) & ~(size_t)255; return o; };
     const long max_tiles = (P + trows - 1) / trows + n_experts;
     const size_t o_grp = take((size_t)(n_experts + 1) * 4), o_tp = take((size_t)(n_experts + 1) * 4);
-    const size_t o_tg = take((size_t)max_tiles * 4);
+    const size_t o_tg = take((size_t)(max_tiles + 4) * sizeof(TileRec));
     const size_t o_pos = take((size_t)P * 4), o_row = take((size_t)P * 4);
     const size_t o_ch = take(route_chist_bytes(P, n_experts));
     const size_t o_x8 = take((size_t)n * hidden), o_xs = take((size_t)n * hidden / 32);
@@ -1635,7 +1636,8 @@ static int enqueue_moe_grouped_mx(float *out, const float *x, int n, const DSV4E
     }
     HIPCHK(g.moe_ws.need(off), "grouped MoE workspace");
     uint8_t *ws = (uint8_t *)g.moe_ws.p;
-    int *grp = (int *)(ws + o_grp), *tp = (int *)(ws + o_tp), *tg = (int *)(ws + o_tg);
+    int *grp = (int *)(ws + o_grp), *tp = (int *)(ws + o_tp);
+    TileRec *tg = (TileRec *)(ws + o_tg);
     int *pos = (int *)(ws + o_pos), *row = (int *)(ws + o_row);
     uint8_t *x8 = ws + o_x8, *xs = ws + o_xs, *mid = ws + o_mid, *ms = ws + o_ms;
     float *y = (float *)(ws + o_y);
@@ -1650,7 +1652,7 @@ static int enqueue_moe_grouped_mx(float *out, const float *x, int n, const DSV4E
 
     RouteArgs ra;
     ra.idx = idx; ra.npairs = (int)P; ra.topk = topk; ra.n_experts = n_experts;
-    ra.tile_rows = trows; ra.grp_off = grp; ra.tile_pre = tp; ra.tile_grp = tg; ra.pos = pos;
+    ra.tile_rows = trows; ra.grp_off = grp; ra.tile_pre = tp; ra.tile_rec = tg; ra.pos = pos;
     ra.row_tok = row;
     ra.row_k = nullptr;
     ra.chist = (int *)(ws + o_ch);
@@ -1686,7 +1688,7 @@ static int enqueue_moe_grouped_mx(float *out, const float *x, int n, const DSV4E
     HIPCHK(hipStreamWaitEvent(st, g.xq, 0), "quant wait");
     GroupedMxArgs ga;
     memset(&ga, 0, sizeof ga);
-    ga.table = table; ga.n_experts = n_experts; ga.grp_off = grp; ga.tile_pre = tp; ga.tile_grp = tg;
+    ga.table = table; ga.n_experts = n_experts; ga.grp_off = grp; ga.tile_pre = tp; ga.tile_rec = tg;
     ga.row_tok = row; ga.B = x8; ga.BS = xs; ga.nrows = n; ga.K = hidden; ga.N = inter;
     ga.out = mid; ga.out_s = ms; ga.limit = limit; ga.status = g.st;
     /* thin tiles (weight streaming) on a second side stream, beside the fat
@@ -1861,14 +1863,14 @@ int dsv4_hip_moe_grouped_mx_mid_dev(uint8_t *mid, uint8_t *mid_s, int *row_tok, 
     size_t off = 0;
     auto take = [&](size_t b) { const size_t o = off; off += (b + 255) & ~(size_t)255; return o; };
     const size_t o_grp = take((size_t)(n_experts + 1) * 4), o_tp = take((size_t)(n_experts + 1) * 4);
-    const size_t o_tg = take((size_t)max_tiles * 4), o_pos = take((size_t)P * 4);
+    const size_t o_tg = take((size_t)(max_tiles + 4) * sizeof(TileRec)), o_pos = take((size_t)P * 4);
     const size_t o_ch = take(route_chist_bytes(P, n_experts));
     const size_t o_x8 = take((size_t)n * hidden), o_xs = take((size_t)n * hidden / 32);
     HIPCHK(g.moe_ws.need(off), "grouped MoE workspace");
     uint8_t *ws = (uint8_t *)g.moe_ws.p;
     RouteArgs ra;
     ra.idx = idx; ra.npairs = (int)P; ra.topk = topk; ra.n_experts = n_experts; ra.tile_rows = trows;
-    ra.grp_off = (int *)(ws + o_grp); ra.tile_pre = (int *)(ws + o_tp); ra.tile_grp = (int *)(ws + o_tg);
+    ra.grp_off = (int *)(ws + o_grp); ra.tile_pre = (int *)(ws + o_tp); ra.tile_rec = (TileRec *)(ws + o_tg);
     ra.pos = (int *)(ws + o_pos); ra.row_tok = row_tok; ra.row_k = row_k; ra.status = g.st;
     ra.chist = (int *)(ws + o_ch);
     HIPCHK(moe_route_launch(ra, st), "route launch");
@@ -1876,7 +1878,7 @@ int dsv4_hip_moe_grouped_mx_mid_dev(uint8_t *mid, uint8_t *mid_s, int *row_tok, 
     GroupedMxArgs ga;
     memset(&ga, 0, sizeof ga);
     ga.table = experts; ga.n_experts = n_experts; ga.grp_off = ra.grp_off; ga.tile_pre = ra.tile_pre;
-    ga.tile_grp = ra.tile_grp; ga.row_tok = row_tok; ga.B = ws + o_x8; ga.BS = ws + o_xs; ga.nrows = n;
+    ga.tile_rec = ra.tile_rec; ga.row_tok = row_tok; ga.B = ws + o_x8; ga.BS = ws + o_xs; ga.nrows = n;
     ga.K = hidden; ga.N = inter; ga.out = mid; ga.out_s = mid_s; ga.limit = limit; ga.status = g.st;
     HIPCHK(grouped_mx_launch(true, ga, max_tiles, st, st), "routed gate/up launch");
     return 0;
@@ -1970,13 +1972,13 @@ int dsv4_hip_moe_route_dev(int *ex_off, int *ex_tok, int *ex_k, int *pos, const 
     const int trows = 16;
     const long max_tiles = (P + trows - 1) / trows + n_experts;
     const size_t o_tp = 0, o_tg = (((size_t)n_experts + 1) * 4 + 255) & ~(size_t)255;
-    const size_t o_ch = (o_tg + (size_t)max_tiles * 4 + 255) & ~(size_t)255;
+    const size_t o_ch = (o_tg + (size_t)(max_tiles + 4) * sizeof(TileRec) + 255) & ~(size_t)255;
     HIPCHK(g.small.need(o_ch + route_chist_bytes(P, n_experts)), "route workspace");
     RouteArgs ra;
     ra.idx = idx; ra.npairs = (int)P; ra.topk = topk; ra.n_experts = n_experts;
     ra.tile_rows = trows; ra.grp_off = ex_off;
     ra.tile_pre = (int *)((uint8_t *)g.small.p + o_tp);
-    ra.tile_grp = (int *)((uint8_t *)g.small.p + o_tg);
+    ra.tile_rec = (TileRec *)((uint8_t *)g.small.p + o_tg);
     ra.pos = pos; ra.row_tok = ex_tok; ra.row_k = ex_k; ra.status = g.st;
     ra.chist = (int *)((uint8_t *)g.small.p + o_ch);
     HIPCHK(moe_route_launch(ra, (hipStream_t)stream), "route launch");
