@@ -712,7 +712,13 @@ __device__ __forceinline__ void dma4(const void *src, uint8_t *dst)
     __builtin_amdgcn_global_load_lds(gptr(src), (lds_void *)dst, 4, 0, 0);
 }
 
+/* Default ring depth: FP4 16-row tiles two stages (2 x 25 KiB, three
+ * workgroups per CU overlap each other's pipeline ramp), FP8 16-row tiles
+ * three (3 x 40 KiB), 64-row tiles FP4 three, FP8 two. */
 template <int WF, int TT>
+constexpr int g2_stages() { return TT == 1 ? (WF == FMT_FP4_E8M0 ? 2 : 3) : (WF == FMT_FP4_E8M0 ? 3 : 2); }
+
+template <int WF, int TT, int STAGES = g2_stages<WF, TT>()>
 struct G2 {
     static constexpr bool FP4 = WF == FMT_FP4_E8M0;
     static constexpr int WB = FP4 ? KS / 2 : KS;         /* weight bytes per row per stage */
@@ -727,9 +733,7 @@ struct G2 {
     static constexpr int OFF_PAD = OFF_S + (FP4 ? ROWS * 8 : 0);   /* scale loads of waves 4+ */
     static constexpr int OFF_B = OFF_PAD + (FP4 && NWAVE > 4 ? 256 : 0);
     static constexpr int STAGE = OFF_B + TOK * KS * 2;
-    /* FP4 16-row tiles: 3 x 25 KiB, two workgroups per CU overlap each
-     * other's pipeline ramp */
-    static constexpr int NST = (FP4 && TT == 1) ? 2 : (FP4 || TT == 1) ? 3 : 2;
+    static constexpr int NST = STAGES;
     static constexpr int LDS = NST * STAGE;
     static constexpr int NW = ROWS * WB / 1024 / NWAVE;  /* weight loads per wave per stage */
     static constexpr int NS = FP4 ? 1 : 0;               /* scale loads                */
@@ -756,10 +760,10 @@ __device__ __forceinline__ int bchunk(int gq, int sg)
 
 } // namespace
 
-template <int WF, bool SWIGLU, int TT>
+template <int WF, bool SWIGLU, int TT, int NS>
 __global__ __launch_bounds__(512) void k_grouped2(GroupedArgs a)
 {
-    using C = G2<WF, TT>;
+    using C = G2<WF, TT, NS>;
     constexpr bool FP4 = C::FP4;
     constexpr int FEAT = SWIGLU ? 64 : 128;
     extern __shared__ __align__(16) uint8_t lds[];
@@ -1323,20 +1327,43 @@ hipError_t to_f16_rows_launch(uint16_t *o, int *ex, const float *x, int rows, in
 
 int grouped_rows_per_tile(int tt) { return 16 * tt; }
 
-template <int WF, bool SW, int TT>
-static hipError_t grouped2(const GroupedArgs &a, long items, hipStream_t st)
+template <int WF, bool SW, int TT, int NS>
+static hipError_t grouped2_ns(const GroupedArgs &a, long items, hipStream_t st)
 {
     static bool attr_done = false;
     if (!attr_done) {
-        const hipError_t e = hipFuncSetAttribute((const void *)k_grouped2<WF, SW, TT>,
+        const hipError_t e = hipFuncSetAttribute((const void *)k_grouped2<WF, SW, TT, NS>,
                                                  hipFuncAttributeMaxDynamicSharedMemorySize,
-                                                 G2<WF, TT>::LDS);
+                                                 G2<WF, TT, NS>::LDS);
         if (e != hipSuccess) return e;
         attr_done = true;
     }
-    constexpr int lds_bytes = G2<WF, TT>::LDS, threads = 64 * G2<WF, TT>::NWAVE;
-    hipLaunchKernelGGL((k_grouped2<WF, SW, TT>), dim3((unsigned)items), dim3(threads), lds_bytes, st, a);
+    constexpr int lds_bytes = G2<WF, TT, NS>::LDS, threads = 64 * G2<WF, TT, NS>::NWAVE;
+    hipLaunchKernelGGL((k_grouped2<WF, SW, TT, NS>), dim3((unsigned)items), dim3(threads), lds_bytes, st, a);
     return hipGetLastError();
+}
+
+/* FP8 16-row tiles: when the grid outnumbers the CUs, two stages (2 x 40
+ * KiB) so two workgroups share a CU (4096 x 4096 FP8 drop-in matmul, 192
+ * tokens in 384 workgroups: 36.1 -> 29.7 us); up to one workgroup per CU the
+ * three-stage ring keeps more of a lone workgroup's loads in flight (128
+ * tokens 23.7 against 24.3 us, the batched decode's shared expert). */
+template <int WF, bool SW, int TT>
+static hipError_t grouped2(const GroupedArgs &a, long items, hipStream_t st)
+{
+    if constexpr (WF != FMT_FP4_E8M0 && TT == 1) {
+        static int cus = 0;
+        if (cus == 0) {
+            int dev = 0;
+            if (hipGetDevice(&dev) != hipSuccess ||
+                hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) {
+                (void)hipGetLastError();
+                cus = 256;
+            }
+        }
+        if (items > cus) return grouped2_ns<WF, SW, TT, 2>(a, items, st);
+    }
+    return grouped2_ns<WF, SW, TT, g2_stages<WF, TT>()>(a, items, st);
 }
 
 template <int WF, bool SW>

@@ -339,6 +339,26 @@ def test_seam_gemm_bits_equal_grouped_form(lib, pkg, oracle, fmt):
     m.drop()
 
 
+@pytest.mark.parametrize("fmt", ["fp8", "fp8f"])
+def test_fp8_16_token_tiles_ring_depths(lib, pkg, oracle, fmt):
+    """FP8 weights, 32-192 tokens: 16-token tiles with a two-stage ring when
+    the grid outnumbers the CUs (150 tokens x 4096 rows: 320 workgroups),
+    a three-stage ring otherwise (the first 96 tokens alone: 192). Against
+    the oracle, and the shared tokens bit for bit the same in both."""
+    rows, cols, nt, nt_small = 4096, 1024, 150, 96
+    rng = np.random.default_rng(150 + len(fmt))
+    m, want_of = _fp8_resident(lib, pkg, oracle, fmt, rng, rows, cols)
+    x = rng.standard_normal(nt * cols).astype(np.float32)
+    got = lib.mmq_n(m.desc, x, nt).reshape(nt, rows)
+    want = want_of(x, nt).reshape(nt, rows)
+    for t in range(nt):
+        e = rel_l2(got[t], want[t])
+        assert e <= REL_L2_TOL, f"token {t}: rel L2 {e:.3e}"
+    small = lib.mmq_n(m.desc, np.ascontiguousarray(x[:nt_small * cols]), nt_small).reshape(nt_small, rows)
+    assert np.array_equal(bits(small), bits(got[:nt_small]))
+    m.drop()
+
+
 # ------------------------------------------------ 0 means the whole result ----
 
 def test_scale_byte_outside_fp16_range_returns_minus1(lib, pkg, oracle):
