@@ -243,8 +243,9 @@ def test_mmq_n_token_groups(lib, pkg, oracle, nt, fmt):
 
 @pytest.mark.parametrize("fmt,rows,cols,nt", [
     ("fp8", 200, 1024, 7),      # rows past the last whole 16-row tile; one token group per workgroup
-    ("fp8f", 4096, 2048, 29),   # many row blocks: token groups split over workgroups
-    ("fp4", 72, 8192, 13),      # few row blocks: every token group in each workgroup
+    ("fp8f", 4096, 2048, 29),   # 256 row blocks: 8 groups walked four per workgroup, the last of one token
+    ("fp8", 2048, 4096, 27),    # 128 row blocks: 14 two-token groups in parts of 4, 4, 4 and 2
+    ("fp4", 72, 8192, 13),      # five row blocks, one-token groups: one group per workgroup
 ])
 def test_mmq_n_presplit_shapes(lib, pkg, oracle, fmt, rows, cols, nt):
     """From five tokens the MFMA GEMV splits x once and walks the token
